@@ -1,0 +1,18 @@
+"""htree_amd: hierarchical tree sparse attention on MI355X (gfx950).
+
+Drop-in for the reference's src/parallel.py / src/backward.py entry points:
+    htree_forward(q, k, v, compression_rate, max_top_nodes, top_k_per_layer,
+                  scale, rope_base, _save_for_backward, _save_parents)
+    htree_backward(dO, q, output, bwd_ctx) -> (dq, dk, dv)
+    htree_forward_triton_autograd(q, k, v, ...)   (name kept for drop-in use;
+                                                   runs the HIP kernels)
+"""
+from .parallel import (HTREE_SCORE_NEG_INF, HTREE_SCORE_VALID_THRESHOLD, htree_forward,
+                       htree_forward_parents, rope_cache)
+
+
+__all__ = [
+    "htree_forward", "htree_forward_parents", "htree_backward", "htree_forward_triton_autograd",
+    "htree_forward_autograd", "HTreeTritonFunction", "HTreeFunction", "rope_cache",
+    "HTREE_SCORE_NEG_INF", "HTREE_SCORE_VALID_THRESHOLD",
+]

@@ -1,0 +1,122 @@
+// Shared device helpers and the tree-workspace plan for the htree HIP kernels
+// (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "htree.h"
+
+namespace htree {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kWavesPerBlock = 4;
+constexpr int kMaxTK = 64;
+
+// ---------------------------------------------------------------- plan
+// Packed operand tree, per level l (all bf16, Np = N rounded up to 16):
+//   KH/KL [B][H_kv][Np][D]      hi / lo bf16 split of R(K_l[node], node mod CR)
+//   VH/VL [B][H_kv][Np/16][D][16]  V_l transposed in blocks of 16 nodes
+// Scores always use the split product (plain bf16 scores err by ~2e-2 when
+// |q||k| is large, e.g. clustered keys); VL exists for fp32/fp16 inputs only
+// (bf16 V is exact in VH).
+// Rows >= N of the padding are zero.
+struct Plan {
+  int L;
+  bool precise;  // fp32 / fp16 inputs: split operands everywhere
+  int64_t N[HTREE_MAX_LEVELS];
+  int64_t Np[HTREE_MAX_LEVELS];
+  int64_t pw[HTREE_MAX_LEVELS];  // CR^l
+  int64_t off_kh[HTREE_MAX_LEVELS], off_kl[HTREE_MAX_LEVELS];
+  int64_t off_vh[HTREE_MAX_LEVELS], off_vl[HTREE_MAX_LEVELS];
+  int64_t bytes;
+  int max_tiles;  // candidate tiles of 16 per level: TK * max(CR,16) / 16
+  int cr_log2;
+};
+
+int make_plan(const htree_dims* d, Plan* p);
+
+// ---------------------------------------------------------------- device
+__device__ __forceinline__ f32x4 mma32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma16(s16x4 a, s16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float bf_to_f(uint16_t x) {
+  return __uint_as_float((uint32_t)x << 16);
+}
+__device__ __forceinline__ uint16_t f_to_bf(float x) {  // round to nearest even
+  __bf16 b = (__bf16)x;
+  return __builtin_bit_cast(uint16_t, b);
+}
+__device__ __forceinline__ short f_to_bfs(float x) { return (short)f_to_bf(x); }
+
+// hi + lo bf16 split of an fp32 value (|x - hi - lo| <= 2^-17 |x|)
+__device__ __forceinline__ void split_bf(float x, uint16_t& hi, uint16_t& lo) {
+  hi = f_to_bf(x);
+  lo = f_to_bf(x - bf_to_f(hi));
+}
+
+template <typename T>
+struct Io;
+template <>
+struct Io<float> {
+  static __device__ __forceinline__ float ld(const float* p) { return *p; }
+  static __device__ __forceinline__ void st(float* p, float v) { *p = v; }
+  static __device__ __forceinline__ void ld8(const float* p, float* o) {
+    float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  }
+};
+template <>
+struct Io<__bf16> {
+  static __device__ __forceinline__ float ld(const __bf16* p) { return (float)*p; }
+  static __device__ __forceinline__ void st(__bf16* p, float v) { *p = (__bf16)v; }
+  static __device__ __forceinline__ void ld8(const __bf16* p, float* o) {
+    uint4 r = *(const uint4*)p;
+    uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = __uint_as_float(w[i] << 16);
+      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+};
+template <>
+struct Io<_Float16> {
+  static __device__ __forceinline__ float ld(const _Float16* p) { return (float)*p; }
+  static __device__ __forceinline__ void st(_Float16* p, float v) { *p = (_Float16)v; }
+  static __device__ __forceinline__ void ld8(const _Float16* p, float* o) {
+    typedef __attribute__((ext_vector_type(8))) _Float16 h8;
+    h8 r = *(const h8*)p;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (float)r[i];
+  }
+};
+
+// Orders LDS traffic between the lanes of one wave (no block barrier: each
+// wave of a block works on its own query group).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+__device__ __forceinline__ int mbcnt64(unsigned long long m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                   __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+}
+
+}  // namespace htree

@@ -1,0 +1,453 @@
+// Fused htree forward: one wave per query group (b, t, h_kv) walks every
+// tree level top -> bottom with its online-softmax state in registers.
+//
+// Reference behaviour (file:line in /root/reference):
+//   candidate expansion, rightmost truncation ...... src/naive.py:180-191,
+//                                                    src/parallel.py:409-426
+//   RoPE on q at n_c-1 and on k at the flat position src/naive.py:193-199
+//   group-shared importance, forced rightmost,
+//   stable top-k (lower position wins ties) ....... src/naive.py:88-105,201-207,
+//                                                    src/parallel.py:721-771
+//   online softmax of the non-selected candidates . src/naive.py:73-85,209-213
+//   cross-level merge, out = o / s ................. src/naive.py:215-231,
+//                                                    src/parallel.py:248-363
+//
+// Layout of the work (gfx950, wave64, MFMA 16x16):
+//   candidates are processed in tiles of 16 consecutive children of one
+//   parent (one tile per parent when CR < 16).  RoPE uses angle addition:
+//   R(q, a) . R(k, j) = R(q, a - s*CR) . R(k, j mod CR) for j in parent slot
+//   s, so K is stored pre-rotated by its node's child index and the query is
+//   rotated once per tile.
+//   Scores use a split-bf16 product (qh*kh + qh*kl + ql*kh, error ~1e-5 of
+//   |q||k| scale); P.V uses plain bf16 for bf16 inputs (V exact, P rounded)
+//   and the split product for fp32/fp16 inputs.
+//   O is accumulated transposed (O^T = V^T P^T) so that each lane owns one
+//   query head and the softmax rescale needs no cross-lane traffic.
+#include <string.h>
+
+#include "htree_common.h"
+
+namespace htree {
+
+struct LevelPtrs {
+  const uint16_t* kh;
+  const uint16_t* kl;
+  const uint16_t* vh;
+  const uint16_t* vl;
+  int64_t N, Np, pw;
+};
+
+struct FwdArgs {
+  LevelPtrs lv[HTREE_MAX_LEVELS];
+  const void* q;
+  void* out;
+  float* gmax;
+  float* gsum;
+  int32_t* parents;
+  const float* cosb;
+  const float* sinb;
+  int32_t B, T, H, Hkv, G, CR, crlg, TK, L;
+  float scale;
+  int32_t per_xcd;
+};
+
+template <int MAXSLOT>
+struct WaveLds {
+  int32_t par[2][kMaxTK];
+  float imp[MAXSLOT * 64];
+  float mt[MAXSLOT * 4];
+  unsigned long long selmask[MAXSLOT];
+};
+
+// d-slot of k-step m for lane group kg: the four lane groups cover 8
+// consecutive elements each; steps m and m + D/64 hold the RoPE pair
+// (d, d + D/2) so both halves of a pair live in the same lane.
+template <int D>
+__device__ __forceinline__ int dslot(int kg, int m) {
+  constexpr int SPH = D / 64;
+  return 8 * kg + 32 * (m % SPH) + (D / 2) * (m / SPH);
+}
+
+// Rotates the lane's query fragment by table row `row` (R(x,p) of
+// src/naive.py:22-28).
+template <int D>
+__device__ __forceinline__ void rot_q(const float (&qf)[D / 32][8], const float* __restrict__ cosr,
+                                      const float* __restrict__ sinr, int kg,
+                                      float (&qr)[D / 32][8]) {
+  constexpr int SPH = D / 64;
+#pragma unroll
+  for (int m = 0; m < SPH; ++m) {
+    const int i0 = dslot<D>(kg, m);
+    float c[8], s[8];
+    Io<float>::ld8(cosr + i0, c);
+    Io<float>::ld8(sinr + i0, s);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float lo = qf[m][e], hi = qf[m + SPH][e];
+      qr[m][e] = lo * c[e] - hi * s[e];
+      qr[m + SPH][e] = lo * s[e] + hi * c[e];
+    }
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void to_bf(const float (&x)[D / 32][8], bf16x8 (&h)[D / 32]) {
+#pragma unroll
+  for (int m = 0; m < D / 32; ++m)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[m][e] = (__bf16)x[m][e];
+}
+
+template <int D>
+__device__ __forceinline__ void to_bf_split(const float (&x)[D / 32][8], bf16x8 (&h)[D / 32],
+                                            bf16x8 (&lo)[D / 32]) {
+#pragma unroll
+  for (int m = 0; m < D / 32; ++m)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const __bf16 hb = (__bf16)x[m][e];
+      h[m][e] = hb;
+      lo[m][e] = (__bf16)(x[m][e] - (float)hb);
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void load_kfrag(const uint16_t* __restrict__ row, int kg,
+                                           bf16x8 (&f)[D / 32]) {
+#pragma unroll
+  for (int m = 0; m < D / 32; ++m) f[m] = *(const bf16x8*)(row + dslot<D>(kg, m));
+}
+
+template <int D, bool PREC, typename TIn, int MAXSLOT>
+__global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
+  constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
+  __shared__ WaveLds<MAXSLOT> lds_all[kWavesPerBlock];
+
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int u16 = lane & 15, kg = lane >> 4;
+  // XCD-aware order: hardware deals blocks round-robin over the 8 XCDs; give
+  // each XCD a contiguous range of query groups (same (b, h_kv) tree).
+  const int bid = blockIdx.x;
+  const int64_t lb = (int64_t)(bid & 7) * a.per_xcd + (bid >> 3);
+  const int64_t grp = lb * kWavesPerBlock + wv;
+  if (grp >= (int64_t)a.B * a.Hkv * a.T) return;
+  const int t = (int)(grp % a.T);
+  const int bh = (int)(grp / a.T);
+  const int h = bh % a.Hkv;
+  const int b = bh / a.Hkv;
+  WaveLds<MAXSLOT>& W = lds_all[wv];
+  const int G = a.G, CR = a.CR, crlg = a.crlg, TK = a.TK;
+  const int CRU = CR < 16 ? CR : 16;
+  const bool wide = CR >= 16;
+
+  // query fragment: lane holds q[g = u16][d-slots of kg], pre-scaled
+  float qf[KS][8];
+  {
+    const bool gv = u16 < G;
+    const TIn* qp = (const TIn*)a.q + (((int64_t)b * a.T + t) * a.H + h * G + (gv ? u16 : 0)) * D;
+#pragma unroll
+    for (int m = 0; m < KS; ++m) {
+      Io<TIn>::ld8(qp + dslot<D>(kg, m), qf[m]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[m][e] = gv ? qf[m][e] * a.scale : 0.f;
+    }
+  }
+
+  float m_run = -INFINITY, l_part = 0.f;
+  f32x4 O[ND];
+#pragma unroll
+  for (int n = 0; n < ND; ++n) O[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // virtual parents of the top level (src/naive.py:108-118)
+  {
+    const int64_t nvp = (t / a.lv[a.L - 1].pw) / CR + 1;
+    if (lane < TK) W.par[0][lane] = lane < nvp ? lane : -1;
+  }
+  int cur = 0;
+
+  for (int l = a.L - 1; l >= 0; --l) {
+    wave_sync();
+    const LevelPtrs P = a.lv[l];
+    const int pv = lane < TK ? W.par[cur][lane] : -1;
+    const int np = __popcll(__ballot(pv >= 0));
+    if (np <= 0) break;  // unreachable: every level keeps >= 1 parent
+    const int ct = (int)((t / P.pw) & (CR - 1));
+    const int nc = ((np - 1) << crlg) + ct + 1;
+    const int apos = nc - 1;
+    const int nt = wide ? (nc + 15) >> 4 : np;
+    if (a.parents && lane < TK)
+      a.parents[((((int64_t)l * a.B + b) * a.T + t) * a.Hkv + h) * TK + lane] = pv;
+    const int64_t hrow = ((int64_t)b * a.Hkv + h) * P.Np;
+    const uint16_t* KH = P.kh + hrow * D;
+    const uint16_t* KL = P.kl + hrow * D;
+    const uint16_t* VH = P.vh + hrow * D;
+    const uint16_t* VL = PREC ? P.vl + hrow * D : nullptr;
+    const bool upper = l > 0;
+
+    // ------------------------------------------------ selection (upper levels)
+    if (upper) {
+      float Mrun = -INFINITY;
+      for (int tau = 0; tau < nt; ++tau) {
+        const int s = wide ? (tau << 4) >> crlg : tau;
+        const int node0 = (W.par[cur][s] << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0);
+        const int prow = apos - (s << crlg);
+        float qr[KS][8];
+        rot_q<D>(qf, a.cosb + (int64_t)prow * HALF, a.sinb + (int64_t)prow * HALF, kg, qr);
+        bf16x8 qh[KS], ql[KS];
+        to_bf_split<D>(qr, qh, ql);
+        const int pos = wide ? (tau << 4) + u16 : (tau << crlg) + u16;
+        const bool cv = u16 < CRU && pos < nc;
+        const uint16_t* krow = KH + (int64_t)(node0 + (cv ? u16 : 0)) * D;
+        const uint16_t* klrow = KL + (int64_t)(node0 + (cv ? u16 : 0)) * D;
+        bf16x8 kh[KS], kl[KS];
+        load_kfrag<D>(krow, kg, kh);
+        load_kfrag<D>(klrow, kg, kl);
+        f32x4 S = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < KS; ++m) {
+          S = mma32(qh[m], kh[m], S);
+          S = mma32(qh[m], kl[m], S);
+          S = mma32(ql[m], kh[m], S);
+        }
+        // S[r] = score[g = 4kg + r][candidate u16]
+        float tm = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (cv && 4 * kg + r < G) tm = fmaxf(tm, S[r]);
+        tm = wave_max(tm);
+        Mrun = fmaxf(Mrun, tm);
+        float e = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (cv && 4 * kg + r < G) e += expf(S[r] - Mrun);
+        e += __shfl_xor(e, 16);
+        e += __shfl_xor(e, 32);
+        if (kg == 0) W.imp[(tau << 4) + u16] = e;
+        if (lane == 0) W.mt[tau] = Mrun;
+      }
+      wave_sync();
+
+      // importance of position j lives in lane j % 64 of slot j / 64; the
+      // key is the float's bit pattern + 1 (0 = no candidate), so unsigned
+      // order is importance order and exact ties are resolved by position.
+      const int take = TK < nc ? TK : nc;
+      const int nslot = (nt + 3) >> 2;
+      uint32_t key[MAXSLOT];
+#pragma unroll
+      for (int sl = 0; sl < MAXSLOT; ++sl) {
+        key[sl] = 0u;
+        if (sl < nslot) {
+          const int tau = 4 * sl + kg;
+          const int pos = wide ? (tau << 4) + u16 : (tau << crlg) + u16;
+          if (tau < nt && u16 < CRU && pos < nc) {
+            float v;
+            if (pos == apos) {
+              v = 1e6f;  // rightmost candidate always kept (src/naive.py:93)
+            } else {
+              v = W.imp[64 * sl + lane];
+              const float mt = W.mt[tau];
+              if (mt != Mrun) v *= expf(mt - Mrun);
+            }
+            key[sl] = __float_as_uint(v) + 1u;
+          }
+        }
+      }
+      uint32_t thr = 0u;
+      for (int bit = 30; bit >= 0; --bit) {
+        const uint32_t c = thr | (1u << bit);
+        int cnt = 0;
+#pragma unroll
+        for (int sl = 0; sl < MAXSLOT; ++sl)
+          if (sl < nslot) cnt += __popcll(__ballot(key[sl] >= c));
+        if (cnt >= take) thr = c;
+      }
+      int ngt = 0;
+#pragma unroll
+      for (int sl = 0; sl < MAXSLOT; ++sl)
+        if (sl < nslot) ngt += __popcll(__ballot(key[sl] > thr));
+      const int need = take - ngt;
+      int eq_before = 0, sel_before = 0;
+      const int nxt = cur ^ 1;
+#pragma unroll
+      for (int sl = 0; sl < MAXSLOT; ++sl) {
+        if (sl < nslot) {
+          const unsigned long long em = __ballot(key[sl] == thr);
+          const bool sel = key[sl] > thr || (key[sl] == thr && eq_before + mbcnt64(em) < need);
+          const unsigned long long sm = __ballot(sel);
+          if (lane == 0) W.selmask[sl] = sm;
+          if (sel) {
+            const int tau = 4 * sl + kg;
+            const int s = wide ? (tau << 4) >> crlg : tau;
+            const int node =
+                (W.par[cur][s] << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0) + u16;
+            W.par[nxt][sel_before + mbcnt64(sm)] = node;
+          }
+          eq_before += __popcll(em);
+          sel_before += __popcll(sm);
+        }
+      }
+      if (lane >= take && lane < TK) W.par[nxt][lane] = -1;
+      wave_sync();
+    }
+
+    // ------------------------------------------------ accumulation
+    for (int tau = 0; tau < nt; ++tau) {
+      const int s = wide ? (tau << 4) >> crlg : tau;
+      const int node0 = (W.par[cur][s] << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0);
+      const int prow = apos - (s << crlg);
+      const unsigned long long smask = upper ? W.selmask[tau >> 2] : 0ull;
+      float qr[KS][8];
+      rot_q<D>(qf, a.cosb + (int64_t)prow * HALF, a.sinb + (int64_t)prow * HALF, kg, qr);
+      bf16x8 qh[KS], ql[KS];
+      to_bf_split<D>(qr, qh, ql);
+      const int posk = wide ? (tau << 4) + u16 : (tau << crlg) + u16;
+      const bool cvk = u16 < CRU && posk < nc;
+      const int64_t krow = (int64_t)(node0 + (cvk ? u16 : 0)) * D;
+      bf16x8 kh[KS], kl[KS];
+      load_kfrag<D>(KH + krow, kg, kh);
+      load_kfrag<D>(KL + krow, kg, kl);
+      f32x4 S = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < KS; ++m) {
+        S = mma32(kh[m], qh[m], S);
+        S = mma32(kl[m], qh[m], S);
+        S = mma32(kh[m], ql[m], S);
+      }
+      // S[r] = score[candidate 4kg + r][g = u16]
+      float sv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int cu = 4 * kg + r;
+        const int pos = wide ? (tau << 4) + cu : (tau << crlg) + cu;
+        const bool ok = cu < CRU && pos < nc && !((smask >> ((16 * (tau & 3) + cu) & 63)) & 1ull);
+        sv[r] = ok ? S[r] : -INFINITY;
+      }
+      float tm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+      tm = fmaxf(tm, __shfl_xor(tm, 16));
+      tm = fmaxf(tm, __shfl_xor(tm, 32));
+      if (!__any(tm > -INFINITY)) continue;  // every candidate of the tile passed down
+      const float mnew = fmaxf(m_run, tm);
+      const float mref = mnew == -INFINITY ? 0.f : mnew;
+      const float alpha = __builtin_amdgcn_exp2f((m_run - mref) * kLog2e);
+      m_run = mnew;
+      float p[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f((sv[r] - mref) * kLog2e);
+      l_part = l_part * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+#pragma unroll
+      for (int n = 0; n < ND; ++n) O[n] *= alpha;
+      s16x4 ph, pl;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint16_t hb = f_to_bf(p[r]);
+        ph[r] = (short)hb;
+        pl[r] = PREC ? f_to_bfs(p[r] - bf_to_f(hb)) : (short)0;
+      }
+      // V^T fragment: nodes node0 + 4kg + 0..3 at d = 16n + u16
+      const int vn = node0 + (4 * kg < CRU ? 4 * kg : 0);
+      const int64_t vbase = ((int64_t)(vn >> 4) * D + u16) * 16 + (vn & 15);
+#pragma unroll
+      for (int n = 0; n < ND; ++n) {
+        const s16x4 vf = *(const s16x4*)(VH + vbase + (int64_t)n * 256);
+        O[n] = mma16(vf, ph, O[n]);
+        if (PREC) {
+          const s16x4 vfl = *(const s16x4*)(VL + vbase + (int64_t)n * 256);
+          O[n] = mma16(vf, pl, O[n]);
+          O[n] = mma16(vfl, ph, O[n]);
+        }
+      }
+    }
+    cur ^= 1;
+  }
+
+  // final normalisation (src/parallel.py:321-363): out = o / s
+  float lt = l_part + __shfl_xor(l_part, 16);
+  lt += __shfl_xor(lt, 32);
+  if (u16 < G) {
+    const int64_t hq = ((int64_t)b * a.T + t) * a.H + h * G + u16;
+    TIn* op = (TIn*)a.out + hq * D;
+#pragma unroll
+    for (int n = 0; n < ND; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Io<TIn>::st(op + 16 * n + 4 * kg + r, O[n][r] / lt);
+    if (kg == 0) {
+      a.gmax[hq] = m_run;
+      a.gsum[hq] = lt;
+    }
+  }
+}
+
+template <int D, bool PREC, typename TIn>
+static void launch_fwd(const FwdArgs& a, int max_tiles, dim3 grid, hipStream_t st) {
+  if (max_tiles <= 16)
+    hipLaunchKernelGGL((fwd_kernel<D, PREC, TIn, 4>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((fwd_kernel<D, PREC, TIn, 16>), grid, dim3(256), 0, st, a);
+}
+
+template <int D>
+static void launch_fwd_d(int dtype, const FwdArgs& a, int max_tiles, dim3 grid, hipStream_t st) {
+  if (dtype == HTREE_BF16)
+    launch_fwd<D, false, __bf16>(a, max_tiles, grid, st);
+  else if (dtype == HTREE_F16)
+    launch_fwd<D, true, _Float16>(a, max_tiles, grid, st);
+  else
+    launch_fwd<D, true, float>(a, max_tiles, grid, st);
+}
+
+}  // namespace htree
+
+using namespace htree;
+
+extern "C" int htree_forward(const htree_dims* d, float scale, const void* q,
+                             const void* tree_ws, int64_t tree_ws_bytes,
+                             const float* cos_table, const float* sin_table, void* out,
+                             float* gmax, float* gsum, int32_t* parents, void* stream) {
+  Plan P;
+  int rc = make_plan(d, &P);
+  if (rc) return rc;
+  if (!q || !tree_ws || !cos_table || !sin_table || !out || !gmax || !gsum) return HTREE_ENULL;
+  if (tree_ws_bytes < P.bytes) return HTREE_EWORKSPACE;
+  FwdArgs a;
+  memset(&a, 0, sizeof(a));
+  const char* base = (const char*)tree_ws;
+  for (int l = 0; l < P.L; ++l) {
+    a.lv[l].kh = (const uint16_t*)(base + P.off_kh[l]);
+    a.lv[l].kl = P.off_kl[l] >= 0 ? (const uint16_t*)(base + P.off_kl[l]) : nullptr;
+    a.lv[l].vh = (const uint16_t*)(base + P.off_vh[l]);
+    a.lv[l].vl = P.off_vl[l] >= 0 ? (const uint16_t*)(base + P.off_vl[l]) : nullptr;
+    a.lv[l].N = P.N[l];
+    a.lv[l].Np = P.Np[l];
+    a.lv[l].pw = P.pw[l];
+  }
+  a.q = q;
+  a.out = out;
+  a.gmax = gmax;
+  a.gsum = gsum;
+  a.parents = parents;
+  a.cosb = cos_table;
+  a.sinb = sin_table;
+  a.B = d->B;
+  a.T = d->T;
+  a.H = d->H;
+  a.Hkv = d->H_kv;
+  a.G = d->H / d->H_kv;
+  a.CR = d->compression_rate;
+  a.crlg = P.cr_log2;
+  a.TK = d->top_k;
+  a.L = P.L;
+  a.scale = scale;
+  const int64_t groups = (int64_t)d->B * d->H_kv * d->T;
+  const int64_t nblk = (groups + kWavesPerBlock - 1) / kWavesPerBlock;
+  const int64_t per = (nblk + 7) / 8;
+  if (per * 8 > 0x7fffffff) return HTREE_EUNSUPPORTED;
+  a.per_xcd = (int32_t)per;
+  const dim3 grid((unsigned)(per * 8));
+  hipStream_t st = (hipStream_t)stream;
+  if (d->D == 128)
+    launch_fwd_d<128>(d->dtype, a, P.max_tiles, grid, st);
+  else
+    launch_fwd_d<64>(d->dtype, a, P.max_tiles, grid, st);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? HTREE_OK : (int)e;
+}

@@ -1,0 +1,102 @@
+/*
+ * htree.h -- C ABI of the MI355X (gfx950) hierarchical tree sparse attention.
+ *
+ * Every pointer argument is a DEVICE pointer unless stated otherwise; the
+ * library never allocates device memory on these entry points and keeps no
+ * pointer after it returns.  Work is enqueued on `stream` (a hipStream_t
+ * passed as void*, NULL = the default stream) and is stream-ordered; the
+ * entry points do not synchronise.
+ *
+ * Return value: 0 on success; < 0 an argument / configuration error (see
+ * htree_strerror); > 0 a hipError_t from a launch.
+ *
+ * Tensor layouts (row-major, contiguous):
+ *   q, out      [B, T, H, D]         dtype of htree_dims.dtype
+ *   k, v        [B, T, H_kv, D]      level 0 of the tree
+ *   level l     [B, N_l, H_kv, D]    N_0 = T, N_{l+1} = ceil(N_l / CR) while
+ *                                    N_l > max_top_nodes
+ *   gmax, gsum  [B, T, H]            fp32 online-softmax state
+ *   parents     [L, B, T, H_kv, TK]  int32, list used at each level l:
+ *                                    ascending level-(l+1) node ids, -1 padded
+ *   cos, sin    [rope_rows, D/2]     fp32 RoPE tables
+ *   dq          [B, T, H, D] fp32; dk, dv [B, T, H_kv, D] fp32
+ */
+#ifndef HTREE_AMD_H_
+#define HTREE_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HTREE_MAX_LEVELS 16
+
+enum htree_dtype { HTREE_F32 = 0, HTREE_BF16 = 1, HTREE_F16 = 2 };
+
+enum htree_status {
+  HTREE_OK = 0,
+  HTREE_ENULL = -1,        /* a required pointer is NULL */
+  HTREE_ESHAPE = -2,       /* H % H_kv != 0, non-positive sizes, odd D ... */
+  HTREE_ECONFIG = -3,      /* compression_rate / top_k / max_top_nodes break the
+                              algorithm's rules (powers of two,
+                              max_top_nodes <= top_k * compression_rate) */
+  HTREE_EUNSUPPORTED = -4, /* legal for the reference, outside this build:
+                              D not in {64,128}, G = H/H_kv > 16,
+                              compression_rate < 4,
+                              top_k * max(CR,16) / 16 > 64 */
+  HTREE_EWORKSPACE = -5    /* workspace too small */
+};
+
+/* Problem description shared by every entry point (host struct). */
+typedef struct htree_dims {
+  int32_t B, T, H, H_kv, D;
+  int32_t compression_rate; /* CR: children per tree node                  */
+  int32_t top_k;            /* TK: parents kept per layer (top_k_per_layer) */
+  int32_t max_top_nodes;    /* MTN: build levels while N_l > MTN            */
+  int32_t dtype;            /* enum htree_dtype of q, k, v, out             */
+  int32_t rope_rows;        /* rows of the cos/sin tables (>= top_k * CR)   */
+} htree_dims;
+
+/* Static description of a status code (host). */
+const char* htree_strerror(int status);
+
+/* Validates `d` and returns the level count and sizes N_0..N_{L-1} (host).
+ * Replaces the level loop of src/parallel.py:941-945 / src/naive.py:49-50. */
+int htree_levels(const htree_dims* d, int32_t* num_levels,
+                 int64_t* level_nodes /* [HTREE_MAX_LEVELS] */);
+
+/* Bytes of the packed operand tree that htree_tree_build writes and
+ * htree_forward / htree_backward read (host). */
+int htree_tree_workspace_bytes(const htree_dims* d, int64_t* bytes);
+
+/* Tree build: writes levels 1..L-1 of K and V in the input dtype (mean of
+ * <= CR children, rounded to the dtype per level) into level_k[l] /
+ * level_v[l] (level_k[0] / level_v[0] are ignored: level 0 is k / v), and
+ * the packed operand tree into tree_ws.
+ * Replaces htree_build_kernel (src/parallel.py:87-181) and its host loop
+ * (src/parallel.py:947-978, src/backward.py:848-878).
+ * level_k, level_v: HOST arrays of HTREE_MAX_LEVELS device pointers. */
+int htree_tree_build(const htree_dims* d, const void* k, const void* v,
+                     void* const* level_k, void* const* level_v,
+                     const float* cos_table, const float* sin_table,
+                     void* tree_ws, int64_t tree_ws_bytes, void* stream);
+
+/* Forward over all levels in one launch: candidate expansion, group-shared
+ * Top-K selection, online softmax over the non-selected candidates of every
+ * level, final normalisation.  parents may be NULL.
+ * Replaces the per-level kernels of htree_forward (src/parallel.py:874-1159):
+ * htree_bottom_accumulate_gqa_kernel (:369-530),
+ * htree_select_accumulate_gqa_kernel (:537-867),
+ * htree_merge_to_global_kernel (:248-318),
+ * htree_final_normalize_kernel (:321-363). */
+int htree_forward(const htree_dims* d, float scale, const void* q,
+                  const void* tree_ws, int64_t tree_ws_bytes,
+                  const float* cos_table, const float* sin_table, void* out,
+                  float* gmax, float* gsum, int32_t* parents, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HTREE_AMD_H_ */
