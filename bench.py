@@ -1,0 +1,232 @@
+"""Benchmark of the htree hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C2] [--no-cpu]
+
+Workload ("C2"): B=1, T=32768, Hq=32, Hkv=2 (group
+16), D=128, bf16, causal, CR=16, MTN=128, TK=16; q/k/v/dO iid N(0,1) drawn
+on the host from a fixed seed and copied to HBM before timing.
+
+A step is one forward (`htree_forward`: tree build + fused kernel) plus one
+backward (`htree_backward` from the saved context) when the backward is
+built; `value` = B*T / step time (tokens/s).  The roofline object is for the
+dominant kernel (the fused forward), timed with HIP events on the stream it
+runs on, against the gathered-bytes model in htree_amd/workmodel.py.
+The CPU baseline times the CPU restatement of src/naive.py (oracle/,
+single-threaded C) on a bounded random sample of the same workload's query
+rows; it is a reported baseline only.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "fwd & bwd tokens/s at T=32K, Hq=32/Hkv=2, D=128, bf16; % of HBM roofline"
+HBM_PEAK = 8.0e12
+
+WORKLOADS = {
+    # name: (B, T, Hq, Hkv, D, CR, TK, MTN)
+    "C2": (1, 32768, 32, 2, 128, 16, 16, 128),
+    "C3": (4, 16384, 32, 4, 128, 16, 16, 128),
+    "C4": (1, 131072, 64, 8, 128, 32, 32, 256),
+    "C5": (2, 65536, 32, 2, 128, 16, 16, 128),
+}
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(q, k, v, dO, out, gmax, gsum, parents, CR, TK, MTN, budget_s=12.0):
+    """Oracle (CPU restatement of src/naive.py, one thread) on random query
+    rows of the workload until `budget_s` seconds of forward work have run,
+    then the same rows through the backward's per-row work."""
+    import numpy as np
+
+    from oracle import oracle as orc
+
+    B, T, H, D = q.shape
+    qn = q.float().cpu().numpy()
+    tree = orc.Tree(k.float().cpu().numpy(), v.float().cpu().numpy(), CR, MTN, TK, "bfloat16")
+    rng = np.random.default_rng(0)
+    done, t_fwd, rows_all = 0, 0.0, []
+    while t_fwd < budget_s and done < B * T:
+        rows = np.stack([rng.integers(0, B, 64), rng.integers(0, T, 64)], 1).astype(np.int32)
+        t0 = time.perf_counter()
+        orc.forward(qn, tree, D ** -0.5, rows=rows)
+        t_fwd += time.perf_counter() - t0
+        done += len(rows)
+        rows_all.append(rows)
+    rows = np.concatenate(rows_all)
+    res = dict(fwd_tok_s=done / t_fwd, fwd_rows=done, fwd_s=t_fwd)
+    if parents is not None:
+        par = parents.cpu().numpy()[:, rows[:, 0], rows[:, 1]]
+        gm = gmax.cpu().numpy()[rows[:, 0], rows[:, 1]]
+        gs = gsum.cpu().numpy()[rows[:, 0], rows[:, 1]]
+        o = out.float().cpu().numpy()[rows[:, 0], rows[:, 1]]
+        d = dO.float().cpu().numpy()[rows[:, 0], rows[:, 1]]
+        delta = (o.astype(np.float64) * d).sum(-1).astype(np.float32)
+        t0 = time.perf_counter()
+        orc.backward_dq_rows(qn, tree, D ** -0.5, rows, par, gm, gs, delta, d)
+        t_bwd = time.perf_counter() - t0
+        res.update(bwd_tok_s=len(rows) / t_bwd, bwd_s=t_bwd)
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="C2", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--kernel-iters", type=int, default=20)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported in this build "
+              "(the path shards over (b, h_kv) with no communication; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import htree_amd
+    from htree_amd import _native as N
+    from htree_amd.workmodel import work
+
+    B, T, H, Hkv, D, CR, TK, MTN = WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator().manual_seed(1234)
+    q = torch.randn(B, T, H, D, generator=g).bfloat16().to(dev)
+    k = torch.randn(B, T, Hkv, D, generator=g).bfloat16().to(dev)
+    v = torch.randn(B, T, Hkv, D, generator=g).bfloat16().to(dev)
+    dO = torch.randn(B, T, H, D, generator=g).bfloat16().to(dev)
+    has_bwd = hasattr(htree_amd, "htree_backward")
+    torch.cuda.synchronize()
+    print(f"# workload {args.workload} B={B} T={T} H={H} Hkv={Hkv} D={D} CR={CR} TK={TK} MTN={MTN}"
+          f" backward={'yes' if has_bwd else 'not built'}", file=sys.stderr, flush=True)
+
+    def step():
+        out, ctx = htree_amd.htree_forward(q, k, v, CR, MTN, TK, _save_for_backward=True)
+        if has_bwd:
+            htree_amd.htree_backward(dO, q, out, ctx)
+        return out, ctx
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out, ctx = step()
+    torch.cuda.synchronize()
+    step_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    print(f"# timed {args.steps} steps: {step_ms:.3f} ms/step", file=sys.stderr, flush=True)
+
+    # fwd / bwd split and the fused forward kernel alone, with HIP events
+    stream = torch.cuda.current_stream(dev)
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    e0, e1, e2 = ev(), ev(), ev()
+    e0.record(stream)
+    for _ in range(args.steps):
+        out, ctx = htree_amd.htree_forward(q, k, v, CR, MTN, TK, _save_for_backward=True)
+    e1.record(stream)
+    if has_bwd:
+        for _ in range(args.steps):
+            htree_amd.htree_backward(dO, q, out, ctx)
+    e2.record(stream)
+    torch.cuda.synchronize()
+    fwd_ms = e0.elapsed_time(e1) / args.steps
+    bwd_ms = e1.elapsed_time(e2) / args.steps if has_bwd else None
+
+    d = ctx["dims"]
+    ws = ctx["packed_tree"]
+    cos, sin = ctx["cos_cache"], ctx["sin_cache"]
+    gmax, gsum = ctx["global_max"], ctx["global_sum"]
+    lib = N.lib()
+    scale = float(D ** -0.5)
+    sp = N.stream_ptr(dev)
+    k0, k1 = ev(), ev()
+    k0.record(stream)
+    for _ in range(args.kernel_iters):
+        rc = lib.htree_forward(d, scale, N.ptr(q), N.ptr(ws), ws.numel(), N.ptr(cos), N.ptr(sin),
+                               N.ptr(out), N.ptr(gmax), N.ptr(gsum), None, sp)
+        N.check(rc, "htree_forward")
+    k1.record(stream)
+    torch.cuda.synchronize()
+    kern_ms = k0.elapsed_time(k1) / args.kernel_iters
+
+    w = work(B, T, H, Hkv, D, CR, TK, MTN, 2)
+    achieved = w.fwd_kernel_bytes / (kern_ms * 1e-3)
+    fwd_tok = B * T / (fwd_ms * 1e-3)
+    step_s = (fwd_ms + (bwd_ms or 0.0)) * 1e-3
+    res = {
+        "metric": METRIC,
+        "value": B * T / step_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": fwd_ms + (bwd_ms or 0.0),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: q,k,v,dO iid N(0,1) from torch.Generator seed 1234",
+        "config": {
+            "workload": f"{args.workload}: B={B} T={T} Hq={H} Hkv={Hkv} D={D} bf16 causal "
+                        f"CR={CR} MTN={MTN} TK={TK}",
+            "step": "htree_forward + htree_backward" if has_bwd else "htree_forward (backward not built)",
+        },
+        "fwd": {"ms": fwd_ms, "tokens_per_s": fwd_tok,
+                "hbm_roofline_frac": w.fwd_bytes / (fwd_ms * 1e-3) / HBM_PEAK,
+                "algorithmic_bytes": w.fwd_bytes},
+        "bwd": None if not has_bwd else {
+            "ms": bwd_ms, "tokens_per_s": B * T / (bwd_ms * 1e-3),
+            "hbm_roofline_frac": w.bwd_bytes / (bwd_ms * 1e-3) / HBM_PEAK,
+            "algorithmic_bytes": w.bwd_bytes},
+        "wall_ms_per_step": step_ms,
+        "roofline": {
+            "kernel": "htree::fwd_kernel (fused forward, all levels)",
+            "bound": "hbm",
+            "achieved": achieved / 1e9,
+            "peak": HBM_PEAK / 1e9,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK,
+            "traffic": None,
+            "algorithmic_bytes_per_launch": w.fwd_kernel_bytes,
+            "avg_launch_ms": kern_ms,
+        },
+    }
+    if not args.no_cpu:
+        cb = cpu_baseline(q, k, v, dO, out, gmax, gsum, ctx.get("parents_stacked"), CR, TK, MTN)
+        tot = 1.0 / (1.0 / cb["fwd_tok_s"] + (1.0 / cb["bwd_tok_s"] if has_bwd and "bwd_tok_s" in cb else 0.0))
+        res["cpu_baseline"] = {
+            "value": tot, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{cb['fwd_rows']} random query rows (b,t) of {args.workload} through the "
+                      f"oracle's forward ({cb['fwd_s']:.1f} s)"
+                      + (f" and backward per-row work ({cb['bwd_s']:.1f} s)" if "bwd_s" in cb else "")
+                      + f"; host CPU: {cpu_model()}, os.cpu_count()={os.cpu_count()}",
+            "fwd_tokens_per_s": cb["fwd_tok_s"],
+            "bwd_tokens_per_s": cb.get("bwd_tok_s"),
+        }
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -9,6 +9,8 @@ Drop-in for the reference's src/parallel.py / src/backward.py entry points:
 """
 from .parallel import (HTREE_SCORE_NEG_INF, HTREE_SCORE_VALID_THRESHOLD, htree_forward,
                        htree_forward_parents, rope_cache)
+from .backward import (HTreeFunction, HTreeTritonFunction, htree_backward, htree_forward_autograd,
+                       htree_forward_triton_autograd)
 
 
 __all__ = [

@@ -1,0 +1,972 @@
+// htree backward (dq, dk, dv) with the selection held fixed (the parent lists
+// saved by the forward), deterministic: no floating-point atomics.
+//
+// Reference behaviour (file:line in /root/reference):
+//   delta = rowsum(dO * O) ............... src/backward.py:45-68, naive.py:333
+//   P = exp(S - gmax) / gsum, dS = P (dP - delta),
+//   dq += scale R^-1(dS K~, n_c-1), dK~ += dS^T q~, dV += P^T dO
+//                                          src/backward.py:119-436 (dq),
+//                                          :443-780 (dkv), naive.py:343-386
+//   accumulated = candidates not passed to the next level
+//                                          src/backward.py:392-400, naive.py:355-361
+//   mean-pool backward, top-down ......... src/backward.py:787-841, naive.py:388-394
+//
+// Structure:
+//   prep     per (b,t,h_kv): delta; q and dO transposed per query group
+//            ([d][g], 16 heads padded) for the K-stationary products.
+//   pack     per level: K~ (pre-rotated) transposed per 16-node block, V rows.
+//   index    per level: bitmap parent x query (integer atomicOr), row counts,
+//            scan, extraction of each parent's queries in t order (CSR), and
+//            a table of fixed-size pieces of every row.
+//   dkv      one wave per (piece, 16-child tile): K~/V tile stationary in
+//            registers, loops over the piece's queries; partial dK/dV per piece.
+//   reduce   sums each tile's pieces in piece order into the level's dK/dV.
+//   dq       one wave per query group over all levels (Q-stationary).
+//   pool     dK_{l-1}[child] += dK_l[parent] / n_children, top-down.
+#include <string.h>
+
+#include "htree_common.h"
+
+namespace htree {
+
+constexpr int kGP = 16;  // query heads per group, padded
+
+struct BwdPlan {
+  Plan P;
+  int G, tpp;  // tiles per parent
+  int64_t W;   // bitmap words per row
+  int64_t rows[HTREE_MAX_LEVELS];
+  int64_t max_rows, max_entries, piece, max_pieces;
+  int64_t off_delta, off_qt[2], off_dot[2];
+  int64_t off_kt[2][HTREE_MAX_LEVELS], off_vr[2][HTREE_MAX_LEVELS];
+  int64_t off_dk[HTREE_MAX_LEVELS], off_dv[HTREE_MAX_LEVELS];
+  int64_t off_bitmap, off_cnt, off_rowoff, off_pcnt, off_poff, off_npieces, off_ptab, off_csr,
+      off_partial;
+  int64_t bytes;
+};
+
+static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
+  memset(b, 0, sizeof(*b));
+  int rc = make_plan(d, &b->P);
+  if (rc) return rc;
+  const Plan& P = b->P;
+  const int CR = d->compression_rate;
+  b->G = d->H / d->H_kv;
+  b->tpp = CR > 16 ? CR / 16 : 1;
+  b->W = (d->T + 31) / 32;
+  const int64_t BH = (int64_t)d->B * d->H_kv;
+  b->max_rows = 0;
+  for (int l = 0; l < P.L; ++l) {
+    b->rows[l] = BH * ((P.N[l] + CR - 1) / CR);
+    if (b->rows[l] > b->max_rows) b->max_rows = b->rows[l];
+  }
+  b->max_entries = BH * d->T * d->top_k;
+  int64_t piece = 64;
+  while (piece * 8192 < b->max_entries) piece *= 2;
+  b->piece = piece;
+  b->max_pieces = (b->max_entries + piece - 1) / piece + b->max_rows;
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    int64_t o = off;
+    off += (bytes + 255) / 256 * 256;
+    return o;
+  };
+  const int64_t BTH = (int64_t)d->B * d->T * d->H_kv;
+  b->off_delta = take((int64_t)d->B * d->T * d->H * 4);
+  for (int s = 0; s < 2; ++s) {
+    b->off_qt[s] = (s == 0 || P.precise) ? take(BTH * d->D * kGP * 2) : -1;
+    b->off_dot[s] = (s == 0 || P.precise) ? take(BTH * d->D * kGP * 2) : -1;
+  }
+  for (int l = 0; l < P.L; ++l) {
+    const int64_t elems = BH * P.Np[l] * d->D;
+    for (int s = 0; s < 2; ++s) {
+      b->off_kt[s][l] = take(elems * 2);  // dq = dS K~ cancels (sum dS = 0): split K~
+      b->off_vr[s][l] = (s == 0 || P.precise) ? take(elems * 2) : -1;
+    }
+    b->off_dk[l] = l > 0 ? take((int64_t)d->B * P.N[l] * d->H_kv * d->D * 4) : -1;
+    b->off_dv[l] = l > 0 ? take((int64_t)d->B * P.N[l] * d->H_kv * d->D * 4) : -1;
+  }
+  b->off_bitmap = take(b->max_rows * b->W * 4);
+  b->off_cnt = take((b->max_rows + 1) * 4);
+  b->off_rowoff = take((b->max_rows + 1) * 4);
+  b->off_pcnt = take((b->max_rows + 1) * 4);
+  b->off_poff = take((b->max_rows + 1) * 4);
+  b->off_npieces = take(4);
+  b->off_ptab = take(b->max_pieces * 3 * 4);
+  b->off_csr = take(b->max_entries * 4);
+  b->off_partial = take(b->max_pieces * b->tpp * 16 * (int64_t)d->D * 2 * 4);
+  b->bytes = off;
+  return HTREE_OK;
+}
+
+// ---------------------------------------------------------------- helpers
+template <int D>
+__device__ __forceinline__ int dslot(int kg, int m) {
+  constexpr int SPH = D / 64;
+  return 8 * kg + 32 * (m % SPH) + (D / 2) * (m / SPH);
+}
+
+template <int D>
+__device__ __forceinline__ void rot_frag(const float (&x)[D / 32][8], const float* __restrict__ cosr,
+                                         const float* __restrict__ sinr, int kg,
+                                         float (&y)[D / 32][8]) {
+  constexpr int SPH = D / 64;
+#pragma unroll
+  for (int m = 0; m < SPH; ++m) {
+    const int i0 = dslot<D>(kg, m);
+    float c[8], s[8];
+    Io<float>::ld8(cosr + i0, c);
+    Io<float>::ld8(sinr + i0, s);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float lo = x[m][e], hi = x[m + SPH][e];
+      y[m][e] = lo * c[e] - hi * s[e];
+      y[m + SPH][e] = lo * s[e] + hi * c[e];
+    }
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void split_frag(const float (&x)[D / 32][8], bf16x8 (&h)[D / 32],
+                                           bf16x8 (&lo)[D / 32]) {
+#pragma unroll
+  for (int m = 0; m < D / 32; ++m)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const __bf16 hb = (__bf16)x[m][e];
+      h[m][e] = hb;
+      lo[m][e] = (__bf16)(x[m][e] - (float)hb);
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void load_frag(const uint16_t* __restrict__ row, int kg,
+                                          bf16x8 (&f)[D / 32]) {
+#pragma unroll
+  for (int m = 0; m < D / 32; ++m) f[m] = *(const bf16x8*)(row + dslot<D>(kg, m));
+}
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ s16x4 pack4(const float (&p)[4]) {
+  s16x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = f_to_bfs(p[i]);
+  return r;
+}
+__device__ __forceinline__ void pack4_split(const float (&p)[4], s16x4& h, s16x4& l) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint16_t hb = f_to_bf(p[i]);
+    h[i] = (short)hb;
+    l[i] = f_to_bfs(p[i] - bf_to_f(hb));
+  }
+}
+
+// ---------------------------------------------------------------- prep
+// One wave per (b, t, h_kv): delta[g] = sum_d dO * O (fp32), and q / dO
+// transposed to [d][16] (bf16 hi, and lo for fp32/fp16 inputs) through LDS.
+template <int D, typename T>
+__global__ __launch_bounds__(256) void prep_kernel(const T* __restrict__ q, const T* __restrict__ o,
+                                                   const T* __restrict__ dO, int64_t ngroups, int H,
+                                                   int G, float* __restrict__ delta,
+                                                   uint16_t* __restrict__ qt_h, uint16_t* __restrict__ qt_l,
+                                                   uint16_t* __restrict__ dot_h,
+                                                   uint16_t* __restrict__ dot_l) {
+  constexpr int KS = D / 32;
+  __shared__ uint16_t tr[kWavesPerBlock][4][D * kGP];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int u16 = lane & 15, kg = lane >> 4;
+  const int64_t grp = (int64_t)blockIdx.x * kWavesPerBlock + wv;
+  if (grp >= ngroups) return;
+  const int Hkv = H / G;
+  const int64_t bt = grp / Hkv;
+  const int h = (int)(grp % Hkv);
+  const bool gv = u16 < G;
+  const int64_t row = (bt * H + h * G + (gv ? u16 : 0)) * D;
+  float qf[KS][8], of[KS][8], df[KS][8];
+  float dl = 0.f;
+#pragma unroll
+  for (int m = 0; m < KS; ++m) {
+    Io<T>::ld8(q + row + dslot<D>(kg, m), qf[m]);
+    Io<T>::ld8(o + row + dslot<D>(kg, m), of[m]);
+    Io<T>::ld8(dO + row + dslot<D>(kg, m), df[m]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (!gv) qf[m][e] = df[m][e] = of[m][e] = 0.f;
+      dl += df[m][e] * of[m][e];
+    }
+  }
+  dl += __shfl_xor(dl, 16);
+  dl += __shfl_xor(dl, 32);
+  if (gv && kg == 0) delta[bt * H + h * G + u16] = dl;
+  uint16_t(*L)[D * kGP] = tr[wv];
+#pragma unroll
+  for (int m = 0; m < KS; ++m)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int dd = dslot<D>(kg, m) + e;
+      uint16_t hi, lo;
+      split_bf(qf[m][e], hi, lo);
+      L[0][dd * kGP + u16] = hi;
+      L[1][dd * kGP + u16] = lo;
+      split_bf(df[m][e], hi, lo);
+      L[2][dd * kGP + u16] = hi;
+      L[3][dd * kGP + u16] = lo;
+    }
+  wave_sync();
+  const int64_t ob = grp * D * kGP;
+  for (int i = lane * 8; i < D * kGP; i += 64 * 8) {
+    *(uint4*)(qt_h + ob + i) = *(const uint4*)(&L[0][i]);
+    *(uint4*)(dot_h + ob + i) = *(const uint4*)(&L[2][i]);
+    if (qt_l) *(uint4*)(qt_l + ob + i) = *(const uint4*)(&L[1][i]);
+    if (dot_l) *(uint4*)(dot_l + ob + i) = *(const uint4*)(&L[3][i]);
+  }
+}
+
+// ---------------------------------------------------------------- pack
+// KT[blk][d][16] = KH[blk*16 + c][d] (K~ transposed per block); VR[node][d]
+// = VH[blk][d][c] (V rows).  One thread per (bh, node, d).
+__global__ __launch_bounds__(256) void pack_bwd_kernel(
+    const uint16_t* __restrict__ kh, const uint16_t* __restrict__ kl,
+    const uint16_t* __restrict__ vh, const uint16_t* __restrict__ vl, int64_t Np, int D,
+    int64_t total, uint16_t* __restrict__ kt_h, uint16_t* __restrict__ kt_l,
+    uint16_t* __restrict__ vr_h, uint16_t* __restrict__ vr_l) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int dd = (int)(idx % D);
+  const int64_t r = idx / D;  // bh * Np + node
+  const int64_t node = r % Np;
+  const int64_t bh = r / Np;
+  const int64_t tr = ((bh * (Np / 16) + node / 16) * D + dd) * 16 + (node & 15);
+  kt_h[tr] = kh[idx];
+  if (kt_l) kt_l[tr] = kl[idx];
+  vr_h[idx] = vh[tr];
+  if (vr_l) vr_l[idx] = vl[tr];
+}
+
+// ---------------------------------------------------------------- index
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// bit (row = (b,h,parent), t) for every valid entry of the level's lists
+__global__ __launch_bounds__(256) void bitmap_set_kernel(const int32_t* __restrict__ par, int T,
+                                                         int Hkv, int TK, int64_t Pl, int64_t W,
+                                                         int64_t total, uint32_t* __restrict__ bm) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int p = par[idx];
+  if (p < 0) return;
+  int64_t r = idx / TK;
+  const int h = (int)(r % Hkv);
+  r /= Hkv;
+  const int t = (int)(r % T);
+  const int64_t b = r / T;
+  const int64_t row = (b * Hkv + h) * Pl + p;
+  atomicOr(&bm[row * W + (t >> 5)], 1u << (t & 31));
+}
+
+// one wave per row: number of queries and of pieces
+__global__ __launch_bounds__(256) void row_count_kernel(const uint32_t* __restrict__ bm, int64_t nrows,
+                                                        int64_t W, int piece, int32_t* __restrict__ cnt,
+                                                        int32_t* __restrict__ pcnt) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (row >= nrows) return;
+  int c = 0;
+  for (int64_t w = lane; w < W; w += 64) c += __popc(bm[row * W + w]);
+  c = wave_sum_i(c);
+  if (lane == 0) {
+    cnt[row] = c;
+    pcnt[row] = (c + piece - 1) / piece;
+  }
+}
+
+// exclusive scan of n ints (one block of 1024 threads); out[n] = total
+__global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ in, int64_t n,
+                                                    int32_t* __restrict__ out) {
+  __shared__ int32_t part[1024];
+  const int tid = threadIdx.x;
+  const int64_t per = (n + 1023) / 1024;
+  const int64_t s0 = tid * per;
+  const int64_t e0 = s0 + per < n ? s0 + per : n;
+  int32_t acc = 0;
+  for (int64_t i = s0; i < e0; ++i) acc += in[i];
+  part[tid] = acc;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {
+    const int32_t v = tid >= o ? part[tid - o] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  int32_t run = tid > 0 ? part[tid - 1] : 0;
+  for (int64_t i = s0; i < e0; ++i) {
+    out[i] = run;
+    run += in[i];
+  }
+  if (tid == 1023) out[n] = part[1023];
+}
+
+// one wave per row: writes the row's query indices in ascending t
+__global__ __launch_bounds__(256) void extract_kernel(const uint32_t* __restrict__ bm, int64_t nrows,
+                                                      int64_t W, const int32_t* __restrict__ rowoff,
+                                                      int32_t* __restrict__ csr) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (row >= nrows) return;
+  int64_t base = rowoff[row];
+  for (int64_t w0 = 0; w0 < W; w0 += 64) {
+    const int64_t w = w0 + lane;
+    uint32_t x = w < W ? bm[row * W + w] : 0u;
+    const int c = __popc(x);
+    int inc = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(inc, o);
+      if (lane >= o) inc += v;
+    }
+    int64_t pos = base + inc - c;
+    while (x) {
+      const int bit = __ffs(x) - 1;
+      csr[pos++] = (int32_t)(w * 32 + bit);
+      x &= x - 1;
+    }
+    base += __shfl(inc, 63);
+  }
+}
+
+// piece table: (row, first entry, count) for every piece of every row
+__global__ __launch_bounds__(256) void piece_kernel(const int32_t* __restrict__ cnt,
+                                                    const int32_t* __restrict__ rowoff,
+                                                    const int32_t* __restrict__ poff, int64_t nrows,
+                                                    int piece, int32_t* __restrict__ ptab,
+                                                    int32_t* __restrict__ npieces) {
+  const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (row == 0) *npieces = poff[nrows];
+  if (row >= nrows) return;
+  const int c = cnt[row];
+  for (int i = 0, k = poff[row]; i * piece < c; ++i, ++k) {
+    ptab[3 * k] = (int32_t)row;
+    ptab[3 * k + 1] = rowoff[row] + i * piece;
+    ptab[3 * k + 2] = c - i * piece < piece ? c - i * piece : piece;
+  }
+}
+
+// ---------------------------------------------------------------- dkv
+struct DkvArgs {
+  const uint16_t *kh, *kl;      // K~ rows (hi/lo), [B][Hkv][Np][D]
+  const uint16_t *vr_h, *vr_l;  // V rows
+  const uint16_t *qt_h, *qt_l, *dot_h, *dot_l;  // [B*T*Hkv][D][16]
+  const void* q;
+  const void* dO;
+  const float *gmax, *gsum, *delta;
+  const int32_t* par;       // lists used at this level [B,T,Hkv,TK]
+  const int32_t* par_next;  // lists used at level l-1 (nullptr at l = 0)
+  const int32_t *ptab, *npieces, *csr;
+  const float *cosb, *sinb;
+  float* partial;
+  int64_t N, Np, pw, Pl;
+  int32_t T, H, Hkv, G, CR, crlg, TK, tpp;
+  float scale;
+};
+
+template <int D, bool PREC, typename TIn>
+__global__ __launch_bounds__(256) void dkv_kernel(const DkvArgs a) {
+  constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
+  __shared__ int32_t sel16[kWavesPerBlock][16];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int u16 = lane & 15, kg = lane >> 4;
+  const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wv;
+  const int64_t pc = gw / a.tpp;
+  const int tile = (int)(gw % a.tpp);
+  if (pc >= *a.npieces) return;
+  const int32_t row = a.ptab[3 * pc], e0 = a.ptab[3 * pc + 1], ne = a.ptab[3 * pc + 2];
+  const int64_t bh = row / a.Pl;
+  const int p = (int)(row % a.Pl);
+  const int h = (int)(bh % a.Hkv);
+  const int64_t b = bh / a.Hkv;
+  const int CR = a.CR, crlg = a.crlg, TK = a.TK, G = a.G;
+  const int CRU = CR < 16 ? CR : 16;
+  const int coff = CR >= 16 ? tile * 16 : 0;  // first child of the tile
+  const int node0 = (p << crlg) + coff;
+  if (node0 >= a.N) return;  // tile past the last node (CR > 16): no children, never read
+  // stationary K~ / V fragments of the tile's children (lane cand = u16)
+  bf16x8 kh[KS], kl[KS], vh[KS], vl[KS];
+  {
+    const int64_t r = (bh * a.Np + node0 + (u16 < CRU ? u16 : 0)) * D;
+    load_frag<D>(a.kh + r, kg, kh);
+    load_frag<D>(a.kl + r, kg, kl);
+    load_frag<D>(a.vr_h + r, kg, vh);
+    if (PREC) load_frag<D>(a.vr_l + r, kg, vl);
+  }
+  f32x4 dv[ND], dk[ND];
+#pragma unroll
+  for (int n = 0; n < ND; ++n) dv[n] = dk[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int32_t* S16 = sel16[wv];
+
+  for (int e = 0; e < ne; ++e) {
+    const int t = a.csr[e0 + e];
+    const int64_t bt = b * a.T + t;
+    const int64_t grp = bt * a.Hkv + h;
+    const int32_t* pl = a.par + grp * TK;
+    const int pe = lane < TK ? pl[lane] : -1;
+    const int np = __popcll(__ballot(pe >= 0));
+    const int s = __popcll(__ballot(pe >= 0 && pe < p));
+    const int ct = (int)((t / a.pw) & (CR - 1));
+    const int nc = ((np - 1) << crlg) + ct + 1;
+    const int rho = nc - 1 - (s << crlg);
+    const int j0 = (s << crlg) + coff;
+    bool ok = u16 < CRU && j0 + u16 < nc;
+    if (a.par_next) {
+      if (lane < 16) S16[lane] = 0;
+      wave_sync();
+      const int en = lane < TK ? a.par_next[grp * TK + lane] : -1;
+      if (en >= node0 && en < node0 + 16) S16[en - node0] = 1;
+      wave_sync();
+      ok = ok && S16[u16] == 0;
+      wave_sync();
+    }
+    if (!__any(ok)) continue;
+    // rotated, scaled query fragment (lane g = u16)
+    const bool gv = u16 < G;
+    float qf[KS][8], qr[KS][8];
+    {
+      const TIn* qp = (const TIn*)a.q + (bt * a.H + h * G + (gv ? u16 : 0)) * D;
+#pragma unroll
+      for (int m = 0; m < KS; ++m) {
+        Io<TIn>::ld8(qp + dslot<D>(kg, m), qf[m]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qf[m][i] = gv ? qf[m][i] * a.scale : 0.f;
+      }
+    }
+    rot_frag<D>(qf, a.cosb + (int64_t)rho * HALF, a.sinb + (int64_t)rho * HALF, kg, qr);
+    bf16x8 qh[KS], ql[KS];
+    split_frag<D>(qr, qh, ql);
+    f32x4 S = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < KS; ++m) {
+      S = mma32(qh[m], kh[m], S);
+      S = mma32(qh[m], kl[m], S);
+      S = mma32(ql[m], kh[m], S);
+    }
+    // dP[g][cand] = dO[g] . V[cand]
+    f32x4 dP = {0.f, 0.f, 0.f, 0.f};
+    {
+      float df[KS][8];
+      const TIn* dp = (const TIn*)a.dO + (bt * a.H + h * G + (gv ? u16 : 0)) * D;
+#pragma unroll
+      for (int m = 0; m < KS; ++m) {
+        Io<TIn>::ld8(dp + dslot<D>(kg, m), df[m]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) df[m][i] = gv ? df[m][i] : 0.f;
+      }
+      bf16x8 dh[KS], dlo[KS];
+      split_frag<D>(df, dh, dlo);
+#pragma unroll
+      for (int m = 0; m < KS; ++m) {
+        dP = mma32(dh[m], vh[m], dP);
+        if (PREC) {
+          dP = mma32(dh[m], vl[m], dP);
+          dP = mma32(dlo[m], vh[m], dP);
+        }
+      }
+    }
+    // S[r], dP[r]: head g = 4kg + r, candidate u16
+    float pr[4], ds[4];
+    {
+      const int g0 = 4 * kg;
+      const int64_t hq = bt * a.H + h * G + (g0 < G ? g0 : 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool v = ok && g0 + r < G;
+        const float gm = v ? a.gmax[hq + r] : 0.f;
+        const float gs = v ? a.gsum[hq + r] : 1.f;
+        const float dl = v ? a.delta[hq + r] : 0.f;
+        pr[r] = v ? __builtin_amdgcn_exp2f((S[r] - gm) * kLog2e) / gs : 0.f;
+        ds[r] = pr[r] * (dP[r] - dl);
+      }
+    }
+    // dV[cand][d] += sum_g P[g][cand] dO[g][d];  u[cand][d] = sum_g dS[g][cand] q[g][d]
+    const int64_t tb = grp * D * kGP + 4 * kg;
+    // P and dS split into bf16 hi + lo: dV sums P over many queries of one
+    // node (P ~ 1 for clustered keys), dq / dK sums of dS cancel
+    s16x4 ph, plo, dh4, dl4;
+    pack4_split(ds, dh4, dl4);
+    pack4_split(pr, ph, plo);
+    f32x4 u[ND];
+#pragma unroll
+    for (int n = 0; n < ND; ++n) {
+      const int64_t o = tb + (int64_t)(16 * n + u16) * kGP;
+      const s16x4 dot = *(const s16x4*)(a.dot_h + o);
+      const s16x4 qt = *(const s16x4*)(a.qt_h + o);
+      dv[n] = mma16(ph, dot, dv[n]);
+      dv[n] = mma16(plo, dot, dv[n]);
+      u[n] = mma16(dh4, qt, f32x4{0.f, 0.f, 0.f, 0.f});
+      u[n] = mma16(dl4, qt, u[n]);
+      if (PREC) {
+        const s16x4 dotl = *(const s16x4*)(a.dot_l + o);
+        const s16x4 qtl = *(const s16x4*)(a.qt_l + o);
+        dv[n] = mma16(ph, dotl, dv[n]);
+        u[n] = mma16(dh4, qtl, u[n]);
+      }
+    }
+    // u[n][r] = value at candidate 4kg + r, d = 16n + u16; rotate by rho
+    // (d/dK~ of q~ . K~ is q~ = scale R(q, rho)); scale applied at the end
+#pragma unroll
+    for (int n = 0; n < ND / 2; ++n) {
+      const int i = 16 * n + u16;
+      const float c = a.cosb[(int64_t)rho * HALF + i], sn = a.sinb[(int64_t)rho * HALF + i];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float lo = u[n][r], hi = u[n + ND / 2][r];
+        dk[n][r] += lo * c - hi * sn;
+        dk[n + ND / 2][r] += lo * sn + hi * c;
+      }
+    }
+  }
+  // dk of the node = scale R^-1(dK~, node mod CR); write this piece's partial
+  float* out = a.partial + ((pc * a.tpp + tile) * 16) * (int64_t)D * 2;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int cand = 4 * kg + r;
+    const int c = (coff + cand) & (CR - 1);
+#pragma unroll
+    for (int n = 0; n < ND / 2; ++n) {
+      const int i = 16 * n + u16;
+      const float cs = a.cosb[(int64_t)c * HALF + i], sn = a.sinb[(int64_t)c * HALF + i];
+      const float lo = dk[n][r], hi = dk[n + ND / 2][r];
+      out[cand * D + i] = a.scale * (lo * cs + hi * sn);
+      out[cand * D + i + HALF] = a.scale * (hi * cs - lo * sn);
+    }
+#pragma unroll
+    for (int n = 0; n < ND; ++n) out[16 * D + cand * D + 16 * n + u16] = dv[n][r];
+  }
+}
+
+// sums the pieces of each tile in order into dK_l / dV_l [B, N, Hkv, D]
+__global__ __launch_bounds__(256) void dkv_reduce_kernel(const float* __restrict__ partial,
+                                                         const int32_t* __restrict__ poff, int64_t N,
+                                                         int Hkv, int D, int CR, int crlg, int tpp,
+                                                         int64_t Pl, int64_t total,
+                                                         float* __restrict__ dk, float* __restrict__ dv) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int dd = (int)(idx % D);
+  int64_t r = idx / D;
+  const int h = (int)(r % Hkv);
+  r /= Hkv;
+  const int64_t node = r % N;
+  const int64_t b = r / N;
+  const int64_t p = node >> crlg;
+  const int cin = (int)(node & (CR - 1));
+  const int tile = CR >= 16 ? cin >> 4 : 0;
+  const int cand = CR >= 16 ? (cin & 15) : cin;
+  const int64_t row = (b * Hkv + h) * Pl + p;
+  float sk = 0.f, sv = 0.f;
+  for (int32_t k = poff[row]; k < poff[row + 1]; ++k) {
+    const float* pp = partial + (((int64_t)k * tpp + tile) * 16) * D * 2;
+    sk += pp[cand * D + dd];
+    sv += pp[16 * D + cand * D + dd];
+  }
+  dk[idx] = sk;
+  dv[idx] = sv;
+}
+
+// dK_{l-1}[child] += dK_l[parent] / n_children(parent)
+__global__ __launch_bounds__(256) void pool_bwd_kernel(const float* __restrict__ gp, float* __restrict__ gc,
+                                                       int64_t Nc, int64_t Np, int Hkv, int D, int CR,
+                                                       int64_t total) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int dd = (int)(idx % D);
+  int64_t r = idx / D;
+  const int h = (int)(r % Hkv);
+  r /= Hkv;
+  const int64_t c = r % Nc;
+  const int64_t b = r / Nc;
+  const int64_t p = c / CR;
+  const int64_t s0 = p * CR;
+  const int64_t cnt = (s0 + CR < Nc ? s0 + CR : Nc) - s0;
+  gc[idx] += gp[((b * Np + p) * Hkv + h) * D + dd] / (float)cnt;
+}
+
+// ---------------------------------------------------------------- dq
+struct DqLevel {
+  const uint16_t *kh, *kl, *kt_h, *kt_l, *vr_h, *vr_l;
+  int64_t Np, pw;
+};
+
+struct DqArgs {
+  DqLevel lv[HTREE_MAX_LEVELS];
+  const void* q;
+  const void* dO;
+  const float *gmax, *gsum, *delta;
+  const int32_t* parents;  // [L,B,T,Hkv,TK]
+  const float *cosb, *sinb;
+  float* dq;
+  int32_t B, T, H, Hkv, G, CR, crlg, TK, L;
+  float scale;
+};
+
+template <int D, bool PREC, typename TIn>
+__global__ __launch_bounds__(256) void dq_kernel(const DqArgs a) {
+  constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
+  __shared__ int32_t lst[kWavesPerBlock][2][kMaxTK];
+  __shared__ uint32_t selw[kWavesPerBlock][32];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int u16 = lane & 15, kg = lane >> 4;
+  const int64_t grp = (int64_t)blockIdx.x * kWavesPerBlock + wv;
+  if (grp >= (int64_t)a.B * a.T * a.Hkv) return;
+  const int h = (int)(grp % a.Hkv);
+  const int64_t bt = grp / a.Hkv;
+  const int t = (int)(bt % a.T);
+  const int G = a.G, CR = a.CR, crlg = a.crlg, TK = a.TK;
+  const int CRU = CR < 16 ? CR : 16;
+  const bool wide = CR >= 16;
+  const bool gv = u16 < G;
+  const int64_t hq = bt * a.H + h * G + (gv ? u16 : 0);
+  float qf[KS][8];
+  bf16x8 dh[KS], dlo[KS];
+  {
+    const TIn* qp = (const TIn*)a.q + hq * D;
+    const TIn* dp = (const TIn*)a.dO + hq * D;
+    float df[KS][8];
+#pragma unroll
+    for (int m = 0; m < KS; ++m) {
+      Io<TIn>::ld8(qp + dslot<D>(kg, m), qf[m]);
+      Io<TIn>::ld8(dp + dslot<D>(kg, m), df[m]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        qf[m][i] = gv ? qf[m][i] * a.scale : 0.f;
+        df[m][i] = gv ? df[m][i] : 0.f;
+      }
+    }
+    split_frag<D>(df, dh, dlo);
+  }
+  const float gm = gv ? a.gmax[hq] : 0.f;
+  const float gs = gv ? a.gsum[hq] : 1.f;
+  const float dl = gv ? a.delta[hq] : 0.f;
+  f32x4 acc[ND];
+#pragma unroll
+  for (int n = 0; n < ND; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int32_t(*LS)[kMaxTK] = lst[wv];
+  uint32_t* SW = selw[wv];
+  const int64_t lstride = (int64_t)a.B * a.T * a.Hkv * TK;
+
+  for (int l = a.L - 1; l >= 0; --l) {
+    const DqLevel P = a.lv[l];
+    wave_sync();
+    const int pe = lane < TK ? a.parents[l * lstride + grp * TK + lane] : -1;
+    if (lane < TK) LS[0][lane] = pe;
+    if (lane < 32) SW[lane] = 0u;
+    const int np = __popcll(__ballot(pe >= 0));
+    if (np <= 0) continue;
+    const int ct = (int)((t / P.pw) & (CR - 1));
+    const int nc = ((np - 1) << crlg) + ct + 1;
+    const int apos = nc - 1;
+    const int nt = wide ? (nc + 15) >> 4 : np;
+    wave_sync();
+    if (l > 0) {
+      // positions of the nodes passed to level l-1 (not accumulated here)
+      const int en = lane < TK ? a.parents[(l - 1) * lstride + grp * TK + lane] : -1;
+      if (en >= 0) {
+        const int pp = en >> crlg;
+        int lo = 0, hi = np - 1;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (LS[0][mid] < pp) lo = mid + 1; else hi = mid;
+        }
+        const int j = (lo << crlg) + (en & (CR - 1));
+        atomicOr(&SW[(wide ? j : ((lo << 4) + (en & (CR - 1)))) >> 5],
+                 1u << ((wide ? j : ((lo << 4) + (en & (CR - 1)))) & 31));
+      }
+      wave_sync();
+    }
+    const int64_t hrow = (((int64_t)(grp / a.Hkv) / a.T) * a.Hkv + h) * P.Np;
+    for (int tau = 0; tau < nt; ++tau) {
+      const int s = wide ? (tau << 4) >> crlg : tau;
+      const int node0 = (LS[0][s] << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0);
+      const int prow = apos - (s << crlg);
+      float qr[KS][8];
+      rot_frag<D>(qf, a.cosb + (int64_t)prow * HALF, a.sinb + (int64_t)prow * HALF, kg, qr);
+      bf16x8 qh[KS], ql[KS];
+      split_frag<D>(qr, qh, ql);
+      const int posk = wide ? (tau << 4) + u16 : (tau << crlg) + u16;
+      const bool cvk = u16 < CRU && posk < nc;
+      const int64_t krow = (hrow + node0 + (cvk ? u16 : 0)) * D;
+      bf16x8 kh[KS], kl[KS], vh[KS], vl[KS];
+      load_frag<D>(P.kh + krow, kg, kh);
+      load_frag<D>(P.kl + krow, kg, kl);
+      load_frag<D>(P.vr_h + krow, kg, vh);
+      if (PREC) load_frag<D>(P.vr_l + krow, kg, vl);
+      f32x4 S = {0.f, 0.f, 0.f, 0.f}, dP = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < KS; ++m) {
+        S = mma32(kh[m], qh[m], S);
+        S = mma32(kl[m], qh[m], S);
+        S = mma32(kh[m], ql[m], S);
+        dP = mma32(vh[m], dh[m], dP);
+        if (PREC) {
+          dP = mma32(vl[m], dh[m], dP);
+          dP = mma32(vh[m], dlo[m], dP);
+        }
+      }
+      // S[r], dP[r]: candidate 4kg + r, head u16
+      const uint32_t sw = SW[((wide ? (tau << 4) : (tau << 4))) >> 5];
+      float ds[4];
+      bool anyv = false;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int cu = 4 * kg + r;
+        const int pos = wide ? (tau << 4) + cu : (tau << crlg) + cu;
+        const int bitpos = ((tau << 4) + cu) & 31;
+        const bool v = gv && cu < CRU && pos < nc && !((sw >> bitpos) & 1u);
+        const float pr = v ? __builtin_amdgcn_exp2f((S[r] - gm) * kLog2e) / gs : 0.f;
+        ds[r] = pr * (dP[r] - dl);
+        anyv |= v;
+      }
+      if (!__any(anyv)) continue;
+      // dq = sum_cand dS K~ cancels (sum_cand dS = 0 per head): split both
+      // factors so clustered keys keep their small residual
+      s16x4 d4h, d4l;
+      pack4_split(ds, d4h, d4l);
+      // dq~^T[d][g] = sum_cand K~[cand][d] dS[g][cand]
+      const int vn = node0 + (4 * kg < CRU ? 4 * kg : 0);
+      const int64_t tbase = ((hrow + (vn & ~15)) / 16 * D + u16) * 16 + (vn & 15);
+      f32x4 tq[ND];
+#pragma unroll
+      for (int n = 0; n < ND; ++n) {
+        const s16x4 kt = *(const s16x4*)(P.kt_h + tbase + (int64_t)n * 256);
+        const s16x4 ktl = *(const s16x4*)(P.kt_l + tbase + (int64_t)n * 256);
+        tq[n] = mma16(kt, d4h, f32x4{0.f, 0.f, 0.f, 0.f});
+        tq[n] = mma16(kt, d4l, tq[n]);
+        tq[n] = mma16(ktl, d4h, tq[n]);
+      }
+      // tq[n][r] at d = 16n + 4kg + r, head u16: rotate back by prow
+#pragma unroll
+      for (int n = 0; n < ND / 2; ++n) {
+        const int i0 = 16 * n + 4 * kg;
+        const float4 c4 = *(const float4*)(a.cosb + (int64_t)prow * HALF + i0);
+        const float4 s4 = *(const float4*)(a.sinb + (int64_t)prow * HALF + i0);
+        const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float lo = tq[n][r], hi = tq[n + ND / 2][r];
+          acc[n][r] += lo * cc[r] + hi * ss[r];
+          acc[n + ND / 2][r] += hi * cc[r] - lo * ss[r];
+        }
+      }
+    }
+  }
+  if (gv) {
+    float* o = a.dq + hq * D;
+#pragma unroll
+    for (int n = 0; n < ND; ++n)
+      *(float4*)(o + 16 * n + 4 * kg) =
+          make_float4(a.scale * acc[n][0], a.scale * acc[n][1], a.scale * acc[n][2], a.scale * acc[n][3]);
+  }
+}
+
+// ---------------------------------------------------------------- host
+template <int D, bool PREC, typename T>
+static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const void* q,
+                      const void* out, const void* dO, const float* gmax, const float* gsum,
+                      const int32_t* parents, const char* tws, const float* cosb, const float* sinb,
+                      float* dq, float* dk, float* dv, char* ws, hipStream_t st) {
+  const Plan& P = BP.P;
+  const int64_t BH = (int64_t)d->B * d->H_kv;
+  const int64_t groups = (int64_t)d->B * d->T * d->H_kv;
+  const int G = BP.G;
+  const int CR = d->compression_rate;
+  const int64_t lstride = groups * d->top_k;
+  auto U16 = [&](int64_t off) { return off >= 0 ? (uint16_t*)(ws + off) : nullptr; };
+  float* delta = (float*)(ws + BP.off_delta);
+  hipLaunchKernelGGL((prep_kernel<D, T>), dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, st,
+                     (const T*)q, (const T*)out, (const T*)dO, groups, d->H, G, delta,
+                     U16(BP.off_qt[0]), U16(BP.off_qt[1]), U16(BP.off_dot[0]), U16(BP.off_dot[1]));
+  for (int l = 0; l < P.L; ++l) {
+    const int64_t total = BH * P.Np[l] * d->D;
+    hipLaunchKernelGGL(pack_bwd_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
+                       (const uint16_t*)(tws + P.off_kh[l]), (const uint16_t*)(tws + P.off_kl[l]),
+                       (const uint16_t*)(tws + P.off_vh[l]),
+                       P.off_vl[l] >= 0 ? (const uint16_t*)(tws + P.off_vl[l]) : nullptr, P.Np[l],
+                       d->D, total, U16(BP.off_kt[0][l]), U16(BP.off_kt[1][l]),
+                       U16(BP.off_vr[0][l]), U16(BP.off_vr[1][l]));
+  }
+  uint32_t* bm = (uint32_t*)(ws + BP.off_bitmap);
+  int32_t* cnt = (int32_t*)(ws + BP.off_cnt);
+  int32_t* rowoff = (int32_t*)(ws + BP.off_rowoff);
+  int32_t* pcnt = (int32_t*)(ws + BP.off_pcnt);
+  int32_t* poff = (int32_t*)(ws + BP.off_poff);
+  int32_t* npieces = (int32_t*)(ws + BP.off_npieces);
+  int32_t* ptab = (int32_t*)(ws + BP.off_ptab);
+  int32_t* csr = (int32_t*)(ws + BP.off_csr);
+  float* partial = (float*)(ws + BP.off_partial);
+  for (int l = P.L - 1; l >= 0; --l) {
+    const int64_t Pl = (P.N[l] + CR - 1) / CR;
+    const int64_t nrows = BP.rows[l];
+    const int64_t words = nrows * BP.W;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st, bm,
+                       words);
+    const int64_t ent = lstride;
+    hipLaunchKernelGGL(bitmap_set_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
+                       parents + l * lstride, d->T, d->H_kv, d->top_k, Pl, BP.W, ent, bm);
+    hipLaunchKernelGGL(row_count_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, st, bm,
+                       nrows, BP.W, (int)BP.piece, cnt, pcnt);
+    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, cnt, nrows, rowoff);
+    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, pcnt, nrows, poff);
+    hipLaunchKernelGGL(extract_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, st, bm,
+                       nrows, BP.W, rowoff, csr);
+    hipLaunchKernelGGL(piece_kernel, dim3((unsigned)((nrows + 255) / 256)), dim3(256), 0, st, cnt,
+                       rowoff, poff, nrows, (int)BP.piece, ptab, npieces);
+    DkvArgs a;
+    memset(&a, 0, sizeof(a));
+    a.kh = (const uint16_t*)(tws + P.off_kh[l]);
+    a.kl = (const uint16_t*)(tws + P.off_kl[l]);
+    a.vr_h = U16(BP.off_vr[0][l]);
+    a.vr_l = U16(BP.off_vr[1][l]);
+    a.qt_h = U16(BP.off_qt[0]);
+    a.qt_l = U16(BP.off_qt[1]);
+    a.dot_h = U16(BP.off_dot[0]);
+    a.dot_l = U16(BP.off_dot[1]);
+    a.q = q;
+    a.dO = dO;
+    a.gmax = gmax;
+    a.gsum = gsum;
+    a.delta = delta;
+    a.par = parents + l * lstride;
+    a.par_next = l > 0 ? parents + (l - 1) * lstride : nullptr;
+    a.ptab = ptab;
+    a.npieces = npieces;
+    a.csr = csr;
+    a.cosb = cosb;
+    a.sinb = sinb;
+    a.partial = partial;
+    a.N = P.N[l];
+    a.Np = P.Np[l];
+    a.pw = P.pw[l];
+    a.Pl = Pl;
+    a.T = d->T;
+    a.H = d->H;
+    a.Hkv = d->H_kv;
+    a.G = G;
+    a.CR = CR;
+    a.crlg = P.cr_log2;
+    a.TK = d->top_k;
+    a.tpp = BP.tpp;
+    a.scale = scale;
+    const int64_t waves = BP.max_pieces * BP.tpp;
+    hipLaunchKernelGGL((dkv_kernel<D, PREC, T>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+                       st, a);
+    float* dkl = l == 0 ? dk : (float*)(ws + BP.off_dk[l]);
+    float* dvl = l == 0 ? dv : (float*)(ws + BP.off_dv[l]);
+    const int64_t tot = (int64_t)d->B * P.N[l] * d->H_kv * d->D;
+    hipLaunchKernelGGL(dkv_reduce_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st,
+                       partial, poff, P.N[l], d->H_kv, d->D, CR, P.cr_log2, BP.tpp, Pl, tot, dkl,
+                       dvl);
+  }
+  // dq over all levels
+  {
+    DqArgs a;
+    memset(&a, 0, sizeof(a));
+    for (int l = 0; l < P.L; ++l) {
+      a.lv[l].kh = (const uint16_t*)(tws + P.off_kh[l]);
+      a.lv[l].kl = (const uint16_t*)(tws + P.off_kl[l]);
+      a.lv[l].kt_h = U16(BP.off_kt[0][l]);
+      a.lv[l].kt_l = U16(BP.off_kt[1][l]);
+      a.lv[l].vr_h = U16(BP.off_vr[0][l]);
+      a.lv[l].vr_l = U16(BP.off_vr[1][l]);
+      a.lv[l].Np = P.Np[l];
+      a.lv[l].pw = P.pw[l];
+    }
+    a.q = q;
+    a.dO = dO;
+    a.gmax = gmax;
+    a.gsum = gsum;
+    a.delta = delta;
+    a.parents = parents;
+    a.cosb = cosb;
+    a.sinb = sinb;
+    a.dq = dq;
+    a.B = d->B;
+    a.T = d->T;
+    a.H = d->H;
+    a.Hkv = d->H_kv;
+    a.G = G;
+    a.CR = CR;
+    a.crlg = P.cr_log2;
+    a.TK = d->top_k;
+    a.L = P.L;
+    a.scale = scale;
+    hipLaunchKernelGGL((dq_kernel<D, PREC, T>), dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, st,
+                       a);
+  }
+  // mean-pool backward, top-down
+  for (int l = P.L - 1; l >= 1; --l) {
+    const float* gpk = (const float*)(ws + BP.off_dk[l]);
+    const float* gpv = (const float*)(ws + BP.off_dv[l]);
+    float* gck = l - 1 == 0 ? dk : (float*)(ws + BP.off_dk[l - 1]);
+    float* gcv = l - 1 == 0 ? dv : (float*)(ws + BP.off_dv[l - 1]);
+    const int64_t tot = (int64_t)d->B * P.N[l - 1] * d->H_kv * d->D;
+    hipLaunchKernelGGL(pool_bwd_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, gpk,
+                       gck, P.N[l - 1], P.N[l], d->H_kv, d->D, CR, tot);
+    hipLaunchKernelGGL(pool_bwd_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, gpv,
+                       gcv, P.N[l - 1], P.N[l], d->H_kv, d->D, CR, tot);
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? HTREE_OK : (int)e;
+}
+
+}  // namespace htree
+
+using namespace htree;
+
+extern "C" {
+
+int htree_backward_workspace_bytes(const htree_dims* d, int64_t* bytes) {
+  BwdPlan BP;
+  int rc = make_bwd_plan(d, &BP);
+  if (rc) return rc;
+  if (!bytes) return HTREE_ENULL;
+  *bytes = BP.bytes;
+  return HTREE_OK;
+}
+
+int htree_backward(const htree_dims* d, float scale, const void* q, const void* out,
+                   const void* dO, const float* gmax, const float* gsum, const int32_t* parents,
+                   const void* tree_ws, int64_t tree_ws_bytes, const float* cos_table,
+                   const float* sin_table, float* dq, float* dk, float* dv, void* bwd_ws,
+                   int64_t bwd_ws_bytes, void* stream) {
+  BwdPlan BP;
+  int rc = make_bwd_plan(d, &BP);
+  if (rc) return rc;
+  if (!q || !out || !dO || !gmax || !gsum || !parents || !tree_ws || !cos_table || !sin_table ||
+      !dq || !dk || !dv || !bwd_ws)
+    return HTREE_ENULL;
+  if (tree_ws_bytes < BP.P.bytes || bwd_ws_bytes < BP.bytes) return HTREE_EWORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  const char* tws = (const char*)tree_ws;
+  char* ws = (char*)bwd_ws;
+#define HT_BWD(DD, PR, TT)                                                                      \
+  return backward_t<DD, PR, TT>(d, BP, scale, q, out, dO, gmax, gsum, parents, tws, cos_table, \
+                                sin_table, dq, dk, dv, ws, st)
+  if (d->D == 128) {
+    if (d->dtype == HTREE_BF16) HT_BWD(128, false, __bf16);
+    if (d->dtype == HTREE_F16) HT_BWD(128, true, _Float16);
+    HT_BWD(128, true, float);
+  } else {
+    if (d->dtype == HTREE_BF16) HT_BWD(64, false, __bf16);
+    if (d->dtype == HTREE_F16) HT_BWD(64, true, _Float16);
+    HT_BWD(64, true, float);
+  }
+#undef HT_BWD
+}
+
+}  // extern "C"

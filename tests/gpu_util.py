@@ -76,3 +76,36 @@ def check_forward(q, k, v, CR, TK, MTN, dtype, rows=None, out_dev=None, parents_
     rep["out_worst"] = worst
     assert ok, f"output outside tolerance: worst {worst:.3f} of the bar"
     return rep
+
+
+def oracle_grads(q, k, v, dO, CR, TK, MTN, dtype, parents_dev, out_dev, tree=None):
+    """Oracle gradients (src/naive.py:320-396 restated) with the selection
+    held at the device's parent lists: oracle forward teacher-forced on them
+    (gmax, gsum), then the analytical backward.  The backward is a function
+    of the `output` it is handed (delta = rowsum(dO * output),
+    src/backward.py:966-976), so the oracle gets the device's output: a
+    1-ulp difference of the two forwards' rounded outputs would otherwise
+    reach dq through delta times the keys' common mean."""
+    B, T, H, D = q.shape
+    if tree is None:
+        tree = orc.Tree(k.float().numpy(), v.float().numpy(), CR, MTN, TK, dtype)
+    L = tree.L
+    rows = orc.all_rows(B, T)
+    par = np.ascontiguousarray(parents_dev.reshape(L, B * T, *parents_dev.shape[3:]))
+    fw = orc.forward(q.float().numpy(), tree, D ** -0.5, rows=rows, forced=par)
+    bw = orc.backward(q.float().numpy(), tree, D ** -0.5, parents_dev, fw["gmax"].reshape(B, T, H),
+                      fw["gsum"].reshape(B, T, H), out_dev.reshape(B, T, H, D), dO.float().numpy())
+    return bw, fw
+
+
+def check_backward(q, k, v, dO, CR, TK, MTN, dtype, out_dev, parents_dev, gmax_dev, gsum_dev,
+                   dq, dk, dv, tree=None):
+    """Device grads (fp32 numpy) vs the oracle's, same selection; bar as TOL."""
+    bw, _ = oracle_grads(q, k, v, dO, CR, TK, MTN, dtype, parents_dev, out_dev, tree)
+    rep = {}
+    for name, got, ref in (("dq", dq, bw["dq"]), ("dk", dk, bw["dk"]), ("dv", dv, bw["dv"])):
+        ok, worst = close(got, ref, dtype)
+        rep[name] = worst
+        assert np.all(np.isfinite(got)), f"{name} not finite"
+        assert ok, f"{name} outside tolerance: worst {worst:.3f} of the bar"
+    return rep
