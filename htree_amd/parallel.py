@@ -52,13 +52,13 @@ def _validate(q, k, v, compression_rate, max_top_nodes, top_k_per_layer):
     assert k.shape[:2] == (B, T) and v.shape[:2] == (B, T), "q/k/v batch and length must match"
     assert k.shape[3] == K and v.shape[3] == K, "this implementation needs K == V == head_dim"
     assert q.dtype == k.dtype == v.dtype, "q, k, v must share one dtype"
-    assert q.is_cuda and k.is_cuda and v.is_cuda, "htree_amd runs on the GPU (no CPU fallback)"
     assert (top_k_per_layer & (top_k_per_layer - 1)) == 0, "top_k_per_layer (TOP_K) must be a power of 2"
     assert (compression_rate & (compression_rate - 1)) == 0, "compression_rate must be a power of 2"
     assert (max_top_nodes & (max_top_nodes - 1)) == 0, "max_top_nodes must be a power of 2"
     assert max_top_nodes <= top_k_per_layer * compression_rate, (
         f"max_top_nodes ({max_top_nodes}) must be <= top_k_per_layer*compression_rate "
         f"({top_k_per_layer}*{compression_rate}={top_k_per_layer * compression_rate})")
+    assert q.is_cuda and k.is_cuda and v.is_cuda, "htree_amd runs on the GPU (no CPU fallback)"
 
 
 def make_dims(q, k, compression_rate, max_top_nodes, top_k_per_layer):

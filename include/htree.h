@@ -95,6 +95,24 @@ int htree_forward(const htree_dims* d, float scale, const void* q,
                   const float* cos_table, const float* sin_table, void* out,
                   float* gmax, float* gsum, int32_t* parents, void* stream);
 
+/* Bytes of the backward workspace (host). */
+int htree_backward_workspace_bytes(const htree_dims* d, int64_t* bytes);
+
+/* Backward with the selection held fixed: dq, dk, dv in fp32 (dk, dv after
+ * the mean-pool backward onto level 0).  `out` is the forward output handed
+ * to the backward (delta = rowsum(dO * out)); gmax, gsum and parents are
+ * what htree_forward wrote; tree_ws is the packed tree of htree_tree_build.
+ * Deterministic: no floating-point atomics.
+ * Replaces htree_backward (src/backward.py:941-1119) and its kernels K0
+ * (:45-68), K1a/K1b (:119-436), K2 (:75-112), K3/K3u (:443-780),
+ * K4 (:787-841); the parents come from the forward instead of
+ * _recompute_parents (:881-934). */
+int htree_backward(const htree_dims* d, float scale, const void* q, const void* out,
+                   const void* dO, const float* gmax, const float* gsum,
+                   const int32_t* parents, const void* tree_ws, int64_t tree_ws_bytes,
+                   const float* cos_table, const float* sin_table, float* dq, float* dk,
+                   float* dv, void* bwd_ws, int64_t bwd_ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

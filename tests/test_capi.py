@@ -1,0 +1,119 @@
+"""CPU tests of the C ABI (no kernel launches): the library loads, exports
+every function include/htree.h declares, validates configurations like the
+reference (AssertionError), and plans levels and workspaces."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from htree_amd import _native as N
+from htree_amd.workmodel import level_sizes, work
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    hdr = open(os.path.join(ROOT, "include", "htree.h")).read()
+    return sorted(set(re.findall(r"^(?:int|const char\*|int64_t)\s+(htree_\w+)\s*\(", hdr, re.M)))
+
+
+def test_header_and_exports_agree():
+    decl = declared_functions()
+    assert set(decl) == set(N.EXPORTS), (decl, N.EXPORTS)
+    lib = N.lib()
+    for name in decl:
+        assert hasattr(lib, name), f"libhtree_amd.so does not export {name}"
+
+
+def test_strerror_covers_codes():
+    for rc in (N.HTREE_OK, N.HTREE_ENULL, N.HTREE_ESHAPE, N.HTREE_ECONFIG, N.HTREE_EUNSUPPORTED,
+               N.HTREE_EWORKSPACE):
+        assert len(N.strerror(rc)) > 0
+    assert N.strerror(-99) == "unknown htree status"
+
+
+def dims(**kw):
+    base = dict(B=1, T=32768, H=32, H_kv=2, D=128, compression_rate=16, top_k=16,
+                max_top_nodes=128, dtype=torch.bfloat16, rope_rows=1152)
+    base.update(kw)
+    return N.dims(base["B"], base["T"], base["H"], base["H_kv"], base["D"], base["compression_rate"],
+                  base["top_k"], base["max_top_nodes"], base["dtype"], base["rope_rows"])
+
+
+@pytest.mark.parametrize("T,CR,MTN", [(32768, 16, 128), (131072, 32, 256), (65536, 16, 128),
+                                      (2048, 16, 64), (300, 4, 32), (64, 16, 64), (65, 16, 64)])
+def test_levels_follow_reference_rule(T, CR, MTN):
+    d = dims(T=T, compression_rate=CR, max_top_nodes=MTN, top_k=max(MTN // CR, 8),
+             rope_rows=max(MTN + 1024, max(MTN // CR, 8) * CR))
+    assert N.levels(d) == level_sizes(T, CR, MTN)
+
+
+def test_baseline_level_counts():
+    # SURVEY: C4 has 3 levels by the reference's rule, C5 has 4
+    assert len(N.levels(dims(T=131072, H=64, H_kv=8, compression_rate=32, top_k=32,
+                             max_top_nodes=256, rope_rows=1280))) == 3
+    assert len(N.levels(dims(T=65536))) == 4
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(H=30, H_kv=4), N.HTREE_ESHAPE),
+    (dict(T=0), N.HTREE_ESHAPE),
+    (dict(top_k=12), N.HTREE_ECONFIG),                 # not a power of two
+    (dict(compression_rate=24), N.HTREE_ECONFIG),
+    (dict(max_top_nodes=512), N.HTREE_ECONFIG),        # > top_k * CR
+    (dict(rope_rows=100), N.HTREE_ECONFIG),
+    (dict(D=96), N.HTREE_EUNSUPPORTED),
+    (dict(H=64, H_kv=2), N.HTREE_EUNSUPPORTED),        # group of 32
+    (dict(top_k=128, max_top_nodes=128, rope_rows=2048), N.HTREE_EUNSUPPORTED),
+])
+def test_invalid_configs_raise_assertion(kw, code):
+    d = dims(**kw)
+    rc = N.lib().htree_levels(ctypes.byref(d), None, None)
+    assert rc == code
+    with pytest.raises(AssertionError):
+        N.levels(d)
+
+
+def test_null_pointers_rejected_without_launch():
+    d = dims()
+    lib = N.lib()
+    assert lib.htree_forward(d, 0.1, None, None, 0, None, None, None, None, None, None, None) == N.HTREE_ENULL
+    assert lib.htree_tree_build(d, None, None, None, None, None, None, None, 0, None) == N.HTREE_ENULL
+    nb = ctypes.c_int64()
+    assert lib.htree_backward_workspace_bytes(ctypes.byref(d), ctypes.byref(nb)) == 0 and nb.value > 0
+    assert lib.htree_backward(d, 0.1, *([None] * 7), 0, *([None] * 6), 0, None) == N.HTREE_ENULL
+
+
+def test_workspace_too_small_rejected():
+    d = dims(T=4096)
+    need = N.tree_workspace_bytes(d)
+    fake = ctypes.c_void_p(16)  # never dereferenced: the size check comes first
+    rc = N.lib().htree_forward(d, 0.1, fake, fake, need - 1, fake, fake, fake, fake, fake, None, None)
+    assert rc == N.HTREE_EWORKSPACE
+
+
+def test_python_api_validates_like_reference():
+    import htree_amd
+
+    q = torch.zeros(1, 64, 4, 64)
+    k = torch.zeros(1, 64, 1, 64)
+    with pytest.raises(AssertionError, match="power of 2"):
+        htree_amd.htree_forward(q, k, k, 16, 64, 12)
+    with pytest.raises(AssertionError, match="divisible"):
+        htree_amd.htree_forward(torch.zeros(1, 64, 3, 64), torch.zeros(1, 64, 2, 64),
+                                torch.zeros(1, 64, 2, 64), 16, 64, 8)
+    with pytest.raises(AssertionError, match="GPU"):  # no CPU fallback
+        htree_amd.htree_forward(q, k, k, 16, 64, 8)
+
+
+def test_work_model_matches_baseline_table():
+    # algorithmic bytes of the gathered-bytes model
+    w2 = work(1, 32768, 32, 2, 128, 16, 16, 128, 2)
+    assert abs(w2.fwd_bytes / 1e9 - 18.36) < 0.01 and abs(w2.bwd_bytes / 1e9 - 18.45) < 0.015
+    w3 = work(4, 16384, 32, 4, 128, 16, 16, 128, 2)
+    assert abs(w3.fwd_bytes / 1e9 - 65.99) < 0.01 and abs(w3.bwd_bytes / 1e9 - 65.33) < 0.01
+    w5 = work(2, 65536, 32, 2, 128, 16, 16, 128, 2)
+    assert abs(w5.fwd_bytes / 1e9 - 83.63) < 0.01
+    assert abs(w2.mean_k_rows - 545.6) < 0.1 and abs(w2.mean_v_rows - 514.6) < 0.1
