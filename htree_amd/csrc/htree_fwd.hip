@@ -377,10 +377,431 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
   }
 }
 
+
+// ---------------------------------------------------------------- DPP helpers
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// sum / max over the 16 lanes of a row (quad xor 1, quad xor 2, half-row
+// mirror, row mirror); every lane of the row gets the result
+__device__ __forceinline__ float row_sum16(float x) {
+  x += dpp<0xB1>(x);
+  x += dpp<0x4E>(x);
+  x += dpp<0x141>(x);
+  x += dpp<0x140>(x);
+  return x;
+}
+__device__ __forceinline__ float row_max16(float x) {
+  x = fmaxf(x, dpp<0xB1>(x));
+  x = fmaxf(x, dpp<0x4E>(x));
+  x = fmaxf(x, dpp<0x141>(x));
+  x = fmaxf(x, dpp<0x140>(x));
+  return x;
+}
+__device__ __forceinline__ float wave_max_uniform(float x) {
+  x = row_max16(x);
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+// exp(x) for x <= 0 (x = -inf gives 0) including subnormal results, which
+// torch's CPU exp produces and the selection's exact-tie order depends on;
+// v_exp_f32 does not return subnormals, so those are scaled by 2^-64.
+__device__ __forceinline__ float exp_sel(float x) {
+  const float t = x * kLog2e;
+  const float r = __builtin_amdgcn_exp2f(t);
+  const float rs = __builtin_amdgcn_exp2f(t + 64.f) * 5.42101086242752217e-20f;
+  return t < -126.f ? rs : r;
+}
+
+// Shared Top-K of the group (src/naive.py:88-105): importance of position j
+// is imp[j] (lane j % 64 of slot j / 64), the rightmost (position apos) is
+// forced first; a 31-step bitwise radix select on float bits + 1 finds the
+// take-th largest key, ties at the threshold go to the lowest positions
+// (stable descending sort).  Writes the selected nodes in ascending order
+// (= ascending position) to par_next, -1 padded to TK, and one selection
+// bitmask per slot to selmask.
+template <int MAXSLOT>
+__device__ __forceinline__ void select_topk(const float* __restrict__ imp, const float* mt,
+                                            float Mrun, int nt, int nc, int apos, int TK,
+                                            bool wide, int crlg, int CR, int CRU,
+                                            const int32_t* par_cur, int32_t* par_next,
+                                            unsigned long long* selmask, int lane) {
+  const int u16 = lane & 15, kg = lane >> 4;
+  const int take = TK < nc ? TK : nc;
+  const int nslot = (nt + 3) >> 2;
+  uint32_t key[MAXSLOT];
+#pragma unroll
+  for (int sl = 0; sl < MAXSLOT; ++sl) {
+    key[sl] = 0u;
+    if (sl < nslot) {
+      const int tau = 4 * sl + kg;
+      const int pos = wide ? (tau << 4) + u16 : (tau << crlg) + u16;
+      if (tau < nt && u16 < CRU && pos < nc) {
+        float v;
+        if (pos == apos) {
+          v = 1e6f;  // rightmost candidate always kept (src/naive.py:93)
+        } else {
+          v = imp[64 * sl + lane];
+          if (mt) {
+            const float m = mt[tau];
+            if (m != Mrun) v *= expf(m - Mrun);
+          }
+        }
+        key[sl] = __float_as_uint(v) + 1u;
+      }
+    }
+  }
+  uint32_t thr = 0u;
+  for (int bit = 30; bit >= 0; --bit) {
+    const uint32_t c = thr | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int sl = 0; sl < MAXSLOT; ++sl)
+      if (sl < nslot) cnt += __popcll(__ballot(key[sl] >= c));
+    if (cnt >= take) thr = c;
+  }
+  int ngt = 0;
+#pragma unroll
+  for (int sl = 0; sl < MAXSLOT; ++sl)
+    if (sl < nslot) ngt += __popcll(__ballot(key[sl] > thr));
+  const int need = take - ngt;
+  int eq_before = 0, sel_before = 0;
+#pragma unroll
+  for (int sl = 0; sl < MAXSLOT; ++sl) {
+    if (sl < nslot) {
+      const unsigned long long em = __ballot(key[sl] == thr);
+      const bool sel = key[sl] > thr || (key[sl] == thr && eq_before + mbcnt64(em) < need);
+      const unsigned long long sm = __ballot(sel);
+      if (lane == 0) selmask[sl] = sm;
+      if (sel) {
+        const int tau = 4 * sl + kg;
+        const int s = wide ? (tau << 4) >> crlg : tau;
+        par_next[sel_before + mbcnt64(sm)] =
+            (par_cur[s] << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0) + u16;
+      }
+      eq_before += __popcll(em);
+      sel_before += __popcll(sm);
+    }
+  }
+  if (lane >= take && lane < TK) par_next[lane] = -1;
+}
+
+// ---------------------------------------------------------------- single-pass forward
+// For levels of at most 16 candidate tiles (TK * max(CR,16) <= 256): every
+// tile is scored once (S^T, candidates x heads) into LDS; the selection uses
+// the exact level max and the accumulation reuses the scores.  Tiles are
+// walked in descending parent slot, so the query rotation advances by the
+// constant angle CR (R(q, a - s CR) = R(R(q, a - (s+1) CR), CR)), and the K
+// and V gathers are double-buffered one tile ahead.
+struct WaveLdsR {
+  f32x4 st[16][64];  // S^T of every tile, one f32x4 per lane
+  int32_t par[2][kMaxTK];
+  float imp[256];
+  float xrow[64];
+  unsigned long long selmask[4];
+};
+
+template <int D>
+__device__ __forceinline__ void rot_by(float (&x)[D / 32][8], const float* __restrict__ cosr,
+                                       const float* __restrict__ sinr, int kg) {
+  constexpr int SPH = D / 64;
+#pragma unroll
+  for (int m = 0; m < SPH; ++m) {
+    const int i0 = dslot<D>(kg, m);
+    float c[8], s[8];
+    Io<float>::ld8(cosr + i0, c);
+    Io<float>::ld8(sinr + i0, s);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float lo = x[m][e], hi = x[m + SPH][e];
+      x[m][e] = lo * c[e] - hi * s[e];
+      x[m + SPH][e] = lo * s[e] + hi * c[e];
+    }
+  }
+}
+
+// Query fragment of a lane (head u16, the lane group's d-slots) kept in its
+// input type; get() returns it in fp32 times `scale`.
+template <int D, typename TIn>
+struct QFrag {
+  float f[D / 32][8];
+  __device__ __forceinline__ void load(const TIn* p, int kg, bool gv) {
+#pragma unroll
+    for (int m = 0; m < D / 32; ++m) {
+      Io<TIn>::ld8(p + dslot<D>(kg, m), f[m]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[m][e] = gv ? f[m][e] : 0.f;
+    }
+  }
+  __device__ __forceinline__ void get(float (&x)[D / 32][8], float scale) const {
+#pragma unroll
+    for (int m = 0; m < D / 32; ++m)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[m][e] = f[m][e] * scale;
+  }
+};
+template <int D>
+struct QFrag<D, __bf16> {
+  uint4 w[D / 32];  // 8 bf16 per k-step, exact
+  __device__ __forceinline__ void load(const __bf16* p, int kg, bool gv) {
+#pragma unroll
+    for (int m = 0; m < D / 32; ++m) {
+      const uint4 r = *(const uint4*)(p + dslot<D>(kg, m));
+      w[m] = gv ? r : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  __device__ __forceinline__ void get(float (&x)[D / 32][8], float scale) const {
+#pragma unroll
+    for (int m = 0; m < D / 32; ++m) {
+      const uint32_t v[4] = {w[m].x, w[m].y, w[m].z, w[m].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[m][2 * i] = __uint_as_float(v[i] << 16) * scale;
+        x[m][2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u) * scale;
+      }
+    }
+  }
+};
+
+template <int D, bool PREC, typename TIn>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fwd_reg_kernel(const FwdArgs a) {
+  constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
+  __shared__ WaveLdsR lds_all[kWavesPerBlock];
+  __shared__ float rot_cr[2][HALF];  // cos / sin of the angle CR
+
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int u16 = lane & 15, kg = lane >> 4;
+  const int G = a.G, CR = a.CR, crlg = a.crlg, TK = a.TK;
+  if (threadIdx.x < HALF) {
+    rot_cr[0][threadIdx.x] = a.cosb[(int64_t)CR * HALF + threadIdx.x];
+    rot_cr[1][threadIdx.x] = a.sinb[(int64_t)CR * HALF + threadIdx.x];
+  }
+  __syncthreads();
+  const int bid = blockIdx.x;
+  const int64_t lb = (int64_t)(bid & 7) * a.per_xcd + (bid >> 3);
+  const int64_t grp = lb * kWavesPerBlock + wv;
+  if (grp >= (int64_t)a.B * a.Hkv * a.T) return;
+  const int t = (int)(grp % a.T);
+  const int bh = (int)(grp / a.T);
+  const int h = bh % a.Hkv;
+  const int b = bh / a.Hkv;
+  WaveLdsR& W = lds_all[wv];
+  const int CRU = CR < 16 ? CR : 16;
+  const bool wide = CR >= 16;
+  const bool gv = u16 < G;
+
+  // the query stays in its input type (16-bit types packed: 16 registers)
+  QFrag<D, TIn> qin;
+  qin.load((const TIn*)a.q + (((int64_t)b * a.T + t) * a.H + h * G + (gv ? u16 : 0)) * D, kg, gv);
+
+  float m_run = -INFINITY, l_part = 0.f;
+  f32x4 O[ND];
+#pragma unroll
+  for (int n = 0; n < ND; ++n) O[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  {
+    const int64_t nvp = (t / a.lv[a.L - 1].pw) / CR + 1;
+    if (lane < TK) W.par[0][lane] = lane < nvp ? lane : -1;
+  }
+  int cur = 0;
+
+  for (int l = a.L - 1; l >= 0; --l) {
+    wave_sync();
+    const LevelPtrs P = a.lv[l];
+    const int pv = lane < TK ? W.par[cur][lane] : -1;
+    const int np = __popcll(__ballot(pv >= 0));
+    if (np <= 0) break;  // unreachable: every level keeps >= 1 parent
+    const int ct = (int)((t / P.pw) & (CR - 1));
+    const int nc = ((np - 1) << crlg) + ct + 1;
+    const int apos = nc - 1;
+    const int nt = wide ? (nc + 15) >> 4 : np;
+    if (a.parents && lane < TK)
+      a.parents[((((int64_t)l * a.B + b) * a.T + t) * a.Hkv + h) * TK + lane] = pv;
+    const int64_t hrow = ((int64_t)b * a.Hkv + h) * P.Np;
+    const uint16_t* KH = P.kh + hrow * D;
+    const uint16_t* KL = P.kl + hrow * D;
+    const uint16_t* VH = P.vh + hrow * D;
+    const uint16_t* VL = PREC ? P.vl + hrow * D : nullptr;
+    const int32_t* pc = W.par[cur];
+    auto node0_of = [&](int tau) {
+      const int s = wide ? (tau << 4) >> crlg : tau;
+      return (pc[s] << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0);
+    };
+    auto kload = [&](int tau, bf16x8 (&kh)[KS], bf16x8 (&kl)[KS]) {
+      const int posk = wide ? (tau << 4) + u16 : (tau << crlg) + u16;
+      const bool cvk = u16 < CRU && posk < nc;
+      const int64_t krow = (int64_t)(node0_of(tau) + (cvk ? u16 : 0)) * D;
+      load_kfrag<D>(KH + krow, kg, kh);
+      load_kfrag<D>(KL + krow, kg, kl);
+    };
+
+    // ---- scores of every tile (descending slot), S^T into LDS
+    // first slot s = np-1: angle apos - (np-1) CR = ct; scale folded in
+    float qr[KS][8];
+    qin.get(qr, a.scale);
+    rot_by<D>(qr, a.cosb + (int64_t)ct * HALF, a.sinb + (int64_t)ct * HALF, kg);
+    int cur_slot = (wide ? ((nt - 1) << 4) >> crlg : nt - 1);
+    float lmax = -INFINITY;
+    auto score = [&](int tau, const bf16x8 (&kh)[KS], const bf16x8 (&kl)[KS]) {
+      const int s = wide ? (tau << 4) >> crlg : tau;
+      if (s != cur_slot) {  // slots are visited in descending order, one step apart
+        rot_by<D>(qr, rot_cr[0], rot_cr[1], kg);
+        cur_slot = s;
+      }
+      bf16x8 qh[KS], ql[KS];
+      to_bf_split<D>(qr, qh, ql);
+      f32x4 S = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < KS; ++m) {
+        S = mma32(kh[m], qh[m], S);
+        S = mma32(kl[m], qh[m], S);
+        S = mma32(kh[m], ql[m], S);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int cu = 4 * kg + r;
+        const int pos = wide ? (tau << 4) + cu : (tau << crlg) + cu;
+        const bool ok = gv && cu < CRU && pos < nc;
+        S[r] = ok ? S[r] : -INFINITY;
+        lmax = fmaxf(lmax, S[r]);
+      }
+      W.st[tau][lane] = S;
+    };
+    {
+      bf16x8 ah[KS], al[KS], bh_[KS], bl[KS];
+      kload(nt - 1, ah, al);
+      if (nt >= 2) kload(nt - 2, bh_, bl);
+      for (int tau = nt - 1; tau >= 0; tau -= 2) {
+        score(tau, ah, al);
+        if (tau >= 2) kload(tau - 2, ah, al);
+        if (tau >= 1) {
+          score(tau - 1, bh_, bl);
+          if (tau >= 3) kload(tau - 3, bh_, bl);
+        }
+      }
+    }
+
+    if (l > 0) {
+      // ---- importance sum_g exp(s - M), M = max over the level's scores
+      const float M = wave_max_uniform(lmax);
+      for (int tau = 0; tau < nt; ++tau) {
+        const f32x4 S = W.st[tau][lane];
+        float e[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) e[r] = row_sum16(exp_sel(S[r] - M));
+        const float mine = u16 == 0 ? e[0] : u16 == 1 ? e[1] : u16 == 2 ? e[2] : e[3];
+        if (u16 < 4) W.imp[(tau << 4) + 4 * kg + u16] = mine;
+      }
+      wave_sync();
+      select_topk<4>(W.imp, nullptr, M, nt, nc, apos, TK, wide, crlg, CR, CRU, W.par[cur],
+                     W.par[cur ^ 1], W.selmask, lane);
+      wave_sync();
+    }
+
+    // ---- per-head max over the accumulated candidates (rows kg via LDS)
+    const bool upper = l > 0;
+    auto masked = [&](int tau) {
+      f32x4 S = W.st[tau][lane];
+      if (upper) {
+        const unsigned long long sm = W.selmask[tau >> 2];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if ((sm >> ((16 * (tau & 3) + 4 * kg + r) & 63)) & 1ull) S[r] = -INFINITY;
+      }
+      return S;
+    };
+    float gmx = -INFINITY;
+    for (int tau = 0; tau < nt; ++tau) {
+      const f32x4 S = masked(tau);
+      gmx = fmaxf(fmaxf(gmx, fmaxf(S[0], S[1])), fmaxf(S[2], S[3]));
+    }
+    W.xrow[u16 * 4 + kg] = gmx;
+    wave_sync();
+    {
+      const float4 x4 = *(const float4*)(&W.xrow[u16 * 4]);
+      gmx = fmaxf(fmaxf(x4.x, x4.y), fmaxf(x4.z, x4.w));
+    }
+    const float mnew = fmaxf(m_run, gmx);
+    const float mref = mnew == -INFINITY ? 0.f : mnew;
+    const float alpha = __builtin_amdgcn_exp2f((m_run - mref) * kLog2e);
+    m_run = mnew;
+    l_part *= alpha;
+#pragma unroll
+    for (int n = 0; n < ND; ++n) O[n] *= alpha;
+
+    // ---- O^T += V^T P^T over the tiles, V double-buffered
+    auto vload = [&](int tau, s16x4 (&vh)[ND], s16x4 (&vl)[ND]) {
+      const int vn = node0_of(tau) + (4 * kg < CRU ? 4 * kg : 0);
+      const int64_t vbase = ((int64_t)(vn >> 4) * D + u16) * 16 + (vn & 15);
+#pragma unroll
+      for (int n = 0; n < ND; ++n) {
+        vh[n] = *(const s16x4*)(VH + vbase + (int64_t)n * 256);
+        if (PREC) vl[n] = *(const s16x4*)(VL + vbase + (int64_t)n * 256);
+      }
+    };
+    auto pv_tile = [&](int tau, const s16x4 (&vh)[ND], const s16x4 (&vl)[ND]) {
+      const f32x4 S = masked(tau);
+      float p[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f((S[r] - mref) * kLog2e);
+      l_part += (p[0] + p[1]) + (p[2] + p[3]);
+      s16x4 ph, pl;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint16_t hb = f_to_bf(p[r]);
+        ph[r] = (short)hb;
+        pl[r] = PREC ? f_to_bfs(p[r] - bf_to_f(hb)) : (short)0;
+      }
+#pragma unroll
+      for (int n = 0; n < ND; ++n) {
+        O[n] = mma16(vh[n], ph, O[n]);
+        if (PREC) {
+          O[n] = mma16(vh[n], pl, O[n]);
+          O[n] = mma16(vl[n], ph, O[n]);
+        }
+      }
+    };
+    {
+      s16x4 av[ND], avl[ND], bv[ND], bvl[ND];
+      vload(0, av, avl);
+      if (nt >= 2) vload(1, bv, bvl);
+      for (int tau = 0; tau < nt; tau += 2) {
+        pv_tile(tau, av, avl);
+        if (tau + 2 < nt) vload(tau + 2, av, avl);
+        if (tau + 1 < nt) {
+          pv_tile(tau + 1, bv, bvl);
+          if (tau + 3 < nt) vload(tau + 3, bv, bvl);
+        }
+      }
+    }
+    cur ^= 1;
+  }
+
+  float lt = l_part + __shfl_xor(l_part, 16);
+  lt += __shfl_xor(lt, 32);
+  if (gv) {
+    const int64_t hq = ((int64_t)b * a.T + t) * a.H + h * G + u16;
+    TIn* op = (TIn*)a.out + hq * D;
+    const float inv = 1.f / lt;
+#pragma unroll
+    for (int n = 0; n < ND; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Io<TIn>::st(op + 16 * n + 4 * kg + r, O[n][r] * inv);
+    if (kg == 0) {
+      a.gmax[hq] = m_run;
+      a.gsum[hq] = lt;
+    }
+  }
+}
+
 template <int D, bool PREC, typename TIn>
 static void launch_fwd(const FwdArgs& a, int max_tiles, dim3 grid, hipStream_t st) {
   if (max_tiles <= 16)
-    hipLaunchKernelGGL((fwd_kernel<D, PREC, TIn, 4>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((fwd_reg_kernel<D, PREC, TIn>), grid, dim3(256), 0, st, a);
   else
     hipLaunchKernelGGL((fwd_kernel<D, PREC, TIn, 16>), grid, dim3(256), 0, st, a);
 }
