@@ -41,7 +41,7 @@ struct BwdPlan {
   int64_t off_kt[2][HTREE_MAX_LEVELS], off_vr[2][HTREE_MAX_LEVELS];
   int64_t off_dk[HTREE_MAX_LEVELS], off_dv[HTREE_MAX_LEVELS];
   int64_t off_bitmap, off_cnt, off_rowoff, off_pcnt, off_poff, off_npieces, off_ptab, off_csr,
-      off_partial;
+      off_partial, off_csr_row, off_rec;
   int64_t bytes;
 };
 
@@ -94,17 +94,14 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
   b->off_npieces = take(4);
   b->off_ptab = take(b->max_pieces * 3 * 4);
   b->off_csr = take(b->max_entries * 4);
+  b->off_csr_row = take(b->max_entries * 4);
+  b->off_rec = take(b->max_entries * 16);
   b->off_partial = take(b->max_pieces * b->tpp * 16 * (int64_t)d->D * 2 * 4);
   b->bytes = off;
   return HTREE_OK;
 }
 
 // ---------------------------------------------------------------- helpers
-template <int D>
-__device__ __forceinline__ int dslot(int kg, int m) {
-  constexpr int SPH = D / 64;
-  return 8 * kg + 32 * (m % SPH) + (D / 2) * (m / SPH);
-}
 
 template <int D>
 __device__ __forceinline__ void rot_frag(const float (&x)[D / 32][8], const float* __restrict__ cosr,
@@ -127,6 +124,25 @@ __device__ __forceinline__ void rot_frag(const float (&x)[D / 32][8], const floa
 }
 
 template <int D>
+__device__ __forceinline__ void rot_by_fr(float (&x)[D / 32][8], const float* cosr, const float* sinr,
+                                          int kg) {
+  constexpr int SPH = D / 64;
+#pragma unroll
+  for (int m = 0; m < SPH; ++m) {
+    const int i0 = dslot<D>(kg, m);
+    float c[8], s[8];
+    Io<float>::ld8(cosr + i0, c);
+    Io<float>::ld8(sinr + i0, s);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float lo = x[m][e], hi = x[m + SPH][e];
+      x[m][e] = lo * c[e] - hi * s[e];
+      x[m + SPH][e] = lo * s[e] + hi * c[e];
+    }
+  }
+}
+
+template <int D>
 __device__ __forceinline__ void split_frag(const float (&x)[D / 32][8], bf16x8 (&h)[D / 32],
                                            bf16x8 (&lo)[D / 32]) {
 #pragma unroll
@@ -137,6 +153,14 @@ __device__ __forceinline__ void split_frag(const float (&x)[D / 32][8], bf16x8 (
       h[m][e] = hb;
       lo[m][e] = (__bf16)(x[m][e] - (float)hb);
     }
+}
+
+template <int D>
+__device__ __forceinline__ void to_bf8(const float (&x)[D / 32][8], bf16x8 (&h)[D / 32]) {
+#pragma unroll
+  for (int m = 0; m < D / 32; ++m)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[m][e] = (__bf16)x[m][e];
 }
 
 template <int D>
@@ -317,7 +341,8 @@ __global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ 
 // one wave per row: writes the row's query indices in ascending t
 __global__ __launch_bounds__(256) void extract_kernel(const uint32_t* __restrict__ bm, int64_t nrows,
                                                       int64_t W, const int32_t* __restrict__ rowoff,
-                                                      int32_t* __restrict__ csr) {
+                                                      int32_t* __restrict__ csr,
+                                                      int32_t* __restrict__ csr_row) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
   if (row >= nrows) return;
@@ -335,6 +360,7 @@ __global__ __launch_bounds__(256) void extract_kernel(const uint32_t* __restrict
     int64_t pos = base + inc - c;
     while (x) {
       const int bit = __ffs(x) - 1;
+      csr_row[pos] = (int32_t)row;
       csr[pos++] = (int32_t)(w * 32 + bit);
       x &= x - 1;
     }
@@ -359,6 +385,47 @@ __global__ __launch_bounds__(256) void piece_kernel(const int32_t* __restrict__ 
   }
 }
 
+
+// Per entry (query t of parent p's row): the rotation row rho = n_c - 1 -
+// s CR of p's slot s in t's list, and the mask of p's children that t
+// accumulates at this level (valid positions, not passed to level l-1).
+__global__ __launch_bounds__(256) void record_kernel(const int32_t* __restrict__ csr,
+                                                     const int32_t* __restrict__ csr_row,
+                                                     const int32_t* __restrict__ ntot,
+                                                     const int32_t* __restrict__ par,
+                                                     const int32_t* __restrict__ par_next, int T,
+                                                     int Hkv, int TK, int64_t Pl, int64_t pw, int CR,
+                                                     int crlg, int4* __restrict__ rec) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= *ntot) return;
+  const int t = csr[e];
+  const int64_t row = csr_row[e];
+  const int p = (int)(row % Pl);
+  const int64_t bh = row / Pl;
+  const int h = (int)(bh % Hkv);
+  const int64_t grp = ((bh / Hkv) * T + t) * Hkv + h;
+  const int32_t* pl = par + grp * TK;
+  int np = 0, s = 0;
+  for (int i = 0; i < TK; ++i) {
+    const int v = pl[i];
+    np += v >= 0;
+    s += (v >= 0 && v < p);
+  }
+  const int ct = (int)((t / pw) & (CR - 1));
+  const int nc = ((np - 1) << crlg) + ct + 1;
+  const int nvalid = nc - (s << crlg);  // children of p that are candidates
+  unsigned long long m = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
+  if (CR < 64) m &= (1ull << CR) - 1ull;
+  if (par_next) {
+    const int32_t* pn = par_next + grp * TK;
+    for (int i = 0; i < TK; ++i) {
+      const int v = pn[i];
+      if (v >= 0 && (v >> crlg) == p) m &= ~(1ull << (v & (CR - 1)));
+    }
+  }
+  rec[e] = make_int4(t, nc - 1 - (s << crlg), (int)(uint32_t)m, (int)(uint32_t)(m >> 32));
+}
+
 // ---------------------------------------------------------------- dkv
 struct DkvArgs {
   const uint16_t *kh, *kl;      // K~ rows (hi/lo), [B][Hkv][Np][D]
@@ -367,9 +434,8 @@ struct DkvArgs {
   const void* q;
   const void* dO;
   const float *gmax, *gsum, *delta;
-  const int32_t* par;       // lists used at this level [B,T,Hkv,TK]
-  const int32_t* par_next;  // lists used at level l-1 (nullptr at l = 0)
-  const int32_t *ptab, *npieces, *csr;
+  const int32_t *ptab, *npieces;
+  const int4* rec;  // per entry: t, rho, accumulate mask (lo, hi)
   const float *cosb, *sinb;
   float* partial;
   int64_t N, Np, pw, Pl;
@@ -378,9 +444,8 @@ struct DkvArgs {
 };
 
 template <int D, bool PREC, typename TIn>
-__global__ __launch_bounds__(256) void dkv_kernel(const DkvArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void dkv_kernel(const DkvArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
-  __shared__ int32_t sel16[kWavesPerBlock][16];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int u16 = lane & 15, kg = lane >> 4;
   const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wv;
@@ -409,31 +474,18 @@ __global__ __launch_bounds__(256) void dkv_kernel(const DkvArgs a) {
   f32x4 dv[ND], dk[ND];
 #pragma unroll
   for (int n = 0; n < ND; ++n) dv[n] = dk[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  int32_t* S16 = sel16[wv];
-
+  int4 rn = ne > 0 ? a.rec[e0] : make_int4(0, 0, 0, 0);
   for (int e = 0; e < ne; ++e) {
-    const int t = a.csr[e0 + e];
+    const int4 rc = rn;
+    if (e + 1 < ne) rn = a.rec[e0 + e + 1];  // next entry's record in flight
+    const int t = rc.x;
+    const int rho = rc.y;
+    const unsigned long long m64 = ((unsigned long long)(uint32_t)rc.w << 32) | (uint32_t)rc.z;
+    const uint32_t tmask = (uint32_t)(m64 >> coff) & (CR < 16 ? ((1u << CR) - 1u) : 0xffffu);
+    if (tmask == 0u) continue;  // every child of the tile passed down or past the query
+    const bool ok = (tmask >> u16) & 1u;
     const int64_t bt = b * a.T + t;
     const int64_t grp = bt * a.Hkv + h;
-    const int32_t* pl = a.par + grp * TK;
-    const int pe = lane < TK ? pl[lane] : -1;
-    const int np = __popcll(__ballot(pe >= 0));
-    const int s = __popcll(__ballot(pe >= 0 && pe < p));
-    const int ct = (int)((t / a.pw) & (CR - 1));
-    const int nc = ((np - 1) << crlg) + ct + 1;
-    const int rho = nc - 1 - (s << crlg);
-    const int j0 = (s << crlg) + coff;
-    bool ok = u16 < CRU && j0 + u16 < nc;
-    if (a.par_next) {
-      if (lane < 16) S16[lane] = 0;
-      wave_sync();
-      const int en = lane < TK ? a.par_next[grp * TK + lane] : -1;
-      if (en >= node0 && en < node0 + 16) S16[en - node0] = 1;
-      wave_sync();
-      ok = ok && S16[u16] == 0;
-      wave_sync();
-    }
-    if (!__any(ok)) continue;
     // rotated, scaled query fragment (lane g = u16)
     const bool gv = u16 < G;
     float qf[KS][8], qr[KS][8];
@@ -468,7 +520,10 @@ __global__ __launch_bounds__(256) void dkv_kernel(const DkvArgs a) {
         for (int i = 0; i < 8; ++i) df[m][i] = gv ? df[m][i] : 0.f;
       }
       bf16x8 dh[KS], dlo[KS];
-      split_frag<D>(df, dh, dlo);
+      if (PREC)
+        split_frag<D>(df, dh, dlo);
+      else
+        to_bf8<D>(df, dh);  // 16-bit inputs are exact in bf16 hi
 #pragma unroll
       for (int m = 0; m < KS; ++m) {
         dP = mma32(dh[m], vh[m], dP);
@@ -615,48 +670,82 @@ struct DqArgs {
   float scale;
 };
 
+// rotation of a dq^T accumulator (C layout: d = 16n + 4kg + r, head u16)
+// by the angle whose cos/sin (length D/2) are c / sn: x <- R(x, angle)
+template <int D>
+__device__ __forceinline__ void rot_acc(f32x4 (&x)[D / 16], const float* c, const float* sn,
+                                        int kg) {
+  constexpr int ND = D / 16;
+#pragma unroll
+  for (int n = 0; n < ND / 2; ++n) {
+    const int i0 = 16 * n + 4 * kg;
+    const float4 c4 = *(const float4*)(c + i0);
+    const float4 s4 = *(const float4*)(sn + i0);
+    const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float lo = x[n][r], hi = x[n + ND / 2][r];
+      x[n][r] = lo * cc[r] - hi * ss[r];
+      x[n + ND / 2][r] = lo * ss[r] + hi * cc[r];
+    }
+  }
+}
+
+// Q-stationary dq over all levels.  Tiles are walked in ascending parent
+// slot s, whose query angle a - s CR falls by CR per slot: the query
+// fragment advances by R(., -CR) and the tile contributions are gathered in
+// a frame that turns with it, X <- R(X, -CR) + dq~_tile, so that
+//   sum_s R^-1(dq~_s, a - s CR) = R^-1(X, n_c-1 - (np-1) CR) = R(X, -c_t)
+// needs one table rotation per level.
 template <int D, bool PREC, typename TIn>
-__global__ __launch_bounds__(256) void dq_kernel(const DqArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void dq_kernel(const DqArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
-  __shared__ int32_t lst[kWavesPerBlock][2][kMaxTK];
+  __shared__ int32_t lst[kWavesPerBlock][kMaxTK];
   __shared__ uint32_t selw[kWavesPerBlock][32];
+  __shared__ float rot_m[2][HALF];  // cos(CR theta), -sin(CR theta)
+  __shared__ f32x4 acc_l[kWavesPerBlock][D / 16][64];  // dq over the finished levels
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int u16 = lane & 15, kg = lane >> 4;
+  const int G = a.G, CR = a.CR, crlg = a.crlg, TK = a.TK;
+  if (threadIdx.x < HALF) {
+    rot_m[0][threadIdx.x] = a.cosb[(int64_t)CR * HALF + threadIdx.x];
+    rot_m[1][threadIdx.x] = -a.sinb[(int64_t)CR * HALF + threadIdx.x];
+  }
+  __syncthreads();
   const int64_t grp = (int64_t)blockIdx.x * kWavesPerBlock + wv;
   if (grp >= (int64_t)a.B * a.T * a.Hkv) return;
   const int h = (int)(grp % a.Hkv);
   const int64_t bt = grp / a.Hkv;
   const int t = (int)(bt % a.T);
-  const int G = a.G, CR = a.CR, crlg = a.crlg, TK = a.TK;
+  const int64_t b = bt / a.T;
   const int CRU = CR < 16 ? CR : 16;
   const bool wide = CR >= 16;
   const bool gv = u16 < G;
   const int64_t hq = bt * a.H + h * G + (gv ? u16 : 0);
-  float qf[KS][8];
+  QFrag<D, TIn> qin;
+  qin.load((const TIn*)a.q + hq * D, kg, gv);
   bf16x8 dh[KS], dlo[KS];
   {
-    const TIn* qp = (const TIn*)a.q + hq * D;
     const TIn* dp = (const TIn*)a.dO + hq * D;
     float df[KS][8];
 #pragma unroll
     for (int m = 0; m < KS; ++m) {
-      Io<TIn>::ld8(qp + dslot<D>(kg, m), qf[m]);
       Io<TIn>::ld8(dp + dslot<D>(kg, m), df[m]);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        qf[m][i] = gv ? qf[m][i] * a.scale : 0.f;
-        df[m][i] = gv ? df[m][i] : 0.f;
-      }
+      for (int i = 0; i < 8; ++i) df[m][i] = gv ? df[m][i] : 0.f;
     }
-    split_frag<D>(df, dh, dlo);
+    if (PREC)
+      split_frag<D>(df, dh, dlo);
+    else
+      to_bf8<D>(df, dh);
   }
   const float gm = gv ? a.gmax[hq] : 0.f;
   const float gs = gv ? a.gsum[hq] : 1.f;
   const float dl = gv ? a.delta[hq] : 0.f;
-  f32x4 acc[ND];
+  f32x4(*AC)[64] = acc_l[wv];
 #pragma unroll
-  for (int n = 0; n < ND; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  int32_t(*LS)[kMaxTK] = lst[wv];
+  for (int n = 0; n < ND; ++n) AC[n][lane] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int32_t* LS = lst[wv];
   uint32_t* SW = selw[wv];
   const int64_t lstride = (int64_t)a.B * a.T * a.Hkv * TK;
 
@@ -664,7 +753,7 @@ __global__ __launch_bounds__(256) void dq_kernel(const DqArgs a) {
     const DqLevel P = a.lv[l];
     wave_sync();
     const int pe = lane < TK ? a.parents[l * lstride + grp * TK + lane] : -1;
-    if (lane < TK) LS[0][lane] = pe;
+    if (lane < TK) LS[lane] = pe;
     if (lane < 32) SW[lane] = 0u;
     const int np = __popcll(__ballot(pe >= 0));
     if (np <= 0) continue;
@@ -681,31 +770,57 @@ __global__ __launch_bounds__(256) void dq_kernel(const DqArgs a) {
         int lo = 0, hi = np - 1;
         while (lo < hi) {
           const int mid = (lo + hi) >> 1;
-          if (LS[0][mid] < pp) lo = mid + 1; else hi = mid;
+          if (LS[mid] < pp) lo = mid + 1; else hi = mid;
         }
-        const int j = (lo << crlg) + (en & (CR - 1));
-        atomicOr(&SW[(wide ? j : ((lo << 4) + (en & (CR - 1)))) >> 5],
-                 1u << ((wide ? j : ((lo << 4) + (en & (CR - 1)))) & 31));
+        const int j = (lo << 4) * (wide ? 0 : 1) + (wide ? (lo << crlg) : 0) + (en & (CR - 1));
+        atomicOr(&SW[j >> 5], 1u << (j & 31));
       }
       wave_sync();
     }
-    const int64_t hrow = (((int64_t)(grp / a.Hkv) / a.T) * a.Hkv + h) * P.Np;
-    for (int tau = 0; tau < nt; ++tau) {
+    const int64_t hrow = (b * a.Hkv + h) * P.Np;
+    auto node0_of = [&](int tau) {
       const int s = wide ? (tau << 4) >> crlg : tau;
-      const int node0 = (LS[0][s] << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0);
-      const int prow = apos - (s << crlg);
-      float qr[KS][8];
-      rot_frag<D>(qf, a.cosb + (int64_t)prow * HALF, a.sinb + (int64_t)prow * HALF, kg, qr);
-      bf16x8 qh[KS], ql[KS];
-      split_frag<D>(qr, qh, ql);
+      return (LS[s] << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0);
+    };
+    auto kload = [&](int tau, bf16x8 (&kh)[KS], bf16x8 (&kl)[KS]) {
       const int posk = wide ? (tau << 4) + u16 : (tau << crlg) + u16;
       const bool cvk = u16 < CRU && posk < nc;
-      const int64_t krow = (hrow + node0 + (cvk ? u16 : 0)) * D;
-      bf16x8 kh[KS], kl[KS], vh[KS], vl[KS];
+      const int64_t krow = (hrow + node0_of(tau) + (cvk ? u16 : 0)) * D;
       load_frag<D>(P.kh + krow, kg, kh);
       load_frag<D>(P.kl + krow, kg, kl);
-      load_frag<D>(P.vr_h + krow, kg, vh);
-      if (PREC) load_frag<D>(P.vr_l + krow, kg, vl);
+    };
+    // query frame of slot 0: angle apos
+    float qr[KS][8];
+    qin.get(qr, a.scale);
+    rot_by_fr<D>(qr, a.cosb + (int64_t)apos * HALF, a.sinb + (int64_t)apos * HALF, kg);
+    f32x4 X[ND];
+#pragma unroll
+    for (int n = 0; n < ND; ++n) X[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    int cur_slot = 0;
+    auto tile = [&](int tau, const bf16x8 (&kh)[KS], const bf16x8 (&kl)[KS]) {
+      const int s = wide ? (tau << 4) >> crlg : tau;
+      if (s != cur_slot) {  // ascending slots, one step apart
+        rot_by_fr<D>(qr, rot_m[0], rot_m[1], kg);
+        rot_acc<D>(X, rot_m[0], rot_m[1], kg);
+        cur_slot = s;
+      }
+      const int node0 = node0_of(tau);
+      const int posk = wide ? (tau << 4) + u16 : (tau << crlg) + u16;
+      const bool cvk = u16 < CRU && posk < nc;
+      const int64_t vrow = (hrow + node0 + (cvk ? u16 : 0)) * D;
+      bf16x8 vh[KS], vl[KS];
+      load_frag<D>(P.vr_h + vrow, kg, vh);
+      if (PREC) load_frag<D>(P.vr_l + vrow, kg, vl);
+      const int vn = node0 + (4 * kg < CRU ? 4 * kg : 0);
+      const int64_t tbase = ((hrow + (vn & ~15)) / 16 * D + u16) * 16 + (vn & 15);
+      s16x4 kt[ND], ktl[ND];
+#pragma unroll
+      for (int n = 0; n < ND; ++n) {
+        kt[n] = *(const s16x4*)(P.kt_h + tbase + (int64_t)n * 256);
+        ktl[n] = *(const s16x4*)(P.kt_l + tbase + (int64_t)n * 256);
+      }
+      bf16x8 qh[KS], ql[KS];
+      split_frag<D>(qr, qh, ql);
       f32x4 S = {0.f, 0.f, 0.f, 0.f}, dP = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int m = 0; m < KS; ++m) {
@@ -719,58 +834,63 @@ __global__ __launch_bounds__(256) void dq_kernel(const DqArgs a) {
         }
       }
       // S[r], dP[r]: candidate 4kg + r, head u16
-      const uint32_t sw = SW[((wide ? (tau << 4) : (tau << 4))) >> 5];
+      const uint32_t sw = SW[(tau << 4) >> 5];
       float ds[4];
       bool anyv = false;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int cu = 4 * kg + r;
         const int pos = wide ? (tau << 4) + cu : (tau << crlg) + cu;
-        const int bitpos = ((tau << 4) + cu) & 31;
-        const bool v = gv && cu < CRU && pos < nc && !((sw >> bitpos) & 1u);
+        const bool v = gv && cu < CRU && pos < nc && !((sw >> (((tau << 4) + cu) & 31)) & 1u);
         const float pr = v ? __builtin_amdgcn_exp2f((S[r] - gm) * kLog2e) / gs : 0.f;
         ds[r] = pr * (dP[r] - dl);
         anyv |= v;
       }
-      if (!__any(anyv)) continue;
+      if (!__any(anyv)) return;
       // dq = sum_cand dS K~ cancels (sum_cand dS = 0 per head): split both
       // factors so clustered keys keep their small residual
       s16x4 d4h, d4l;
       pack4_split(ds, d4h, d4l);
-      // dq~^T[d][g] = sum_cand K~[cand][d] dS[g][cand]
-      const int vn = node0 + (4 * kg < CRU ? 4 * kg : 0);
-      const int64_t tbase = ((hrow + (vn & ~15)) / 16 * D + u16) * 16 + (vn & 15);
-      f32x4 tq[ND];
 #pragma unroll
       for (int n = 0; n < ND; ++n) {
-        const s16x4 kt = *(const s16x4*)(P.kt_h + tbase + (int64_t)n * 256);
-        const s16x4 ktl = *(const s16x4*)(P.kt_l + tbase + (int64_t)n * 256);
-        tq[n] = mma16(kt, d4h, f32x4{0.f, 0.f, 0.f, 0.f});
-        tq[n] = mma16(kt, d4l, tq[n]);
-        tq[n] = mma16(ktl, d4h, tq[n]);
+        X[n] = mma16(kt[n], d4h, X[n]);
+        X[n] = mma16(kt[n], d4l, X[n]);
+        X[n] = mma16(ktl[n], d4h, X[n]);
       }
-      // tq[n][r] at d = 16n + 4kg + r, head u16: rotate back by prow
+    };
+    for (int tau = 0; tau < nt; ++tau) {
+      bf16x8 kh[KS], kl[KS];
+      kload(tau, kh, kl);
+      tile(tau, kh, kl);
+    }
+    // back to the query's frame: R(X, -c_t)
+    {
 #pragma unroll
       for (int n = 0; n < ND / 2; ++n) {
         const int i0 = 16 * n + 4 * kg;
-        const float4 c4 = *(const float4*)(a.cosb + (int64_t)prow * HALF + i0);
-        const float4 s4 = *(const float4*)(a.sinb + (int64_t)prow * HALF + i0);
+        const float4 c4 = *(const float4*)(a.cosb + (int64_t)ct * HALF + i0);
+        const float4 s4 = *(const float4*)(a.sinb + (int64_t)ct * HALF + i0);
         const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
+        f32x4 lo4 = AC[n][lane], hi4 = AC[n + ND / 2][lane];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float lo = tq[n][r], hi = tq[n + ND / 2][r];
-          acc[n][r] += lo * cc[r] + hi * ss[r];
-          acc[n + ND / 2][r] += hi * cc[r] - lo * ss[r];
+          const float lo = X[n][r], hi = X[n + ND / 2][r];
+          lo4[r] += lo * cc[r] + hi * ss[r];
+          hi4[r] += hi * cc[r] - lo * ss[r];
         }
+        AC[n][lane] = lo4;
+        AC[n + ND / 2][lane] = hi4;
       }
     }
   }
   if (gv) {
     float* o = a.dq + hq * D;
 #pragma unroll
-    for (int n = 0; n < ND; ++n)
+    for (int n = 0; n < ND; ++n) {
+      const f32x4 v = AC[n][lane];
       *(float4*)(o + 16 * n + 4 * kg) =
-          make_float4(a.scale * acc[n][0], a.scale * acc[n][1], a.scale * acc[n][2], a.scale * acc[n][3]);
+          make_float4(a.scale * v[0], a.scale * v[1], a.scale * v[2], a.scale * v[3]);
+    }
   }
 }
 
@@ -808,6 +928,8 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
   int32_t* npieces = (int32_t*)(ws + BP.off_npieces);
   int32_t* ptab = (int32_t*)(ws + BP.off_ptab);
   int32_t* csr = (int32_t*)(ws + BP.off_csr);
+  int32_t* csr_row = (int32_t*)(ws + BP.off_csr_row);
+  int4* recs = (int4*)(ws + BP.off_rec);
   float* partial = (float*)(ws + BP.off_partial);
   for (int l = P.L - 1; l >= 0; --l) {
     const int64_t Pl = (P.N[l] + CR - 1) / CR;
@@ -823,9 +945,13 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, cnt, nrows, rowoff);
     hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, pcnt, nrows, poff);
     hipLaunchKernelGGL(extract_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, st, bm,
-                       nrows, BP.W, rowoff, csr);
+                       nrows, BP.W, rowoff, csr, csr_row);
     hipLaunchKernelGGL(piece_kernel, dim3((unsigned)((nrows + 255) / 256)), dim3(256), 0, st, cnt,
                        rowoff, poff, nrows, (int)BP.piece, ptab, npieces);
+    hipLaunchKernelGGL(record_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st, csr,
+                       csr_row, rowoff + nrows, parents + l * lstride,
+                       l > 0 ? parents + (l - 1) * lstride : nullptr, d->T, d->H_kv, d->top_k, Pl,
+                       P.pw[l], CR, P.cr_log2, recs);
     DkvArgs a;
     memset(&a, 0, sizeof(a));
     a.kh = (const uint16_t*)(tws + P.off_kh[l]);
@@ -841,11 +967,9 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.gmax = gmax;
     a.gsum = gsum;
     a.delta = delta;
-    a.par = parents + l * lstride;
-    a.par_next = l > 0 ? parents + (l - 1) * lstride : nullptr;
     a.ptab = ptab;
     a.npieces = npieces;
-    a.csr = csr;
+    a.rec = recs;
     a.cosb = cosb;
     a.sinb = sinb;
     a.partial = partial;

@@ -59,14 +59,6 @@ struct WaveLds {
   unsigned long long selmask[MAXSLOT];
 };
 
-// d-slot of k-step m for lane group kg: the four lane groups cover 8
-// consecutive elements each; steps m and m + D/64 hold the RoPE pair
-// (d, d + D/2) so both halves of a pair live in the same lane.
-template <int D>
-__device__ __forceinline__ int dslot(int kg, int m) {
-  constexpr int SPH = D / 64;
-  return 8 * kg + 32 * (m % SPH) + (D / 2) * (m / SPH);
-}
 
 // Rotates the lane's query fragment by table row `row` (R(x,p) of
 // src/naive.py:22-28).
@@ -524,49 +516,6 @@ __device__ __forceinline__ void rot_by(float (&x)[D / 32][8], const float* __res
     }
   }
 }
-
-// Query fragment of a lane (head u16, the lane group's d-slots) kept in its
-// input type; get() returns it in fp32 times `scale`.
-template <int D, typename TIn>
-struct QFrag {
-  float f[D / 32][8];
-  __device__ __forceinline__ void load(const TIn* p, int kg, bool gv) {
-#pragma unroll
-    for (int m = 0; m < D / 32; ++m) {
-      Io<TIn>::ld8(p + dslot<D>(kg, m), f[m]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) f[m][e] = gv ? f[m][e] : 0.f;
-    }
-  }
-  __device__ __forceinline__ void get(float (&x)[D / 32][8], float scale) const {
-#pragma unroll
-    for (int m = 0; m < D / 32; ++m)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[m][e] = f[m][e] * scale;
-  }
-};
-template <int D>
-struct QFrag<D, __bf16> {
-  uint4 w[D / 32];  // 8 bf16 per k-step, exact
-  __device__ __forceinline__ void load(const __bf16* p, int kg, bool gv) {
-#pragma unroll
-    for (int m = 0; m < D / 32; ++m) {
-      const uint4 r = *(const uint4*)(p + dslot<D>(kg, m));
-      w[m] = gv ? r : make_uint4(0u, 0u, 0u, 0u);
-    }
-  }
-  __device__ __forceinline__ void get(float (&x)[D / 32][8], float scale) const {
-#pragma unroll
-    for (int m = 0; m < D / 32; ++m) {
-      const uint32_t v[4] = {w[m].x, w[m].y, w[m].z, w[m].w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x[m][2 * i] = __uint_as_float(v[i] << 16) * scale;
-        x[m][2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u) * scale;
-      }
-    }
-  }
-};
 
 template <int D, bool PREC, typename TIn>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fwd_reg_kernel(const FwdArgs a) {

@@ -43,7 +43,7 @@ enum htree_status {
                               max_top_nodes <= top_k * compression_rate) */
   HTREE_EUNSUPPORTED = -4, /* legal for the reference, outside this build:
                               D not in {64,128}, G = H/H_kv > 16,
-                              compression_rate < 4,
+                              compression_rate outside [4, 64],
                               top_k * max(CR,16) / 16 > 64 */
   HTREE_EWORKSPACE = -5    /* workspace too small */
 };
