@@ -146,21 +146,13 @@ template <int D>
 __device__ __forceinline__ void split_frag(const float (&x)[D / 32][8], bf16x8 (&h)[D / 32],
                                            bf16x8 (&lo)[D / 32]) {
 #pragma unroll
-  for (int m = 0; m < D / 32; ++m)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const __bf16 hb = (__bf16)x[m][e];
-      h[m][e] = hb;
-      lo[m][e] = (__bf16)(x[m][e] - (float)hb);
-    }
+  for (int m = 0; m < D / 32; ++m) split8(x[m], h[m], lo[m]);
 }
 
 template <int D>
 __device__ __forceinline__ void to_bf8(const float (&x)[D / 32][8], bf16x8 (&h)[D / 32]) {
 #pragma unroll
-  for (int m = 0; m < D / 32; ++m)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) h[m][e] = (__bf16)x[m][e];
+  for (int m = 0; m < D / 32; ++m) h[m] = pack8(x[m]);
 }
 
 template <int D>
@@ -177,19 +169,48 @@ __device__ __forceinline__ int wave_sum_i(int v) {
 }
 
 __device__ __forceinline__ s16x4 pack4(const float (&p)[4]) {
-  s16x4 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r[i] = f_to_bfs(p[i]);
-  return r;
+  return __builtin_bit_cast(s16x4, make_uint2(cvt_pk_bf16(p[0], p[1]), cvt_pk_bf16(p[2], p[3])));
 }
 __device__ __forceinline__ void pack4_split(const float (&p)[4], s16x4& h, s16x4& l) {
+  uint32_t hw[2], lw[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint16_t hb = f_to_bf(p[i]);
-    h[i] = (short)hb;
-    l[i] = f_to_bfs(p[i] - bf_to_f(hb));
+  for (int i = 0; i < 2; ++i) {
+    hw[i] = cvt_pk_bf16(p[2 * i], p[2 * i + 1]);
+    lw[i] = cvt_pk_bf16(p[2 * i] - __uint_as_float(hw[i] << 16),
+                        p[2 * i + 1] - __uint_as_float(hw[i] & 0xffff0000u));
   }
+  h = __builtin_bit_cast(s16x4, make_uint2(hw[0], hw[1]));
+  l = __builtin_bit_cast(s16x4, make_uint2(lw[0], lw[1]));
 }
+
+// dO fragment (lane head u16, the lane group's d-slots) as MFMA operands:
+// bf16 inputs load straight into the operand (exact); other types are split
+// into bf16 hi + lo.
+template <int D, typename TIn>
+struct DoFrag {
+  static __device__ __forceinline__ void load(const TIn* p, int kg, bool gv, bf16x8 (&h)[D / 32],
+                                              bf16x8 (&lo)[D / 32]) {
+    float f[D / 32][8];
+#pragma unroll
+    for (int m = 0; m < D / 32; ++m) {
+      Io<TIn>::ld8(p + dslot<D>(kg, m), f[m]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[m][e] = gv ? f[m][e] : 0.f;
+    }
+    split_frag<D>(f, h, lo);
+  }
+};
+template <int D>
+struct DoFrag<D, __bf16> {
+  static __device__ __forceinline__ void load(const __bf16* p, int kg, bool gv, bf16x8 (&h)[D / 32],
+                                              bf16x8 (&)[D / 32]) {
+#pragma unroll
+    for (int m = 0; m < D / 32; ++m) {
+      const uint4 r = *(const uint4*)(p + dslot<D>(kg, m));
+      h[m] = __builtin_bit_cast(bf16x8, gv ? r : make_uint4(0u, 0u, 0u, 0u));
+    }
+  }
+};
 
 // ---------------------------------------------------------------- prep
 // One wave per (b, t, h_kv): delta[g] = sum_d dO * O (fp32), and q / dO
@@ -486,19 +507,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     const bool ok = (tmask >> u16) & 1u;
     const int64_t bt = b * a.T + t;
     const int64_t grp = bt * a.Hkv + h;
-    // rotated, scaled query fragment (lane g = u16)
+    // rotated query fragment (lane g = u16); the score scale is applied to S
     const bool gv = u16 < G;
-    float qf[KS][8], qr[KS][8];
+    float qr[KS][8];
     {
-      const TIn* qp = (const TIn*)a.q + (bt * a.H + h * G + (gv ? u16 : 0)) * D;
-#pragma unroll
-      for (int m = 0; m < KS; ++m) {
-        Io<TIn>::ld8(qp + dslot<D>(kg, m), qf[m]);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) qf[m][i] = gv ? qf[m][i] * a.scale : 0.f;
-      }
+      QFrag<D, TIn> qin;
+      qin.load((const TIn*)a.q + (bt * a.H + h * G + (gv ? u16 : 0)) * D, kg, gv);
+      qin.get(qr, 1.f);
     }
-    rot_frag<D>(qf, a.cosb + (int64_t)rho * HALF, a.sinb + (int64_t)rho * HALF, kg, qr);
+    rot_by_fr<D>(qr, a.cosb + (int64_t)rho * HALF, a.sinb + (int64_t)rho * HALF, kg);
     bf16x8 qh[KS], ql[KS];
     split_frag<D>(qr, qh, ql);
     f32x4 S = {0.f, 0.f, 0.f, 0.f};
@@ -508,22 +525,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
       S = mma32(qh[m], kl[m], S);
       S = mma32(ql[m], kh[m], S);
     }
+    S *= a.scale;
     // dP[g][cand] = dO[g] . V[cand]
     f32x4 dP = {0.f, 0.f, 0.f, 0.f};
     {
-      float df[KS][8];
       const TIn* dp = (const TIn*)a.dO + (bt * a.H + h * G + (gv ? u16 : 0)) * D;
-#pragma unroll
-      for (int m = 0; m < KS; ++m) {
-        Io<TIn>::ld8(dp + dslot<D>(kg, m), df[m]);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) df[m][i] = gv ? df[m][i] : 0.f;
-      }
       bf16x8 dh[KS], dlo[KS];
-      if (PREC)
-        split_frag<D>(df, dh, dlo);
-      else
-        to_bf8<D>(df, dh);  // 16-bit inputs are exact in bf16 hi
+      DoFrag<D, TIn>::load(dp, kg, gv, dh, dlo);
 #pragma unroll
       for (int m = 0; m < KS; ++m) {
         dP = mma32(dh[m], vh[m], dP);
@@ -725,20 +733,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   QFrag<D, TIn> qin;
   qin.load((const TIn*)a.q + hq * D, kg, gv);
   bf16x8 dh[KS], dlo[KS];
-  {
-    const TIn* dp = (const TIn*)a.dO + hq * D;
-    float df[KS][8];
-#pragma unroll
-    for (int m = 0; m < KS; ++m) {
-      Io<TIn>::ld8(dp + dslot<D>(kg, m), df[m]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) df[m][i] = gv ? df[m][i] : 0.f;
-    }
-    if (PREC)
-      split_frag<D>(df, dh, dlo);
-    else
-      to_bf8<D>(df, dh);
-  }
+  DoFrag<D, TIn>::load((const TIn*)a.dO + hq * D, kg, gv, dh, dlo);
   const float gm = gv ? a.gmax[hq] : 0.f;
   const float gs = gv ? a.gsum[hq] : 1.f;
   const float dl = gv ? a.delta[hq] : 0.f;
@@ -811,14 +806,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
       bf16x8 vh[KS], vl[KS];
       load_frag<D>(P.vr_h + vrow, kg, vh);
       if (PREC) load_frag<D>(P.vr_l + vrow, kg, vl);
-      const int vn = node0 + (4 * kg < CRU ? 4 * kg : 0);
-      const int64_t tbase = ((hrow + (vn & ~15)) / 16 * D + u16) * 16 + (vn & 15);
-      s16x4 kt[ND], ktl[ND];
-#pragma unroll
-      for (int n = 0; n < ND; ++n) {
-        kt[n] = *(const s16x4*)(P.kt_h + tbase + (int64_t)n * 256);
-        ktl[n] = *(const s16x4*)(P.kt_l + tbase + (int64_t)n * 256);
-      }
       bf16x8 qh[KS], ql[KS];
       split_frag<D>(qr, qh, ql);
       f32x4 S = {0.f, 0.f, 0.f, 0.f}, dP = {0.f, 0.f, 0.f, 0.f};
@@ -848,7 +835,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
       }
       if (!__any(anyv)) return;
       // dq = sum_cand dS K~ cancels (sum_cand dS = 0 per head): split both
-      // factors so clustered keys keep their small residual
+      // factors so clustered keys keep their small residual.  The K~^T
+      // loads stay below the score math (keeps the tile within 256 VGPRs).
+      __builtin_amdgcn_sched_barrier(0);
+      const int vn = node0 + (4 * kg < CRU ? 4 * kg : 0);
+      const int64_t tbase = ((hrow + (vn & ~15)) / 16 * D + u16) * 16 + (vn & 15);
+      s16x4 kt[ND], ktl[ND];
+#pragma unroll
+      for (int n = 0; n < ND; ++n) {
+        kt[n] = *(const s16x4*)(P.kt_h + tbase + (int64_t)n * 256);
+        ktl[n] = *(const s16x4*)(P.kt_l + tbase + (int64_t)n * 256);
+      }
       s16x4 d4h, d4l;
       pack4_split(ds, d4h, d4l);
 #pragma unroll

@@ -101,6 +101,37 @@ struct Io<_Float16> {
   }
 };
 
+
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2v;
+
+// two fp32 -> packed bf16 pair (one v_cvt_pk_bf16_f32, round to nearest even)
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+  const f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v));
+}
+
+// hi + lo bf16 split of 8 fp32 values, in pairs: 6 VALU ops per pair
+__device__ __forceinline__ void split8(const float (&x)[8], bf16x8& hi, bf16x8& lo) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    h[i] = cvt_pk_bf16(x[2 * i], x[2 * i + 1]);
+    const float h0 = __uint_as_float(h[i] << 16), h1 = __uint_as_float(h[i] & 0xffff0000u);
+    l[i] = cvt_pk_bf16(x[2 * i] - h0, x[2 * i + 1] - h1);
+  }
+  hi = __builtin_bit_cast(bf16x8, make_uint4(h[0], h[1], h[2], h[3]));
+  lo = __builtin_bit_cast(bf16x8, make_uint4(l[0], l[1], l[2], l[3]));
+}
+
+// 8 fp32 -> bf16x8 (round to nearest even), in pairs
+__device__ __forceinline__ bf16x8 pack8(const float (&x)[8]) {
+  return __builtin_bit_cast(bf16x8, make_uint4(cvt_pk_bf16(x[0], x[1]), cvt_pk_bf16(x[2], x[3]),
+                                               cvt_pk_bf16(x[4], x[5]), cvt_pk_bf16(x[6], x[7])));
+}
+
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
 // Orders LDS traffic between the lanes of one wave (no block barrier: each
 // wave of a block works on its own query group).
 __device__ __forceinline__ void wave_sync() {

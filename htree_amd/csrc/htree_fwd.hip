@@ -85,22 +85,14 @@ __device__ __forceinline__ void rot_q(const float (&qf)[D / 32][8], const float*
 template <int D>
 __device__ __forceinline__ void to_bf(const float (&x)[D / 32][8], bf16x8 (&h)[D / 32]) {
 #pragma unroll
-  for (int m = 0; m < D / 32; ++m)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) h[m][e] = (__bf16)x[m][e];
+  for (int m = 0; m < D / 32; ++m) h[m] = pack8(x[m]);
 }
 
 template <int D>
 __device__ __forceinline__ void to_bf_split(const float (&x)[D / 32][8], bf16x8 (&h)[D / 32],
                                             bf16x8 (&lo)[D / 32]) {
 #pragma unroll
-  for (int m = 0; m < D / 32; ++m)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const __bf16 hb = (__bf16)x[m][e];
-      h[m][e] = hb;
-      lo[m][e] = (__bf16)(x[m][e] - (float)hb);
-    }
+  for (int m = 0; m < D / 32; ++m) split8(x[m], h[m], lo[m]);
 }
 
 template <int D>
@@ -405,9 +397,12 @@ __device__ __forceinline__ float wave_max_uniform(float x) {
 // v_exp_f32 does not return subnormals, so those are scaled by 2^-64.
 __device__ __forceinline__ float exp_sel(float x) {
   const float t = x * kLog2e;
-  const float r = __builtin_amdgcn_exp2f(t);
-  const float rs = __builtin_amdgcn_exp2f(t + 64.f) * 5.42101086242752217e-20f;
-  return t < -126.f ? rs : r;
+  float r = __builtin_amdgcn_exp2f(t);
+  if (__builtin_expect(__any(t < -126.f), 0)) {
+    const float rs = __builtin_amdgcn_exp2f(t + 64.f) * 5.42101086242752217e-20f;
+    r = t < -126.f ? rs : r;
+  }
+  return r;
 }
 
 // Shared Top-K of the group (src/naive.py:88-105): importance of position j
@@ -488,8 +483,10 @@ __device__ __forceinline__ void select_topk(const float* __restrict__ imp, const
 // tile is scored once (S^T, candidates x heads) into LDS; the selection uses
 // the exact level max and the accumulation reuses the scores.  Tiles are
 // walked in descending parent slot, so the query rotation advances by the
-// constant angle CR (R(q, a - s CR) = R(R(q, a - (s+1) CR), CR)), and the K
-// and V gathers are double-buffered one tile ahead.
+// constant angle CR (R(q, a - s CR) = R(R(q, a - (s+1) CR), CR)).  The V
+// gathers are double-buffered one tile ahead; the K gathers are not (a
+// second K buffer spills registers at two waves per SIMD, which costs more
+// than it hides).
 struct WaveLdsR {
   f32x4 st[16][64];  // S^T of every tile, one f32x4 per lane
   int32_t par[2][kMaxTK];
@@ -589,15 +586,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     };
 
     // ---- scores of every tile (descending slot), S^T into LDS
-    // first slot s = np-1: angle apos - (np-1) CR = ct; scale folded in
     float qr[KS][8];
     qin.get(qr, a.scale);
     rot_by<D>(qr, a.cosb + (int64_t)ct * HALF, a.sinb + (int64_t)ct * HALF, kg);
-    int cur_slot = (wide ? ((nt - 1) << 4) >> crlg : nt - 1);
+    int cur_slot = uniform(wide ? ((nt - 1) << 4) >> crlg : nt - 1);
     float lmax = -INFINITY;
     auto score = [&](int tau, const bf16x8 (&kh)[KS], const bf16x8 (&kl)[KS]) {
-      const int s = wide ? (tau << 4) >> crlg : tau;
-      if (s != cur_slot) {  // slots are visited in descending order, one step apart
+      const int s = uniform(wide ? (tau << 4) >> crlg : tau);
+      if (s != cur_slot) {
         rot_by<D>(qr, rot_cr[0], rot_cr[1], kg);
         cur_slot = s;
       }
@@ -620,18 +616,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       }
       W.st[tau][lane] = S;
     };
-    {
-      bf16x8 ah[KS], al[KS], bh_[KS], bl[KS];
-      kload(nt - 1, ah, al);
-      if (nt >= 2) kload(nt - 2, bh_, bl);
-      for (int tau = nt - 1; tau >= 0; tau -= 2) {
-        score(tau, ah, al);
-        if (tau >= 2) kload(tau - 2, ah, al);
-        if (tau >= 1) {
-          score(tau - 1, bh_, bl);
-          if (tau >= 3) kload(tau - 3, bh_, bl);
-        }
-      }
+    for (int tau = nt - 1; tau >= 0; --tau) {
+      bf16x8 kh[KS], kl[KS];
+      kload(tau, kh, kl);
+      score(tau, kh, kl);
     }
 
     if (l > 0) {
