@@ -12,14 +12,15 @@
 //   mean-pool backward, top-down ......... src/backward.py:787-841, naive.py:388-394
 //
 // Structure:
-//   prep     per (b,t,h_kv): delta; q and dO transposed per query group
-//            ([d][g], 16 heads padded) for the K-stationary products.
+//   prep     per (b,t,h_kv): delta = rowsum(dO * out).
 //   pack     per level: K~ (pre-rotated) transposed per 16-node block, V rows.
 //   index    per level: bitmap parent x query (integer atomicOr), row counts,
 //            scan, extraction of each parent's queries in t order (CSR), and
 //            a table of fixed-size pieces of every row.
 //   dkv      one wave per (piece, 16-child tile): K~/V tile stationary in
-//            registers, loops over the piece's queries; partial dK/dV per piece.
+//            registers, loops over the piece's queries, whose q / dO rows,
+//            RoPE row and softmax state are staged into LDS by asynchronous
+//            global->LDS copies one entry ahead; partial dK/dV per piece.
 //   reduce   sums each tile's pieces in piece order into the level's dK/dV.
 //   dq       one wave per query group over all levels (Q-stationary).
 //   pool     dK_{l-1}[child] += dK_l[parent] / n_children, top-down.
@@ -29,7 +30,6 @@
 
 namespace htree {
 
-constexpr int kGP = 16;  // query heads per group, padded
 
 struct BwdPlan {
   Plan P;
@@ -37,7 +37,7 @@ struct BwdPlan {
   int64_t W;   // bitmap words per row
   int64_t rows[HTREE_MAX_LEVELS];
   int64_t max_rows, max_entries, piece, max_pieces;
-  int64_t off_delta, off_qt[2], off_dot[2];
+  int64_t off_delta;
   int64_t off_kt[2][HTREE_MAX_LEVELS], off_vr[2][HTREE_MAX_LEVELS];
   int64_t off_dk[HTREE_MAX_LEVELS], off_dv[HTREE_MAX_LEVELS];
   int64_t off_bitmap, off_cnt, off_rowoff, off_pcnt, off_poff, off_npieces, off_ptab, off_csr,
@@ -71,12 +71,7 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
     off += (bytes + 255) / 256 * 256;
     return o;
   };
-  const int64_t BTH = (int64_t)d->B * d->T * d->H_kv;
   b->off_delta = take((int64_t)d->B * d->T * d->H * 4);
-  for (int s = 0; s < 2; ++s) {
-    b->off_qt[s] = (s == 0 || P.precise) ? take(BTH * d->D * kGP * 2) : -1;
-    b->off_dot[s] = (s == 0 || P.precise) ? take(BTH * d->D * kGP * 2) : -1;
-  }
   for (int l = 0; l < P.L; ++l) {
     const int64_t elems = BH * P.Np[l] * d->D;
     for (int s = 0; s < 2; ++s) {
@@ -213,17 +208,13 @@ struct DoFrag<D, __bf16> {
 };
 
 // ---------------------------------------------------------------- prep
-// One wave per (b, t, h_kv): delta[g] = sum_d dO * O (fp32), and q / dO
-// transposed to [d][16] (bf16 hi, and lo for fp32/fp16 inputs) through LDS.
+// delta[b,t,h] = sum_d dO * O in fp32 (src/backward.py:45-68); one wave per
+// (b, t, h_kv), lane = (head u16, d-slots of kg).
 template <int D, typename T>
-__global__ __launch_bounds__(256) void prep_kernel(const T* __restrict__ q, const T* __restrict__ o,
-                                                   const T* __restrict__ dO, int64_t ngroups, int H,
-                                                   int G, float* __restrict__ delta,
-                                                   uint16_t* __restrict__ qt_h, uint16_t* __restrict__ qt_l,
-                                                   uint16_t* __restrict__ dot_h,
-                                                   uint16_t* __restrict__ dot_l) {
+__global__ __launch_bounds__(256) void prep_kernel(const T* __restrict__ o, const T* __restrict__ dO,
+                                                   int64_t ngroups, int H, int G,
+                                                   float* __restrict__ delta) {
   constexpr int KS = D / 32;
-  __shared__ uint16_t tr[kWavesPerBlock][4][D * kGP];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int u16 = lane & 15, kg = lane >> 4;
   const int64_t grp = (int64_t)blockIdx.x * kWavesPerBlock + wv;
@@ -233,44 +224,18 @@ __global__ __launch_bounds__(256) void prep_kernel(const T* __restrict__ q, cons
   const int h = (int)(grp % Hkv);
   const bool gv = u16 < G;
   const int64_t row = (bt * H + h * G + (gv ? u16 : 0)) * D;
-  float qf[KS][8], of[KS][8], df[KS][8];
   float dl = 0.f;
 #pragma unroll
   for (int m = 0; m < KS; ++m) {
-    Io<T>::ld8(q + row + dslot<D>(kg, m), qf[m]);
-    Io<T>::ld8(o + row + dslot<D>(kg, m), of[m]);
-    Io<T>::ld8(dO + row + dslot<D>(kg, m), df[m]);
+    float of[8], df[8];
+    Io<T>::ld8(o + row + dslot<D>(kg, m), of);
+    Io<T>::ld8(dO + row + dslot<D>(kg, m), df);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      if (!gv) qf[m][e] = df[m][e] = of[m][e] = 0.f;
-      dl += df[m][e] * of[m][e];
-    }
+    for (int e = 0; e < 8; ++e) dl += df[e] * of[e];
   }
   dl += __shfl_xor(dl, 16);
   dl += __shfl_xor(dl, 32);
   if (gv && kg == 0) delta[bt * H + h * G + u16] = dl;
-  uint16_t(*L)[D * kGP] = tr[wv];
-#pragma unroll
-  for (int m = 0; m < KS; ++m)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int dd = dslot<D>(kg, m) + e;
-      uint16_t hi, lo;
-      split_bf(qf[m][e], hi, lo);
-      L[0][dd * kGP + u16] = hi;
-      L[1][dd * kGP + u16] = lo;
-      split_bf(df[m][e], hi, lo);
-      L[2][dd * kGP + u16] = hi;
-      L[3][dd * kGP + u16] = lo;
-    }
-  wave_sync();
-  const int64_t ob = grp * D * kGP;
-  for (int i = lane * 8; i < D * kGP; i += 64 * 8) {
-    *(uint4*)(qt_h + ob + i) = *(const uint4*)(&L[0][i]);
-    *(uint4*)(dot_h + ob + i) = *(const uint4*)(&L[2][i]);
-    if (qt_l) *(uint4*)(qt_l + ob + i) = *(const uint4*)(&L[1][i]);
-    if (dot_l) *(uint4*)(dot_l + ob + i) = *(const uint4*)(&L[3][i]);
-  }
 }
 
 // ---------------------------------------------------------------- pack
@@ -451,7 +416,6 @@ __global__ __launch_bounds__(256) void record_kernel(const int32_t* __restrict__
 struct DkvArgs {
   const uint16_t *kh, *kl;      // K~ rows (hi/lo), [B][Hkv][Np][D]
   const uint16_t *vr_h, *vr_l;  // V rows
-  const uint16_t *qt_h, *qt_l, *dot_h, *dot_l;  // [B*T*Hkv][D][16]
   const void* q;
   const void* dO;
   const float *gmax, *gsum, *delta;
@@ -459,14 +423,96 @@ struct DkvArgs {
   const int4* rec;  // per entry: t, rho, accumulate mask (lo, hi)
   const float *cosb, *sinb;
   float* partial;
-  int64_t N, Np, pw, Pl;
+  int64_t N, Np, pw, Pl, BTH;  // BTH = B*T*H (length of gmax / gsum / delta)
   int32_t T, H, Hkv, G, CR, crlg, TK, tpp;
   float scale;
 };
 
+// One entry's inputs staged in LDS by asynchronous global->LDS copies
+// (global_load_lds): the 16 query rows and 16 dO rows of the query group,
+// the RoPE row rho, and gmax / gsum / delta of the 16 heads.
+template <int D, typename TIn>
+struct Stage {
+  static constexpr int ROWB = 16 * D * (int)sizeof(TIn);  // 16 head rows
+  static constexpr int OFF_DO = ROWB;
+  static constexpr int OFF_TAB = 2 * ROWB;          // cos [D/2] then sin [D/2] (1 KB area)
+  static constexpr int OFF_SM = 2 * ROWB + 1024;    // gmax[16], gsum[16], delta[16], pad
+  static constexpr int BYTES = 2 * ROWB + 1024 + 256;
+  static constexpr int SLOTS = BYTES * 2 <= 20 * 1024 ? 2 : 1;  // double-buffer if it fits
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int D, typename TIn>
+__device__ __forceinline__ void stage_issue(char* slot, const DkvArgs& a, int64_t hq0, int rho,
+                                            int lane) {
+  using St = Stage<D, TIn>;
+  constexpr int HALF = D / 2;
+  const int valid = a.G * D * (int)sizeof(TIn);  // bytes of the group's rows
+  const char* qs = (const char*)a.q + hq0 * D * (int64_t)sizeof(TIn);
+  const char* ds = (const char*)a.dO + hq0 * D * (int64_t)sizeof(TIn);
+#pragma unroll
+  for (int j = 0; j < St::ROWB / 1024; ++j) {
+    int off = (j * 64 + lane) * 16;
+    off = off < valid ? off : 0;  // rows past the group: in-bounds filler, never used
+    __builtin_amdgcn_global_load_lds(qs + off, (lds_void*)(slot + j * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(ds + off, (lds_void*)(slot + St::OFF_DO + j * 1024), 16, 0, 0);
+  }
+  {
+    constexpr int CH = HALF / 4;  // 16-byte chunks of one table row
+    const float* src = lane < CH ? a.cosb + (int64_t)rho * HALF + 4 * lane
+                       : lane < 2 * CH ? a.sinb + (int64_t)rho * HALF + 4 * (lane - CH)
+                                       : a.cosb + (int64_t)rho * HALF;
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)(slot + St::OFF_TAB), 16, 0, 0);
+  }
+  {
+    const int g = lane & 15, which = lane >> 4;
+    int64_t i = hq0 + g;
+    i = (g < a.G && i < a.BTH) ? i : hq0;
+    const float* src = which == 0 ? a.gmax + i : which == 1 ? a.gsum + i : a.delta + i;
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)(slot + St::OFF_SM), 4, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void wait_stage() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the staged copies have landed in LDS
+  __builtin_amdgcn_wave_barrier();
+}
+
+// 4 consecutive heads g0..g0+3 of column d of the staged rows, as bf16
+// (hi, and lo for non-bf16 inputs)
+template <int D, typename TIn>
+struct ColT {
+  static __device__ __forceinline__ void get(const char* rows, int g0, int d, s16x4& h, s16x4& l) {
+    float f[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = (float)((const TIn*)rows)[(g0 + i) * D + d];
+    pack4_split(f, h, l);
+  }
+};
+template <int D>
+struct ColT<D, __bf16> {
+  static __device__ __forceinline__ void get(const char* rows, int g0, int d, s16x4& h, s16x4& l) {
+    const uint16_t* r = (const uint16_t*)rows;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) h[i] = (short)r[(g0 + i) * D + d];
+    (void)l;
+  }
+};
+
+// Row fragment (head u16, the lane group's d-slots) of the staged rows
+template <int D, typename TIn>
+__device__ __forceinline__ void row_frag(const char* rows, int u16, int kg, float (&x)[D / 32][8]) {
+  const TIn* r = (const TIn*)rows + u16 * D;
+#pragma unroll
+  for (int m = 0; m < D / 32; ++m) Io<TIn>::ld8(r + dslot<D>(kg, m), x[m]);
+}
+
 template <int D, bool PREC, typename TIn>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void dkv_kernel(const DkvArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
+  using St = Stage<D, TIn>;
+  __shared__ __attribute__((aligned(16))) char stage_all[kWavesPerBlock][St::SLOTS][St::BYTES];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int u16 = lane & 15, kg = lane >> 4;
   const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wv;
@@ -478,11 +524,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   const int p = (int)(row % a.Pl);
   const int h = (int)(bh % a.Hkv);
   const int64_t b = bh / a.Hkv;
-  const int CR = a.CR, crlg = a.crlg, TK = a.TK, G = a.G;
+  const int CR = a.CR, crlg = a.crlg, G = a.G;
   const int CRU = CR < 16 ? CR : 16;
   const int coff = CR >= 16 ? tile * 16 : 0;  // first child of the tile
   const int node0 = (p << crlg) + coff;
   if (node0 >= a.N) return;  // tile past the last node (CR > 16): no children, never read
+  const uint32_t cmask = CR < 16 ? ((1u << CR) - 1u) : 0xffffu;
+  auto tile_mask = [&](const int4& rc) {
+    const unsigned long long m64 = ((unsigned long long)(uint32_t)rc.w << 32) | (uint32_t)rc.z;
+    return (uint32_t)(m64 >> coff) & cmask;
+  };
   // stationary K~ / V fragments of the tile's children (lane cand = u16)
   bf16x8 kh[KS], kl[KS], vh[KS], vl[KS];
   {
@@ -495,27 +546,44 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   f32x4 dv[ND], dk[ND];
 #pragma unroll
   for (int n = 0; n < ND; ++n) dv[n] = dk[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  int4 rn = ne > 0 ? a.rec[e0] : make_int4(0, 0, 0, 0);
-  for (int e = 0; e < ne; ++e) {
-    const int4 rc = rn;
-    if (e + 1 < ne) rn = a.rec[e0 + e + 1];  // next entry's record in flight
-    const int t = rc.x;
-    const int rho = rc.y;
-    const unsigned long long m64 = ((unsigned long long)(uint32_t)rc.w << 32) | (uint32_t)rc.z;
-    const uint32_t tmask = (uint32_t)(m64 >> coff) & (CR < 16 ? ((1u << CR) - 1u) : 0xffffu);
-    if (tmask == 0u) continue;  // every child of the tile passed down or past the query
-    const bool ok = (tmask >> u16) & 1u;
-    const int64_t bt = b * a.T + t;
-    const int64_t grp = bt * a.Hkv + h;
-    // rotated query fragment (lane g = u16); the score scale is applied to S
-    const bool gv = u16 < G;
-    float qr[KS][8];
-    {
-      QFrag<D, TIn> qin;
-      qin.load((const TIn*)a.q + (bt * a.H + h * G + (gv ? u16 : 0)) * D, kg, gv);
-      qin.get(qr, 1.f);
+  const bool gv = u16 < G;
+  auto hq0_of = [&](int t) { return ((b * a.T + t) * a.Hkv + h) * (int64_t)G; };
+
+  // entries whose tile mask is empty are skipped without staging
+  int e = 0;
+  int4 rc = make_int4(0, 0, 0, 0);
+  while (e < ne) {
+    rc = a.rec[e0 + e];
+    if (tile_mask(rc)) break;
+    ++e;
+  }
+  int slot = 0;
+  if (e < ne) stage_issue<D, TIn>(stage_all[wv][0], a, hq0_of(rc.x), rc.y, lane);
+  while (e < ne) {
+    // next entry with work, staged into the other slot while this one computes
+    int en = e + 1;
+    int4 rn = make_int4(0, 0, 0, 0);
+    while (en < ne) {
+      rn = a.rec[e0 + en];
+      if (tile_mask(rn)) break;
+      ++en;
     }
-    rot_by_fr<D>(qr, a.cosb + (int64_t)rho * HALF, a.sinb + (int64_t)rho * HALF, kg);
+    wait_stage();
+    if (St::SLOTS == 2 && en < ne)
+      stage_issue<D, TIn>(stage_all[wv][slot ^ 1], a, hq0_of(rn.x), rn.y, lane);
+    const char* S0 = stage_all[wv][St::SLOTS == 2 ? slot : 0];
+    const float* tab = (const float*)(S0 + St::OFF_TAB);  // cos [HALF], sin [HALF]
+    const float* sm = (const float*)(S0 + St::OFF_SM);    // gmax, gsum, delta [16 each]
+    const bool ok = (tile_mask(rc) >> u16) & 1u;
+
+    // rotated query fragment (lane g = u16); the score scale is applied to S
+    float qr[KS][8];
+    row_frag<D, TIn>(S0, u16, kg, qr);
+#pragma unroll
+    for (int m = 0; m < KS; ++m)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qr[m][i] = gv ? qr[m][i] : 0.f;
+    rot_by_fr<D>(qr, tab, tab + HALF, kg);
     bf16x8 qh[KS], ql[KS];
     split_frag<D>(qr, qh, ql);
     f32x4 S = {0.f, 0.f, 0.f, 0.f};
@@ -529,9 +597,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     // dP[g][cand] = dO[g] . V[cand]
     f32x4 dP = {0.f, 0.f, 0.f, 0.f};
     {
-      const TIn* dp = (const TIn*)a.dO + (bt * a.H + h * G + (gv ? u16 : 0)) * D;
+      float df[KS][8];
+      row_frag<D, TIn>(S0 + St::OFF_DO, u16, kg, df);
       bf16x8 dh[KS], dlo[KS];
-      DoFrag<D, TIn>::load(dp, kg, gv, dh, dlo);
+#pragma unroll
+      for (int m = 0; m < KS; ++m) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) df[m][i] = gv ? df[m][i] : 0.f;
+        if (PREC)
+          split8(df[m], dh[m], dlo[m]);
+        else
+          dh[m] = pack8(df[m]);  // exact for bf16 inputs
+      }
 #pragma unroll
       for (int m = 0; m < KS; ++m) {
         dP = mma32(dh[m], vh[m], dP);
@@ -544,20 +621,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     // S[r], dP[r]: head g = 4kg + r, candidate u16
     float pr[4], ds[4];
     {
-      const int g0 = 4 * kg;
-      const int64_t hq = bt * a.H + h * G + (g0 < G ? g0 : 0);
+      const float4 gm4 = *(const float4*)(sm + 4 * kg);
+      const float4 gs4 = *(const float4*)(sm + 16 + 4 * kg);
+      const float4 dl4 = *(const float4*)(sm + 32 + 4 * kg);
+      const float gm[4] = {gm4.x, gm4.y, gm4.z, gm4.w}, gs[4] = {gs4.x, gs4.y, gs4.z, gs4.w};
+      const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const bool v = ok && g0 + r < G;
-        const float gm = v ? a.gmax[hq + r] : 0.f;
-        const float gs = v ? a.gsum[hq + r] : 1.f;
-        const float dl = v ? a.delta[hq + r] : 0.f;
-        pr[r] = v ? __builtin_amdgcn_exp2f((S[r] - gm) * kLog2e) / gs : 0.f;
-        ds[r] = pr[r] * (dP[r] - dl);
+        const bool v = ok && 4 * kg + r < G;
+        pr[r] = v ? __builtin_amdgcn_exp2f((S[r] - gm[r]) * kLog2e) / gs[r] : 0.f;
+        ds[r] = pr[r] * (dP[r] - dl[r]);
       }
     }
     // dV[cand][d] += sum_g P[g][cand] dO[g][d];  u[cand][d] = sum_g dS[g][cand] q[g][d]
-    const int64_t tb = grp * D * kGP + 4 * kg;
     // P and dS split into bf16 hi + lo: dV sums P over many queries of one
     // node (P ~ 1 for clustered keys), dq / dK sums of dS cancel
     s16x4 ph, plo, dh4, dl4;
@@ -566,16 +642,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     f32x4 u[ND];
 #pragma unroll
     for (int n = 0; n < ND; ++n) {
-      const int64_t o = tb + (int64_t)(16 * n + u16) * kGP;
-      const s16x4 dot = *(const s16x4*)(a.dot_h + o);
-      const s16x4 qt = *(const s16x4*)(a.qt_h + o);
+      s16x4 dot, dotl, qt, qtl;
+      ColT<D, TIn>::get(S0 + St::OFF_DO, 4 * kg, 16 * n + u16, dot, dotl);
+      ColT<D, TIn>::get(S0, 4 * kg, 16 * n + u16, qt, qtl);
       dv[n] = mma16(ph, dot, dv[n]);
       dv[n] = mma16(plo, dot, dv[n]);
       u[n] = mma16(dh4, qt, f32x4{0.f, 0.f, 0.f, 0.f});
       u[n] = mma16(dl4, qt, u[n]);
       if (PREC) {
-        const s16x4 dotl = *(const s16x4*)(a.dot_l + o);
-        const s16x4 qtl = *(const s16x4*)(a.qt_l + o);
         dv[n] = mma16(ph, dotl, dv[n]);
         u[n] = mma16(dh4, qtl, u[n]);
       }
@@ -585,7 +659,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
 #pragma unroll
     for (int n = 0; n < ND / 2; ++n) {
       const int i = 16 * n + u16;
-      const float c = a.cosb[(int64_t)rho * HALF + i], sn = a.sinb[(int64_t)rho * HALF + i];
+      const float c = tab[i], sn = tab[HALF + i];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float lo = u[n][r], hi = u[n + ND / 2][r];
@@ -593,7 +667,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
         dk[n + ND / 2][r] += lo * sn + hi * c;
       }
     }
+    if (St::SLOTS == 1 && en < ne) {
+      wave_sync();  // every lane has read the slot
+      stage_issue<D, TIn>(stage_all[wv][0], a, hq0_of(rn.x), rn.y, lane);
+    }
+    slot ^= 1;
+    e = en;
+    rc = rn;
   }
+  wait_stage();
   // dk of the node = scale R^-1(dK~, node mod CR); write this piece's partial
   float* out = a.partial + ((pc * a.tpp + tile) * 16) * (int64_t)D * 2;
 #pragma unroll
@@ -906,8 +988,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
   auto U16 = [&](int64_t off) { return off >= 0 ? (uint16_t*)(ws + off) : nullptr; };
   float* delta = (float*)(ws + BP.off_delta);
   hipLaunchKernelGGL((prep_kernel<D, T>), dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, st,
-                     (const T*)q, (const T*)out, (const T*)dO, groups, d->H, G, delta,
-                     U16(BP.off_qt[0]), U16(BP.off_qt[1]), U16(BP.off_dot[0]), U16(BP.off_dot[1]));
+                     (const T*)out, (const T*)dO, groups, d->H, G, delta);
   for (int l = 0; l < P.L; ++l) {
     const int64_t total = BH * P.Np[l] * d->D;
     hipLaunchKernelGGL(pack_bwd_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
@@ -955,10 +1036,6 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.kl = (const uint16_t*)(tws + P.off_kl[l]);
     a.vr_h = U16(BP.off_vr[0][l]);
     a.vr_l = U16(BP.off_vr[1][l]);
-    a.qt_h = U16(BP.off_qt[0]);
-    a.qt_l = U16(BP.off_qt[1]);
-    a.dot_h = U16(BP.off_dot[0]);
-    a.dot_l = U16(BP.off_dot[1]);
     a.q = q;
     a.dO = dO;
     a.gmax = gmax;
@@ -974,6 +1051,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.Np = P.Np[l];
     a.pw = P.pw[l];
     a.Pl = Pl;
+    a.BTH = (int64_t)d->B * d->T * d->H;
     a.T = d->T;
     a.H = d->H;
     a.Hkv = d->H_kv;
