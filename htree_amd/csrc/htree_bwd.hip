@@ -30,6 +30,7 @@
 
 namespace htree {
 
+constexpr int64_t kDsBudget = 24ll << 30;  // bytes of stored dS before dq recomputes
 
 struct BwdPlan {
   Plan P;
@@ -41,7 +42,11 @@ struct BwdPlan {
   int64_t off_kt[2][HTREE_MAX_LEVELS], off_vr[2][HTREE_MAX_LEVELS];
   int64_t off_dk[HTREE_MAX_LEVELS], off_dv[HTREE_MAX_LEVELS];
   int64_t off_bitmap, off_cnt, off_rowoff, off_pcnt, off_poff, off_npieces, off_ptab, off_csr,
-      off_partial, off_csr_row, off_rec;
+      off_partial, off_csr_row;
+  int64_t off_rec[HTREE_MAX_LEVELS];   // per-entry records of each level
+  int64_t off_emap[HTREE_MAX_LEVELS];  // (query group, slot) -> entry, per level
+  int64_t off_ds[HTREE_MAX_LEVELS];    // dS of every entry tile (bf16 hi, lo), per level
+  bool use_ds;                         // dq from the stored dS (else recomputed)
   int64_t bytes;
 };
 
@@ -90,7 +95,15 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
   b->off_ptab = take(b->max_pieces * 3 * 4);
   b->off_csr = take(b->max_entries * 4);
   b->off_csr_row = take(b->max_entries * 4);
-  b->off_rec = take(b->max_entries * 16);
+  // dS of every (entry, tile), 1 KB each, kept for the dq pass when the whole
+  // backward's worth fits the budget; otherwise dq recomputes the scores
+  const int64_t ds_level = b->max_entries * b->tpp * 1024;
+  b->use_ds = ds_level * P.L <= kDsBudget;
+  for (int l = 0; l < P.L; ++l) {
+    b->off_rec[l] = (b->use_ds || l == 0) ? take(b->max_entries * 16) : b->off_rec[0];
+    b->off_emap[l] = b->use_ds ? take(b->max_entries * 4) : -1;
+    b->off_ds[l] = b->use_ds ? take(ds_level) : -1;
+  }
   b->off_partial = take(b->max_pieces * b->tpp * 16 * (int64_t)d->D * 2 * 4);
   b->bytes = off;
   return HTREE_OK;
@@ -381,7 +394,8 @@ __global__ __launch_bounds__(256) void record_kernel(const int32_t* __restrict__
                                                      const int32_t* __restrict__ par,
                                                      const int32_t* __restrict__ par_next, int T,
                                                      int Hkv, int TK, int64_t Pl, int64_t pw, int CR,
-                                                     int crlg, int4* __restrict__ rec) {
+                                                     int crlg, int4* __restrict__ rec,
+                                                     int32_t* __restrict__ emap) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= *ntot) return;
   const int t = csr[e];
@@ -410,6 +424,7 @@ __global__ __launch_bounds__(256) void record_kernel(const int32_t* __restrict__
     }
   }
   rec[e] = make_int4(t, nc - 1 - (s << crlg), (int)(uint32_t)m, (int)(uint32_t)(m >> 32));
+  if (emap) emap[grp * TK + s] = (int32_t)e;
 }
 
 // ---------------------------------------------------------------- dkv
@@ -423,6 +438,7 @@ struct DkvArgs {
   const int4* rec;  // per entry: t, rho, accumulate mask (lo, hi)
   const float *cosb, *sinb;
   float* partial;
+  uint16_t* ds;  // nullable: dS per (entry, tile) for the dq pass
   int64_t N, Np, pw, Pl, BTH;  // BTH = B*T*H (length of gmax / gsum / delta)
   int32_t T, H, Hkv, G, CR, crlg, TK, tpp;
   float scale;
@@ -639,6 +655,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     s16x4 ph, plo, dh4, dl4;
     pack4_split(ds, dh4, dl4);
     pack4_split(pr, ph, plo);
+    if (a.ds) {
+      // dS[g][cand] for the dq pass: hi then lo, 16 x 16 each, row g
+      uint16_t* o = a.ds + ((int64_t)(e0 + e) * a.tpp + tile) * 512 + 64 * kg + u16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        o[16 * r] = (uint16_t)dh4[r];
+        o[256 + 16 * r] = (uint16_t)dl4[r];
+      }
+    }
     f32x4 u[ND];
 #pragma unroll
     for (int n = 0; n < ND; ++n) {
@@ -973,6 +998,179 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   }
 }
 
+// Q-stationary dq from the dS stored by dkv: per tile only
+// dq~^T += K~^T dS^T (K~^T block and dS staged into LDS by asynchronous
+// copies one tile ahead), with the slot frame of dq_kernel.
+struct DqDsLevel {
+  const uint16_t *kt_h, *kt_l;  // K~ transposed per 16-node block
+  const int4* rec;
+  const int32_t* emap;
+  const uint16_t* ds;
+  int64_t Np, pw;
+};
+
+struct DqDsArgs {
+  DqDsLevel lv[HTREE_MAX_LEVELS];
+  const int32_t* parents;  // [L,B,T,Hkv,TK]
+  const float *cosb, *sinb;
+  float* dq;
+  int32_t B, T, H, Hkv, G, CR, crlg, TK, L, tpp;
+  float scale;
+};
+
+template <int D>
+struct DqStage {
+  static constexpr int KTB = 16 * D * 2;  // one 16-node block of K~^T, bf16
+  static constexpr int OFF_KL = KTB;
+  static constexpr int OFF_DS = 2 * KTB;  // dS hi, lo (1 KB)
+  static constexpr int BYTES = 2 * KTB + 1024;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void dq_ds_kernel(const DqDsArgs a) {
+  constexpr int ND = D / 16, HALF = D / 2;
+  using St = DqStage<D>;
+  __shared__ __attribute__((aligned(16))) char stage_all[kWavesPerBlock][2][St::BYTES];
+  __shared__ int32_t lst[kWavesPerBlock][kMaxTK];
+  __shared__ int32_t lem[kWavesPerBlock][kMaxTK];
+  __shared__ float rot_m[2][HALF];  // cos(CR theta), -sin(CR theta)
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int u16 = lane & 15, kg = lane >> 4;
+  const int G = a.G, CR = a.CR, crlg = a.crlg, TK = a.TK, tpp = a.tpp;
+  if (threadIdx.x < HALF) {
+    rot_m[0][threadIdx.x] = a.cosb[(int64_t)CR * HALF + threadIdx.x];
+    rot_m[1][threadIdx.x] = -a.sinb[(int64_t)CR * HALF + threadIdx.x];
+  }
+  __syncthreads();
+  const int64_t grp = (int64_t)blockIdx.x * kWavesPerBlock + wv;
+  if (grp >= (int64_t)a.B * a.T * a.Hkv) return;
+  const int h = (int)(grp % a.Hkv);
+  const int64_t bt = grp / a.Hkv;
+  const int t = (int)(bt % a.T);
+  const int64_t b = bt / a.T;
+  const bool wide = CR >= 16;
+  const bool gv = u16 < G;
+  int32_t* LS = lst[wv];
+  int32_t* LE = lem[wv];
+  const int64_t lstride = (int64_t)a.B * a.T * a.Hkv * TK;
+  f32x4 acc[ND];
+#pragma unroll
+  for (int n = 0; n < ND; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int l = a.L - 1; l >= 0; --l) {
+    const DqDsLevel P = a.lv[l];
+    wave_sync();
+    const int pe = lane < TK ? a.parents[l * lstride + grp * TK + lane] : -1;
+    const int np = __popcll(__ballot(pe >= 0));
+    if (np <= 0) continue;
+    if (lane < TK) {
+      LS[lane] = pe;
+      LE[lane] = pe >= 0 ? P.emap[grp * TK + lane] : 0;
+    }
+    const int ct = (int)((t / P.pw) & (CR - 1));
+    const int nc = ((np - 1) << crlg) + ct + 1;
+    const int nt = wide ? (nc + 15) >> 4 : np;
+    wave_sync();
+    const int64_t hrow = (b * a.Hkv + h) * P.Np;
+    // tile tau: slot, chunk (tile within the parent), entry, work mask
+    auto info = [&](int tau, int& s, int& chunk, int& e, uint32_t& msk) {
+      s = wide ? (tau << 4) >> crlg : tau;
+      chunk = wide ? ((tau << 4) & (CR - 1)) >> 4 : 0;
+      e = LE[s];
+      const int4 rc = P.rec[e];
+      const unsigned long long m64 = ((unsigned long long)(uint32_t)rc.w << 32) | (uint32_t)rc.z;
+      msk = (uint32_t)(m64 >> (chunk << 4)) & (CR < 16 ? ((1u << CR) - 1u) : 0xffffu);
+    };
+    auto issue = [&](int tau, int s, int chunk, int e, char* slot) {
+      const int node0 = (LS[s] << crlg) + (chunk << 4);
+      const int64_t blk = (hrow + (node0 & ~15)) / 16;
+      const char* kth = (const char*)(P.kt_h + blk * D * 16);
+      const char* ktl = (const char*)(P.kt_l + blk * D * 16);
+#pragma unroll
+      for (int j = 0; j < St::KTB / 1024; ++j) {
+        __builtin_amdgcn_global_load_lds(kth + (j * 64 + lane) * 16, (lds_void*)(slot + j * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(ktl + (j * 64 + lane) * 16,
+                                         (lds_void*)(slot + St::OFF_KL + j * 1024), 16, 0, 0);
+      }
+      const char* dsp = (const char*)(P.ds + ((int64_t)e * tpp + chunk) * 512);
+      __builtin_amdgcn_global_load_lds(dsp + lane * 16, (lds_void*)(slot + St::OFF_DS), 16, 0, 0);
+    };
+    f32x4 X[ND];
+#pragma unroll
+    for (int n = 0; n < ND; ++n) X[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // ascending tiles with work; the next one is staged while this one computes
+    int tau = 0, s = 0, chunk = 0, e = 0;
+    uint32_t msk = 0u;
+    while (tau < nt) {
+      info(tau, s, chunk, e, msk);
+      if (msk) break;
+      ++tau;
+    }
+    int cur_slot = 0, buf = 0;
+    if (tau < nt) issue(tau, s, chunk, e, stage_all[wv][0]);
+    while (tau < nt) {
+      int tn = tau + 1, sn = 0, chn = 0, en = 0;
+      uint32_t mn = 0u;
+      while (tn < nt) {
+        info(tn, sn, chn, en, mn);
+        if (mn) break;
+        ++tn;
+      }
+      wait_stage();
+      if (tn < nt) issue(tn, sn, chn, en, stage_all[wv][buf ^ 1]);
+      while (cur_slot < s) {  // ascending slots: the frame turns by -CR per slot
+        rot_acc<D>(X, rot_m[0], rot_m[1], kg);
+        ++cur_slot;
+      }
+      const char* S0 = stage_all[wv][buf];
+      const int node0 = (LS[s] << crlg) + (chunk << 4);
+      const int coln = (node0 & 15) + (4 * kg < (CR < 16 ? CR : 16) ? 4 * kg : 0);
+      const s16x4 dsh = *(const s16x4*)(S0 + St::OFF_DS + (u16 * 16 + 4 * kg) * 2);
+      const s16x4 dsl = *(const s16x4*)(S0 + St::OFF_DS + 512 + (u16 * 16 + 4 * kg) * 2);
+#pragma unroll
+      for (int n = 0; n < ND; ++n) {
+        const int off = ((16 * n + u16) * 16 + coln) * 2;
+        const s16x4 kt = *(const s16x4*)(S0 + off);
+        const s16x4 ktl = *(const s16x4*)(S0 + St::OFF_KL + off);
+        X[n] = mma16(kt, dsh, X[n]);
+        X[n] = mma16(kt, dsl, X[n]);
+        X[n] = mma16(ktl, dsh, X[n]);
+      }
+      buf ^= 1;
+      tau = tn;
+      s = sn;
+      chunk = chn;
+      e = en;
+    }
+    wait_stage();
+    while (cur_slot < np - 1) {
+      rot_acc<D>(X, rot_m[0], rot_m[1], kg);
+      ++cur_slot;
+    }
+    // back to the query's frame: R(X, -c_t)
+#pragma unroll
+    for (int n = 0; n < ND / 2; ++n) {
+      const int i0 = 16 * n + 4 * kg;
+      const float4 c4 = *(const float4*)(a.cosb + (int64_t)ct * HALF + i0);
+      const float4 s4 = *(const float4*)(a.sinb + (int64_t)ct * HALF + i0);
+      const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float lo = X[n][r], hi = X[n + ND / 2][r];
+        acc[n][r] += lo * cc[r] + hi * ss[r];
+        acc[n + ND / 2][r] += hi * cc[r] - lo * ss[r];
+      }
+    }
+  }
+  if (gv) {
+    float* o = a.dq + (bt * a.H + h * G + u16) * D;
+#pragma unroll
+    for (int n = 0; n < ND; ++n)
+      *(float4*)(o + 16 * n + 4 * kg) =
+          make_float4(a.scale * acc[n][0], a.scale * acc[n][1], a.scale * acc[n][2], a.scale * acc[n][3]);
+  }
+}
+
 // ---------------------------------------------------------------- host
 template <int D, bool PREC, typename T>
 static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const void* q,
@@ -1007,7 +1205,6 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
   int32_t* ptab = (int32_t*)(ws + BP.off_ptab);
   int32_t* csr = (int32_t*)(ws + BP.off_csr);
   int32_t* csr_row = (int32_t*)(ws + BP.off_csr_row);
-  int4* recs = (int4*)(ws + BP.off_rec);
   float* partial = (float*)(ws + BP.off_partial);
   for (int l = P.L - 1; l >= 0; --l) {
     const int64_t Pl = (P.N[l] + CR - 1) / CR;
@@ -1026,10 +1223,12 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
                        nrows, BP.W, rowoff, csr, csr_row);
     hipLaunchKernelGGL(piece_kernel, dim3((unsigned)((nrows + 255) / 256)), dim3(256), 0, st, cnt,
                        rowoff, poff, nrows, (int)BP.piece, ptab, npieces);
+    int4* recs = (int4*)(ws + BP.off_rec[l]);
     hipLaunchKernelGGL(record_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st, csr,
                        csr_row, rowoff + nrows, parents + l * lstride,
                        l > 0 ? parents + (l - 1) * lstride : nullptr, d->T, d->H_kv, d->top_k, Pl,
-                       P.pw[l], CR, P.cr_log2, recs);
+                       P.pw[l], CR, P.cr_log2, recs,
+                       BP.use_ds ? (int32_t*)(ws + BP.off_emap[l]) : nullptr);
     DkvArgs a;
     memset(&a, 0, sizeof(a));
     a.kh = (const uint16_t*)(tws + P.off_kh[l]);
@@ -1047,6 +1246,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.cosb = cosb;
     a.sinb = sinb;
     a.partial = partial;
+    a.ds = BP.use_ds ? U16(BP.off_ds[l]) : nullptr;
     a.N = P.N[l];
     a.Np = P.Np[l];
     a.pw = P.pw[l];
@@ -1072,7 +1272,35 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
                        dvl);
   }
   // dq over all levels
-  {
+  if (BP.use_ds) {
+    DqDsArgs a;
+    memset(&a, 0, sizeof(a));
+    for (int l = 0; l < P.L; ++l) {
+      a.lv[l].kt_h = U16(BP.off_kt[0][l]);
+      a.lv[l].kt_l = U16(BP.off_kt[1][l]);
+      a.lv[l].rec = (const int4*)(ws + BP.off_rec[l]);
+      a.lv[l].emap = (const int32_t*)(ws + BP.off_emap[l]);
+      a.lv[l].ds = U16(BP.off_ds[l]);
+      a.lv[l].Np = P.Np[l];
+      a.lv[l].pw = P.pw[l];
+    }
+    a.parents = parents;
+    a.cosb = cosb;
+    a.sinb = sinb;
+    a.dq = dq;
+    a.B = d->B;
+    a.T = d->T;
+    a.H = d->H;
+    a.Hkv = d->H_kv;
+    a.G = G;
+    a.CR = CR;
+    a.crlg = P.cr_log2;
+    a.TK = d->top_k;
+    a.L = P.L;
+    a.tpp = BP.tpp;
+    a.scale = scale;
+    hipLaunchKernelGGL((dq_ds_kernel<D>), dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, st, a);
+  } else {
     DqArgs a;
     memset(&a, 0, sizeof(a));
     for (int l = 0; l < P.L; ++l) {
