@@ -44,7 +44,7 @@ struct BwdPlan {
   int64_t off_bitmap, off_cnt, off_rowoff, off_pcnt, off_poff, off_npieces, off_ptab, off_csr,
       off_partial, off_csr_row;
   int64_t off_rec[HTREE_MAX_LEVELS];   // per-entry records of each level
-  int64_t off_emap[HTREE_MAX_LEVELS];  // (query group, slot) -> entry, per level
+  int64_t off_emap[HTREE_MAX_LEVELS];  // (query group, slot) -> {entry, mask}, per level
   int64_t off_ds[HTREE_MAX_LEVELS];    // dS of every entry tile (bf16 hi, lo), per level
   bool use_ds;                         // dq from the stored dS (else recomputed)
   int64_t bytes;
@@ -101,7 +101,7 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
   b->use_ds = ds_level * P.L <= kDsBudget;
   for (int l = 0; l < P.L; ++l) {
     b->off_rec[l] = (b->use_ds || l == 0) ? take(b->max_entries * 16) : b->off_rec[0];
-    b->off_emap[l] = b->use_ds ? take(b->max_entries * 4) : -1;
+    b->off_emap[l] = b->use_ds ? take(b->max_entries * 16) : -1;
     b->off_ds[l] = b->use_ds ? take(ds_level) : -1;
   }
   b->off_partial = take(b->max_pieces * b->tpp * 16 * (int64_t)d->D * 2 * 4);
@@ -395,7 +395,7 @@ __global__ __launch_bounds__(256) void record_kernel(const int32_t* __restrict__
                                                      const int32_t* __restrict__ par_next, int T,
                                                      int Hkv, int TK, int64_t Pl, int64_t pw, int CR,
                                                      int crlg, int4* __restrict__ rec,
-                                                     int32_t* __restrict__ emap) {
+                                                     int4* __restrict__ emap) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= *ntot) return;
   const int t = csr[e];
@@ -424,7 +424,7 @@ __global__ __launch_bounds__(256) void record_kernel(const int32_t* __restrict__
     }
   }
   rec[e] = make_int4(t, nc - 1 - (s << crlg), (int)(uint32_t)m, (int)(uint32_t)(m >> 32));
-  if (emap) emap[grp * TK + s] = (int32_t)e;
+  if (emap) emap[grp * TK + s] = make_int4((int)e, (int)(uint32_t)m, (int)(uint32_t)(m >> 32), 0);
 }
 
 // ---------------------------------------------------------------- dkv
@@ -999,12 +999,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
 }
 
 // Q-stationary dq from the dS stored by dkv: per tile only
-// dq~^T += K~^T dS^T (K~^T block and dS staged into LDS by asynchronous
-// copies one tile ahead), with the slot frame of dq_kernel.
+// dq~^T += K~^T dS^T.  Each wave owns one LDS slot: the tile's K~^T block
+// and dS land there by asynchronous copies, move to registers, and the next
+// tile's copies are issued before the MFMAs, so one tile is always in
+// flight without holding registers (4 waves per SIMD).
+// dq is carried across levels in one accumulator X: at a level's start X is
+// turned into the frame of slot 0 (R(X, a), a = n_c - 1), each slot step
+// turns it by -CR, and R(., -c_t) at the end brings it back, so that
+//   X_end = X_start + sum_s R^-1(dq~_s, a - s CR).
 struct DqDsLevel {
   const uint16_t *kt_h, *kt_l;  // K~ transposed per 16-node block
-  const int4* rec;
-  const int32_t* emap;
+  const int4* emap;             // (query group, slot) -> {entry, mask lo, mask hi, 0}
   const uint16_t* ds;
   int64_t Np, pw;
 };
@@ -1027,16 +1032,14 @@ struct DqStage {
 };
 
 template <int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void dq_ds_kernel(const DqDsArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void dq_ds_kernel(const DqDsArgs a) {
   constexpr int ND = D / 16, HALF = D / 2;
   using St = DqStage<D>;
-  __shared__ __attribute__((aligned(16))) char stage_all[kWavesPerBlock][2][St::BYTES];
-  __shared__ int32_t lst[kWavesPerBlock][kMaxTK];
-  __shared__ int32_t lem[kWavesPerBlock][kMaxTK];
+  __shared__ __attribute__((aligned(16))) char stage_all[kWavesPerBlock][St::BYTES];
   __shared__ float rot_m[2][HALF];  // cos(CR theta), -sin(CR theta)
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int u16 = lane & 15, kg = lane >> 4;
-  const int G = a.G, CR = a.CR, crlg = a.crlg, TK = a.TK, tpp = a.tpp;
+  const int CR = a.CR, crlg = a.crlg, TK = a.TK, tpp = a.tpp;
   if (threadIdx.x < HALF) {
     rot_m[0][threadIdx.x] = a.cosb[(int64_t)CR * HALF + threadIdx.x];
     rot_m[1][threadIdx.x] = -a.sinb[(int64_t)CR * HALF + threadIdx.x];
@@ -1049,40 +1052,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   const int t = (int)(bt % a.T);
   const int64_t b = bt / a.T;
   const bool wide = CR >= 16;
-  const bool gv = u16 < G;
-  int32_t* LS = lst[wv];
-  int32_t* LE = lem[wv];
+  const uint32_t cmask = CR < 16 ? ((1u << CR) - 1u) : 0xffffu;
+  char* slot = stage_all[wv];
   const int64_t lstride = (int64_t)a.B * a.T * a.Hkv * TK;
-  f32x4 acc[ND];
+  f32x4 X[ND];
 #pragma unroll
-  for (int n = 0; n < ND; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int n = 0; n < ND; ++n) X[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int l = a.L - 1; l >= 0; --l) {
     const DqDsLevel P = a.lv[l];
     wave_sync();
+    // lane s holds slot s: parent, entry, children mask (read with readlane)
     const int pe = lane < TK ? a.parents[l * lstride + grp * TK + lane] : -1;
     const int np = __popcll(__ballot(pe >= 0));
     if (np <= 0) continue;
-    if (lane < TK) {
-      LS[lane] = pe;
-      LE[lane] = pe >= 0 ? P.emap[grp * TK + lane] : 0;
-    }
+    const int4 sr = pe >= 0 ? P.emap[grp * TK + lane] : make_int4(0, 0, 0, 0);
     const int ct = (int)((t / P.pw) & (CR - 1));
-    const int nc = ((np - 1) << crlg) + ct + 1;
-    const int nt = wide ? (nc + 15) >> 4 : np;
-    wave_sync();
+    const int apos = ((np - 1) << crlg) + ct;
+    const int nt = wide ? ((apos + 16) >> 4) : np;
     const int64_t hrow = (b * a.Hkv + h) * P.Np;
-    // tile tau: slot, chunk (tile within the parent), entry, work mask
-    auto info = [&](int tau, int& s, int& chunk, int& e, uint32_t& msk) {
+    // tile tau -> slot s, tile of the parent (chunk), children mask
+    auto tmask = [&](int tau, int& s, int& chunk) {
       s = wide ? (tau << 4) >> crlg : tau;
       chunk = wide ? ((tau << 4) & (CR - 1)) >> 4 : 0;
-      e = LE[s];
-      const int4 rc = P.rec[e];
-      const unsigned long long m64 = ((unsigned long long)(uint32_t)rc.w << 32) | (uint32_t)rc.z;
-      msk = (uint32_t)(m64 >> (chunk << 4)) & (CR < 16 ? ((1u << CR) - 1u) : 0xffffu);
+      const uint32_t mlo = (uint32_t)__builtin_amdgcn_readlane(sr.y, s);
+      const uint32_t mhi = (uint32_t)__builtin_amdgcn_readlane(sr.z, s);
+      const unsigned long long m64 = ((unsigned long long)mhi << 32) | mlo;
+      return (uint32_t)(m64 >> (chunk << 4)) & cmask;
     };
-    auto issue = [&](int tau, int s, int chunk, int e, char* slot) {
-      const int node0 = (LS[s] << crlg) + (chunk << 4);
+    auto next_tile = [&](int tau, int& s, int& chunk) {
+      while (tau < nt && !tmask(tau, s, chunk)) ++tau;
+      return tau;
+    };
+    auto issue = [&](int s, int chunk) {
+      const int node0 = (__builtin_amdgcn_readlane(pe, s) << crlg) + (chunk << 4);
       const int64_t blk = (hrow + (node0 & ~15)) / 16;
       const char* kth = (const char*)(P.kt_h + blk * D * 16);
       const char* ktl = (const char*)(P.kt_l + blk * D * 16);
@@ -1092,82 +1095,76 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
         __builtin_amdgcn_global_load_lds(ktl + (j * 64 + lane) * 16,
                                          (lds_void*)(slot + St::OFF_KL + j * 1024), 16, 0, 0);
       }
-      const char* dsp = (const char*)(P.ds + ((int64_t)e * tpp + chunk) * 512);
+      const char* dsp = (const char*)(P.ds + ((int64_t)__builtin_amdgcn_readlane(sr.x, s) * tpp + chunk) * 512);
       __builtin_amdgcn_global_load_lds(dsp + lane * 16, (lds_void*)(slot + St::OFF_DS), 16, 0, 0);
     };
-    f32x4 X[ND];
-#pragma unroll
-    for (int n = 0; n < ND; ++n) X[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // ascending tiles with work; the next one is staged while this one computes
-    int tau = 0, s = 0, chunk = 0, e = 0;
-    uint32_t msk = 0u;
+    // into the frame of slot 0
+    rot_acc<D>(X, a.cosb + (int64_t)apos * HALF, a.sinb + (int64_t)apos * HALF, kg);
+    int s = 0, chunk = 0, cur_slot = 0;
+    int tau = next_tile(0, s, chunk);
+    if (tau < nt) issue(s, chunk);
     while (tau < nt) {
-      info(tau, s, chunk, e, msk);
-      if (msk) break;
-      ++tau;
-    }
-    int cur_slot = 0, buf = 0;
-    if (tau < nt) issue(tau, s, chunk, e, stage_all[wv][0]);
-    while (tau < nt) {
-      int tn = tau + 1, sn = 0, chn = 0, en = 0;
-      uint32_t mn = 0u;
-      while (tn < nt) {
-        info(tn, sn, chn, en, mn);
-        if (mn) break;
-        ++tn;
-      }
-      wait_stage();
-      if (tn < nt) issue(tn, sn, chn, en, stage_all[wv][buf ^ 1]);
+      int sn = 0, chn = 0;
+      const int tn = next_tile(tau + 1, sn, chn);
       while (cur_slot < s) {  // ascending slots: the frame turns by -CR per slot
         rot_acc<D>(X, rot_m[0], rot_m[1], kg);
         ++cur_slot;
       }
-      const char* S0 = stage_all[wv][buf];
-      const int node0 = (LS[s] << crlg) + (chunk << 4);
+      const int node0 = (__builtin_amdgcn_readlane(pe, s) << crlg) + (chunk << 4);
       const int coln = (node0 & 15) + (4 * kg < (CR < 16 ? CR : 16) ? 4 * kg : 0);
-      const s16x4 dsh = *(const s16x4*)(S0 + St::OFF_DS + (u16 * 16 + 4 * kg) * 2);
-      const s16x4 dsl = *(const s16x4*)(S0 + St::OFF_DS + 512 + (u16 * 16 + 4 * kg) * 2);
+      wait_stage();
+      s16x4 kt[ND], ktl[ND];
 #pragma unroll
       for (int n = 0; n < ND; ++n) {
         const int off = ((16 * n + u16) * 16 + coln) * 2;
-        const s16x4 kt = *(const s16x4*)(S0 + off);
-        const s16x4 ktl = *(const s16x4*)(S0 + St::OFF_KL + off);
-        X[n] = mma16(kt, dsh, X[n]);
-        X[n] = mma16(kt, dsl, X[n]);
-        X[n] = mma16(ktl, dsh, X[n]);
+        kt[n] = *(const s16x4*)(slot + off);
+        ktl[n] = *(const s16x4*)(slot + St::OFF_KL + off);
       }
-      buf ^= 1;
+      const s16x4 dsh = *(const s16x4*)(slot + St::OFF_DS + (u16 * 16 + 4 * kg) * 2);
+      const s16x4 dsl = *(const s16x4*)(slot + St::OFF_DS + 512 + (u16 * 16 + 4 * kg) * 2);
+      // the slot's reads have landed before the next copies overwrite it
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      __builtin_amdgcn_wave_barrier();
+      if (tn < nt) issue(sn, chn);
+#pragma unroll
+      for (int n = 0; n < ND; ++n) {
+        X[n] = mma16(kt[n], dsh, X[n]);
+        X[n] = mma16(kt[n], dsl, X[n]);
+        X[n] = mma16(ktl[n], dsh, X[n]);
+      }
       tau = tn;
       s = sn;
       chunk = chn;
-      e = en;
     }
-    wait_stage();
     while (cur_slot < np - 1) {
       rot_acc<D>(X, rot_m[0], rot_m[1], kg);
       ++cur_slot;
     }
     // back to the query's frame: R(X, -c_t)
+    {
+      const float* c = a.cosb + (int64_t)ct * HALF;
+      const float* sn = a.sinb + (int64_t)ct * HALF;
 #pragma unroll
-    for (int n = 0; n < ND / 2; ++n) {
-      const int i0 = 16 * n + 4 * kg;
-      const float4 c4 = *(const float4*)(a.cosb + (int64_t)ct * HALF + i0);
-      const float4 s4 = *(const float4*)(a.sinb + (int64_t)ct * HALF + i0);
-      const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
+      for (int n = 0; n < ND / 2; ++n) {
+        const int i0 = 16 * n + 4 * kg;
+        const float4 c4 = *(const float4*)(c + i0);
+        const float4 s4 = *(const float4*)(sn + i0);
+        const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float lo = X[n][r], hi = X[n + ND / 2][r];
-        acc[n][r] += lo * cc[r] + hi * ss[r];
-        acc[n + ND / 2][r] += hi * cc[r] - lo * ss[r];
+        for (int r = 0; r < 4; ++r) {
+          const float lo = X[n][r], hi = X[n + ND / 2][r];
+          X[n][r] = lo * cc[r] + hi * ss[r];
+          X[n + ND / 2][r] = hi * cc[r] - lo * ss[r];
+        }
       }
     }
   }
-  if (gv) {
-    float* o = a.dq + (bt * a.H + h * G + u16) * D;
+  if (u16 < a.G) {
+    float* o = a.dq + (bt * a.H + h * a.G + u16) * D;
 #pragma unroll
     for (int n = 0; n < ND; ++n)
       *(float4*)(o + 16 * n + 4 * kg) =
-          make_float4(a.scale * acc[n][0], a.scale * acc[n][1], a.scale * acc[n][2], a.scale * acc[n][3]);
+          make_float4(a.scale * X[n][0], a.scale * X[n][1], a.scale * X[n][2], a.scale * X[n][3]);
   }
 }
 
@@ -1228,7 +1225,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
                        csr_row, rowoff + nrows, parents + l * lstride,
                        l > 0 ? parents + (l - 1) * lstride : nullptr, d->T, d->H_kv, d->top_k, Pl,
                        P.pw[l], CR, P.cr_log2, recs,
-                       BP.use_ds ? (int32_t*)(ws + BP.off_emap[l]) : nullptr);
+                       BP.use_ds ? (int4*)(ws + BP.off_emap[l]) : nullptr);
     DkvArgs a;
     memset(&a, 0, sizeof(a));
     a.kh = (const uint16_t*)(tws + P.off_kh[l]);
@@ -1278,8 +1275,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     for (int l = 0; l < P.L; ++l) {
       a.lv[l].kt_h = U16(BP.off_kt[0][l]);
       a.lv[l].kt_l = U16(BP.off_kt[1][l]);
-      a.lv[l].rec = (const int4*)(ws + BP.off_rec[l]);
-      a.lv[l].emap = (const int32_t*)(ws + BP.off_emap[l]);
+      a.lv[l].emap = (const int4*)(ws + BP.off_emap[l]);
       a.lv[l].ds = U16(BP.off_ds[l]);
       a.lv[l].Np = P.Np[l];
       a.lv[l].pw = P.pw[l];
