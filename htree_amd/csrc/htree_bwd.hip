@@ -252,8 +252,10 @@ __global__ __launch_bounds__(256) void prep_kernel(const T* __restrict__ o, cons
 }
 
 // ---------------------------------------------------------------- pack
-// KT[blk][d][16] = KH[blk*16 + c][d] (K~ transposed per block); VR[node][d]
-// = VH[blk][d][c] (V rows).  One thread per (bh, node, d).
+// KT: K~ transposed per 16-node block, element (d, c) of block blk at
+// blk*16D + (d/16)*256 + (c/4)*64 + (d%16)*4 + c%4, so that the 4-node pieces
+// one MFMA operand read takes lie contiguous; the V source VH[blk][d][c] is
+// written back as rows VR[node][d].  One thread per (bh, node, d).
 __global__ __launch_bounds__(256) void pack_bwd_kernel(
     const uint16_t* __restrict__ kh, const uint16_t* __restrict__ kl,
     const uint16_t* __restrict__ vh, const uint16_t* __restrict__ vl, int64_t Np, int D,
@@ -265,11 +267,14 @@ __global__ __launch_bounds__(256) void pack_bwd_kernel(
   const int64_t r = idx / D;  // bh * Np + node
   const int64_t node = r % Np;
   const int64_t bh = r / Np;
-  const int64_t tr = ((bh * (Np / 16) + node / 16) * D + dd) * 16 + (node & 15);
+  const int c = (int)(node & 15);
+  const int64_t tr = (bh * (Np / 16) + node / 16) * D * 16 + (dd >> 4) * 256 + (c >> 2) * 64 +
+                     (dd & 15) * 4 + (c & 3);
+  const int64_t vsrc = ((bh * (Np / 16) + node / 16) * D + dd) * 16 + c;
   kt_h[tr] = kh[idx];
   if (kt_l) kt_l[tr] = kl[idx];
-  vr_h[idx] = vh[tr];
-  if (vr_l) vr_l[idx] = vl[tr];
+  vr_h[idx] = vh[vsrc];
+  if (vr_l) vr_l[idx] = vl[vsrc];
 }
 
 // ---------------------------------------------------------------- index
@@ -444,49 +449,88 @@ struct DkvArgs {
   float scale;
 };
 
-// One entry's inputs staged in LDS by asynchronous global->LDS copies
-// (global_load_lds): the 16 query rows and 16 dO rows of the query group,
-// the RoPE row rho, and gmax / gsum / delta of the 16 heads.
+// One entry's inputs staged in LDS by asynchronous copies: the 16 query
+// rows and 16 dO rows of the query group, the RoPE row rho, and gmax / gsum /
+// delta of the 16 heads.  Head rows are padded by one 16-byte chunk (pitch
+// RP), so that 8 lanes reading one chunk position of 8 heads, and lanes
+// reading one column of 4 heads, hit distinct LDS banks with linear addresses.
 template <int D, typename TIn>
 struct Stage {
-  static constexpr int ROWB = 16 * D * (int)sizeof(TIn);  // 16 head rows
+  static constexpr int CPR = D * (int)sizeof(TIn) / 16;  // chunks per head row
+  static constexpr int RP = (CPR + 1) * 16;               // padded row pitch (bytes)
+  static constexpr int NCH = 16 * (CPR + 1);              // chunks of 16 padded rows
+  static constexpr int ROWB = 16 * RP;
   static constexpr int OFF_DO = ROWB;
-  static constexpr int OFF_TAB = 2 * ROWB;          // cos [D/2] then sin [D/2] (1 KB area)
-  static constexpr int OFF_SM = 2 * ROWB + 1024;    // gmax[16], gsum[16], delta[16], pad
-  static constexpr int BYTES = 2 * ROWB + 1024 + 256;
+  static constexpr int OFF_TAB = 2 * ROWB;          // cos [D/2] then sin [D/2]
+  static constexpr int OFF_SM = OFF_TAB + D * 4;    // gmax[16], gsum[16], delta[16], pad
+  static constexpr int BYTES = OFF_SM + 256;
   static constexpr int SLOTS = BYTES * 2 <= 20 * 1024 ? 2 : 1;  // double-buffer if it fits
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+// byte offset of element e of head row g in a staged block
+template <int D, typename TIn>
+__device__ __forceinline__ int row_off(int g, int e) {
+  return g * Stage<D, TIn>::RP + e * (int)sizeof(TIn);
+}
+
+// buffer resource over `bytes` bytes at `base` (raw, byte-addressed); base
+// and bytes are wave-uniform and are moved to scalar registers here
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int bytes) {
+  const uint64_t p = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0,
+                                           __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+// Asynchronous copies of one entry's inputs into `slot` (buffer loads into
+// LDS: the bases live in scalar registers, the lanes hold 32-bit offsets).
 template <int D, typename TIn>
 __device__ __forceinline__ void stage_issue(char* slot, const DkvArgs& a, int64_t hq0, int rho,
                                             int lane) {
   using St = Stage<D, TIn>;
   constexpr int HALF = D / 2;
-  const int valid = a.G * D * (int)sizeof(TIn);  // bytes of the group's rows
-  const char* qs = (const char*)a.q + hq0 * D * (int64_t)sizeof(TIn);
-  const char* ds = (const char*)a.dO + hq0 * D * (int64_t)sizeof(TIn);
+  constexpr int ES = (int)sizeof(TIn);
+  constexpr int CPR = St::CPR;
+  const int G = a.G;
+  // the lane offsets below are cheap to recompute: keep them out of the
+  // registers held across the entry loop
+  int lane_c = lane;
+  asm volatile("" : "+v"(lane_c));
+  lane = lane_c;
+  const __amdgpu_buffer_rsrc_t rq = buf_rsrc((const char*)a.q + hq0 * D * ES, G * D * ES);
+  const __amdgpu_buffer_rsrc_t rd = buf_rsrc((const char*)a.dO + hq0 * D * ES, G * D * ES);
 #pragma unroll
-  for (int j = 0; j < St::ROWB / 1024; ++j) {
-    int off = (j * 64 + lane) * 16;
-    off = off < valid ? off : 0;  // rows past the group: in-bounds filler, never used
-    __builtin_amdgcn_global_load_lds(qs + off, (lds_void*)(slot + j * 1024), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(ds + off, (lds_void*)(slot + St::OFF_DO + j * 1024), 16, 0, 0);
+  for (int j = 0; j < (St::NCH + 63) / 64; ++j) {
+    const int P = j * 64 + lane;  // LDS chunk: padded row g, chunk c (c == CPR: pad)
+    const int g = P / (CPR + 1);
+    const int c = P - g * (CPR + 1);
+    int off = (g * CPR + (c < CPR ? c : 0)) * 16;
+    off = g < G ? off : 0;  // rows past the group: in-bounds filler, never used
+    if ((St::NCH % 64 == 0) || P < St::NCH) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void*)(slot + j * 1024), 16, off, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_void*)(slot + St::OFF_DO + j * 1024), 16,
+                                               off, 0, 0, 0);
+    }
   }
-  {
-    constexpr int CH = HALF / 4;  // 16-byte chunks of one table row
-    const float* src = lane < CH ? a.cosb + (int64_t)rho * HALF + 4 * lane
-                       : lane < 2 * CH ? a.sinb + (int64_t)rho * HALF + 4 * (lane - CH)
-                                       : a.cosb + (int64_t)rho * HALF;
-    __builtin_amdgcn_global_load_lds(src, (lds_void*)(slot + St::OFF_TAB), 16, 0, 0);
+  constexpr int CH = HALF / 4;  // 16-byte chunks of one table row
+  if (lane < CH) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(a.cosb + (int64_t)rho * HALF, HALF * 4),
+                                             (lds_void*)(slot + St::OFF_TAB), 16, lane * 16, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(a.sinb + (int64_t)rho * HALF, HALF * 4),
+                                             (lds_void*)(slot + St::OFF_TAB + HALF * 4), 16,
+                                             lane * 16, 0, 0, 0);
   }
-  {
-    const int g = lane & 15, which = lane >> 4;
-    int64_t i = hq0 + g;
-    i = (g < a.G && i < a.BTH) ? i : hq0;
-    const float* src = which == 0 ? a.gmax + i : which == 1 ? a.gsum + i : a.delta + i;
-    __builtin_amdgcn_global_load_lds(src, (lds_void*)(slot + St::OFF_SM), 4, 0, 0);
+  if (lane < 16) {
+    const int i = (lane < G ? lane : 0) * 4;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(a.gmax + hq0, G * 4),
+                                             (lds_void*)(slot + St::OFF_SM), 4, i, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(a.gsum + hq0, G * 4),
+                                             (lds_void*)(slot + St::OFF_SM + 64), 4, i, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(a.delta + hq0, G * 4),
+                                             (lds_void*)(slot + St::OFF_SM + 128), 4, i, 0, 0, 0);
   }
 }
 
@@ -502,33 +546,72 @@ struct ColT {
   static __device__ __forceinline__ void get(const char* rows, int g0, int d, s16x4& h, s16x4& l) {
     float f[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) f[i] = (float)((const TIn*)rows)[(g0 + i) * D + d];
+    for (int i = 0; i < 4; ++i) f[i] = (float)*(const TIn*)(rows + row_off<D, TIn>(g0 + i, d));
     pack4_split(f, h, l);
   }
 };
 template <int D>
 struct ColT<D, __bf16> {
   static __device__ __forceinline__ void get(const char* rows, int g0, int d, s16x4& h, s16x4& l) {
-    const uint16_t* r = (const uint16_t*)rows;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) h[i] = (short)r[(g0 + i) * D + d];
+    for (int i = 0; i < 4; ++i) h[i] = *(const short*)(rows + row_off<D, __bf16>(g0 + i, d));
     (void)l;
   }
 };
 
+// one 16-byte chunk of TIn values as floats
+template <typename TIn>
+__device__ __forceinline__ void ld_chunk(const TIn* p, float* o) {
+  Io<TIn>::ld8(p, o);
+}
+template <>
+__device__ __forceinline__ void ld_chunk<float>(const float* p, float* o) {
+  const float4 a = *(const float4*)p;
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+}
+
 // Row fragment (head u16, the lane group's d-slots) of the staged rows
 template <int D, typename TIn>
 __device__ __forceinline__ void row_frag(const char* rows, int u16, int kg, float (&x)[D / 32][8]) {
-  const TIn* r = (const TIn*)rows + u16 * D;
+  constexpr int PER = 16 / (int)sizeof(TIn);  // elements per chunk
 #pragma unroll
-  for (int m = 0; m < D / 32; ++m) Io<TIn>::ld8(r + dslot<D>(kg, m), x[m]);
+  for (int m = 0; m < D / 32; ++m) {
+    const int e0 = dslot<D>(kg, m);
+#pragma unroll
+    for (int c = 0; c < 8 / PER; ++c)
+      ld_chunk<TIn>((const TIn*)(rows + row_off<D, TIn>(u16, e0 + c * PER)), x[m] + c * PER);
+  }
 }
+
+// dO row fragment as MFMA operands: bf16 rows load straight into the operand
+// (exact); other types are split into bf16 hi + lo.
+template <int D, typename TIn>
+struct DoRow {
+  static __device__ __forceinline__ void get(const char* rows, int u16, int kg, bf16x8 (&h)[D / 32],
+                                             bf16x8 (&lo)[D / 32]) {
+    float df[D / 32][8];
+    row_frag<D, TIn>(rows, u16, kg, df);
+#pragma unroll
+    for (int m = 0; m < D / 32; ++m) split8(df[m], h[m], lo[m]);
+  }
+};
+template <int D>
+struct DoRow<D, __bf16> {
+  static __device__ __forceinline__ void get(const char* rows, int u16, int kg, bf16x8 (&h)[D / 32],
+                                             bf16x8 (&lo)[D / 32]) {
+#pragma unroll
+    for (int m = 0; m < D / 32; ++m)
+      h[m] = *(const bf16x8*)(rows + row_off<D, __bf16>(u16, dslot<D>(kg, m)));
+    (void)lo;
+  }
+};
 
 template <int D, bool PREC, typename TIn>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void dkv_kernel(const DkvArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
   using St = Stage<D, TIn>;
-  __shared__ __attribute__((aligned(16))) char stage_all[kWavesPerBlock][St::SLOTS][St::BYTES];
+  __shared__ __attribute__((aligned(16))) char stage_a[kWavesPerBlock][St::BYTES];
+  __shared__ __attribute__((aligned(16))) char stage_b[kWavesPerBlock][St::SLOTS == 2 ? St::BYTES : 16];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int u16 = lane & 15, kg = lane >> 4;
   const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wv;
@@ -565,40 +648,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   const bool gv = u16 < G;
   auto hq0_of = [&](int t) { return ((b * a.T + t) * a.Hkv + h) * (int64_t)G; };
 
-  // entries whose tile mask is empty are skipped without staging
-  int e = 0;
-  int4 rc = make_int4(0, 0, 0, 0);
-  while (e < ne) {
-    rc = a.rec[e0 + e];
-    if (tile_mask(rc)) break;
-    ++e;
-  }
-  int slot = 0;
-  if (e < ne) stage_issue<D, TIn>(stage_all[wv][0], a, hq0_of(rc.x), rc.y, lane);
-  while (e < ne) {
-    // next entry with work, staged into the other slot while this one computes
-    int en = e + 1;
-    int4 rn = make_int4(0, 0, 0, 0);
-    while (en < ne) {
-      rn = a.rec[e0 + en];
-      if (tile_mask(rn)) break;
-      ++en;
+  // The piece's records are held 64 at a time in the lanes (lane i = entry
+  // base + i) with a ballot of the entries whose tile mask is not empty;
+  // empty entries are skipped without staging.
+  int base = -64;
+  int4 rb = make_int4(0, 0, 0, 0);
+  unsigned long long work = 0ull;
+  auto next_work = [&](int e) {  // first entry >= e with work, or ne
+    while (e < ne) {
+      if (e >= base + 64) {
+        base = e & ~63;
+        const bool in = base + lane < ne;
+        rb = in ? a.rec[e0 + base + lane] : make_int4(0, 0, 0, 0);
+        work = __ballot(in && tile_mask(rb) != 0u);
+      }
+      const unsigned long long m = work >> (e - base);
+      if (m) return e + (int)__builtin_ctzll(m);
+      e = base + 64;
     }
+    return ne;
+  };
+  auto rec_of = [&](int e) {  // e lies in the held batch
+    const int i = e - base;
+    return make_int4(__builtin_amdgcn_readlane(rb.x, i), __builtin_amdgcn_readlane(rb.y, i),
+                     __builtin_amdgcn_readlane(rb.z, i), __builtin_amdgcn_readlane(rb.w, i));
+  };
+  int e = next_work(0);
+  int4 rc = e < ne ? rec_of(e) : make_int4(0, 0, 0, 0);
+  // One entry: the next entry's copies go into `nxt`, then this entry is
+  // computed from `cur`.  cur and nxt are restrict-qualified and lie in
+  // different LDS arrays, so the compiler can tell that the reads of cur need
+  // not wait for the copies into nxt.
+  auto step = [&](const char* __restrict__ S0, char* __restrict__ nxt, const int4 rc, const int en,
+                  const int4 rn) __attribute__((always_inline)) {
     wait_stage();
-    if (St::SLOTS == 2 && en < ne)
-      stage_issue<D, TIn>(stage_all[wv][slot ^ 1], a, hq0_of(rn.x), rn.y, lane);
-    const char* S0 = stage_all[wv][St::SLOTS == 2 ? slot : 0];
+    if (nxt && en < ne) stage_issue<D, TIn>(nxt, a, hq0_of(rn.x), rn.y, lane);
     const float* tab = (const float*)(S0 + St::OFF_TAB);  // cos [HALF], sin [HALF]
     const float* sm = (const float*)(S0 + St::OFF_SM);    // gmax, gsum, delta [16 each]
     const bool ok = (tile_mask(rc) >> u16) & 1u;
 
     // rotated query fragment (lane g = u16); the score scale is applied to S
+    // (heads past the group hold finite filler: their P and dS are zeroed below)
     float qr[KS][8];
     row_frag<D, TIn>(S0, u16, kg, qr);
-#pragma unroll
-    for (int m = 0; m < KS; ++m)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qr[m][i] = gv ? qr[m][i] : 0.f;
     rot_by_fr<D>(qr, tab, tab + HALF, kg);
     bf16x8 qh[KS], ql[KS];
     split_frag<D>(qr, qh, ql);
@@ -613,18 +705,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     // dP[g][cand] = dO[g] . V[cand]
     f32x4 dP = {0.f, 0.f, 0.f, 0.f};
     {
-      float df[KS][8];
-      row_frag<D, TIn>(S0 + St::OFF_DO, u16, kg, df);
       bf16x8 dh[KS], dlo[KS];
-#pragma unroll
-      for (int m = 0; m < KS; ++m) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) df[m][i] = gv ? df[m][i] : 0.f;
-        if (PREC)
-          split8(df[m], dh[m], dlo[m]);
-        else
-          dh[m] = pack8(df[m]);  // exact for bf16 inputs
-      }
+      DoRow<D, TIn>::get(S0 + St::OFF_DO, u16, kg, dh, dlo);
 #pragma unroll
       for (int m = 0; m < KS; ++m) {
         dP = mma32(dh[m], vh[m], dP);
@@ -656,12 +738,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     pack4_split(ds, dh4, dl4);
     pack4_split(pr, ph, plo);
     if (a.ds) {
-      // dS[g][cand] for the dq pass: hi then lo, 16 x 16 each, row g
-      uint16_t* o = a.ds + ((int64_t)(e0 + e) * a.tpp + tile) * 512 + 64 * kg + u16;
+      // dS[g][cand] for the dq pass: hi then lo, 16 x 16 each, element
+      // (g, cand) at (cand / 4) * 64 + g * 4 + cand % 4
+      uint16_t* o = a.ds + ((int64_t)(e0 + e) * a.tpp + tile) * 512 + (u16 >> 2) * 64 + 16 * kg +
+                    (u16 & 3);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        o[16 * r] = (uint16_t)dh4[r];
-        o[256 + 16 * r] = (uint16_t)dl4[r];
+        o[4 * r] = (uint16_t)dh4[r];
+        o[256 + 4 * r] = (uint16_t)dl4[r];
       }
     }
     f32x4 u[ND];
@@ -692,13 +776,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
         dk[n + ND / 2][r] += lo * sn + hi * c;
       }
     }
-    if (St::SLOTS == 1 && en < ne) {
-      wave_sync();  // every lane has read the slot
-      stage_issue<D, TIn>(stage_all[wv][0], a, hq0_of(rn.x), rn.y, lane);
+  };
+  if (e < ne) stage_issue<D, TIn>(stage_a[wv], a, hq0_of(rc.x), rc.y, lane);
+  if constexpr (St::SLOTS == 2) {
+    while (e < ne) {
+      int en = next_work(e + 1);
+      int4 rn = en < ne ? rec_of(en) : make_int4(0, 0, 0, 0);
+      step(stage_a[wv], stage_b[wv], rc, en, rn);
+      e = en;
+      rc = rn;
+      if (e >= ne) break;
+      en = next_work(e + 1);
+      rn = en < ne ? rec_of(en) : make_int4(0, 0, 0, 0);
+      step(stage_b[wv], stage_a[wv], rc, en, rn);
+      e = en;
+      rc = rn;
     }
-    slot ^= 1;
-    e = en;
-    rc = rn;
+  } else {
+    while (e < ne) {
+      const int en = next_work(e + 1);
+      const int4 rn = en < ne ? rec_of(en) : make_int4(0, 0, 0, 0);
+      step(stage_a[wv], nullptr, rc, en, rn);
+      if (en < ne) {
+        wave_sync();  // every lane has read the slot
+        stage_issue<D, TIn>(stage_a[wv], a, hq0_of(rn.x), rn.y, lane);
+      }
+      e = en;
+      rc = rn;
+    }
   }
   wait_stage();
   // dk of the node = scale R^-1(dK~, node mod CR); write this piece's partial
@@ -946,7 +1051,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
       // loads stay below the score math (keeps the tile within 256 VGPRs).
       __builtin_amdgcn_sched_barrier(0);
       const int vn = node0 + (4 * kg < CRU ? 4 * kg : 0);
-      const int64_t tbase = ((hrow + (vn & ~15)) / 16 * D + u16) * 16 + (vn & 15);
+      const int64_t tbase = (hrow + (vn & ~15)) / 16 * D * 16 + ((vn & 15) >> 2) * 64 + u16 * 4;
       s16x4 kt[ND], ktl[ND];
 #pragma unroll
       for (int n = 0; n < ND; ++n) {
@@ -1111,17 +1216,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void d
         ++cur_slot;
       }
       const int node0 = (__builtin_amdgcn_readlane(pe, s) << crlg) + (chunk << 4);
-      const int coln = (node0 & 15) + (4 * kg < (CR < 16 ? CR : 16) ? 4 * kg : 0);
+      const int piece = ((node0 & 15) >> 2) + (4 * kg < (CR < 16 ? CR : 16) ? kg : 0);
       wait_stage();
       s16x4 kt[ND], ktl[ND];
 #pragma unroll
       for (int n = 0; n < ND; ++n) {
-        const int off = ((16 * n + u16) * 16 + coln) * 2;
+        const int off = n * 512 + piece * 128 + u16 * 8;
         kt[n] = *(const s16x4*)(slot + off);
         ktl[n] = *(const s16x4*)(slot + St::OFF_KL + off);
       }
-      const s16x4 dsh = *(const s16x4*)(slot + St::OFF_DS + (u16 * 16 + 4 * kg) * 2);
-      const s16x4 dsl = *(const s16x4*)(slot + St::OFF_DS + 512 + (u16 * 16 + 4 * kg) * 2);
+      const s16x4 dsh = *(const s16x4*)(slot + St::OFF_DS + kg * 128 + u16 * 8);
+      const s16x4 dsl = *(const s16x4*)(slot + St::OFF_DS + 512 + kg * 128 + u16 * 8);
       // the slot's reads have landed before the next copies overwrite it
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
       __builtin_amdgcn_wave_barrier();
