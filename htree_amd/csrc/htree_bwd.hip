@@ -550,11 +550,18 @@ struct ColT {
     pack4_split(f, h, l);
   }
 };
+// bf16: one transposing LDS read (ds_read_b64_tr_b16).  Within each group of
+// 16 lanes, lane m receives element m % 4 of the 8-byte pieces addressed by
+// lanes m / 4 + 4t (t = 0..3); lane i of group kg therefore addresses head
+// 4 kg + i / 4, columns d - u16 + 4 (i % 4) .. +3, and receives heads
+// 4 kg .. 4 kg + 3 of column d.
 template <int D>
 struct ColT<D, __bf16> {
   static __device__ __forceinline__ void get(const char* rows, int g0, int d, s16x4& h, s16x4& l) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) h[i] = *(const short*)(rows + row_off<D, __bf16>(g0 + i, d));
+    const int u16 = __lane_id() & 15;
+    const char* p = rows + row_off<D, __bf16>(g0 + (u16 >> 2), d - u16 + 4 * (u16 & 3));
+    h = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(const __attribute__((address_space(3))) void*)p);
     (void)l;
   }
 };
