@@ -14,15 +14,19 @@
 // Structure:
 //   prep     per (b,t,h_kv): delta = rowsum(dO * out).
 //   pack     per level: K~ (pre-rotated) transposed per 16-node block, V rows.
-//   index    per level: bitmap parent x query (integer atomicOr), row counts,
-//            scan, extraction of each parent's queries in t order (CSR), and
-//            a table of fixed-size pieces of every row.
+//   index    per level: bitmap parent x query (integer atomicOr), per-row
+//            prefix of the bitmap words' popcounts, row scan, a table of
+//            fixed-size pieces of every row, and one record per (parent row,
+//            query) entry in t order, placed from the word prefix.
 //   dkv      one wave per (piece, 16-child tile): K~/V tile stationary in
 //            registers, loops over the piece's queries, whose q / dO rows,
 //            RoPE row and softmax state are staged into LDS by asynchronous
-//            global->LDS copies one entry ahead; partial dK/dV per piece.
+//            copies one entry ahead; partial dK/dV per piece; stores each
+//            entry's dS for the dq pass.
 //   reduce   sums each tile's pieces in piece order into the level's dK/dV.
-//   dq       one wave per query group over all levels (Q-stationary).
+//   dq       one wave per query group over all levels (Q-stationary), from
+//            the stored dS (or recomputing the scores when the stored dS
+//            would exceed its memory budget).
 //   pool     dK_{l-1}[child] += dK_l[parent] / n_children, top-down.
 #include <string.h>
 
@@ -41,8 +45,8 @@ struct BwdPlan {
   int64_t off_delta;
   int64_t off_kt[2][HTREE_MAX_LEVELS], off_vr[2][HTREE_MAX_LEVELS];
   int64_t off_dk[HTREE_MAX_LEVELS], off_dv[HTREE_MAX_LEVELS];
-  int64_t off_bitmap, off_cnt, off_rowoff, off_pcnt, off_poff, off_npieces, off_ptab, off_csr,
-      off_partial, off_csr_row;
+  int64_t off_bitmap, off_wpre, off_cnt, off_rowoff, off_pcnt, off_poff, off_npieces, off_ptab,
+      off_partial;
   int64_t off_rec[HTREE_MAX_LEVELS];   // per-entry records of each level
   int64_t off_emap[HTREE_MAX_LEVELS];  // (query group, slot) -> {entry, mask}, per level
   int64_t off_ds[HTREE_MAX_LEVELS];    // dS of every entry tile (bf16 hi, lo), per level
@@ -87,14 +91,13 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
     b->off_dv[l] = l > 0 ? take((int64_t)d->B * P.N[l] * d->H_kv * d->D * 4) : -1;
   }
   b->off_bitmap = take(b->max_rows * b->W * 4);
+  b->off_wpre = take(b->max_rows * b->W * 4);
   b->off_cnt = take((b->max_rows + 1) * 4);
   b->off_rowoff = take((b->max_rows + 1) * 4);
   b->off_pcnt = take((b->max_rows + 1) * 4);
   b->off_poff = take((b->max_rows + 1) * 4);
   b->off_npieces = take(4);
   b->off_ptab = take(b->max_pieces * 3 * 4);
-  b->off_csr = take(b->max_entries * 4);
-  b->off_csr_row = take(b->max_entries * 4);
   // dS of every (entry, tile), 1 KB each, kept for the dq pass when the whole
   // backward's worth fits the budget; otherwise dq recomputes the scores
   const int64_t ds_level = b->max_entries * b->tpp * 1024;
@@ -300,19 +303,37 @@ __global__ __launch_bounds__(256) void bitmap_set_kernel(const int32_t* __restri
   atomicOr(&bm[row * W + (t >> 5)], 1u << (t & 31));
 }
 
-// one wave per row: number of queries and of pieces
-__global__ __launch_bounds__(256) void row_count_kernel(const uint32_t* __restrict__ bm, int64_t nrows,
-                                                        int64_t W, int piece, int32_t* __restrict__ cnt,
-                                                        int32_t* __restrict__ pcnt) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  if (row >= nrows) return;
+// One block per row: exclusive prefix of the per-word popcounts of the
+// row's bitmap (wpre), the row's query count and its number of pieces.
+__global__ __launch_bounds__(256) void row_scan_kernel(const uint32_t* __restrict__ bm, int64_t W,
+                                                       int piece, int32_t* __restrict__ wpre,
+                                                       int32_t* __restrict__ cnt,
+                                                       int32_t* __restrict__ pcnt) {
+  __shared__ int32_t part[256];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t per = (W + 255) / 256;
+  const int64_t w0 = tid * per;
+  const int64_t w1 = w0 + per < W ? w0 + per : W;
+  const uint32_t* r = bm + row * W;
   int c = 0;
-  for (int64_t w = lane; w < W; w += 64) c += __popc(bm[row * W + w]);
-  c = wave_sum_i(c);
-  if (lane == 0) {
-    cnt[row] = c;
-    pcnt[row] = (c + piece - 1) / piece;
+  for (int64_t w = w0; w < w1; ++w) c += __popc(r[w]);
+  part[tid] = c;
+  __syncthreads();
+  for (int o = 1; o < 256; o <<= 1) {
+    const int32_t v = tid >= o ? part[tid - o] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  int run = tid > 0 ? part[tid - 1] : 0;
+  for (int64_t w = w0; w < w1; ++w) {
+    wpre[row * W + w] = run;
+    run += __popc(r[w]);
+  }
+  if (tid == 255) {
+    cnt[row] = part[255];
+    pcnt[row] = (part[255] + piece - 1) / piece;
   }
 }
 
@@ -342,36 +363,6 @@ __global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ 
   if (tid == 1023) out[n] = part[1023];
 }
 
-// one wave per row: writes the row's query indices in ascending t
-__global__ __launch_bounds__(256) void extract_kernel(const uint32_t* __restrict__ bm, int64_t nrows,
-                                                      int64_t W, const int32_t* __restrict__ rowoff,
-                                                      int32_t* __restrict__ csr,
-                                                      int32_t* __restrict__ csr_row) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  if (row >= nrows) return;
-  int64_t base = rowoff[row];
-  for (int64_t w0 = 0; w0 < W; w0 += 64) {
-    const int64_t w = w0 + lane;
-    uint32_t x = w < W ? bm[row * W + w] : 0u;
-    const int c = __popc(x);
-    int inc = c;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int v = __shfl_up(inc, o);
-      if (lane >= o) inc += v;
-    }
-    int64_t pos = base + inc - c;
-    while (x) {
-      const int bit = __ffs(x) - 1;
-      csr_row[pos] = (int32_t)row;
-      csr[pos++] = (int32_t)(w * 32 + bit);
-      x &= x - 1;
-    }
-    base += __shfl(inc, 63);
-  }
-}
-
 // piece table: (row, first entry, count) for every piece of every row
 __global__ __launch_bounds__(256) void piece_kernel(const int32_t* __restrict__ cnt,
                                                     const int32_t* __restrict__ rowoff,
@@ -390,46 +381,52 @@ __global__ __launch_bounds__(256) void piece_kernel(const int32_t* __restrict__ 
 }
 
 
-// Per entry (query t of parent p's row): the rotation row rho = n_c - 1 -
-// s CR of p's slot s in t's list, and the mask of p's children that t
-// accumulates at this level (valid positions, not passed to level l-1).
-__global__ __launch_bounds__(256) void record_kernel(const int32_t* __restrict__ csr,
-                                                     const int32_t* __restrict__ csr_row,
-                                                     const int32_t* __restrict__ ntot,
-                                                     const int32_t* __restrict__ par,
-                                                     const int32_t* __restrict__ par_next, int T,
-                                                     int Hkv, int TK, int64_t Pl, int64_t pw, int CR,
-                                                     int crlg, int4* __restrict__ rec,
+// One lane per (query group, slot s): the entry of (parent p's row, t) is
+// found from the row bitmap's word prefix, and gets the rotation row
+// rho = n_c - 1 - s CR and the mask of p's children that t accumulates at
+// this level (valid positions, not passed to level l-1).  A query group's
+// TK slots are TK consecutive lanes of one wave; its next-level list is read
+// by shuffles.  emap (nullable) maps (query group, slot) to {entry, mask}.
+__global__ __launch_bounds__(256) void record_kernel(const int32_t* __restrict__ par,
+                                                     const int32_t* __restrict__ par_next,
+                                                     const uint32_t* __restrict__ bm,
+                                                     const int32_t* __restrict__ wpre,
+                                                     const int32_t* __restrict__ rowoff, int T,
+                                                     int Hkv, int TK, int64_t Pl, int64_t W,
+                                                     int64_t pw, int CR, int crlg, int64_t total,
+                                                     int4* __restrict__ rec,
                                                      int4* __restrict__ emap) {
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= *ntot) return;
-  const int t = csr[e];
-  const int64_t row = csr_row[e];
-  const int p = (int)(row % Pl);
-  const int64_t bh = row / Pl;
-  const int h = (int)(bh % Hkv);
-  const int64_t grp = ((bh / Hkv) * T + t) * Hkv + h;
-  const int32_t* pl = par + grp * TK;
-  int np = 0, s = 0;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool in = idx < total;
+  const int lane = threadIdx.x & 63;
+  const int base = lane & ~(TK - 1);
+  const int p = in ? par[idx] : -1;
+  const unsigned long long gmask = (TK >= 64 ? ~0ull : ((1ull << TK) - 1ull)) << base;
+  const int np = __popcll(__ballot(p >= 0) & gmask);
+  const int vn = (in && par_next) ? par_next[idx] : -1;
+  unsigned long long drop = 0ull;  // children of p passed to level l-1
   for (int i = 0; i < TK; ++i) {
-    const int v = pl[i];
-    np += v >= 0;
-    s += (v >= 0 && v < p);
+    const int v = __shfl(vn, base + i);
+    if (v >= 0 && (v >> crlg) == p) drop |= 1ull << (v & (CR - 1));
   }
+  if (p < 0) return;
+  const int64_t grp = idx / TK;
+  const int s = (int)(idx % TK);
+  const int h = (int)(grp % Hkv);
+  const int64_t bt = grp / Hkv;
+  const int t = (int)(bt % T);
+  const int64_t b = bt / T;
   const int ct = (int)((t / pw) & (CR - 1));
   const int nc = ((np - 1) << crlg) + ct + 1;
   const int nvalid = nc - (s << crlg);  // children of p that are candidates
   unsigned long long m = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
   if (CR < 64) m &= (1ull << CR) - 1ull;
-  if (par_next) {
-    const int32_t* pn = par_next + grp * TK;
-    for (int i = 0; i < TK; ++i) {
-      const int v = pn[i];
-      if (v >= 0 && (v >> crlg) == p) m &= ~(1ull << (v & (CR - 1)));
-    }
-  }
+  m &= ~drop;
+  const int64_t row = (b * Hkv + h) * Pl + p;
+  const int64_t wi = row * W + (t >> 5);
+  const int e = rowoff[row] + wpre[wi] + __popc(bm[wi] & ((1u << (t & 31)) - 1u));
   rec[e] = make_int4(t, nc - 1 - (s << crlg), (int)(uint32_t)m, (int)(uint32_t)(m >> 32));
-  if (emap) emap[grp * TK + s] = make_int4((int)e, (int)(uint32_t)m, (int)(uint32_t)(m >> 32), 0);
+  if (emap) emap[idx] = make_int4(e, (int)(uint32_t)m, (int)(uint32_t)(m >> 32), 0);
 }
 
 // ---------------------------------------------------------------- dkv
@@ -1312,8 +1309,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
   int32_t* poff = (int32_t*)(ws + BP.off_poff);
   int32_t* npieces = (int32_t*)(ws + BP.off_npieces);
   int32_t* ptab = (int32_t*)(ws + BP.off_ptab);
-  int32_t* csr = (int32_t*)(ws + BP.off_csr);
-  int32_t* csr_row = (int32_t*)(ws + BP.off_csr_row);
+  int32_t* wpre = (int32_t*)(ws + BP.off_wpre);
   float* partial = (float*)(ws + BP.off_partial);
   for (int l = P.L - 1; l >= 0; --l) {
     const int64_t Pl = (P.N[l] + CR - 1) / CR;
@@ -1324,19 +1320,16 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     const int64_t ent = lstride;
     hipLaunchKernelGGL(bitmap_set_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
                        parents + l * lstride, d->T, d->H_kv, d->top_k, Pl, BP.W, ent, bm);
-    hipLaunchKernelGGL(row_count_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, st, bm,
-                       nrows, BP.W, (int)BP.piece, cnt, pcnt);
+    hipLaunchKernelGGL(row_scan_kernel, dim3((unsigned)nrows), dim3(256), 0, st, bm, BP.W,
+                       (int)BP.piece, wpre, cnt, pcnt);
     hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, cnt, nrows, rowoff);
     hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, pcnt, nrows, poff);
-    hipLaunchKernelGGL(extract_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, st, bm,
-                       nrows, BP.W, rowoff, csr, csr_row);
     hipLaunchKernelGGL(piece_kernel, dim3((unsigned)((nrows + 255) / 256)), dim3(256), 0, st, cnt,
                        rowoff, poff, nrows, (int)BP.piece, ptab, npieces);
     int4* recs = (int4*)(ws + BP.off_rec[l]);
-    hipLaunchKernelGGL(record_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st, csr,
-                       csr_row, rowoff + nrows, parents + l * lstride,
-                       l > 0 ? parents + (l - 1) * lstride : nullptr, d->T, d->H_kv, d->top_k, Pl,
-                       P.pw[l], CR, P.cr_log2, recs,
+    hipLaunchKernelGGL(record_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
+                       parents + l * lstride, l > 0 ? parents + (l - 1) * lstride : nullptr, bm, wpre,
+                       rowoff, d->T, d->H_kv, d->top_k, Pl, BP.W, P.pw[l], CR, P.cr_log2, ent, recs,
                        BP.use_ds ? (int4*)(ws + BP.off_emap[l]) : nullptr);
     DkvArgs a;
     memset(&a, 0, sizeof(a));
