@@ -23,11 +23,12 @@
 //            RoPE row and softmax state are staged into LDS by asynchronous
 //            copies one entry ahead; partial dK/dV per piece; stores each
 //            entry's dS for the dq pass.
-//   reduce   sums each tile's pieces in piece order into the level's dK/dV.
+//   reduce   sums each tile's pieces (fixed order) into the level's dK/dV and
+//            adds the mean-pool backward of the level above,
+//            dK_l[child] += dK_{l+1}[parent] / n_children (levels run top-down).
 //   dq       one wave per query group over all levels (Q-stationary), from
 //            the stored dS (or recomputing the scores when the stored dS
 //            would exceed its memory budget).
-//   pool     dK_{l-1}[child] += dK_l[parent] / n_children, top-down.
 #include <string.h>
 
 #include "htree_common.h"
@@ -829,51 +830,55 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   }
 }
 
-// sums the pieces of each tile in order into dK_l / dV_l [B, N, Hkv, D]
+// dK_l / dV_l [B, N, Hkv, D] of one level: the pieces of each tile are summed
+// (pieces k = first + c + LG i by lane group c, the LG sums then added in a
+// fixed order: deterministic), plus the mean-pool backward of the level above,
+// dK_{l+1}[parent] / n_children(parent), when there is one.  A block covers
+// 256 / LG consecutive values of one (row, tile) partial [k|v][child][d]; LG
+// follows the level's pieces per row.
+template <int LG>
 __global__ __launch_bounds__(256) void dkv_reduce_kernel(const float* __restrict__ partial,
                                                          const int32_t* __restrict__ poff, int64_t N,
                                                          int Hkv, int D, int CR, int crlg, int tpp,
-                                                         int64_t Pl, int64_t total,
+                                                         int64_t Pl, const float* __restrict__ upk,
+                                                         const float* __restrict__ upv, int64_t Nup,
                                                          float* __restrict__ dk, float* __restrict__ dv) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= total) return;
-  const int dd = (int)(idx % D);
-  int64_t r = idx / D;
-  const int h = (int)(r % Hkv);
-  r /= Hkv;
-  const int64_t node = r % N;
-  const int64_t b = r / N;
-  const int64_t p = node >> crlg;
-  const int cin = (int)(node & (CR - 1));
-  const int tile = CR >= 16 ? cin >> 4 : 0;
-  const int cand = CR >= 16 ? (cin & 15) : cin;
-  const int64_t row = (b * Hkv + h) * Pl + p;
-  float sk = 0.f, sv = 0.f;
-  for (int32_t k = poff[row]; k < poff[row + 1]; ++k) {
-    const float* pp = partial + (((int64_t)k * tpp + tile) * 16) * D * 2;
-    sk += pp[cand * D + dd];
-    sv += pp[16 * D + cand * D + dd];
+  constexpr int FPB = 256 / LG;  // values per block
+  __shared__ float red[LG][FPB];
+  const int j = threadIdx.x % FPB, c = threadIdx.x / FPB;
+  const int bpt = 32 * D / FPB;  // blocks per (row, tile)
+  const int64_t rt = blockIdx.x / bpt;
+  const int f = (int)(blockIdx.x % bpt) * FPB + j;  // value within the tile's partial
+  const int kv = f / (16 * D);
+  const int cand = (f / D) & 15;
+  const int dd = f % D;
+  const int tile = (int)(rt % tpp);
+  const int64_t row = rt / tpp;
+  const int64_t p = row % Pl;
+  const int64_t bh = row / Pl;
+  const int h = (int)(bh % Hkv);
+  const int64_t b = bh / Hkv;
+  const int cin = (CR >= 16 ? tile * 16 : 0) + cand;
+  const int64_t node = (p << crlg) + cin;
+  const float* src = partial + f;
+  float acc = 0.f;
+  for (int32_t k = poff[row] + c; k < poff[row + 1]; k += LG)
+    acc += src[((int64_t)k * tpp + tile) * 16 * D * 2];
+  if (LG > 1) {
+    red[c][j] = acc;
+    __syncthreads();
+    if (c != 0) return;
+    acc = red[0][j];
+#pragma unroll
+    for (int i = 1; i < LG; ++i) acc += red[i][j];
   }
-  dk[idx] = sk;
-  dv[idx] = sv;
-}
-
-// dK_{l-1}[child] += dK_l[parent] / n_children(parent)
-__global__ __launch_bounds__(256) void pool_bwd_kernel(const float* __restrict__ gp, float* __restrict__ gc,
-                                                       int64_t Nc, int64_t Np, int Hkv, int D, int CR,
-                                                       int64_t total) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= total) return;
-  const int dd = (int)(idx % D);
-  int64_t r = idx / D;
-  const int h = (int)(r % Hkv);
-  r /= Hkv;
-  const int64_t c = r % Nc;
-  const int64_t b = r / Nc;
-  const int64_t p = c / CR;
-  const int64_t s0 = p * CR;
-  const int64_t cnt = (s0 + CR < Nc ? s0 + CR : Nc) - s0;
-  gc[idx] += gp[((b * Np + p) * Hkv + h) * D + dd] / (float)cnt;
+  if (cin >= CR || node >= N) return;
+  const float* up = kv ? upv : upk;
+  if (up) {
+    const int64_t cnt = (p + 1) * CR < N ? CR : N - p * CR;
+    acc += up[((b * Nup + p) * Hkv + h) * D + dd] / (float)cnt;
+  }
+  (kv ? dv : dk)[((b * N + node) * Hkv + h) * D + dd] = acc;
 }
 
 // ---------------------------------------------------------------- dq
@@ -1368,10 +1373,24 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
                        st, a);
     float* dkl = l == 0 ? dk : (float*)(ws + BP.off_dk[l]);
     float* dvl = l == 0 ? dv : (float*)(ws + BP.off_dv[l]);
-    const int64_t tot = (int64_t)d->B * P.N[l] * d->H_kv * d->D;
-    hipLaunchKernelGGL(dkv_reduce_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st,
-                       partial, poff, P.N[l], d->H_kv, d->D, CR, P.cr_log2, BP.tpp, Pl, tot, dkl,
-                       dvl);
+    const bool top = l == P.L - 1;
+    const float* upk = top ? nullptr : (const float*)(ws + BP.off_dk[l + 1]);
+    const float* upv = top ? nullptr : (const float*)(ws + BP.off_dv[l + 1]);
+    const int64_t nup = top ? 0 : P.N[l + 1];
+    // lane groups per value from the level's mean pieces per row
+    const int64_t avg = lstride / (BP.piece * BP.rows[l]);
+    const int64_t rt = BP.rows[l] * BP.tpp;
+#define HT_RED(LG)                                                                              \
+  hipLaunchKernelGGL(dkv_reduce_kernel<LG>, dim3((unsigned)(rt * 32 * d->D / (256 / LG))),     \
+                     dim3(256), 0, st, partial, poff, P.N[l], d->H_kv, d->D, CR, P.cr_log2,  \
+                     BP.tpp, Pl, upk, upv, nup, dkl, dvl)
+    if (avg >= 64)
+      HT_RED(16);
+    else if (avg >= 8)
+      HT_RED(4);
+    else
+      HT_RED(1);
+#undef HT_RED
   }
   // dq over all levels
   if (BP.use_ds) {
@@ -1435,18 +1454,6 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.scale = scale;
     hipLaunchKernelGGL((dq_kernel<D, PREC, T>), dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, st,
                        a);
-  }
-  // mean-pool backward, top-down
-  for (int l = P.L - 1; l >= 1; --l) {
-    const float* gpk = (const float*)(ws + BP.off_dk[l]);
-    const float* gpv = (const float*)(ws + BP.off_dv[l]);
-    float* gck = l - 1 == 0 ? dk : (float*)(ws + BP.off_dk[l - 1]);
-    float* gcv = l - 1 == 0 ? dv : (float*)(ws + BP.off_dv[l - 1]);
-    const int64_t tot = (int64_t)d->B * P.N[l - 1] * d->H_kv * d->D;
-    hipLaunchKernelGGL(pool_bwd_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, gpk,
-                       gck, P.N[l - 1], P.N[l], d->H_kv, d->D, CR, tot);
-    hipLaunchKernelGGL(pool_bwd_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, gpv,
-                       gcv, P.N[l - 1], P.N[l], d->H_kv, d->D, CR, tot);
   }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? HTREE_OK : (int)e;
