@@ -39,6 +39,19 @@ WORKLOADS = {
 }
 
 
+def measured_traffic(workload: str):
+    """HBM bytes per launch of the fused forward kernel from the committed
+    rocprofv3 PMC summary of this workload (FETCH_SIZE + WRITE_SIZE, each
+    scaled by the same counter's reading of the calibration copy), or None."""
+    path = os.path.join(ROOT, "profiles", f"fwd_reg_kernel_{workload.lower()}_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return {"bytes": rec["traffic_bytes_per_launch"], "source": os.path.relpath(path, ROOT)}
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -169,7 +182,18 @@ def main():
     torch.cuda.synchronize()
     kern_ms = k0.elapsed_time(k1) / args.kernel_iters
 
+    # Calibration copy for the PMC traffic measurement (outside every timed
+    # region): 256 MiB read + 256 MiB written by torch's copy kernel, so that a
+    # `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE` run of this script measures
+    # the counters' scale on a transfer of known size.
+    cal_src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+    cal_dst = torch.empty_like(cal_src)
+    cal_dst.copy_(cal_src)
+    torch.cuda.synchronize()
+    del cal_src, cal_dst
+
     w = work(B, T, H, Hkv, D, CR, TK, MTN, 2)
+    traffic = measured_traffic(args.workload)
     achieved = w.fwd_kernel_bytes / (kern_ms * 1e-3)
     fwd_tok = B * T / (fwd_ms * 1e-3)
     step_s = (fwd_ms + (bwd_ms or 0.0)) * 1e-3
@@ -200,13 +224,14 @@ def main():
             "algorithmic_bytes": w.bwd_bytes},
         "wall_ms_per_step": step_ms,
         "roofline": {
-            "kernel": "htree::fwd_kernel (fused forward, all levels)",
+            "kernel": "htree::fwd_reg_kernel (fused forward, all levels)",
             "bound": "hbm",
             "achieved": achieved / 1e9,
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK,
-            "traffic": None,
+            "traffic": traffic["bytes"] if traffic else None,
+            "traffic_source": traffic["source"] if traffic else None,
             "algorithmic_bytes_per_launch": w.fwd_kernel_bytes,
             "avg_launch_ms": kern_ms,
         },
