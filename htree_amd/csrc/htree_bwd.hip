@@ -732,7 +732,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const bool v = ok && 4 * kg + r < G;
-        pr[r] = v ? __builtin_amdgcn_exp2f((S[r] - gm[r]) * kLog2e) / gs[r] : 0.f;
+        // 1/gsum by v_rcp_f32 (<= 1 ulp) instead of an IEEE division per value
+        pr[r] = v ? __builtin_amdgcn_exp2f((S[r] - gm[r]) * kLog2e) * __builtin_amdgcn_rcpf(gs[r]) : 0.f;
         ds[r] = pr[r] * (dP[r] - dl[r]);
       }
     }
@@ -957,6 +958,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   DoFrag<D, TIn>::load((const TIn*)a.dO + hq * D, kg, gv, dh, dlo);
   const float gm = gv ? a.gmax[hq] : 0.f;
   const float gs = gv ? a.gsum[hq] : 1.f;
+  const float inv_gs = __builtin_amdgcn_rcpf(gs);
   const float dl = gv ? a.delta[hq] : 0.f;
   f32x4(*AC)[64] = acc_l[wv];
 #pragma unroll
@@ -1050,7 +1052,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
         const int cu = 4 * kg + r;
         const int pos = wide ? (tau << 4) + cu : (tau << crlg) + cu;
         const bool v = gv && cu < CRU && pos < nc && !((sw >> (((tau << 4) + cu) & 31)) & 1u);
-        const float pr = v ? __builtin_amdgcn_exp2f((S[r] - gm) * kLog2e) / gs : 0.f;
+        const float pr = v ? __builtin_amdgcn_exp2f((S[r] - gm) * kLog2e) * inv_gs : 0.f;
         ds[r] = pr * (dP[r] - dl);
         anyv |= v;
       }
