@@ -29,6 +29,7 @@ DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 EXPORTS = (
     "htree_strerror", "htree_levels", "htree_tree_workspace_bytes", "htree_tree_build",
     "htree_forward", "htree_backward_workspace_bytes", "htree_backward",
+    "htree_train_scores_bytes", "htree_forward_train", "htree_backward_train",
 )
 
 
@@ -66,11 +67,20 @@ def lib() -> ctypes.CDLL:
     L.htree_tree_build.argtypes = [DP, P, P, ctypes.POINTER(P), ctypes.POINTER(P), P, P, P, I64, P]
     L.htree_forward.restype = ctypes.c_int
     L.htree_forward.argtypes = [DP, F, P, P, I64, P, P, P, P, P, P, P]
+    if hasattr(L, "htree_forward_train"):
+        L.htree_train_scores_bytes.restype = ctypes.c_int
+        L.htree_train_scores_bytes.argtypes = [DP, ctypes.POINTER(I64)]
+        L.htree_forward_train.restype = ctypes.c_int
+        L.htree_forward_train.argtypes = [DP, F, P, P, I64, P, P, P, P, P, P, P, I64, P]
     if hasattr(L, "htree_backward"):
         L.htree_backward_workspace_bytes.restype = ctypes.c_int
         L.htree_backward_workspace_bytes.argtypes = [DP, ctypes.POINTER(I64)]
         L.htree_backward.restype = ctypes.c_int
         L.htree_backward.argtypes = [DP, F, P, P, P, P, P, P, P, I64, P, P, P, P, P, P, I64, P]
+    if hasattr(L, "htree_backward_train"):
+        L.htree_backward_train.restype = ctypes.c_int
+        L.htree_backward_train.argtypes = [DP, F, P, P, P, P, P, P, P, I64, P, P, P, I64, P, P, P,
+                                           P, I64, P]
     _lib = L
     return L
 
@@ -109,6 +119,17 @@ def tree_workspace_bytes(d: HtreeDims) -> int:
     b = ctypes.c_int64()
     check(lib().htree_tree_workspace_bytes(ctypes.byref(d), ctypes.byref(b)),
           "htree_tree_workspace_bytes")
+    return int(b.value)
+
+
+def train_scores_bytes(d: HtreeDims) -> int:
+    """Bytes of the score buffer the training forward keeps for the backward
+    (0: this configuration rebuilds the scores in the backward)."""
+    if not hasattr(lib(), "htree_train_scores_bytes"):
+        return 0
+    b = ctypes.c_int64()
+    check(lib().htree_train_scores_bytes(ctypes.byref(d), ctypes.byref(b)),
+          "htree_train_scores_bytes")
     return int(b.value)
 
 

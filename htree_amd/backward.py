@@ -43,6 +43,8 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
         rope_base = bwd_ctx.get("rope_base", 10000.0)
         _, _, ws, cos, sin = build_tree(k, v, d, d.rope_rows, rope_base)
     parents = bwd_ctx.get("parents_stacked")
+    # the training forward's stored scores go with its own parent lists
+    scores = bwd_ctx.get("train_scores") if parents is not None else None
     if parents is None:
         plp = bwd_ctx.get("per_layer_parents")
         if plp is not None:
@@ -63,12 +65,20 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
             "htree_backward_workspace_bytes")
     bws = torch.empty(nb.value, dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
-        rc = N.lib().htree_backward(
-            d, float(scale), N.ptr(q), N.ptr(output), N.ptr(dO), N.ptr(bwd_ctx["global_max"]),
-            N.ptr(bwd_ctx["global_sum"]), N.ptr(parents), N.ptr(ws), ws.numel(), N.ptr(cos),
-            N.ptr(sin), N.ptr(dq), N.ptr(dk), N.ptr(dv), N.ptr(bws), bws.numel(),
-            N.stream_ptr(dev))
-        N.check(rc, "htree_backward")
+        if scores is not None:
+            rc = N.lib().htree_backward_train(
+                d, float(scale), N.ptr(q), N.ptr(output), N.ptr(dO), N.ptr(bwd_ctx["global_max"]),
+                N.ptr(bwd_ctx["global_sum"]), N.ptr(parents), N.ptr(ws), ws.numel(), N.ptr(cos),
+                N.ptr(sin), N.ptr(scores), scores.numel(), N.ptr(dq), N.ptr(dk), N.ptr(dv),
+                N.ptr(bws), bws.numel(), N.stream_ptr(dev))
+            N.check(rc, "htree_backward_train")
+        else:
+            rc = N.lib().htree_backward(
+                d, float(scale), N.ptr(q), N.ptr(output), N.ptr(dO), N.ptr(bwd_ctx["global_max"]),
+                N.ptr(bwd_ctx["global_sum"]), N.ptr(parents), N.ptr(ws), ws.numel(), N.ptr(cos),
+                N.ptr(sin), N.ptr(dq), N.ptr(dk), N.ptr(dv), N.ptr(bws), bws.numel(),
+                N.stream_ptr(dev))
+            N.check(rc, "htree_backward")
     return dq, dk, dv
 
 
@@ -84,7 +94,8 @@ class HTreeTritonFunction(torch.autograd.Function):
                                      _save_parents=True)
         ctx.save_for_backward(q, k, v, out, bwd_ctx["global_max"], bwd_ctx["global_sum"],
                               bwd_ctx["cos_cache"], bwd_ctx["sin_cache"],
-                              bwd_ctx["parents_stacked"], bwd_ctx["packed_tree"])
+                              bwd_ctx["parents_stacked"], bwd_ctx["packed_tree"],
+                              bwd_ctx["train_scores"])
         ctx.meta = dict(num_layers=bwd_ctx["num_layers"], compression_rate=compression_rate,
                         top_k_per_layer=top_k_per_layer, max_top_nodes=max_top_nodes,
                         scale=bwd_ctx["scale"], dims=bwd_ctx["dims"], rope_base=rope_base)
@@ -92,9 +103,10 @@ class HTreeTritonFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dO):
-        q, k, v, out, gmax, gsum, cos, sin, parents, ws = ctx.saved_tensors
+        q, k, v, out, gmax, gsum, cos, sin, parents, ws, scores = ctx.saved_tensors
         bwd_ctx = dict(ctx.meta, global_max=gmax, global_sum=gsum, layers_k=[k], layers_v=[v],
-                       cos_cache=cos, sin_cache=sin, parents_stacked=parents, packed_tree=ws)
+                       cos_cache=cos, sin_cache=sin, parents_stacked=parents, packed_tree=ws,
+                       train_scores=scores)
         dq, dk, dv = htree_backward(dO, q, out, bwd_ctx)
         return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None
 

@@ -384,7 +384,7 @@ __global__ __launch_bounds__(256) void piece_kernel(const int32_t* __restrict__ 
 
 // One lane per (query group, slot s): the entry of (parent p's row, t) is
 // found from the row bitmap's word prefix, and gets the rotation row
-// rho = n_c - 1 - s CR and the mask of p's children that t accumulates at
+// rho = n_c - 1 - s CR (low 16 bits, the slot s above them) and the mask of p's children that t accumulates at
 // this level (valid positions, not passed to level l-1).  A query group's
 // TK slots are TK consecutive lanes of one wave; its next-level list is read
 // by shuffles.  emap (nullable) maps (query group, slot) to {entry, mask}.
@@ -426,7 +426,7 @@ __global__ __launch_bounds__(256) void record_kernel(const int32_t* __restrict__
   const int64_t row = (b * Hkv + h) * Pl + p;
   const int64_t wi = row * W + (t >> 5);
   const int e = rowoff[row] + wpre[wi] + __popc(bm[wi] & ((1u << (t & 31)) - 1u));
-  rec[e] = make_int4(t, nc - 1 - (s << crlg), (int)(uint32_t)m, (int)(uint32_t)(m >> 32));
+  rec[e] = make_int4(t, (nc - 1 - (s << crlg)) | (s << 16), (int)(uint32_t)m, (int)(uint32_t)(m >> 32));
   if (emap) emap[idx] = make_int4(e, (int)(uint32_t)m, (int)(uint32_t)(m >> 32), 0);
 }
 
@@ -442,8 +442,10 @@ struct DkvArgs {
   const float *cosb, *sinb;
   float* partial;
   uint16_t* ds;  // nullable: dS per (entry, tile) for the dq pass
+  const uint16_t* sc;  // level's stored scores (fp16 S - m_ref) [groups][max_tiles][256]
+  const float* smref;  // level's m_ref [groups][16]
   int64_t N, Np, pw, Pl, BTH;  // BTH = B*T*H (length of gmax / gsum / delta)
-  int32_t T, H, Hkv, G, CR, crlg, TK, tpp;
+  int32_t T, H, Hkv, G, CR, crlg, TK, tpp, max_tiles;
   float scale;
 };
 
@@ -460,8 +462,9 @@ struct Stage {
   static constexpr int ROWB = 16 * RP;
   static constexpr int OFF_DO = ROWB;
   static constexpr int OFF_TAB = 2 * ROWB;          // cos [D/2] then sin [D/2]
-  static constexpr int OFF_SM = OFF_TAB + D * 4;    // gmax[16], gsum[16], delta[16], pad
-  static constexpr int BYTES = OFF_SM + 256;
+  static constexpr int OFF_SM = OFF_TAB + D * 4;    // gmax[16], gsum[16], delta[16], m_ref[16]
+  static constexpr int OFF_SC = OFF_SM + 256;       // stored scores of the tile (fp16, 512 B)
+  static constexpr int BYTES = OFF_SC + 512;
   static constexpr int SLOTS = BYTES * 2 <= 20 * 1024 ? 2 : 1;  // double-buffer if it fits
 };
 
@@ -485,9 +488,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int
 
 // Asynchronous copies of one entry's inputs into `slot` (buffer loads into
 // LDS: the bases live in scalar registers, the lanes hold 32-bit offsets).
-template <int D, typename TIn>
-__device__ __forceinline__ void stage_issue(char* slot, const DkvArgs& a, int64_t hq0, int rho,
-                                            int lane) {
+template <int D, typename TIn, bool HAS_S>
+__device__ __forceinline__ void stage_issue(char* slot, const DkvArgs& a, int64_t grp, int rs,
+                                            int tile, int lane) {
+  const int64_t hq0 = grp * a.G;
+  const int rho = rs & 0xffff;
   using St = Stage<D, TIn>;
   constexpr int HALF = D / 2;
   constexpr int ES = (int)sizeof(TIn);
@@ -529,6 +534,16 @@ __device__ __forceinline__ void stage_issue(char* slot, const DkvArgs& a, int64_
                                              (lds_void*)(slot + St::OFF_SM + 64), 4, i, 0, 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(a.delta + hq0, G * 4),
                                              (lds_void*)(slot + St::OFF_SM + 128), 4, i, 0, 0, 0);
+    if (HAS_S)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(a.smref + grp * 16, 64),
+                                               (lds_void*)(slot + St::OFF_SM + 192), 4, lane * 4, 0,
+                                               0, 0);
+  }
+  if (HAS_S && lane < 32) {
+    const int tau = (rs >> 16) * a.tpp + tile;  // the forward's tile index
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        buf_rsrc(a.sc + (grp * a.max_tiles + tau) * 256, 512), (lds_void*)(slot + St::OFF_SC), 16,
+        lane * 16, 0, 0, 0);
   }
 }
 
@@ -611,7 +626,7 @@ struct DoRow<D, __bf16> {
   }
 };
 
-template <int D, bool PREC, typename TIn>
+template <int D, bool PREC, typename TIn, bool HAS_S>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void dkv_kernel(const DkvArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
   using St = Stage<D, TIn>;
@@ -642,8 +657,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   bf16x8 kh[KS], kl[KS], vh[KS], vl[KS];
   {
     const int64_t r = (bh * a.Np + node0 + (u16 < CRU ? u16 : 0)) * D;
-    load_frag<D>(a.kh + r, kg, kh);
-    load_frag<D>(a.kl + r, kg, kl);
+    if (!HAS_S) {  // K~ only rebuilds the scores
+      load_frag<D>(a.kh + r, kg, kh);
+      load_frag<D>(a.kl + r, kg, kl);
+    }
     load_frag<D>(a.vr_h + r, kg, vh);
     if (PREC) load_frag<D>(a.vr_l + r, kg, vl);
   }
@@ -651,7 +668,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
 #pragma unroll
   for (int n = 0; n < ND; ++n) dv[n] = dk[n] = f32x4{0.f, 0.f, 0.f, 0.f};
   const bool gv = u16 < G;
-  auto hq0_of = [&](int t) { return ((b * a.T + t) * a.Hkv + h) * (int64_t)G; };
+  auto grp_of = [&](int t) { return (b * a.T + t) * a.Hkv + h; };
 
   // The piece's records are held 64 at a time in the lanes (lane i = entry
   // base + i) with a ballot of the entries whose tile mask is not empty;
@@ -687,26 +704,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   auto step = [&](const char* __restrict__ S0, char* __restrict__ nxt, const int4 rc, const int en,
                   const int4 rn) __attribute__((always_inline)) {
     wait_stage();
-    if (nxt && en < ne) stage_issue<D, TIn>(nxt, a, hq0_of(rn.x), rn.y, lane);
+    if (nxt && en < ne) stage_issue<D, TIn, HAS_S>(nxt, a, grp_of(rn.x), rn.y, tile, lane);
     const float* tab = (const float*)(S0 + St::OFF_TAB);  // cos [HALF], sin [HALF]
     const float* sm = (const float*)(S0 + St::OFF_SM);    // gmax, gsum, delta [16 each]
     const bool ok = (tile_mask(rc) >> u16) & 1u;
 
-    // rotated query fragment (lane g = u16); the score scale is applied to S
-    // (heads past the group hold finite filler: their P and dS are zeroed below)
-    float qr[KS][8];
-    row_frag<D, TIn>(S0, u16, kg, qr);
-    rot_by_fr<D>(qr, tab, tab + HALF, kg);
-    bf16x8 qh[KS], ql[KS];
-    split_frag<D>(qr, qh, ql);
     f32x4 S = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (HAS_S) {
+      // scores stored by the forward: fp16 S - m_ref, tile laid out
+      // S[head][cand] (16 x 16).  One transposing read with lane i of group
+      // kg addressing the 8-byte piece i of the group's 128 bytes (heads
+      // 4kg..4kg+3, candidates 4 (i % 4)..+3 of head 4kg + i / 4) gives lane
+      // m heads 4kg..4kg+3 of candidate m.
+      const char* p = S0 + St::OFF_SC + lane * 8;
+      const s16x4 sv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(const __attribute__((address_space(3))) void*)p);
+      const float4 mr = *(const float4*)(sm + 48 + 4 * kg);
+      // (bit_cast the whole vector: bit_cast of one ext-vector element reads
+      // element 0 with this compiler)
+      typedef __attribute__((ext_vector_type(4))) _Float16 h16x4;
+      const h16x4 hv = __builtin_bit_cast(h16x4, sv);
+      S[0] = (float)hv[0] + mr.x;
+      S[1] = (float)hv[1] + mr.y;
+      S[2] = (float)hv[2] + mr.z;
+      S[3] = (float)hv[3] + mr.w;
+    } else {
+      // rotated query fragment (lane g = u16); the score scale is applied to S
+      // (heads past the group hold finite filler: their P and dS are zeroed below)
+      float qr[KS][8];
+      row_frag<D, TIn>(S0, u16, kg, qr);
+      rot_by_fr<D>(qr, tab, tab + HALF, kg);
+      bf16x8 qh[KS], ql[KS];
+      split_frag<D>(qr, qh, ql);
 #pragma unroll
-    for (int m = 0; m < KS; ++m) {
-      S = mma32(qh[m], kh[m], S);
-      S = mma32(qh[m], kl[m], S);
-      S = mma32(ql[m], kh[m], S);
+      for (int m = 0; m < KS; ++m) {
+        S = mma32(qh[m], kh[m], S);
+        S = mma32(qh[m], kl[m], S);
+        S = mma32(ql[m], kh[m], S);
+      }
+      S *= a.scale;
     }
-    S *= a.scale;
     // dP[g][cand] = dO[g] . V[cand]
     f32x4 dP = {0.f, 0.f, 0.f, 0.f};
     {
@@ -783,7 +820,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
       }
     }
   };
-  if (e < ne) stage_issue<D, TIn>(stage_a[wv], a, hq0_of(rc.x), rc.y, lane);
+  if (e < ne) stage_issue<D, TIn, HAS_S>(stage_a[wv], a, grp_of(rc.x), rc.y, tile, lane);
   if constexpr (St::SLOTS == 2) {
     while (e < ne) {
       int en = next_work(e + 1);
@@ -805,7 +842,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
       step(stage_a[wv], nullptr, rc, en, rn);
       if (en < ne) {
         wave_sync();  // every lane has read the slot
-        stage_issue<D, TIn>(stage_a[wv], a, hq0_of(rn.x), rn.y, lane);
+        stage_issue<D, TIn, HAS_S>(stage_a[wv], a, grp_of(rn.x), rn.y, tile, lane);
       }
       e = en;
       rc = rn;
@@ -1289,8 +1326,11 @@ template <int D, bool PREC, typename T>
 static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const void* q,
                       const void* out, const void* dO, const float* gmax, const float* gsum,
                       const int32_t* parents, const char* tws, const float* cosb, const float* sinb,
-                      float* dq, float* dk, float* dv, char* ws, hipStream_t st) {
+                      const char* scores, float* dq, float* dk, float* dv, char* ws,
+                      hipStream_t st) {
   const Plan& P = BP.P;
+  int64_t off_mref = 0;
+  train_scores_bytes(d, P, &off_mref);
   const int64_t BH = (int64_t)d->B * d->H_kv;
   const int64_t groups = (int64_t)d->B * d->T * d->H_kv;
   const int G = BP.G;
@@ -1369,10 +1409,18 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.crlg = P.cr_log2;
     a.TK = d->top_k;
     a.tpp = BP.tpp;
+    a.max_tiles = P.max_tiles;
     a.scale = scale;
     const int64_t waves = BP.max_pieces * BP.tpp;
-    hipLaunchKernelGGL((dkv_kernel<D, PREC, T>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
-                       st, a);
+    if (!PREC && scores) {
+      a.sc = (const uint16_t*)scores + (int64_t)l * groups * P.max_tiles * 256;
+      a.smref = (const float*)(scores + off_mref) + (int64_t)l * groups * 16;
+      hipLaunchKernelGGL((dkv_kernel<D, PREC, T, true>), dim3((unsigned)((waves + 3) / 4)),
+                         dim3(256), 0, st, a);
+    } else {
+      hipLaunchKernelGGL((dkv_kernel<D, PREC, T, false>), dim3((unsigned)((waves + 3) / 4)),
+                         dim3(256), 0, st, a);
+    }
     float* dkl = l == 0 ? dk : (float*)(ws + BP.off_dk[l]);
     float* dvl = l == 0 ? dv : (float*)(ws + BP.off_dv[l]);
     const bool top = l == P.L - 1;
@@ -1476,11 +1524,14 @@ int htree_backward_workspace_bytes(const htree_dims* d, int64_t* bytes) {
   return HTREE_OK;
 }
 
-int htree_backward(const htree_dims* d, float scale, const void* q, const void* out,
-                   const void* dO, const float* gmax, const float* gsum, const int32_t* parents,
-                   const void* tree_ws, int64_t tree_ws_bytes, const float* cos_table,
-                   const float* sin_table, float* dq, float* dk, float* dv, void* bwd_ws,
-                   int64_t bwd_ws_bytes, void* stream) {
+}  // extern "C"
+
+static int backward_impl(const htree_dims* d, float scale, const void* q, const void* out,
+                         const void* dO, const float* gmax, const float* gsum,
+                         const int32_t* parents, const void* tree_ws, int64_t tree_ws_bytes,
+                         const float* cos_table, const float* sin_table, const void* scores_ws,
+                         int64_t scores_bytes, float* dq, float* dk, float* dv, void* bwd_ws,
+                         int64_t bwd_ws_bytes, void* stream) {
   BwdPlan BP;
   int rc = make_bwd_plan(d, &BP);
   if (rc) return rc;
@@ -1488,12 +1539,15 @@ int htree_backward(const htree_dims* d, float scale, const void* q, const void* 
       !dq || !dk || !dv || !bwd_ws)
     return HTREE_ENULL;
   if (tree_ws_bytes < BP.P.bytes || bwd_ws_bytes < BP.bytes) return HTREE_EWORKSPACE;
+  const int64_t sbytes = train_scores_bytes(d, BP.P, nullptr);
+  const char* scores = sbytes > 0 ? (const char*)scores_ws : nullptr;
+  if (scores && scores_bytes < sbytes) return HTREE_EWORKSPACE;
   hipStream_t st = (hipStream_t)stream;
   const char* tws = (const char*)tree_ws;
   char* ws = (char*)bwd_ws;
 #define HT_BWD(DD, PR, TT)                                                                      \
   return backward_t<DD, PR, TT>(d, BP, scale, q, out, dO, gmax, gsum, parents, tws, cos_table, \
-                                sin_table, dq, dk, dv, ws, st)
+                                sin_table, scores, dq, dk, dv, ws, st)
   if (d->D == 128) {
     if (d->dtype == HTREE_BF16) HT_BWD(128, false, __bf16);
     if (d->dtype == HTREE_F16) HT_BWD(128, true, _Float16);
@@ -1504,6 +1558,28 @@ int htree_backward(const htree_dims* d, float scale, const void* q, const void* 
     HT_BWD(64, true, float);
   }
 #undef HT_BWD
+}
+
+extern "C" {
+
+int htree_backward(const htree_dims* d, float scale, const void* q, const void* out,
+                   const void* dO, const float* gmax, const float* gsum, const int32_t* parents,
+                   const void* tree_ws, int64_t tree_ws_bytes, const float* cos_table,
+                   const float* sin_table, float* dq, float* dk, float* dv, void* bwd_ws,
+                   int64_t bwd_ws_bytes, void* stream) {
+  return backward_impl(d, scale, q, out, dO, gmax, gsum, parents, tree_ws, tree_ws_bytes,
+                       cos_table, sin_table, nullptr, 0, dq, dk, dv, bwd_ws, bwd_ws_bytes, stream);
+}
+
+int htree_backward_train(const htree_dims* d, float scale, const void* q, const void* out,
+                         const void* dO, const float* gmax, const float* gsum,
+                         const int32_t* parents, const void* tree_ws, int64_t tree_ws_bytes,
+                         const float* cos_table, const float* sin_table, const void* scores,
+                         int64_t scores_bytes, float* dq, float* dk, float* dv, void* bwd_ws,
+                         int64_t bwd_ws_bytes, void* stream) {
+  return backward_impl(d, scale, q, out, dO, gmax, gsum, parents, tree_ws, tree_ws_bytes,
+                       cos_table, sin_table, scores, scores_bytes, dq, dk, dv, bwd_ws,
+                       bwd_ws_bytes, stream);
 }
 
 }  // extern "C"

@@ -40,6 +40,22 @@ struct Plan {
 
 int make_plan(const htree_dims* d, Plan* p);
 
+// Score buffer written by the training forward for the backward (bf16 inputs,
+// levels of <= 16 candidate tiles): per level, query group and candidate tile
+// 256 fp16 values S - m_ref laid out S[head][cand] (16 x 16), then per level
+// and query group the 16 fp32 m_ref (the head's running max after the
+// level).  0 bytes otherwise.
+inline int64_t train_scores_bytes(const htree_dims* d, const Plan& P, int64_t* off_mref) {
+  const int64_t groups = (int64_t)d->B * d->T * d->H_kv;
+  if (d->dtype != HTREE_BF16 || P.max_tiles > 16) {
+    if (off_mref) *off_mref = 0;
+    return 0;
+  }
+  const int64_t sc = (int64_t)P.L * groups * P.max_tiles * 512;
+  if (off_mref) *off_mref = sc;
+  return sc + (int64_t)P.L * groups * 64;
+}
+
 // ---------------------------------------------------------------- device
 __device__ __forceinline__ f32x4 mma32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);

@@ -44,9 +44,11 @@ struct FwdArgs {
   float* gmax;
   float* gsum;
   int32_t* parents;
+  uint16_t* scores;  // nullable: fp16 S - m_ref per (level, group, tile) for the backward
+  float* smref;      // m_ref per (level, group, head)
   const float* cosb;
   const float* sinb;
-  int32_t B, T, H, Hkv, G, CR, crlg, TK, L;
+  int32_t B, T, H, Hkv, G, CR, crlg, TK, L, max_tiles;
   float scale;
   int32_t per_xcd;
 };
@@ -664,6 +666,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     }
     const float mnew = fmaxf(m_run, gmx);
     const float mref = mnew == -INFINITY ? 0.f : mnew;
+    if (a.scores) {
+      // every tile's scores relative to the head's running max, for the
+      // backward (the accumulated ones are <= 0 there; fp16 RNE)
+      const int64_t lg = (int64_t)l * a.B * a.T * a.Hkv + ((int64_t)b * a.T + t) * a.Hkv + h;
+      // tile layout S[head][cand] (fp16, 16 x 16): this lane's candidates
+      // 4kg..4kg+3 of head u16
+      uint16_t* so = a.scores + lg * a.max_tiles * 256 + u16 * 16 + kg * 4;
+      for (int tau = 0; tau < nt; ++tau) {
+        const f32x4 S = W.st[tau][lane];
+        uint32_t hb[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) hb[r] = __builtin_bit_cast(uint16_t, (_Float16)(S[r] - mref));
+        *(uint2*)(so + tau * 256) = make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
+      }
+      if (kg == 0) a.smref[lg * 16 + u16] = mref;
+    }
     const float alpha = __builtin_amdgcn_exp2f((m_run - mref) * kLog2e);
     m_run = mnew;
     l_part *= alpha;
@@ -757,15 +775,19 @@ static void launch_fwd_d(int dtype, const FwdArgs& a, int max_tiles, dim3 grid, 
 
 using namespace htree;
 
-extern "C" int htree_forward(const htree_dims* d, float scale, const void* q,
-                             const void* tree_ws, int64_t tree_ws_bytes,
-                             const float* cos_table, const float* sin_table, void* out,
-                             float* gmax, float* gsum, int32_t* parents, void* stream) {
+static int forward_impl(const htree_dims* d, float scale, const void* q, const void* tree_ws,
+                        int64_t tree_ws_bytes, const float* cos_table, const float* sin_table,
+                        void* out, float* gmax, float* gsum, int32_t* parents, void* scores,
+                        int64_t scores_bytes, void* stream) {
   Plan P;
   int rc = make_plan(d, &P);
   if (rc) return rc;
   if (!q || !tree_ws || !cos_table || !sin_table || !out || !gmax || !gsum) return HTREE_ENULL;
   if (tree_ws_bytes < P.bytes) return HTREE_EWORKSPACE;
+  int64_t off_mref = 0;
+  const int64_t sbytes = train_scores_bytes(d, P, &off_mref);
+  if (scores && sbytes == 0) scores = nullptr;  // this configuration recomputes in the backward
+  if (scores && scores_bytes < sbytes) return HTREE_EWORKSPACE;
   FwdArgs a;
   memset(&a, 0, sizeof(a));
   const char* base = (const char*)tree_ws;
@@ -783,6 +805,9 @@ extern "C" int htree_forward(const htree_dims* d, float scale, const void* q,
   a.gmax = gmax;
   a.gsum = gsum;
   a.parents = parents;
+  a.scores = (uint16_t*)scores;
+  a.smref = scores ? (float*)((char*)scores + off_mref) : nullptr;
+  a.max_tiles = P.max_tiles;
   a.cosb = cos_table;
   a.sinb = sin_table;
   a.B = d->B;
@@ -808,4 +833,31 @@ extern "C" int htree_forward(const htree_dims* d, float scale, const void* q,
     launch_fwd_d<64>(d->dtype, a, P.max_tiles, grid, st);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? HTREE_OK : (int)e;
+}
+
+extern "C" int htree_forward(const htree_dims* d, float scale, const void* q,
+                             const void* tree_ws, int64_t tree_ws_bytes,
+                             const float* cos_table, const float* sin_table, void* out,
+                             float* gmax, float* gsum, int32_t* parents, void* stream) {
+  return forward_impl(d, scale, q, tree_ws, tree_ws_bytes, cos_table, sin_table, out, gmax, gsum,
+                      parents, nullptr, 0, stream);
+}
+
+extern "C" int htree_train_scores_bytes(const htree_dims* d, int64_t* bytes) {
+  Plan P;
+  int rc = make_plan(d, &P);
+  if (rc) return rc;
+  if (!bytes) return HTREE_ENULL;
+  *bytes = train_scores_bytes(d, P, nullptr);
+  return HTREE_OK;
+}
+
+extern "C" int htree_forward_train(const htree_dims* d, float scale, const void* q,
+                                   const void* tree_ws, int64_t tree_ws_bytes,
+                                   const float* cos_table, const float* sin_table, void* out,
+                                   float* gmax, float* gsum, int32_t* parents, void* scores,
+                                   int64_t scores_bytes, void* stream) {
+  if (!parents) return HTREE_ENULL;
+  return forward_impl(d, scale, q, tree_ws, tree_ws_bytes, cos_table, sin_table, out, gmax, gsum,
+                      parents, scores, scores_bytes, stream);
 }

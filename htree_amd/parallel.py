@@ -12,8 +12,11 @@ Differences, all deliberate:
     top_k_per_layer * max(compression_rate, 16) / 16 <= 64.
   * the RoPE tables are built on the host with the reference's recipe
     (src/parallel.py:983-988) and copied to the device.
-  * bwd_ctx carries two extra keys, `packed_tree` (the MFMA operand copy of
-    the tree, reused by the backward) and `dims`.
+  * bwd_ctx carries extra keys: `packed_tree` (the MFMA operand copy of the
+    tree, reused by the backward), `dims`, `parents_stacked` and
+    `train_scores` (every candidate tile's scores, fp16 relative to the
+    head's running max, so that the backward does not rebuild them; None
+    where the configuration rebuilds them).
 """
 from __future__ import annotations
 
@@ -116,10 +119,19 @@ def htree_forward(
         save_par = _save_for_backward and _save_parents
         parents = (torch.empty(L, B, T, H_kv, top_k_per_layer, dtype=torch.int32, device=q.device)
                    if save_par else None)
-        rc = N.lib().htree_forward(d, float(scale), N.ptr(q), N.ptr(ws), ws.numel(), N.ptr(cos),
-                                   N.ptr(sin), N.ptr(out), N.ptr(gmax), N.ptr(gsum),
-                                   N.ptr(parents), N.stream_ptr(q.device))
-        N.check(rc, "htree_forward")
+        nsc = N.train_scores_bytes(d) if save_par else 0
+        scores = torch.empty(nsc, dtype=torch.uint8, device=q.device) if nsc > 0 else None
+        if scores is not None:
+            rc = N.lib().htree_forward_train(d, float(scale), N.ptr(q), N.ptr(ws), ws.numel(),
+                                             N.ptr(cos), N.ptr(sin), N.ptr(out), N.ptr(gmax),
+                                             N.ptr(gsum), N.ptr(parents), N.ptr(scores), nsc,
+                                             N.stream_ptr(q.device))
+            N.check(rc, "htree_forward_train")
+        else:
+            rc = N.lib().htree_forward(d, float(scale), N.ptr(q), N.ptr(ws), ws.numel(),
+                                       N.ptr(cos), N.ptr(sin), N.ptr(out), N.ptr(gmax),
+                                       N.ptr(gsum), N.ptr(parents), N.stream_ptr(q.device))
+            N.check(rc, "htree_forward")
     if not _save_for_backward:
         return out
     G = H // H_kv
@@ -143,6 +155,7 @@ def htree_forward(
         packed_tree=ws,
         dims=d,
         parents_stacked=parents,
+        train_scores=scores,
     )
     return out, bwd_ctx
 

@@ -113,6 +113,36 @@ int htree_backward(const htree_dims* d, float scale, const void* q, const void* 
                    const float* cos_table, const float* sin_table, float* dq, float* dk,
                    float* dv, void* bwd_ws, int64_t bwd_ws_bytes, void* stream);
 
+/* Bytes of the score buffer htree_forward_train writes for
+ * htree_backward_train (host): per level, query group and 16-candidate tile
+ * the fp16 scores relative to each head's running max, then the fp32 maxima.
+ * 0 when this configuration rebuilds the scores in the backward (inputs not
+ * bf16, or a level with more than 16 candidate tiles).  No counterpart in the
+ * reference, whose backward rebuilds every score from q and the tree
+ * (src/backward.py:236,414,585,747). */
+int htree_train_scores_bytes(const htree_dims* d, int64_t* bytes);
+
+/* htree_forward for training: `parents` is required, and when `scores` is
+ * not NULL (and the configuration keeps scores) every candidate tile's
+ * scores are written there for htree_backward_train.  Replaces the same
+ * reference kernels as htree_forward, as called with _save_for_backward=True
+ * (src/parallel.py:874-1159). */
+int htree_forward_train(const htree_dims* d, float scale, const void* q, const void* tree_ws,
+                        int64_t tree_ws_bytes, const float* cos_table, const float* sin_table,
+                        void* out, float* gmax, float* gsum, int32_t* parents, void* scores,
+                        int64_t scores_bytes, void* stream);
+
+/* htree_backward reading the scores of htree_forward_train (from the same
+ * forward call, with the same parents) instead of rebuilding them; `scores`
+ * NULL behaves as htree_backward.  Replaces what htree_backward replaces
+ * (src/backward.py:941-1119). */
+int htree_backward_train(const htree_dims* d, float scale, const void* q, const void* out,
+                         const void* dO, const float* gmax, const float* gsum,
+                         const int32_t* parents, const void* tree_ws, int64_t tree_ws_bytes,
+                         const float* cos_table, const float* sin_table, const void* scores,
+                         int64_t scores_bytes, float* dq, float* dk, float* dv, void* bwd_ws,
+                         int64_t bwd_ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -57,6 +57,32 @@ def test_backward_skewed():
     print(check_backward(q, k, v, dO, CR, TK, MTN, "bfloat16", out, par, gmax, gsum, dq, dk, dv))
 
 
+@pytest.mark.parametrize("skewed", [False, True], ids=["iid", "skewed"])
+def test_backward_stored_and_rebuilt_scores(skewed):
+    """The training forward keeps every candidate tile's scores (fp16,
+    relative to the head's running max) for the backward; without them the
+    backward rebuilds the scores from q and the tree.  Both meet the bar
+    against the oracle on the same selection."""
+    import htree_amd
+
+    B, T, H, Hkv, D, CR, TK, MTN = 1, 2500, 16, 1, 128, 16, 16, 128
+    if skewed:
+        q, k, v, dO = skewed_inputs(B, T, H, Hkv, D, "bfloat16", 5)
+    else:
+        q, k, v, dO = inputs(B, T, H, Hkv, D, "bfloat16", 8, dO=True)
+    out, par, gmax, gsum, ctx = htree_amd.htree_forward_parents(
+        q.to(DEV), k.to(DEV), v.to(DEV), CR, MTN, TK)
+    assert ctx["train_scores"] is not None
+    f = lambda x: x.float().cpu().numpy()
+    for stored in (True, False):
+        c2 = dict(ctx, train_scores=ctx["train_scores"] if stored else None)
+        dq, dk, dv = htree_amd.htree_backward(dO.to(DEV), q.to(DEV), out, c2)
+        torch.cuda.synchronize()
+        rep = check_backward(q, k, v, dO, CR, TK, MTN, "bfloat16", f(out), par.cpu().numpy(),
+                             f(gmax), f(gsum), f(dq), f(dk), f(dv))
+        print("stored" if stored else "rebuilt", rep, flush=True)
+
+
 @pytest.mark.parametrize("name", ["cr16_tk4_bf16", "cr8_tk16_fp32_g8", "cr16_tk4_fp16_b2"])
 def test_backward_matches_reference_golden(name):
     """Against the reference's own gradients (naive autograd), where the
