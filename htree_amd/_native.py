@@ -30,6 +30,7 @@ EXPORTS = (
     "htree_strerror", "htree_levels", "htree_tree_workspace_bytes", "htree_tree_build",
     "htree_forward", "htree_backward_workspace_bytes", "htree_backward",
     "htree_train_scores_bytes", "htree_forward_train", "htree_backward_train",
+    "htree_forward_trace",
 )
 
 
@@ -72,6 +73,9 @@ def lib() -> ctypes.CDLL:
         L.htree_train_scores_bytes.argtypes = [DP, ctypes.POINTER(I64)]
         L.htree_forward_train.restype = ctypes.c_int
         L.htree_forward_train.argtypes = [DP, F, P, P, I64, P, P, P, P, P, P, P, I64, P]
+    if hasattr(L, "htree_forward_trace"):
+        L.htree_forward_trace.restype = ctypes.c_int
+        L.htree_forward_trace.argtypes = [DP, F, P, P, I64, P, P, P, P, P, P, P, P, P, P]
     if hasattr(L, "htree_backward"):
         L.htree_backward_workspace_bytes.restype = ctypes.c_int
         L.htree_backward_workspace_bytes.argtypes = [DP, ctypes.POINTER(I64)]

@@ -29,6 +29,9 @@
 
 namespace htree {
 
+// max of a level that accumulated nothing (src/naive.py:9, src/parallel.py:75)
+constexpr float kNegInfSentinel = -1.0e10f;
+
 struct LevelPtrs {
   const uint16_t* kh;
   const uint16_t* kl;
@@ -46,6 +49,9 @@ struct FwdArgs {
   int32_t* parents;
   uint16_t* scores;  // nullable: fp16 S - m_ref per (level, group, tile) for the backward
   float* smref;      // m_ref per (level, group, head)
+  float* tmax;       // trace (TRACE kernels only): each level's own state,
+  float* tsum;       //   [L, B, T, H] max / sum and [L, B, T, H, D] output
+  float* tout;
   const float* cosb;
   const float* sinb;
   int32_t B, T, H, Hkv, G, CR, crlg, TK, L, max_tiles;
@@ -97,6 +103,69 @@ __device__ __forceinline__ void to_bf_split(const float (&x)[D / 32][8], bf16x8 
   for (int m = 0; m < D / 32; ++m) split8(x[m], h[m], lo[m]);
 }
 
+// ---------------------------------------------------------------- level trace
+// The TRACE kernels start every level from an empty softmax state, so after
+// the level (m, l, O) is that level's own state (LayerTrace of
+// src/naive.py:13-19, filled at :225-227): max and output relative to the
+// max over the level's accumulated candidates, -1e10 / 0 / 0 where the level
+// accumulated nothing.  O[n][r] is output dim 16n + 4kg + r of head u16.
+template <int D>
+__device__ __forceinline__ void trace_store(const FwdArgs& a, int l, int64_t hq, bool gv, int kg,
+                                            float m, float lpart, const f32x4 (&O)[D / 16]) {
+  float lt = lpart + __shfl_xor(lpart, 16);
+  lt += __shfl_xor(lt, 32);
+  if (!gv) return;
+  const int64_t lh = (int64_t)l * a.B * a.T * a.H + hq;
+  float* op = a.tout + lh * D;
+#pragma unroll
+  for (int n = 0; n < D / 16; ++n)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) op[16 * n + 4 * kg + r] = O[n][r];
+  if (kg == 0) {
+    a.tmax[lh] = m == -INFINITY ? kNegInfSentinel : m;
+    a.tsum[lh] = lt;
+  }
+}
+
+// Merges the levels' states top -> bottom with the guards of
+// src/naive.py:215-223 (a state counts only where its sum > 1e-10); returns
+// the merged sum, the merged max in m and output in O.  Reads back what this
+// lane's trace_store calls wrote.
+template <int D>
+__device__ __forceinline__ float trace_merge(const FwdArgs& a, int64_t hq, bool gv, int kg,
+                                             float& m, f32x4 (&O)[D / 16]) {
+  float gm = kNegInfSentinel, gs = 0.f;
+#pragma unroll
+  for (int n = 0; n < D / 16; ++n) O[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (gv) {
+    for (int l = a.L - 1; l >= 0; --l) {
+      const int64_t lh = (int64_t)l * a.B * a.T * a.H + hq;
+      const float lm = a.tmax[lh], ls = a.tsum[lh];
+      if (!(ls > 1e-10f)) continue;
+      const float* op = a.tout + lh * D;
+      if (gs > 1e-10f) {
+        const float nm = fmaxf(gm, lm);
+        const float sg = expf(gm - nm), sc = expf(lm - nm);
+        gs = gs * sg + ls * sc;
+#pragma unroll
+        for (int n = 0; n < D / 16; ++n)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) O[n][r] = O[n][r] * sg + op[16 * n + 4 * kg + r] * sc;
+        gm = nm;
+      } else {
+        gs = ls;
+#pragma unroll
+        for (int n = 0; n < D / 16; ++n)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) O[n][r] = op[16 * n + 4 * kg + r];
+        gm = lm;
+      }
+    }
+  }
+  m = gm;
+  return gs;
+}
+
 template <int D>
 __device__ __forceinline__ void load_kfrag(const uint16_t* __restrict__ row, int kg,
                                            bf16x8 (&f)[D / 32]) {
@@ -104,7 +173,7 @@ __device__ __forceinline__ void load_kfrag(const uint16_t* __restrict__ row, int
   for (int m = 0; m < D / 32; ++m) f[m] = *(const bf16x8*)(row + dslot<D>(kg, m));
 }
 
-template <int D, bool PREC, typename TIn, int MAXSLOT>
+template <int D, bool PREC, typename TIn, int MAXSLOT, bool TRACE>
 __global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
   __shared__ WaveLds<MAXSLOT> lds_all[kWavesPerBlock];
@@ -277,6 +346,12 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
     }
 
     // ------------------------------------------------ accumulation
+    if (TRACE) {
+      m_run = -INFINITY;
+      l_part = 0.f;
+#pragma unroll
+      for (int n = 0; n < ND; ++n) O[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     for (int tau = 0; tau < nt; ++tau) {
       const int s = wide ? (tau << 4) >> crlg : tau;
       const int node0 = (W.par[cur][s] << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0);
@@ -343,12 +418,20 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
         }
       }
     }
+    if (TRACE)
+      trace_store<D>(a, l, ((int64_t)b * a.T + t) * a.H + h * G + u16, u16 < G, kg, m_run,
+                     l_part, O);
     cur ^= 1;
   }
 
   // final normalisation (src/parallel.py:321-363): out = o / s
-  float lt = l_part + __shfl_xor(l_part, 16);
-  lt += __shfl_xor(lt, 32);
+  float lt;
+  if (TRACE) {
+    lt = trace_merge<D>(a, ((int64_t)b * a.T + t) * a.H + h * G + u16, u16 < G, kg, m_run, O);
+  } else {
+    lt = l_part + __shfl_xor(l_part, 16);
+    lt += __shfl_xor(lt, 32);
+  }
   if (u16 < G) {
     const int64_t hq = ((int64_t)b * a.T + t) * a.H + h * G + u16;
     TIn* op = (TIn*)a.out + hq * D;
@@ -516,7 +599,7 @@ __device__ __forceinline__ void rot_by(float (&x)[D / 32][8], const float* __res
   }
 }
 
-template <int D, bool PREC, typename TIn>
+template <int D, bool PREC, typename TIn, bool TRACE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fwd_reg_kernel(const FwdArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
   __shared__ WaveLdsR lds_all[kWavesPerBlock];
@@ -664,6 +747,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       const float4 x4 = *(const float4*)(&W.xrow[u16 * 4]);
       gmx = fmaxf(fmaxf(x4.x, x4.y), fmaxf(x4.z, x4.w));
     }
+    if (TRACE) {
+      m_run = -INFINITY;
+      l_part = 0.f;
+#pragma unroll
+      for (int n = 0; n < ND; ++n) O[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     const float mnew = fmaxf(m_run, gmx);
     const float mref = mnew == -INFINITY ? 0.f : mnew;
     if (a.scores) {
@@ -733,11 +822,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
         }
       }
     }
+    if (TRACE)
+      trace_store<D>(a, l, ((int64_t)b * a.T + t) * a.H + h * G + u16, gv, kg, m_run, l_part, O);
     cur ^= 1;
   }
 
-  float lt = l_part + __shfl_xor(l_part, 16);
-  lt += __shfl_xor(lt, 32);
+  float lt;
+  if (TRACE) {
+    lt = trace_merge<D>(a, ((int64_t)b * a.T + t) * a.H + h * G + u16, gv, kg, m_run, O);
+  } else {
+    lt = l_part + __shfl_xor(l_part, 16);
+    lt += __shfl_xor(lt, 32);
+  }
   if (gv) {
     const int64_t hq = ((int64_t)b * a.T + t) * a.H + h * G + u16;
     TIn* op = (TIn*)a.out + hq * D;
@@ -755,10 +851,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 
 template <int D, bool PREC, typename TIn>
 static void launch_fwd(const FwdArgs& a, int max_tiles, dim3 grid, hipStream_t st) {
-  if (max_tiles <= 16)
-    hipLaunchKernelGGL((fwd_reg_kernel<D, PREC, TIn>), grid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((fwd_kernel<D, PREC, TIn, 16>), grid, dim3(256), 0, st, a);
+  const bool trace = a.tout != nullptr;
+  if (max_tiles <= 16) {
+    if (trace)
+      hipLaunchKernelGGL((fwd_reg_kernel<D, PREC, TIn, true>), grid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((fwd_reg_kernel<D, PREC, TIn, false>), grid, dim3(256), 0, st, a);
+  } else {
+    if (trace)
+      hipLaunchKernelGGL((fwd_kernel<D, PREC, TIn, 16, true>), grid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((fwd_kernel<D, PREC, TIn, 16, false>), grid, dim3(256), 0, st, a);
+  }
 }
 
 template <int D>
@@ -778,7 +882,8 @@ using namespace htree;
 static int forward_impl(const htree_dims* d, float scale, const void* q, const void* tree_ws,
                         int64_t tree_ws_bytes, const float* cos_table, const float* sin_table,
                         void* out, float* gmax, float* gsum, int32_t* parents, void* scores,
-                        int64_t scores_bytes, void* stream) {
+                        int64_t scores_bytes, float* tmax, float* tsum, float* tout,
+                        void* stream) {
   Plan P;
   int rc = make_plan(d, &P);
   if (rc) return rc;
@@ -807,6 +912,9 @@ static int forward_impl(const htree_dims* d, float scale, const void* q, const v
   a.parents = parents;
   a.scores = (uint16_t*)scores;
   a.smref = scores ? (float*)((char*)scores + off_mref) : nullptr;
+  a.tmax = tmax;
+  a.tsum = tsum;
+  a.tout = tout;
   a.max_tiles = P.max_tiles;
   a.cosb = cos_table;
   a.sinb = sin_table;
@@ -840,7 +948,7 @@ extern "C" int htree_forward(const htree_dims* d, float scale, const void* q,
                              const float* cos_table, const float* sin_table, void* out,
                              float* gmax, float* gsum, int32_t* parents, void* stream) {
   return forward_impl(d, scale, q, tree_ws, tree_ws_bytes, cos_table, sin_table, out, gmax, gsum,
-                      parents, nullptr, 0, stream);
+                      parents, nullptr, 0, nullptr, nullptr, nullptr, stream);
 }
 
 extern "C" int htree_train_scores_bytes(const htree_dims* d, int64_t* bytes) {
@@ -859,5 +967,15 @@ extern "C" int htree_forward_train(const htree_dims* d, float scale, const void*
                                    int64_t scores_bytes, void* stream) {
   if (!parents) return HTREE_ENULL;
   return forward_impl(d, scale, q, tree_ws, tree_ws_bytes, cos_table, sin_table, out, gmax, gsum,
-                      parents, scores, scores_bytes, stream);
+                      parents, scores, scores_bytes, nullptr, nullptr, nullptr, stream);
+}
+
+extern "C" int htree_forward_trace(const htree_dims* d, float scale, const void* q,
+                                   const void* tree_ws, int64_t tree_ws_bytes,
+                                   const float* cos_table, const float* sin_table, void* out,
+                                   float* gmax, float* gsum, int32_t* parents, float* level_max,
+                                   float* level_sum, float* level_out, void* stream) {
+  if (!parents || !level_max || !level_sum || !level_out) return HTREE_ENULL;
+  return forward_impl(d, scale, q, tree_ws, tree_ws_bytes, cos_table, sin_table, out, gmax, gsum,
+                      parents, nullptr, 0, level_max, level_sum, level_out, stream);
 }

@@ -95,6 +95,21 @@ int htree_forward(const htree_dims* d, float scale, const void* q,
                   const float* cos_table, const float* sin_table, void* out,
                   float* gmax, float* gsum, int32_t* parents, void* stream);
 
+/* htree_forward that also keeps every level's own online-softmax state, for
+ * level-by-level parity checks: level_max / level_sum [L, B, T, H] and
+ * level_out [L, B, T, H, D] in fp32, level l at index l; max and unnormalised
+ * output relative to the max over that level's accumulated candidates,
+ * -1e10 / 0 / 0 where the level accumulated nothing.  `parents` is required
+ * (level l's selection is parents[l-1]).  out, gmax and gsum are the merge
+ * of the level states with the guards of src/naive.py:215-231.
+ * Replaces run_parallel_with_trace (correctness_test.py:168-347), which
+ * launches the per-level kernels of src/parallel.py one by one and clones
+ * their state into LayerTrace (src/naive.py:13-19). */
+int htree_forward_trace(const htree_dims* d, float scale, const void* q, const void* tree_ws,
+                        int64_t tree_ws_bytes, const float* cos_table, const float* sin_table,
+                        void* out, float* gmax, float* gsum, int32_t* parents, float* level_max,
+                        float* level_sum, float* level_out, void* stream);
+
 /* Bytes of the backward workspace (host). */
 int htree_backward_workspace_bytes(const htree_dims* d, int64_t* bytes);
 

@@ -1,0 +1,180 @@
+"""GPU parity of the per-level trace (run_parallel_with_trace, the harness of
+correctness_test.py:168-347) against the CPU oracle's trace and against the
+reference's own per-level state (golden fixtures written from
+src/naive.py with return_trace=True).
+
+Per level, teacher-forced on the device's parent lists:
+  * levels that accumulated nothing: -1e10 / 0 / 0 exactly;
+  * layer_max within the score bar below, layer_sum within a relative bar,
+    the normalised level output (layer_output / layer_sum) within the
+    output bar of the dtype (2e-2 abs + 1e-2 rel bf16, 1e-4 fp32, 2e-3
+    fp16).
+The parents and the output must equal the plain forward's (same selection
+code; the output within the dtype bar, since the trace merges the levels
+from their own maxima)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from tests.gpu_util import close, inputs
+from tests.helpers import load_golden
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+# |layer_max - oracle| <= atol + rtol |oracle|: scores come from the split
+# bf16 product (error ~1e-5 of |q||k| scale) of the dtype-rounded inputs
+MAX_TOL = {"float32": (1e-4, 1e-4), "bfloat16": (1e-4, 1e-4), "float16": (1e-4, 1e-4)}
+# relative bar of layer_sum (a score error e moves each term by ~e)
+SUM_RTOL = {"float32": 1e-4, "bfloat16": 2e-4, "float16": 2e-4}
+
+CASES = [
+    # B, T, H, Hkv, D, CR, TK, MTN, dtype, seed
+    (1, 2048, 4, 1, 64, 16, 8, 64, "float32", 11),      # C1 shape, single-pass kernel
+    (2, 1500, 16, 2, 128, 16, 16, 128, "bfloat16", 12),
+    (1, 1100, 8, 1, 128, 16, 16, 128, "float16", 13),
+    (1, 3000, 8, 1, 64, 4, 32, 64, "bfloat16", 14),     # 32 tiles: multi-pass kernel, 4 levels
+    (1, 700, 8, 2, 64, 8, 16, 128, "float32", 15),      # CR < 16
+]
+
+
+def _trace(q, k, v, CR, TK, MTN):
+    import htree_amd
+
+    out, tr = htree_amd.run_parallel_with_trace(q.to(DEV), k.to(DEV), v.to(DEV), CR, MTN, TK,
+                                                None, 10000.0)
+    torch.cuda.synchronize()
+    return out, tr
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+def check_levels(tr, fw, dtype, B, T, H):
+    """Device trace vs an oracle trace computed from the same parent lists."""
+    L = tr["num_layers"]
+    worst = {}
+    for l in range(L - 1, -1, -1):
+        lt = tr["layers"][l]
+        m, s, o = _np(lt.layer_max), _np(lt.layer_sum), _np(lt.layer_output)
+        om = fw["lmax"][l].reshape(B, T, H)
+        osum = fw["lsum"][l].reshape(B, T, H)
+        oo = fw["lout"][l].reshape(B, T, H, -1)
+        empty = osum == 0
+        assert np.array_equal(empty, s == 0), f"level {l}: empty-level rows differ"
+        assert np.all(m[empty] == np.float32(-1e10)), f"level {l}: sentinel max"
+        assert np.all(o[empty] == 0), f"level {l}: output of an empty level"
+        full = ~empty
+        atol, rtol = MAX_TOL[dtype]
+        em = np.abs(m[full] - om[full]) / (atol + rtol * np.abs(om[full]))
+        es = np.abs(s[full] - osum[full]) / (SUM_RTOL[dtype] * osum[full])
+        worst[l] = (float(em.max(initial=0)), float(es.max(initial=0)))
+        assert np.all(em <= 1), f"level {l}: layer_max worst {em.max():.3f} of the bar"
+        assert np.all(es <= 1), f"level {l}: layer_sum worst {es.max():.3f} of the bar"
+        ok, w = close(o[full] / s[full][:, None], oo[full] / osum[full][:, None], dtype)
+        assert ok, f"level {l}: normalised output worst {w:.3f} of the bar"
+    return worst
+
+
+@pytest.mark.parametrize("cfg", CASES, ids=lambda c: f"T{c[1]}D{c[4]}cr{c[5]}tk{c[6]}{c[8]}")
+def test_trace_matches_oracle(cfg):
+    import htree_amd
+
+    B, T, H, Hkv, D, CR, TK, MTN, dtype, seed = cfg
+    print(f"case {cfg}", flush=True)
+    q, k, v = inputs(B, T, H, Hkv, D, dtype, seed)
+    out, tr = _trace(q, k, v, CR, TK, MTN)
+    L = tr["num_layers"]
+    assert tr["num_groups"] == H // Hkv and sorted(tr["layers"]) == list(range(L))
+    assert tr["layers"][0].selected_parents is None
+    # same selection and output as the plain forward
+    out_p, par_p, gmax_p, gsum_p, _ = htree_amd.htree_forward_parents(
+        q.to(DEV), k.to(DEV), v.to(DEV), compression_rate=CR, max_top_nodes=MTN,
+        top_k_per_layer=TK)
+    for l in range(1, L):
+        assert torch.equal(tr["layers"][l].selected_parents, par_p[l - 1]), f"level {l} parents"
+    ok, w = close(_np(out), _np(out_p), dtype)
+    assert ok, f"trace output vs forward output: worst {w:.3f} of the bar"
+    # per-level state, teacher-forced on the device's lists
+    par = np.stack([par_p[l].cpu().numpy() for l in range(L)])  # lists used per level
+    tree = orc.Tree(k.float().numpy(), v.float().numpy(), CR, MTN, TK, dtype)
+    rows = orc.all_rows(B, T)
+    fw = orc.forward(q.float().numpy(), tree, D ** -0.5, rows=rows,
+                     forced=par.reshape(L, B * T, Hkv, TK), trace=True)
+    print(check_levels(tr, fw, dtype, B, T, H), flush=True)
+    # merged state = the forward's global state
+    ok, w = close(_np(tr["global_max"]), fw["gmax"].reshape(B, T, H), "float32")
+    assert ok, f"global max worst {w:.3f}"
+
+
+def test_compare_traces_against_untethered_oracle():
+    """The reference's comparison methodology, device trace vs the oracle's
+    own (not teacher-forced) trace: no level-output alarm, and every Top-K
+    alarm is one of the selection differences the tie band excuses."""
+    import htree_amd
+    from htree_amd.trace import LayerTrace
+    from tests.gpu_util import check_forward
+
+    B, T, H, Hkv, D, CR, TK, MTN, dtype, seed = 2, 1500, 16, 2, 128, 16, 16, 128, "bfloat16", 21
+    q, k, v = inputs(B, T, H, Hkv, D, dtype, seed)
+    out, tr = _trace(q, k, v, CR, TK, MTN)
+    L = tr["num_layers"]
+    tree = orc.Tree(k.float().numpy(), v.float().numpy(), CR, MTN, TK, dtype)
+    fw = orc.forward(q.float().numpy(), tree, D ** -0.5, trace=True)
+    naive = {"num_layers": L, "num_groups": H // Hkv, "layers": {
+        l: LayerTrace(l,
+                      torch.from_numpy(fw["sel"][l].reshape(B, T, Hkv, TK)) if l > 0 else None,
+                      torch.from_numpy(fw["lmax"][l].reshape(B, T, H)),
+                      torch.from_numpy(fw["lsum"][l].reshape(B, T, H)),
+                      torch.from_numpy(fw["lout"][l].reshape(B, T, H, D)))
+        for l in range(L)}}
+    rep = htree_amd.compare_traces(tr, naive, topk_alarm_diff=0, layer_out_alarm_abs=2e-2,
+                                   max_report=10 ** 6)
+    print({"mismatch_counter": rep["mismatch_counter"], "topk": len(rep["topk_alarms"]),
+           "out": len(rep["layer_output_alarms"])}, flush=True)
+    assert rep["layer_output_alarms"] == []
+    par = np.stack([tr["layers"][l].selected_parents.cpu().numpy() if l > 0 else
+                    np.zeros((B, T, Hkv, TK), np.int32) for l in range(L)])
+    par_used = np.concatenate([par[1:], orc.initial_parents(B, T, Hkv, TK, CR, L)[None]], 0)
+    # teacher-forced check on the device's lists: all differences inside the tie band
+    cf = check_forward(q, k, v, CR, TK, MTN, dtype, out_dev=_np(out), parents_dev=par_used,
+                       tree=tree)
+    assert len(rep["topk_alarms"]) <= sum(cf["mismatch"].values())
+
+
+@pytest.mark.parametrize("name", ["cr16_tk4_bf16", "cr8_tk16_fp32_g8", "cr16_tk4_fp16_b2"])
+def test_trace_matches_reference_golden(name):
+    """Device trace vs the reference's own per-level state (src/naive.py with
+    return_trace=True): layer_max / layer_sum on every query group whose
+    selection path matched the reference's down to that level."""
+    g = load_golden(name)
+    print(f"golden {name}", flush=True)
+    out, tr = _trace(g["q"], g["k"], g["v"], g["CR"], g["TK"], g["MTN"])
+    B, T, H, Hkv, TK, L, dtype = g["B"], g["T"], g["H"], g["Hkv"], g["TK"], g["L"], g["dtype"]
+    G = H // Hkv
+    path_ok = np.ones((B, T, Hkv), bool)
+    atol, rtol = MAX_TOL[dtype]
+    for l in range(L - 1, -1, -1):
+        lt = tr["layers"][l]
+        if l > 0:
+            ref = g[f"parents_l{l}"].reshape(B, T, Hkv, TK)
+            sel_ok = np.all(lt.selected_parents.cpu().numpy() == ref, axis=-1)
+        else:
+            sel_ok = np.ones_like(path_ok)
+        rows = np.repeat(path_ok & sel_ok, G, axis=2)  # [B,T,H]
+        assert rows.mean() > 0.99, f"level {l}: only {rows.mean():.4f} of the groups match"
+        m, s = _np(lt.layer_max)[rows], _np(lt.layer_sum)[rows]
+        rm, rs = g[f"lmax_l{l}"][rows], g[f"lsum_l{l}"][rows]
+        assert np.array_equal(rs == 0, s == 0)
+        assert np.all(m[rs == 0] == np.float32(-1e10))
+        full = rs > 0
+        em = np.abs(m[full] - rm[full]) / (atol + rtol * np.abs(rm[full]))
+        es = np.abs(s[full] - rs[full]) / (SUM_RTOL[dtype] * rs[full])
+        print(f"level {l}: max worst {em.max(initial=0):.3f}, sum worst {es.max(initial=0):.3f} "
+              f"of the bars", flush=True)
+        assert np.all(em <= 1), f"level {l} max"
+        assert np.all(es <= 1), f"level {l} sum"
+        path_ok &= sel_ok
