@@ -119,39 +119,13 @@ template <int D>
 __device__ __forceinline__ void rot_frag(const float (&x)[D / 32][8], const float* __restrict__ cosr,
                                          const float* __restrict__ sinr, int kg,
                                          float (&y)[D / 32][8]) {
-  constexpr int SPH = D / 64;
-#pragma unroll
-  for (int m = 0; m < SPH; ++m) {
-    const int i0 = dslot<D>(kg, m);
-    float c[8], s[8];
-    Io<float>::ld8(cosr + i0, c);
-    Io<float>::ld8(sinr + i0, s);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float lo = x[m][e], hi = x[m + SPH][e];
-      y[m][e] = lo * c[e] - hi * s[e];
-      y[m + SPH][e] = lo * s[e] + hi * c[e];
-    }
-  }
+  rope_frag<D>(x, cosr, sinr, kg, y);
 }
 
 template <int D>
 __device__ __forceinline__ void rot_by_fr(float (&x)[D / 32][8], const float* cosr, const float* sinr,
                                           int kg) {
-  constexpr int SPH = D / 64;
-#pragma unroll
-  for (int m = 0; m < SPH; ++m) {
-    const int i0 = dslot<D>(kg, m);
-    float c[8], s[8];
-    Io<float>::ld8(cosr + i0, c);
-    Io<float>::ld8(sinr + i0, s);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float lo = x[m][e], hi = x[m + SPH][e];
-      x[m][e] = lo * c[e] - hi * s[e];
-      x[m + SPH][e] = lo * s[e] + hi * c[e];
-    }
-  }
+  rope_frag<D>(x, cosr, sinr, kg, x);
 }
 
 template <int D>
@@ -1552,6 +1526,10 @@ static int backward_impl(const htree_dims* d, float scale, const void* q, const 
     if (d->dtype == HTREE_BF16) HT_BWD(128, false, __bf16);
     if (d->dtype == HTREE_F16) HT_BWD(128, true, _Float16);
     HT_BWD(128, true, float);
+  } else if (d->D == 32) {
+    if (d->dtype == HTREE_BF16) HT_BWD(32, false, __bf16);
+    if (d->dtype == HTREE_F16) HT_BWD(32, true, _Float16);
+    HT_BWD(32, true, float);
   } else {
     if (d->dtype == HTREE_BF16) HT_BWD(64, false, __bf16);
     if (d->dtype == HTREE_F16) HT_BWD(64, true, _Float16);

@@ -168,11 +168,54 @@ __device__ __forceinline__ int mbcnt64(unsigned long long m) {
 
 // d-slot of k-step m for lane group kg: the four lane groups cover 8
 // consecutive elements each; steps m and m + D/64 hold the RoPE pair
-// (d, d + D/2) so both halves of a pair live in the same lane.
+// (d, d + D/2) so both halves of a pair live in the same lane.  D = 32 has
+// one k-step: lane groups 0, 1 hold the low half, 2, 3 the high half, and a
+// pair's halves sit in lanes 32 apart.
 template <int D>
 __device__ __forceinline__ int dslot(int kg, int m) {
-  constexpr int SPH = D / 64;
-  return 8 * kg + 32 * (m % SPH) + (D / 2) * (m / SPH);
+  if constexpr (D == 32) {
+    return 8 * kg;
+  } else {
+    constexpr int SPH = D / 64;
+    return 8 * kg + 32 * (m % SPH) + (D / 2) * (m / SPH);
+  }
+}
+
+// y = R(x, p) on an operand fragment laid out by dslot (R of
+// src/naive.py:22-28: lo' = lo cos - hi sin, hi' = lo sin + hi cos), with
+// cosr / sinr the table row of angle p.  x and y may alias.
+template <int D>
+__device__ __forceinline__ void rope_frag(const float (&x)[D / 32][8], const float* __restrict__ cosr,
+                                          const float* __restrict__ sinr, int kg,
+                                          float (&y)[D / 32][8]) {
+  if constexpr (D == 32) {
+    float c[8], s[8], t[8];
+    Io<float>::ld8(cosr + 8 * (kg & 1), c);
+    Io<float>::ld8(sinr + 8 * (kg & 1), s);
+    const float sg = kg < 2 ? -1.f : 1.f;  // lo lanes subtract hi sin, hi lanes add lo sin
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float other = __shfl_xor(x[0][e], 32);
+      t[e] = x[0][e] * c[e] + sg * other * s[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[0][e] = t[e];
+  } else {
+    constexpr int SPH = D / 64;
+#pragma unroll
+    for (int m = 0; m < SPH; ++m) {
+      const int i0 = dslot<D>(kg, m);
+      float c[8], s[8];
+      Io<float>::ld8(cosr + i0, c);
+      Io<float>::ld8(sinr + i0, s);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float lo = x[m][e], hi = x[m + SPH][e];
+        y[m][e] = lo * c[e] - hi * s[e];
+        y[m + SPH][e] = lo * s[e] + hi * c[e];
+      }
+    }
+  }
 }
 
 // Query fragment of a lane (head u16, the lane group's d-slots) kept in its

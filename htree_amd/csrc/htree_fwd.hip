@@ -74,20 +74,7 @@ template <int D>
 __device__ __forceinline__ void rot_q(const float (&qf)[D / 32][8], const float* __restrict__ cosr,
                                       const float* __restrict__ sinr, int kg,
                                       float (&qr)[D / 32][8]) {
-  constexpr int SPH = D / 64;
-#pragma unroll
-  for (int m = 0; m < SPH; ++m) {
-    const int i0 = dslot<D>(kg, m);
-    float c[8], s[8];
-    Io<float>::ld8(cosr + i0, c);
-    Io<float>::ld8(sinr + i0, s);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float lo = qf[m][e], hi = qf[m + SPH][e];
-      qr[m][e] = lo * c[e] - hi * s[e];
-      qr[m + SPH][e] = lo * s[e] + hi * c[e];
-    }
-  }
+  rope_frag<D>(qf, cosr, sinr, kg, qr);
 }
 
 template <int D>
@@ -583,20 +570,7 @@ struct WaveLdsR {
 template <int D>
 __device__ __forceinline__ void rot_by(float (&x)[D / 32][8], const float* __restrict__ cosr,
                                        const float* __restrict__ sinr, int kg) {
-  constexpr int SPH = D / 64;
-#pragma unroll
-  for (int m = 0; m < SPH; ++m) {
-    const int i0 = dslot<D>(kg, m);
-    float c[8], s[8];
-    Io<float>::ld8(cosr + i0, c);
-    Io<float>::ld8(sinr + i0, s);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float lo = x[m][e], hi = x[m + SPH][e];
-      x[m][e] = lo * c[e] - hi * s[e];
-      x[m + SPH][e] = lo * s[e] + hi * c[e];
-    }
-  }
+  rope_frag<D>(x, cosr, sinr, kg, x);
 }
 
 template <int D, bool PREC, typename TIn, bool TRACE>
@@ -937,6 +911,8 @@ static int forward_impl(const htree_dims* d, float scale, const void* q, const v
   hipStream_t st = (hipStream_t)stream;
   if (d->D == 128)
     launch_fwd_d<128>(d->dtype, a, P.max_tiles, grid, st);
+  else if (d->D == 32)
+    launch_fwd_d<32>(d->dtype, a, P.max_tiles, grid, st);
   else
     launch_fwd_d<64>(d->dtype, a, P.max_tiles, grid, st);
   hipError_t e = hipGetLastError();

@@ -27,7 +27,7 @@ int make_plan(const htree_dims* d, Plan* p) {
     return HTREE_ECONFIG;
   const int CR = d->compression_rate;
   const int64_t max_tiles = (int64_t)d->top_k * (CR > 16 ? CR : 16) / 16;
-  if ((d->D != 64 && d->D != 128) || d->H / d->H_kv > 16 || CR < 4 || CR > 64 ||
+  if ((d->D != 32 && d->D != 64 && d->D != 128) || d->H / d->H_kv > 16 || CR < 4 || CR > 64 ||
       max_tiles > 64 || d->top_k > kMaxTK)
     return HTREE_EUNSUPPORTED;
 
@@ -189,7 +189,7 @@ const char* htree_strerror(int status) {
              "must be powers of two with max_top_nodes <= top_k_per_layer * compression_rate "
              "and rope_rows >= top_k_per_layer * compression_rate";
     case HTREE_EUNSUPPORTED:
-      return "configuration outside this HIP build: needs D in {64,128}, H/H_kv <= 16, "
+      return "configuration outside this HIP build: needs D in {32,64,128}, H/H_kv <= 16, "
              "4 <= compression_rate <= 64, top_k_per_layer <= 64 and "
              "top_k_per_layer * max(compression_rate,16) / 16 <= 64";
     case HTREE_EWORKSPACE: return "workspace smaller than htree_tree_workspace_bytes()";

@@ -7,7 +7,7 @@ Differences, all deliberate:
     reference asserts equality, src/parallel.py:917); the algorithm never
     relies on equality.  The reference's Triton-tiling asserts
     (top_k % 64 == 0, top_k % compression_rate == 0, :923,1019) do not apply.
-  * limits of this HIP build (AssertionError): head_dim in {64, 128},
+  * limits of this HIP build (AssertionError): head_dim in {32, 64, 128},
     H / H_kv <= 16, compression_rate >= 4, top_k_per_layer <= 64 and
     top_k_per_layer * max(compression_rate, 16) / 16 <= 64.
   * the RoPE tables are built on the host with the reference's recipe

@@ -40,6 +40,10 @@ SMALL = [
     (1, 700, 8, 2, 64, 8, 16, 128, "float32", 5),      # CR < 16
     (1, 900, 4, 1, 128, 32, 8, 256, "bfloat16", 6),    # CR > 16
     (1, 3000, 8, 1, 64, 4, 32, 64, "bfloat16", 7),     # CR = 4, 4 levels
+    (1, 2000, 16, 4, 32, 16, 16, 128, "float32", 8),   # D = 32 (the reference's default head dim)
+    (1, 1500, 16, 4, 32, 16, 8, 128, "float16", 9),
+    (2, 1000, 8, 2, 32, 8, 16, 64, "bfloat16", 10),
+    (1, 2500, 16, 4, 32, 4, 32, 64, "float32", 11),    # D = 32, 32 tiles: multi-pass kernel
 ]
 
 
