@@ -60,6 +60,7 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
   int rc = make_plan(d, &b->P);
   if (rc) return rc;
   const Plan& P = b->P;
+  if (P.wide) return HTREE_EUNSUPPORTED;  // the backward's parent lists live in one wave
   const int CR = d->compression_rate;
   b->G = d->H / d->H_kv;
   b->tpp = CR > 16 ? CR / 16 : 1;

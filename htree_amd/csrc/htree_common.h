@@ -15,7 +15,15 @@ typedef __attribute__((ext_vector_type(4))) float f32x4;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kWavesPerBlock = 4;
-constexpr int kMaxTK = 64;
+constexpr int kMaxTK = 64;       // parent lists of the one-wave-per-group kernels
+constexpr int kMaxTiles = 64;    // candidate tiles per level of those kernels
+// Wide configurations (top_k > kMaxTK or more than kMaxTiles tiles, e.g. the
+// reference's default top_k = 512, CR = 16): one block of kWideWaves waves per
+// query group, kWideC candidate positions per thread in the selection.
+constexpr int kWideWaves = 4;
+constexpr int kWideC = 32;
+constexpr int kWideMaxPos = 64 * kWideWaves * kWideC;  // top_k * CR <= 8192
+constexpr int kWideMaxTK = 512;
 
 // ---------------------------------------------------------------- plan
 // Packed operand tree, per level l (all bf16, Np = N rounded up to 16):
@@ -36,7 +44,27 @@ struct Plan {
   int64_t bytes;
   int max_tiles;  // candidate tiles of 16 per level: TK * max(CR,16) / 16
   int cr_log2;
+  bool wide;      // top_k > kMaxTK or max_tiles > kMaxTiles
 };
+
+// Dynamic LDS of the wide forward (byte offsets): both parent lists, the
+// selection bits, every tile's running max, block reduction slots, and the
+// importance of every candidate position (reused to merge the waves' states).
+struct WideLds {
+  int par, selw, mt, red, imp, bytes;
+};
+__host__ __device__ inline WideLds wide_lds(int TK, int maxpos, int max_tiles, int D) {
+  WideLds w;
+  w.par = 0;
+  w.selw = 8 * TK;
+  w.mt = w.selw + (maxpos + 31) / 32 * 4;
+  w.red = w.mt + 4 * max_tiles;
+  w.imp = (w.red + 256 + 15) / 16 * 16;
+  const int imp_bytes = 4 * maxpos;
+  const int merge_bytes = 4 * kWideWaves * 16 * (D + 3);
+  w.bytes = w.imp + (imp_bytes > merge_bytes ? imp_bytes : merge_bytes);
+  return w;
+}
 
 int make_plan(const htree_dims* d, Plan* p);
 

@@ -448,6 +448,13 @@ __device__ __forceinline__ float row_sum16(float x) {
   x += dpp<0x140>(x);
   return x;
 }
+__device__ __forceinline__ int row_sum16i(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false);
+  return x;
+}
 __device__ __forceinline__ float row_max16(float x) {
   x = fmaxf(x, dpp<0xB1>(x));
   x = fmaxf(x, dpp<0x4E>(x));
@@ -823,10 +830,370 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   }
 }
 
+// ---------------------------------------------------------------- wide forward
+// Levels of up to 8192 candidates (top_k up to 512: the reference's default
+// regime, src/parallel.py:537-867 with TOP_K = 512): one block of four waves
+// per query group.  Tiles are dealt to the waves round-robin; each wave keeps
+// its own online-softmax state (the waves' states are merged at the end, in
+// any order: the output is one softmax over the union of the accumulated
+// candidates).  Upper levels score every tile once for the importance
+// (relative to the wave's running max, rescaled to the level max afterwards)
+// and select with a block-wide radix select over the float bits: thread i
+// holds candidate positions 32i .. 32i+31 in registers, so ties at the
+// threshold go to the lowest positions (stable descending sort, src/naive.py:
+// 88-105) by an exclusive scan in position order.  The accumulation pass
+// recomputes the scores of the non-selected candidates.
+template <int D, bool PREC, typename TIn, bool TRACE>
+__global__ __launch_bounds__(256) void fwd_wide_kernel(const FwdArgs a) {
+  constexpr int KS = D / 32, ND = D / 16, HALF = D / 2, NW = kWideWaves, C = kWideC;
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int u16 = lane & 15, kg = lane >> 4;
+  const int G = a.G, CR = a.CR, crlg = a.crlg, TK = a.TK;
+  const int CRU = CR < 16 ? CR : 16;
+  const bool wide = CR >= 16;
+  const WideLds LO = wide_lds(TK, TK << crlg, a.max_tiles, D);
+  int32_t* par = (int32_t*)(lds + LO.par);      // [2][TK]
+  uint32_t* selw = (uint32_t*)(lds + LO.selw);  // selection bit of every position
+  float* mt = (float*)(lds + LO.mt);            // running max of the wave at each tile
+  int32_t* red = (int32_t*)(lds + LO.red);      // [0,16) counts, [16,32) scans, [32,36) maxima
+  float* imp = (float*)(lds + LO.imp);
+
+  const int64_t grp = (int64_t)(blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
+  if (grp >= (int64_t)a.B * a.Hkv * a.T) return;  // uniform over the block
+  const int t = (int)(grp % a.T);
+  const int bh = (int)(grp / a.T);
+  const int h = bh % a.Hkv;
+  const int b = bh / a.Hkv;
+  const bool gv = u16 < G;
+  const int64_t hq = ((int64_t)b * a.T + t) * a.H + h * G + u16;
+
+  float qf[KS][8];
+  {
+    const TIn* qp = (const TIn*)a.q + (((int64_t)b * a.T + t) * a.H + h * G + (gv ? u16 : 0)) * D;
+#pragma unroll
+    for (int m = 0; m < KS; ++m) {
+      Io<TIn>::ld8(qp + dslot<D>(kg, m), qf[m]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[m][e] = gv ? qf[m][e] * a.scale : 0.f;
+    }
+  }
+  float m_run = -INFINITY, l_part = 0.f;
+  f32x4 O[ND];
+#pragma unroll
+  for (int n = 0; n < ND; ++n) O[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  {
+    const int64_t nvp = (t / a.lv[a.L - 1].pw) / CR + 1;  // src/naive.py:108-118
+    for (int i = tid; i < TK; i += 256) par[i] = i < nvp ? i : -1;
+  }
+
+  // block sum of per-key predicates (one barrier; slots alternate)
+  int rc_sel = 0, rs_sel = 0;
+  auto bcount = [&](const uint32_t (&key)[C], uint32_t thr, bool strict) {
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+      c += strict ? key[i] > thr : key[i] >= thr;
+      if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // keep the compare masks short-lived
+    }
+    c = row_sum16i(c);
+    c += __shfl_xor(c, 16);
+    c += __shfl_xor(c, 32);
+    int32_t* r = red + 8 * rc_sel;
+    rc_sel ^= 1;
+    if (lane == 0) r[wv] = c;
+    __syncthreads();
+    return r[0] + r[1] + r[2] + r[3];
+  };
+  // block exclusive scan in thread order
+  auto bscan = [&](int v) {
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o);
+      if (lane >= o) x += y;
+    }
+    int32_t* r = red + 16 + 8 * rs_sel;
+    rs_sel ^= 1;
+    if (lane == 63) r[wv] = x;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < wv; ++w) base += r[w];
+    return base + x - v;
+  };
+  // merge of the waves' states; the result (max, sum, output) is valid in wave 0
+  auto merge_waves = [&](float& Mo, float& Lo, f32x4 (&Om)[ND]) {
+    float lt = l_part + __shfl_xor(l_part, 16);
+    lt += __shfl_xor(lt, 32);
+    constexpr int DP = D + 1;
+    float* mw = imp;
+    float* lw = imp + NW * 16;
+    float* ow = imp + 2 * NW * 16;
+    __syncthreads();
+    if (kg == 0) {
+      mw[wv * 16 + u16] = m_run;
+      lw[wv * 16 + u16] = lt;
+    }
+#pragma unroll
+    for (int n = 0; n < ND; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ow[(wv * 16 + u16) * DP + 16 * n + 4 * kg + r] = O[n][r];
+    __syncthreads();
+    if (wv == 0) {
+      float M = -INFINITY, L = 0.f;
+#pragma unroll
+      for (int n = 0; n < ND; ++n) Om[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int w = 0; w < NW; ++w) M = fmaxf(M, mw[w * 16 + u16]);
+      if (M > -INFINITY) {
+        for (int w = 0; w < NW; ++w) {
+          const float mw_ = mw[w * 16 + u16];
+          if (mw_ == -INFINITY) continue;
+          const float sc = expf(mw_ - M);
+          L += lw[w * 16 + u16] * sc;
+#pragma unroll
+          for (int n = 0; n < ND; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) Om[n][r] += ow[(w * 16 + u16) * DP + 16 * n + 4 * kg + r] * sc;
+        }
+      }
+      Mo = M;
+      Lo = L;
+    }
+  };
+
+  int cur = 0;
+  for (int l = a.L - 1; l >= 0; --l) {
+    __syncthreads();
+    const LevelPtrs P = a.lv[l];
+    const int32_t* pc = par + cur * TK;
+    int lo = 0, hi = TK;  // the valid entries are a prefix of the list
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (pc[mid] >= 0) lo = mid + 1; else hi = mid;
+    }
+    const int np = lo;
+    const int ct = (int)((t / P.pw) & (CR - 1));
+    const int nc = ((np - 1) << crlg) + ct + 1;
+    const int apos = nc - 1;
+    const int nt = wide ? (nc + 15) >> 4 : np;
+    if (a.parents)
+      for (int i = tid; i < TK; i += 256)
+        a.parents[((((int64_t)l * a.B + b) * a.T + t) * a.Hkv + h) * TK + i] = pc[i];
+    const int64_t hrow = ((int64_t)b * a.Hkv + h) * P.Np;
+    const uint16_t* KH = P.kh + hrow * D;
+    const uint16_t* KL = P.kl + hrow * D;
+    const uint16_t* VH = P.vh + hrow * D;
+    const uint16_t* VL = PREC ? P.vl + hrow * D : nullptr;
+    const bool upper = l > 0;
+    auto slot_of = [&](int tau) { return wide ? (tau << 4) >> crlg : tau; };
+    auto node0_of = [&](int tau) {
+      return (pc[slot_of(tau)] << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0);
+    };
+
+    if (upper) {
+      // ---- importance of every candidate (relative to the wave's running max)
+      float Mrun = -INFINITY;
+      for (int tau = wv; tau < nt; tau += NW) {
+        const int prow = apos - (slot_of(tau) << crlg);
+        float qr[KS][8];
+        rot_q<D>(qf, a.cosb + (int64_t)prow * HALF, a.sinb + (int64_t)prow * HALF, kg, qr);
+        bf16x8 qh[KS], ql[KS];
+        to_bf_split<D>(qr, qh, ql);
+        const int pos = wide ? (tau << 4) + u16 : (tau << crlg) + u16;
+        const bool cv = u16 < CRU && pos < nc;
+        const int64_t krow = (int64_t)(node0_of(tau) + (cv ? u16 : 0)) * D;
+        bf16x8 kh[KS], kl[KS];
+        load_kfrag<D>(KH + krow, kg, kh);
+        load_kfrag<D>(KL + krow, kg, kl);
+        f32x4 S = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < KS; ++m) {
+          S = mma32(qh[m], kh[m], S);
+          S = mma32(qh[m], kl[m], S);
+          S = mma32(ql[m], kh[m], S);
+        }
+        // S[r] = score[g = 4kg + r][candidate u16]
+        float tm = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (cv && 4 * kg + r < G) tm = fmaxf(tm, S[r]);
+        Mrun = fmaxf(Mrun, wave_max(tm));
+        float e = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (cv && 4 * kg + r < G) e += expf(S[r] - Mrun);
+        e += __shfl_xor(e, 16);
+        e += __shfl_xor(e, 32);
+        if (kg == 0 && cv) imp[pos] = e;
+        if (lane == 0) mt[tau] = Mrun;
+      }
+      if (lane == 0) red[32 + wv] = __float_as_int(Mrun);
+      __syncthreads();
+      const float M = fmaxf(fmaxf(__int_as_float(red[32]), __int_as_float(red[33])),
+                            fmaxf(__int_as_float(red[34]), __int_as_float(red[35])));
+      // ---- keys: float bits + 1 (0 = no candidate); rightmost forced (src/naive.py:93)
+      const int take = TK < nc ? TK : nc;
+      uint32_t key[C];
+#pragma unroll
+      for (int i = 0; i < C; ++i) {
+        const int pos = tid * C + i;
+        key[i] = 0u;
+        if (pos < nc) {
+          float v;
+          if (pos == apos) {
+            v = 1e6f;
+          } else {
+            v = imp[pos];
+            const float m = mt[wide ? pos >> 4 : pos >> crlg];
+            if (m != M) v *= expf(m - M);
+          }
+          key[i] = __float_as_uint(v) + 1u;
+        }
+        if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+      }
+      // ---- the take-th largest key, bit by bit from the top
+      uint32_t thr = 0u;
+#pragma unroll 1
+      for (int bit = 30; bit >= 0; --bit) {
+        const uint32_t c = thr | (1u << bit);
+        if (bcount(key, c, false) >= take) thr = c;
+      }
+      const int need = take - bcount(key, thr, true);
+      uint32_t gtb = 0u, eqb = 0u;  // this thread's positions above / at the threshold
+#pragma unroll
+      for (int i = 0; i < C; ++i) {
+        gtb |= (uint32_t)(key[i] > thr) << i;
+        eqb |= (uint32_t)(key[i] == thr) << i;
+        if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+      }
+      // positions at the threshold are taken in position order up to `need`
+      int allow = need - bscan(__popc(eqb));
+      uint32_t bits = gtb;
+      for (uint32_t e = eqb; e != 0u && allow > 0; e &= e - 1u, --allow) bits |= e & (0u - e);
+      int idx = bscan(__popc(bits));
+      int32_t* pn = par + (cur ^ 1) * TK;
+      for (uint32_t bb = bits; bb != 0u; bb &= bb - 1u) {
+        const int pos = tid * C + (__builtin_ffs((int)bb) - 1);
+        pn[idx++] = (pc[pos >> crlg] << crlg) + (pos & (CR - 1));
+      }
+      if (tid * C < (TK << crlg)) selw[tid] = bits;
+      for (int i = take + tid; i < TK; i += 256) pn[i] = -1;
+      __syncthreads();
+    }
+
+    // ---- accumulation of the candidates not passed down
+    if (TRACE) {
+      m_run = -INFINITY;
+      l_part = 0.f;
+#pragma unroll
+      for (int n = 0; n < ND; ++n) O[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int tau = wv; tau < nt; tau += NW) {
+      const int prow = apos - (slot_of(tau) << crlg);
+      const int node0 = node0_of(tau);
+      float qr[KS][8];
+      rot_q<D>(qf, a.cosb + (int64_t)prow * HALF, a.sinb + (int64_t)prow * HALF, kg, qr);
+      bf16x8 qh[KS], ql[KS];
+      to_bf_split<D>(qr, qh, ql);
+      const int posk = wide ? (tau << 4) + u16 : (tau << crlg) + u16;
+      const bool cvk = u16 < CRU && posk < nc;
+      const int64_t krow = (int64_t)(node0 + (cvk ? u16 : 0)) * D;
+      bf16x8 kh[KS], kl[KS];
+      load_kfrag<D>(KH + krow, kg, kh);
+      load_kfrag<D>(KL + krow, kg, kl);
+      f32x4 S = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < KS; ++m) {
+        S = mma32(kh[m], qh[m], S);
+        S = mma32(kl[m], qh[m], S);
+        S = mma32(kh[m], ql[m], S);
+      }
+      // S[r] = score[candidate 4kg + r][g = u16]
+      float sv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int cu = 4 * kg + r;
+        const int pos = wide ? (tau << 4) + cu : (tau << crlg) + cu;
+        bool ok = cu < CRU && pos < nc;
+        if (ok && upper) ok = !((selw[pos >> 5] >> (pos & 31)) & 1u);
+        sv[r] = ok ? S[r] : -INFINITY;
+      }
+      float tm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+      tm = fmaxf(tm, __shfl_xor(tm, 16));
+      tm = fmaxf(tm, __shfl_xor(tm, 32));
+      if (!__any(tm > -INFINITY)) continue;  // every candidate of the tile passed down
+      const float mnew = fmaxf(m_run, tm);
+      const float mref = mnew == -INFINITY ? 0.f : mnew;
+      const float alpha = __builtin_amdgcn_exp2f((m_run - mref) * kLog2e);
+      m_run = mnew;
+      float p[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f((sv[r] - mref) * kLog2e);
+      l_part = l_part * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+#pragma unroll
+      for (int n = 0; n < ND; ++n) O[n] *= alpha;
+      s16x4 ph, pl;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint16_t hb = f_to_bf(p[r]);
+        ph[r] = (short)hb;
+        pl[r] = PREC ? f_to_bfs(p[r] - bf_to_f(hb)) : (short)0;
+      }
+      const int vn = node0 + (4 * kg < CRU ? 4 * kg : 0);
+      const int64_t vbase = ((int64_t)(vn >> 4) * D + u16) * 16 + (vn & 15);
+#pragma unroll
+      for (int n = 0; n < ND; ++n) {
+        const s16x4 vf = *(const s16x4*)(VH + vbase + (int64_t)n * 256);
+        O[n] = mma16(vf, ph, O[n]);
+        if (PREC) {
+          const s16x4 vfl = *(const s16x4*)(VL + vbase + (int64_t)n * 256);
+          O[n] = mma16(vf, pl, O[n]);
+          O[n] = mma16(vfl, ph, O[n]);
+        }
+      }
+    }
+    if (TRACE) {
+      float Ml, Ll;
+      f32x4 Ol[ND];
+      merge_waves(Ml, Ll, Ol);
+      if (wv == 0) trace_store<D>(a, l, hq, gv, kg, Ml, kg == 0 ? Ll : 0.f, Ol);
+    }
+    cur ^= 1;
+  }
+
+  float M, lt;
+  if (TRACE) {
+    if (wv != 0) return;
+    lt = trace_merge<D>(a, hq, gv, kg, M, O);
+  } else {
+    merge_waves(M, lt, O);
+    if (wv != 0) return;
+  }
+  if (gv) {
+    TIn* op = (TIn*)a.out + hq * D;
+    const float inv = 1.f / lt;
+#pragma unroll
+    for (int n = 0; n < ND; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Io<TIn>::st(op + 16 * n + 4 * kg + r, O[n][r] * inv);
+    if (kg == 0) {
+      a.gmax[hq] = M;
+      a.gsum[hq] = lt;
+    }
+  }
+}
+
 template <int D, bool PREC, typename TIn>
-static void launch_fwd(const FwdArgs& a, int max_tiles, dim3 grid, hipStream_t st) {
+static void launch_fwd(const FwdArgs& a, const Plan& P, dim3 grid, hipStream_t st) {
   const bool trace = a.tout != nullptr;
-  if (max_tiles <= 16) {
+  const int max_tiles = P.max_tiles;
+  if (P.wide) {  // one block per query group
+    const unsigned lds = (unsigned)wide_lds(a.TK, a.TK << a.crlg, max_tiles, D).bytes;
+    if (trace)
+      hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, true>), grid, dim3(256), lds, st, a);
+    else
+      hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, false>), grid, dim3(256), lds, st, a);
+  } else if (max_tiles <= 16) {
     if (trace)
       hipLaunchKernelGGL((fwd_reg_kernel<D, PREC, TIn, true>), grid, dim3(256), 0, st, a);
     else
@@ -840,13 +1207,13 @@ static void launch_fwd(const FwdArgs& a, int max_tiles, dim3 grid, hipStream_t s
 }
 
 template <int D>
-static void launch_fwd_d(int dtype, const FwdArgs& a, int max_tiles, dim3 grid, hipStream_t st) {
+static void launch_fwd_d(int dtype, const FwdArgs& a, const Plan& P, dim3 grid, hipStream_t st) {
   if (dtype == HTREE_BF16)
-    launch_fwd<D, false, __bf16>(a, max_tiles, grid, st);
+    launch_fwd<D, false, __bf16>(a, P, grid, st);
   else if (dtype == HTREE_F16)
-    launch_fwd<D, true, _Float16>(a, max_tiles, grid, st);
+    launch_fwd<D, true, _Float16>(a, P, grid, st);
   else
-    launch_fwd<D, true, float>(a, max_tiles, grid, st);
+    launch_fwd<D, true, float>(a, P, grid, st);
 }
 
 }  // namespace htree
@@ -903,18 +1270,20 @@ static int forward_impl(const htree_dims* d, float scale, const void* q, const v
   a.L = P.L;
   a.scale = scale;
   const int64_t groups = (int64_t)d->B * d->H_kv * d->T;
-  const int64_t nblk = (groups + kWavesPerBlock - 1) / kWavesPerBlock;
+  // blocks dealt round-robin to the 8 XCDs: XCD x gets blocks x, x+8, ...,
+  // which map to a contiguous range of query groups (one tree per XCD's L2)
+  const int64_t nblk = P.wide ? groups : (groups + kWavesPerBlock - 1) / kWavesPerBlock;
   const int64_t per = (nblk + 7) / 8;
   if (per * 8 > 0x7fffffff) return HTREE_EUNSUPPORTED;
   a.per_xcd = (int32_t)per;
   const dim3 grid((unsigned)(per * 8));
   hipStream_t st = (hipStream_t)stream;
   if (d->D == 128)
-    launch_fwd_d<128>(d->dtype, a, P.max_tiles, grid, st);
+    launch_fwd_d<128>(d->dtype, a, P, grid, st);
   else if (d->D == 32)
-    launch_fwd_d<32>(d->dtype, a, P.max_tiles, grid, st);
+    launch_fwd_d<32>(d->dtype, a, P, grid, st);
   else
-    launch_fwd_d<64>(d->dtype, a, P.max_tiles, grid, st);
+    launch_fwd_d<64>(d->dtype, a, P, grid, st);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? HTREE_OK : (int)e;
 }

@@ -27,13 +27,15 @@ int make_plan(const htree_dims* d, Plan* p) {
     return HTREE_ECONFIG;
   const int CR = d->compression_rate;
   const int64_t max_tiles = (int64_t)d->top_k * (CR > 16 ? CR : 16) / 16;
+  const bool wide = max_tiles > kMaxTiles || d->top_k > kMaxTK;
   if ((d->D != 32 && d->D != 64 && d->D != 128) || d->H / d->H_kv > 16 || CR < 4 || CR > 64 ||
-      max_tiles > 64 || d->top_k > kMaxTK)
+      (wide && (d->top_k > kWideMaxTK || (int64_t)d->top_k * CR > kWideMaxPos)))
     return HTREE_EUNSUPPORTED;
 
   memset(p, 0, sizeof(*p));
   p->precise = d->dtype != HTREE_BF16;
   p->max_tiles = (int)max_tiles;
+  p->wide = wide;
   int lg = 0;
   while ((1 << lg) < CR) ++lg;
   p->cr_log2 = lg;
@@ -190,8 +192,9 @@ const char* htree_strerror(int status) {
              "and rope_rows >= top_k_per_layer * compression_rate";
     case HTREE_EUNSUPPORTED:
       return "configuration outside this HIP build: needs D in {32,64,128}, H/H_kv <= 16, "
-             "4 <= compression_rate <= 64, top_k_per_layer <= 64 and "
-             "top_k_per_layer * max(compression_rate,16) / 16 <= 64";
+             "4 <= compression_rate <= 64, top_k_per_layer <= 512 and "
+             "top_k_per_layer * compression_rate <= 8192 (where top_k_per_layer > 64 or "
+             "top_k_per_layer * max(compression_rate,16) / 16 > 64)";
     case HTREE_EWORKSPACE: return "workspace smaller than htree_tree_workspace_bytes()";
     default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown htree status";
   }

@@ -66,7 +66,10 @@ def test_baseline_level_counts():
     (dict(rope_rows=100), N.HTREE_ECONFIG),
     (dict(D=96), N.HTREE_EUNSUPPORTED),
     (dict(H=64, H_kv=2), N.HTREE_EUNSUPPORTED),        # group of 32
-    (dict(top_k=128, max_top_nodes=128, rope_rows=2048), N.HTREE_EUNSUPPORTED),
+    (dict(D=16), N.HTREE_EUNSUPPORTED),
+    (dict(top_k=1024, max_top_nodes=128, rope_rows=16384), N.HTREE_EUNSUPPORTED),  # top_k > 512
+    (dict(top_k=512, compression_rate=32, max_top_nodes=128, rope_rows=16384),
+     N.HTREE_EUNSUPPORTED),                            # 16384 candidates per level
 ])
 def test_invalid_configs_raise_assertion(kw, code):
     d = dims(**kw)

@@ -138,3 +138,46 @@ def test_forward_deterministic():
     a = run_fwd(q, k, v, 16, 16, 128)
     b = run_fwd(q, k, v, 16, 16, 128)
     assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+WIDE = [
+    # B, T, H, Hkv, D, CR, TK, MTN, dtype, seed, skewed: top_k > 64 or more than
+    # 64 candidate tiles per level (one block of four waves per query group)
+    (1, 3000, 16, 4, 32, 16, 128, 2048, "float32", 21, False),
+    (1, 12000, 16, 4, 32, 16, 512, 8192, "float16", 22, False),  # correctness_test.py defaults
+    (1, 5000, 8, 2, 64, 4, 256, 1024, "bfloat16", 23, False),     # CR < 16: one tile per parent
+    (1, 6000, 8, 1, 128, 32, 128, 4096, "bfloat16", 24, False),   # CR > 16
+    (1, 8192, 16, 2, 64, 16, 256, 4096, "bfloat16", 25, True),    # many exact-zero importances
+]
+
+
+@pytest.mark.parametrize("cfg", WIDE, ids=lambda c: f"T{c[1]}D{c[4]}cr{c[5]}tk{c[6]}{c[8]}{'skew' if c[10] else ''}")
+def test_forward_wide_matches_oracle(cfg):
+    """The reference's default regime (top_k up to 512, up to 8192 candidates
+    per level): sampled rows against the oracle, teacher-forced on the
+    device's lists; every row through the list invariants."""
+    B, T, H, Hkv, D, CR, TK, MTN, dtype, seed, skewed = cfg
+    print(f"case {cfg}", flush=True)
+    if skewed:
+        q, k, v, _ = skewed_inputs(B, T, H, Hkv, D, dtype, seed)
+    else:
+        q, k, v = inputs(B, T, H, Hkv, D, dtype, seed)
+    out, par, gmax, gsum, ctx = run_fwd(q, k, v, CR, TK, MTN)
+    assert np.all(np.isfinite(out))
+    L = par.shape[0]
+    t = np.arange(T)
+    for l in range(L - 1, 0, -1):
+        sel = par[l - 1]
+        cnt = (sel >= 0).sum(-1)
+        want = np.array([orc.candidate_counts(int(x), CR, TK, L)[l][1] for x in t])
+        assert np.array_equal(cnt, np.broadcast_to(want[None, :, None], cnt.shape)), f"level {l} counts"
+        right = (t // CR ** l).astype(np.int32)
+        assert np.all(np.any(sel == right[None, :, None, None], axis=-1)), f"level {l} rightmost"
+        nxt_valid = sel[..., 1:] >= 0
+        assert np.all((np.diff(sel, axis=-1) > 0) | ~nxt_valid), f"level {l} ascending"
+    rng = np.random.default_rng(seed)
+    n = 160
+    rows = np.stack([rng.integers(0, B, n), np.sort(rng.choice(T, n, replace=False))], 1)
+    rows = np.concatenate([rows, [[0, 0], [0, T - 1]]]).astype(np.int32)
+    rep = check_forward(q, k, v, CR, TK, MTN, dtype, rows=rows, out_dev=out, parents_dev=par)
+    print(rep, flush=True)

@@ -38,6 +38,7 @@ CASES = [
     (1, 3000, 8, 1, 64, 4, 32, 64, "bfloat16", 14),     # 32 tiles: multi-pass kernel, 4 levels
     (1, 700, 8, 2, 64, 8, 16, 128, "float32", 15),      # CR < 16
     (1, 1200, 16, 4, 32, 16, 16, 128, "float16", 16),   # D = 32
+    (1, 1500, 8, 2, 32, 4, 128, 256, "float32", 17),    # top_k 128: block-per-group kernel
 ]
 
 
