@@ -60,7 +60,6 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
   int rc = make_plan(d, &b->P);
   if (rc) return rc;
   const Plan& P = b->P;
-  if (P.wide) return HTREE_EUNSUPPORTED;  // the backward's parent lists live in one wave
   const int CR = d->compression_rate;
   b->G = d->H / d->H_kv;
   b->tpp = CR > 16 ? CR / 16 : 1;
@@ -103,7 +102,8 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
   // dS of every (entry, tile), 1 KB each, kept for the dq pass when the whole
   // backward's worth fits the budget; otherwise dq recomputes the scores
   const int64_t ds_level = b->max_entries * b->tpp * 1024;
-  b->use_ds = ds_level * P.L <= kDsBudget;
+  // (wide configurations: dq recomputes, its list per wave lives in LDS)
+  b->use_ds = !P.wide && ds_level * P.L <= kDsBudget;
   for (int l = 0; l < P.L; ++l) {
     b->off_rec[l] = (b->use_ds || l == 0) ? take(b->max_entries * 16) : b->off_rec[0];
     b->off_emap[l] = b->use_ds ? take(b->max_entries * 16) : -1;
@@ -403,6 +403,60 @@ __global__ __launch_bounds__(256) void record_kernel(const int32_t* __restrict__
   const int e = rowoff[row] + wpre[wi] + __popc(bm[wi] & ((1u << (t & 31)) - 1u));
   rec[e] = make_int4(t, (nc - 1 - (s << crlg)) | (s << 16), (int)(uint32_t)m, (int)(uint32_t)(m >> 32));
   if (emap) emap[idx] = make_int4(e, (int)(uint32_t)m, (int)(uint32_t)(m >> 32), 0);
+}
+
+// record_kernel for lists longer than a wave (top_k > 64): one thread per
+// (query group, slot s); the list's valid length and the children of p in
+// the next-level list come from binary searches (both lists are ascending
+// with a -1 suffix).
+__global__ __launch_bounds__(256) void record_wide_kernel(
+    const int32_t* __restrict__ par, const int32_t* __restrict__ par_next,
+    const uint32_t* __restrict__ bm, const int32_t* __restrict__ wpre,
+    const int32_t* __restrict__ rowoff, int T, int Hkv, int TK, int64_t Pl, int64_t W, int64_t pw,
+    int CR, int crlg, int64_t total, int4* __restrict__ rec) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int p = par[idx];
+  if (p < 0) return;
+  const int64_t grp = idx / TK;
+  const int s = (int)(idx % TK);
+  const int32_t* lst = par + grp * TK;
+  int lo = s + 1, hi = TK;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (lst[mid] >= 0) lo = mid + 1; else hi = mid;
+  }
+  const int np = lo;
+  unsigned long long drop = 0ull;  // children of p passed to level l-1
+  if (par_next) {
+    const int32_t* nx = par_next + grp * TK;
+    const int first = p << crlg;
+    int a = 0, e = TK;
+    while (a < e) {
+      const int mid = (a + e) >> 1;
+      const int v = nx[mid];
+      if (v >= 0 && v < first) a = mid + 1; else e = mid;
+    }
+    for (int i = a; i < TK; ++i) {
+      const int v = nx[i];
+      if (v < 0 || (v >> crlg) != p) break;
+      drop |= 1ull << (v & (CR - 1));
+    }
+  }
+  const int h = (int)(grp % Hkv);
+  const int64_t bt = grp / Hkv;
+  const int t = (int)(bt % T);
+  const int64_t b = bt / T;
+  const int ct = (int)((t / pw) & (CR - 1));
+  const int nc = ((np - 1) << crlg) + ct + 1;
+  const int nvalid = nc - (s << crlg);
+  unsigned long long m = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
+  if (CR < 64) m &= (1ull << CR) - 1ull;
+  m &= ~drop;
+  const int64_t row = (b * Hkv + h) * Pl + p;
+  const int64_t wi = row * W + (t >> 5);
+  const int e = rowoff[row] + wpre[wi] + __popc(bm[wi] & ((1u << (t & 31)) - 1u));
+  rec[e] = make_int4(t, (nc - 1 - (s << crlg)) | (s << 16), (int)(uint32_t)m, (int)(uint32_t)(m >> 32));
 }
 
 // ---------------------------------------------------------------- dkv
@@ -939,11 +993,14 @@ __device__ __forceinline__ void rot_acc(f32x4 (&x)[D / 16], const float* c, cons
 // a frame that turns with it, X <- R(X, -CR) + dq~_tile, so that
 //   sum_s R^-1(dq~_s, a - s CR) = R^-1(X, n_c-1 - (np-1) CR) = R(X, -c_t)
 // needs one table rotation per level.
-template <int D, bool PREC, typename TIn>
+template <int D, bool PREC, typename TIn, int MAXTK>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void dq_kernel(const DqArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
-  __shared__ int32_t lst[kWavesPerBlock][kMaxTK];
-  __shared__ uint32_t selw[kWavesPerBlock][32];
+  // list capacity; selection bits of the 16-candidate tile positions
+  // (kMaxTiles or, for MAXTK = kWideMaxTK, kWideMaxPos / 16 tiles)
+  constexpr int SWW = MAXTK > kMaxTK ? kWideMaxPos / 32 : kMaxTiles / 2;
+  __shared__ int32_t lst[kWavesPerBlock][MAXTK];
+  __shared__ uint32_t selw[kWavesPerBlock][SWW];
   __shared__ float rot_m[2][HALF];  // cos(CR theta), -sin(CR theta)
   __shared__ f32x4 acc_l[kWavesPerBlock][D / 16][64];  // dq over the finished levels
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -982,10 +1039,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   for (int l = a.L - 1; l >= 0; --l) {
     const DqLevel P = a.lv[l];
     wave_sync();
-    const int pe = lane < TK ? a.parents[l * lstride + grp * TK + lane] : -1;
-    if (lane < TK) LS[lane] = pe;
-    if (lane < 32) SW[lane] = 0u;
-    const int np = __popcll(__ballot(pe >= 0));
+    int np = 0;
+    for (int i0 = 0; i0 < TK; i0 += 64) {
+      const int pe = i0 + lane < TK ? a.parents[l * lstride + grp * TK + i0 + lane] : -1;
+      if (i0 + lane < TK) LS[i0 + lane] = pe;
+      np += __popcll(__ballot(pe >= 0));
+    }
+    for (int i = lane; i < SWW; i += 64) SW[i] = 0u;
     if (np <= 0) continue;
     const int ct = (int)((t / P.pw) & (CR - 1));
     const int nc = ((np - 1) << crlg) + ct + 1;
@@ -994,16 +1054,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     wave_sync();
     if (l > 0) {
       // positions of the nodes passed to level l-1 (not accumulated here)
-      const int en = lane < TK ? a.parents[(l - 1) * lstride + grp * TK + lane] : -1;
-      if (en >= 0) {
-        const int pp = en >> crlg;
-        int lo = 0, hi = np - 1;
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if (LS[mid] < pp) lo = mid + 1; else hi = mid;
+      for (int i0 = 0; i0 < TK; i0 += 64) {
+        const int en = i0 + lane < TK ? a.parents[(l - 1) * lstride + grp * TK + i0 + lane] : -1;
+        if (en >= 0) {
+          const int pp = en >> crlg;
+          int lo = 0, hi = np - 1;
+          while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (LS[mid] < pp) lo = mid + 1; else hi = mid;
+          }
+          const int j = (lo << 4) * (wide ? 0 : 1) + (wide ? (lo << crlg) : 0) + (en & (CR - 1));
+          atomicOr(&SW[j >> 5], 1u << (j & 31));
         }
-        const int j = (lo << 4) * (wide ? 0 : 1) + (wide ? (lo << crlg) : 0) + (en & (CR - 1));
-        atomicOr(&SW[j >> 5], 1u << (j & 31));
       }
       wave_sync();
     }
@@ -1349,10 +1411,16 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     hipLaunchKernelGGL(piece_kernel, dim3((unsigned)((nrows + 255) / 256)), dim3(256), 0, st, cnt,
                        rowoff, poff, nrows, (int)BP.piece, ptab, npieces);
     int4* recs = (int4*)(ws + BP.off_rec[l]);
-    hipLaunchKernelGGL(record_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
-                       parents + l * lstride, l > 0 ? parents + (l - 1) * lstride : nullptr, bm, wpre,
-                       rowoff, d->T, d->H_kv, d->top_k, Pl, BP.W, P.pw[l], CR, P.cr_log2, ent, recs,
-                       BP.use_ds ? (int4*)(ws + BP.off_emap[l]) : nullptr);
+    if (d->top_k > 64)
+      hipLaunchKernelGGL(record_wide_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
+                         parents + l * lstride, l > 0 ? parents + (l - 1) * lstride : nullptr, bm,
+                         wpre, rowoff, d->T, d->H_kv, d->top_k, Pl, BP.W, P.pw[l], CR, P.cr_log2,
+                         ent, recs);
+    else
+      hipLaunchKernelGGL(record_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
+                         parents + l * lstride, l > 0 ? parents + (l - 1) * lstride : nullptr, bm,
+                         wpre, rowoff, d->T, d->H_kv, d->top_k, Pl, BP.W, P.pw[l], CR, P.cr_log2,
+                         ent, recs, BP.use_ds ? (int4*)(ws + BP.off_emap[l]) : nullptr);
     DkvArgs a;
     memset(&a, 0, sizeof(a));
     a.kh = (const uint16_t*)(tws + P.off_kh[l]);
@@ -1477,8 +1545,12 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.TK = d->top_k;
     a.L = P.L;
     a.scale = scale;
-    hipLaunchKernelGGL((dq_kernel<D, PREC, T>), dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, st,
-                       a);
+    if (P.wide)
+      hipLaunchKernelGGL((dq_kernel<D, PREC, T, kWideMaxTK>), dim3((unsigned)((groups + 3) / 4)),
+                         dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((dq_kernel<D, PREC, T, kMaxTK>), dim3((unsigned)((groups + 3) / 4)),
+                         dim3(256), 0, st, a);
   }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? HTREE_OK : (int)e;

@@ -160,3 +160,51 @@ def test_autograd_contract():
     for got, ref in ((qg.grad, dq), (kg.grad, dk), (vg.grad, dv)):
         r = torch.from_numpy(ref).bfloat16().float().numpy()
         assert np.array_equal(got.float().cpu().numpy(), r)
+
+
+WIDE = [
+    # top_k > 64 or more than 64 candidate tiles per level
+    (1, 1500, 8, 2, 32, 4, 128, 256, "float32", 41),    # CR 4, 3 levels, evictions at level 1
+    (1, 2000, 8, 2, 64, 16, 128, 1024, "bfloat16", 42),  # 125 tiles at the bottom
+]
+
+
+@pytest.mark.parametrize("cfg", WIDE, ids=lambda c: f"T{c[1]}D{c[4]}cr{c[5]}tk{c[6]}{c[8]}")
+def test_backward_wide_matches_oracle(cfg):
+    B, T, H, Hkv, D, CR, TK, MTN, dtype, seed = cfg
+    print(f"case {cfg}", flush=True)
+    q, k, v, dO = inputs(B, T, H, Hkv, D, dtype, seed, dO=True)
+    out, par, gmax, gsum, dq, dk, dv = run(q, k, v, dO, CR, TK, MTN)
+    rep = check_backward(q, k, v, dO, CR, TK, MTN, dtype, out, par, gmax, gsum, dq, dk, dv)
+    print(rep, flush=True)
+
+
+def test_backward_reference_default_regime():
+    """correctness_test_bwd.py defaults (T=12000, Hq=16, Hkv=4, K=V=32, fp32,
+    CR=16, top_k=512, MTN=8192): dq on sampled rows vs the oracle; the sum
+    of dv over the nodes equals the sum of dO over the group's queries and
+    heads (every head's probabilities sum to 1, the pooling backward keeps
+    sums)."""
+    B, T, H, Hkv, D, CR, TK, MTN = 1, 12000, 16, 4, 32, 16, 512, 8192
+    q, k, v, dO = inputs(B, T, H, Hkv, D, "float32", 43, dO=True)
+    out, par, gmax, gsum, dq, dk, dv = run(q, k, v, dO, CR, TK, MTN)
+    assert np.all(np.isfinite(dq)) and np.all(np.isfinite(dk)) and np.all(np.isfinite(dv))
+    G = H // Hkv
+    want = dO.float().numpy().reshape(B, T, Hkv, G, D).astype(np.float64).sum(axis=(1, 3))
+    got = dv.astype(np.float64).sum(axis=1)
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4 * np.sqrt(T * G))
+    tree = orc.Tree(k.float().numpy(), v.float().numpy(), CR, MTN, TK, "float32")
+    rng = np.random.default_rng(4)
+    n = 40
+    rows = np.stack([np.zeros(n, int), np.sort(rng.choice(T, n, replace=False))], 1).astype(np.int32)
+    rows = np.concatenate([rows, [[0, T - 1]]]).astype(np.int32)
+    pr = par[:, rows[:, 0], rows[:, 1]]
+    fw = orc.forward(q.float().numpy(), tree, D ** -0.5, rows=rows, forced=pr)
+    o = out[rows[:, 0], rows[:, 1]]
+    d = dO.float().numpy()[rows[:, 0], rows[:, 1]]
+    delta = (o.astype(np.float64) * d).sum(-1).astype(np.float32)
+    ref = orc.backward_dq_rows(q.float().numpy(), tree, D ** -0.5, rows, pr, fw["gmax"], fw["gsum"],
+                               delta, d)
+    ok, worst = close(dq[rows[:, 0], rows[:, 1]], ref, "float32")
+    print("default-regime dq worst", worst, flush=True)
+    assert ok
