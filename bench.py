@@ -2,6 +2,11 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C2] [--no-cpu]
 
+Other workloads (--workload): C3, C4, C5, REF_FWD (the
+reference's speed_test.py defaults: T=120000, Hq=64, Hkv=4, D=32, fp32, CR=16,
+top_k=512, MTN=8192; forward only, as that script) and REF_BWD (its
+speed_test_bwd.py defaults: T=12000, the same heads and tree).
+
 Workload ("C2"): B=1, T=32768, Hq=32, Hkv=2 (group
 16), D=128, bf16, causal, CR=16, MTN=128, TK=16; q/k/v/dO iid N(0,1) drawn
 on the host from a fixed seed and copied to HBM before timing.
@@ -31,19 +36,23 @@ METRIC = "fwd & bwd tokens/s at T=32K, Hq=32/Hkv=2, D=128, bf16; % of HBM roofli
 HBM_PEAK = 8.0e12
 
 WORKLOADS = {
-    # name: (B, T, Hq, Hkv, D, CR, TK, MTN)
-    "C2": (1, 32768, 32, 2, 128, 16, 16, 128),
-    "C3": (4, 16384, 32, 4, 128, 16, 16, 128),
-    "C4": (1, 131072, 64, 8, 128, 32, 32, 256),
-    "C5": (2, 65536, 32, 2, 128, 16, 16, 128),
+    # name: (B, T, Hq, Hkv, D, CR, TK, MTN), dtype, backward in the step
+    "C2": ((1, 32768, 32, 2, 128, 16, 16, 128), "bfloat16", True),
+    "C3": ((4, 16384, 32, 4, 128, 16, 16, 128), "bfloat16", True),
+    "C4": ((1, 131072, 64, 8, 128, 32, 32, 256), "bfloat16", True),
+    "C5": ((2, 65536, 32, 2, 128, 16, 16, 128), "bfloat16", True),
+    "REF_FWD": ((1, 120000, 64, 4, 32, 16, 512, 8192), "float32", False),
+    "REF_BWD": ((1, 12000, 64, 4, 32, 16, 512, 8192), "float32", True),
 }
+DT_SHORT = {"bfloat16": "bf16", "float16": "f16", "float32": "f32"}
 
 
 def measured_traffic(workload: str):
     """HBM bytes per launch of the fused forward kernel from the committed
     rocprofv3 PMC summary of this workload (FETCH_SIZE + WRITE_SIZE, each
     scaled by the same counter's reading of the calibration copy), or None."""
-    path = os.path.join(ROOT, "profiles", f"fwd_reg_kernel_{workload.lower()}_traffic.json")
+    kern = "fwd_wide_kernel" if workload.startswith("REF") else "fwd_reg_kernel"
+    path = os.path.join(ROOT, "profiles", f"{kern}_{workload.lower()}_traffic.json")
     try:
         with open(path) as f:
             rec = json.load(f)
@@ -63,7 +72,7 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(q, k, v, dO, out, gmax, gsum, parents, CR, TK, MTN, budget_s=12.0):
+def cpu_baseline(q, k, v, dO, out, gmax, gsum, parents, CR, TK, MTN, dtype, budget_s=12.0):
     """Oracle (CPU restatement of src/naive.py, one thread) on random query
     rows of the workload until `budget_s` seconds of forward work have run,
     then the same rows through the backward's per-row work."""
@@ -73,7 +82,7 @@ def cpu_baseline(q, k, v, dO, out, gmax, gsum, parents, CR, TK, MTN, budget_s=12
 
     B, T, H, D = q.shape
     qn = q.float().cpu().numpy()
-    tree = orc.Tree(k.float().cpu().numpy(), v.float().cpu().numpy(), CR, MTN, TK, "bfloat16")
+    tree = orc.Tree(k.float().cpu().numpy(), v.float().cpu().numpy(), CR, MTN, TK, dtype)
     rng = np.random.default_rng(0)
     done, t_fwd, rows_all = 0, 0.0, []
     while t_fwd < budget_s and done < B * T:
@@ -120,31 +129,33 @@ def main():
     from htree_amd import _native as N
     from htree_amd.workmodel import work
 
-    B, T, H, Hkv, D, CR, TK, MTN = WORKLOADS[args.workload]
+    (B, T, H, Hkv, D, CR, TK, MTN), dtype, with_bwd = WORKLOADS[args.workload]
+    tdt = getattr(torch, dtype)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     g = torch.Generator().manual_seed(1234)
-    q = torch.randn(B, T, H, D, generator=g).bfloat16().to(dev)
-    k = torch.randn(B, T, Hkv, D, generator=g).bfloat16().to(dev)
-    v = torch.randn(B, T, Hkv, D, generator=g).bfloat16().to(dev)
-    dO = torch.randn(B, T, H, D, generator=g).bfloat16().to(dev)
-    has_bwd = hasattr(htree_amd, "htree_backward")
+    q = torch.randn(B, T, H, D, generator=g).to(tdt).to(dev)
+    k = torch.randn(B, T, Hkv, D, generator=g).to(tdt).to(dev)
+    v = torch.randn(B, T, Hkv, D, generator=g).to(tdt).to(dev)
+    dO = torch.randn(B, T, H, D, generator=g).to(tdt).to(dev)
+    has_bwd = with_bwd and hasattr(htree_amd, "htree_backward")
     torch.cuda.synchronize()
-    print(f"# workload {args.workload} B={B} T={T} H={H} Hkv={Hkv} D={D} CR={CR} TK={TK} MTN={MTN}"
-          f" backward={'yes' if has_bwd else 'not built'}", file=sys.stderr, flush=True)
+    print(f"# workload {args.workload} B={B} T={T} H={H} Hkv={Hkv} D={D} {dtype} CR={CR} TK={TK} "
+          f"MTN={MTN} backward={'yes' if has_bwd else 'no'}", file=sys.stderr, flush=True)
 
     def step():
+        if not has_bwd:  # forward only (speed_test.py): nothing kept for a backward
+            return htree_amd.htree_forward(q, k, v, CR, MTN, TK)
         out, ctx = htree_amd.htree_forward(q, k, v, CR, MTN, TK, _save_for_backward=True)
-        if has_bwd:
-            htree_amd.htree_backward(dO, q, out, ctx)
-        return out, ctx
+        htree_amd.htree_backward(dO, q, out, ctx)
+        return out
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        out, ctx = step()
+        step()
     torch.cuda.synchronize()
     step_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     print(f"# timed {args.steps} steps: {step_ms:.3f} ms/step", file=sys.stderr, flush=True)
@@ -155,7 +166,10 @@ def main():
     e0, e1, e2 = ev(), ev(), ev()
     e0.record(stream)
     for _ in range(args.steps):
-        out, ctx = htree_amd.htree_forward(q, k, v, CR, MTN, TK, _save_for_backward=True)
+        if has_bwd:
+            out, ctx = htree_amd.htree_forward(q, k, v, CR, MTN, TK, _save_for_backward=True)
+        else:
+            out = htree_amd.htree_forward(q, k, v, CR, MTN, TK)
     e1.record(stream)
     if has_bwd:
         for _ in range(args.steps):
@@ -164,6 +178,8 @@ def main():
     torch.cuda.synchronize()
     fwd_ms = e0.elapsed_time(e1) / args.steps
     bwd_ms = e1.elapsed_time(e2) / args.steps if has_bwd else None
+    if not has_bwd:
+        out, ctx = htree_amd.htree_forward(q, k, v, CR, MTN, TK, _save_for_backward=True)
 
     d = ctx["dims"]
     ws = ctx["packed_tree"]
@@ -192,13 +208,14 @@ def main():
     torch.cuda.synchronize()
     del cal_src, cal_dst
 
-    w = work(B, T, H, Hkv, D, CR, TK, MTN, 2)
+    w = work(B, T, H, Hkv, D, CR, TK, MTN, tdt.itemsize)
     traffic = measured_traffic(args.workload)
     achieved = w.fwd_kernel_bytes / (kern_ms * 1e-3)
     fwd_tok = B * T / (fwd_ms * 1e-3)
     step_s = (fwd_ms + (bwd_ms or 0.0)) * 1e-3
     res = {
-        "metric": METRIC,
+        "metric": METRIC if args.workload == "C2" else
+        f"{'fwd & bwd' if has_bwd else 'fwd'} tokens/s at {args.workload}; % of HBM roofline",
         "value": B * T / step_s,
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -208,12 +225,12 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": DT_SHORT[dtype],
         "data": "synthetic: q,k,v,dO iid N(0,1) from torch.Generator seed 1234",
         "config": {
-            "workload": f"{args.workload}: B={B} T={T} Hq={H} Hkv={Hkv} D={D} bf16 causal "
-                        f"CR={CR} MTN={MTN} TK={TK}",
-            "step": "htree_forward + htree_backward" if has_bwd else "htree_forward (backward not built)",
+            "workload": f"{args.workload}: B={B} T={T} Hq={H} Hkv={Hkv} D={D} {DT_SHORT[dtype]} "
+                        f"causal CR={CR} MTN={MTN} TK={TK}",
+            "step": "htree_forward + htree_backward" if has_bwd else "htree_forward",
         },
         "fwd": {"ms": fwd_ms, "tokens_per_s": fwd_tok,
                 "hbm_roofline_frac": w.fwd_bytes / (fwd_ms * 1e-3) / HBM_PEAK,
@@ -224,7 +241,8 @@ def main():
             "algorithmic_bytes": w.bwd_bytes},
         "wall_ms_per_step": step_ms,
         "roofline": {
-            "kernel": "htree::fwd_reg_kernel (fused forward, all levels)",
+            "kernel": ("htree::fwd_wide_kernel" if ctx["dims"].top_k > 64 else "htree::fwd_reg_kernel")
+                      + " (fused forward, all levels)",
             "bound": "hbm",
             "achieved": achieved / 1e9,
             "peak": HBM_PEAK / 1e9,
@@ -237,7 +255,8 @@ def main():
         },
     }
     if not args.no_cpu:
-        cb = cpu_baseline(q, k, v, dO, out, gmax, gsum, ctx.get("parents_stacked"), CR, TK, MTN)
+        cb = cpu_baseline(q, k, v, dO, out, gmax, gsum, ctx.get("parents_stacked") if has_bwd else None,
+                          CR, TK, MTN, dtype)
         tot = 1.0 / (1.0 / cb["fwd_tok_s"] + (1.0 / cb["bwd_tok_s"] if has_bwd and "bwd_tok_s" in cb else 0.0))
         res["cpu_baseline"] = {
             "value": tot, "unit": "tokens/s", "cores": 1, "kind": "port",
