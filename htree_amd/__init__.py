@@ -14,11 +14,12 @@ from .parallel import (HTREE_SCORE_NEG_INF, HTREE_SCORE_VALID_THRESHOLD, htree_f
 from .backward import (HTreeFunction, HTreeTritonFunction, htree_backward, htree_forward_autograd,
                        htree_forward_triton_autograd)
 from .trace import LayerTrace, compare_traces, run_parallel_with_trace
+from .topk import topk_rows
 
 
 __all__ = [
     "htree_forward", "htree_forward_parents", "htree_backward", "htree_forward_triton_autograd",
     "htree_forward_autograd", "HTreeTritonFunction", "HTreeFunction", "rope_cache",
     "HTREE_SCORE_NEG_INF", "HTREE_SCORE_VALID_THRESHOLD", "LayerTrace", "run_parallel_with_trace",
-    "compare_traces",
+    "compare_traces", "topk_rows",
 ]

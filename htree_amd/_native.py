@@ -30,7 +30,7 @@ EXPORTS = (
     "htree_strerror", "htree_levels", "htree_tree_workspace_bytes", "htree_tree_build",
     "htree_forward", "htree_backward_workspace_bytes", "htree_backward",
     "htree_train_scores_bytes", "htree_forward_train", "htree_backward_train",
-    "htree_forward_trace",
+    "htree_forward_trace", "htree_topk_rows",
 )
 
 
@@ -76,6 +76,9 @@ def lib() -> ctypes.CDLL:
     if hasattr(L, "htree_forward_trace"):
         L.htree_forward_trace.restype = ctypes.c_int
         L.htree_forward_trace.argtypes = [DP, F, P, P, I64, P, P, P, P, P, P, P, P, P, P]
+    if hasattr(L, "htree_topk_rows"):
+        L.htree_topk_rows.restype = ctypes.c_int
+        L.htree_topk_rows.argtypes = [P, I64, I32, I32, P, I32, P, P, P, P]
     if hasattr(L, "htree_backward"):
         L.htree_backward_workspace_bytes.restype = ctypes.c_int
         L.htree_backward_workspace_bytes.argtypes = [DP, ctypes.POINTER(I64)]

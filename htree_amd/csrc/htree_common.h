@@ -246,6 +246,93 @@ __device__ __forceinline__ void rope_frag(const float (&x)[D / 32][8], const flo
   }
 }
 
+// sum over the 16 lanes of a DPP row (quad xor 1, quad xor 2, half-row
+// mirror, row mirror); every lane of the row gets the result
+__device__ __forceinline__ int row_sum16i(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false);
+  return x;
+}
+
+// Block-wide Top-K of a block of kWideWaves waves: thread i holds the keys of
+// positions C*i .. C*i+C-1 in registers (key 0 = no candidate; a larger key
+// is a larger value).  select() finds the `take` largest keys with a bitwise
+// radix select from bit `top_bit` down (per step: a per-lane count, a DPP row
+// sum and one block barrier; the reduction slots alternate, so a slot is
+// rewritten only after every wave has passed the barrier that follows its
+// last read), gives the ties at the threshold to the lowest positions (the
+// order of a stable descending sort) by an exclusive scan in position order,
+// and returns this thread's selection bits; `before` receives the number of
+// selected positions below this thread's first (their rank in ascending
+// position order).  `red` is 32 ints of LDS.
+template <int C>
+struct BlockSelect {
+  static_assert(C <= 32, "selection bits are one 32-bit word per thread");
+  int32_t* red;
+  int lane, wv;
+  int rc = 0, rs = 0;
+
+  __device__ __forceinline__ int count(const uint32_t (&key)[C], uint32_t thr, bool strict) {
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+      c += strict ? key[i] > thr : key[i] >= thr;
+      if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // keep the compare masks short-lived
+    }
+    c = row_sum16i(c);
+    c += __shfl_xor(c, 16);
+    c += __shfl_xor(c, 32);
+    int32_t* r = red + 8 * rc;
+    rc ^= 1;
+    if (lane == 0) r[wv] = c;
+    __syncthreads();
+    int tot = 0;
+#pragma unroll
+    for (int w = 0; w < kWideWaves; ++w) tot += r[w];
+    return tot;
+  }
+  // exclusive scan in thread order
+  __device__ __forceinline__ int scan(int v) {
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o);
+      if (lane >= o) x += y;
+    }
+    int32_t* r = red + 16 + 8 * rs;
+    rs ^= 1;
+    if (lane == 63) r[wv] = x;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < wv; ++w) base += r[w];
+    return base + x - v;
+  }
+  __device__ __forceinline__ uint32_t select(const uint32_t (&key)[C], int take, int top_bit,
+                                             int& before) {
+    uint32_t thr = 0u;
+#pragma unroll 1
+    for (int bit = top_bit; bit >= 0; --bit) {
+      const uint32_t c = thr | (1u << bit);
+      if (count(key, c, false) >= take) thr = c;
+    }
+    const int need = take - count(key, thr, true);
+    uint32_t gtb = 0u, eqb = 0u;  // this thread's positions above / at the threshold
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+      gtb |= (uint32_t)(key[i] > thr) << i;
+      eqb |= (uint32_t)(key[i] == thr) << i;
+      if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+    }
+    int allow = need - scan(__popc(eqb));
+    uint32_t bits = gtb;
+    for (uint32_t e = eqb; e != 0u && allow > 0; e &= e - 1u, --allow) bits |= e & (0u - e);
+    before = scan(__popc(bits));
+    return bits;
+  }
+};
+
 // Query fragment of a lane (head u16, the lane group's d-slots) kept in its
 // input type; get() returns it in fp32 times `scale`.
 template <int D, typename TIn>

@@ -448,13 +448,6 @@ __device__ __forceinline__ float row_sum16(float x) {
   x += dpp<0x140>(x);
   return x;
 }
-__device__ __forceinline__ int row_sum16i(int x) {
-  x += __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);
-  x += __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);
-  x += __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false);
-  x += __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false);
-  return x;
-}
 __device__ __forceinline__ float row_max16(float x) {
   x = fmaxf(x, dpp<0xB1>(x));
   x = fmaxf(x, dpp<0x4E>(x));
@@ -887,40 +880,7 @@ __global__ __launch_bounds__(256) void fwd_wide_kernel(const FwdArgs a) {
     for (int i = tid; i < TK; i += 256) par[i] = i < nvp ? i : -1;
   }
 
-  // block sum of per-key predicates (one barrier; slots alternate)
-  int rc_sel = 0, rs_sel = 0;
-  auto bcount = [&](const uint32_t (&key)[C], uint32_t thr, bool strict) {
-    int c = 0;
-#pragma unroll
-    for (int i = 0; i < C; ++i) {
-      c += strict ? key[i] > thr : key[i] >= thr;
-      if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // keep the compare masks short-lived
-    }
-    c = row_sum16i(c);
-    c += __shfl_xor(c, 16);
-    c += __shfl_xor(c, 32);
-    int32_t* r = red + 8 * rc_sel;
-    rc_sel ^= 1;
-    if (lane == 0) r[wv] = c;
-    __syncthreads();
-    return r[0] + r[1] + r[2] + r[3];
-  };
-  // block exclusive scan in thread order
-  auto bscan = [&](int v) {
-    int x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(x, o);
-      if (lane >= o) x += y;
-    }
-    int32_t* r = red + 16 + 8 * rs_sel;
-    rs_sel ^= 1;
-    if (lane == 63) r[wv] = x;
-    __syncthreads();
-    int base = 0;
-    for (int w = 0; w < wv; ++w) base += r[w];
-    return base + x - v;
-  };
+  BlockSelect<C> bsel{red, lane, wv};
   // merge of the waves' states; the result (max, sum, output) is valid in wave 0
   auto merge_waves = [&](float& Mo, float& Lo, f32x4 (&Om)[ND]) {
     float lt = l_part + __shfl_xor(l_part, 16);
@@ -1051,26 +1011,9 @@ __global__ __launch_bounds__(256) void fwd_wide_kernel(const FwdArgs a) {
         }
         if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);
       }
-      // ---- the take-th largest key, bit by bit from the top
-      uint32_t thr = 0u;
-#pragma unroll 1
-      for (int bit = 30; bit >= 0; --bit) {
-        const uint32_t c = thr | (1u << bit);
-        if (bcount(key, c, false) >= take) thr = c;
-      }
-      const int need = take - bcount(key, thr, true);
-      uint32_t gtb = 0u, eqb = 0u;  // this thread's positions above / at the threshold
-#pragma unroll
-      for (int i = 0; i < C; ++i) {
-        gtb |= (uint32_t)(key[i] > thr) << i;
-        eqb |= (uint32_t)(key[i] == thr) << i;
-        if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);
-      }
-      // positions at the threshold are taken in position order up to `need`
-      int allow = need - bscan(__popc(eqb));
-      uint32_t bits = gtb;
-      for (uint32_t e = eqb; e != 0u && allow > 0; e &= e - 1u, --allow) bits |= e & (0u - e);
-      int idx = bscan(__popc(bits));
+      // ---- the take-th largest key, bit by bit from the top (keys < 2^31)
+      int idx;
+      const uint32_t bits = bsel.select(key, take, 30, idx);
       int32_t* pn = par + (cur ^ 1) * TK;
       for (uint32_t bb = bits; bb != 0u; bb &= bb - 1u) {
         const int pos = tid * C + (__builtin_ffs((int)bb) - 1);

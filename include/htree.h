@@ -158,6 +158,19 @@ int htree_backward_train(const htree_dims* d, float scale, const void* q, const 
                          int64_t scores_bytes, float* dq, float* dk, float* dv, void* bwd_ws,
                          int64_t bwd_ws_bytes, void* stream);
 
+/* Row-wise Top-K (the selection of the forward's wide kernel, on its own):
+ * for each of `rows` rows of n fp32 values (n <= 8192, 1 <= k <= n), the k
+ * largest, ties to the lower index (a stable descending sort), written in
+ * ascending index order: out_values / out_index [rows, k], and with
+ * n_payload in {1, 8} the payload [rows, n, n_payload] int32 of each
+ * selected element into out_payload [rows, k, n_payload] (n_payload 0: both
+ * may be NULL).  NaN inputs are not supported.  The micro-benchmark of
+ * topk_test/benchmark.py:33-46 (top 512 of 8192, payloads 0/1/8); no
+ * counterpart in the attention path itself. */
+int htree_topk_rows(const float* values, int64_t rows, int32_t n, int32_t k,
+                    const int32_t* payload, int32_t n_payload, float* out_values,
+                    int32_t* out_index, int32_t* out_payload, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
