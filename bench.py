@@ -134,10 +134,23 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     g = torch.Generator().manual_seed(1234)
-    q = torch.randn(B, T, H, D, generator=g).to(tdt).to(dev)
-    k = torch.randn(B, T, Hkv, D, generator=g).to(tdt).to(dev)
-    v = torch.randn(B, T, Hkv, D, generator=g).to(tdt).to(dev)
-    dO = torch.randn(B, T, H, D, generator=g).to(tdt).to(dev)
+    if args.workload == "C5":
+        # BASELINE C5: keys from a 64-component Gaussian mixture (means
+        # N(0, 4 I), sigma 0.5), queries around 4 hot components, V and dO iid
+        mu = 2.0 * torch.randn(64, D, generator=g)
+        hot = torch.randperm(64, generator=g)[:4]
+        k = mu[torch.randint(0, 64, (B, T, Hkv), generator=g)] + 0.5 * torch.randn(B, T, Hkv, D, generator=g)
+        q = mu[hot[torch.randint(0, 4, (B, T, H), generator=g)]] + 0.5 * torch.randn(B, T, H, D, generator=g)
+        v = torch.randn(B, T, Hkv, D, generator=g)
+        dO = torch.randn(B, T, H, D, generator=g)
+        q, k, v, dO = (x.to(tdt).to(dev) for x in (q, k, v, dO))
+        data = "synthetic: C5 skewed keys/queries (64-component mixture, 4 hot), v,dO iid N(0,1), seed 1234"
+    else:
+        q = torch.randn(B, T, H, D, generator=g).to(tdt).to(dev)
+        k = torch.randn(B, T, Hkv, D, generator=g).to(tdt).to(dev)
+        v = torch.randn(B, T, Hkv, D, generator=g).to(tdt).to(dev)
+        dO = torch.randn(B, T, H, D, generator=g).to(tdt).to(dev)
+        data = "synthetic: q,k,v,dO iid N(0,1) from torch.Generator seed 1234"
     has_bwd = with_bwd and hasattr(htree_amd, "htree_backward")
     torch.cuda.synchronize()
     print(f"# workload {args.workload} B={B} T={T} H={H} Hkv={Hkv} D={D} {dtype} CR={CR} TK={TK} "
@@ -226,7 +239,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": DT_SHORT[dtype],
-        "data": "synthetic: q,k,v,dO iid N(0,1) from torch.Generator seed 1234",
+        "data": data,
         "config": {
             "workload": f"{args.workload}: B={B} T={T} Hq={H} Hkv={Hkv} D={D} {DT_SHORT[dtype]} "
                         f"causal CR={CR} MTN={MTN} TK={TK}",
