@@ -29,6 +29,7 @@
 //   dq       one wave per query group over all levels (Q-stationary), from
 //            the stored dS (or recomputing the scores when the stored dS
 //            would exceed its memory budget).
+#include <stdlib.h>
 #include <string.h>
 
 #include "htree_common.h"
@@ -102,8 +103,12 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
   // dS of every (entry, tile), 1 KB each, kept for the dq pass when the whole
   // backward's worth fits the budget; otherwise dq recomputes the scores
   const int64_t ds_level = b->max_entries * b->tpp * 1024;
-  // (wide configurations: dq recomputes, its list per wave lives in LDS)
-  b->use_ds = !P.wide && ds_level * P.L <= kDsBudget;
+  // (wide configurations: dq recomputes, its list per wave lives in LDS).
+  // HTREE_DS_BUDGET_MB overrides the budget (read at every plan: keep it
+  // fixed between the workspace query and the backward call).
+  int64_t budget = kDsBudget;
+  if (const char* e = getenv("HTREE_DS_BUDGET_MB")) budget = (int64_t)atoll(e) << 20;
+  b->use_ds = !P.wide && ds_level * P.L <= budget;
   for (int l = 0; l < P.L; ++l) {
     b->off_rec[l] = (b->use_ds || l == 0) ? take(b->max_entries * 16) : b->off_rec[0];
     b->off_emap[l] = b->use_ds ? take(b->max_entries * 16) : -1;
@@ -1003,6 +1008,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   __shared__ uint32_t selw[kWavesPerBlock][SWW];
   __shared__ float rot_m[2][HALF];  // cos(CR theta), -sin(CR theta)
   __shared__ f32x4 acc_l[kWavesPerBlock][D / 16][64];  // dq over the finished levels
+  // the tile's K~ rows (hi, lo), written from the score operands and read
+  // back transposed for dq~^T = K~^T dS^T (rows padded by 16 bytes)
+  constexpr int KRP = 2 * D + 16;
+  __shared__ __attribute__((aligned(16))) char ktile[kWavesPerBlock][2][16 * KRP];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int u16 = lane & 15, kg = lane >> 4;
   const int G = a.G, CR = a.CR, crlg = a.crlg, TK = a.TK;
@@ -1034,6 +1043,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   for (int n = 0; n < ND; ++n) AC[n][lane] = f32x4{0.f, 0.f, 0.f, 0.f};
   int32_t* LS = lst[wv];
   uint32_t* SW = selw[wv];
+  char* KTh = ktile[wv][0];
+  char* KTl = ktile[wv][1];
   const int64_t lstride = (int64_t)a.B * a.T * a.Hkv * TK;
 
   for (int l = a.L - 1; l >= 0; --l) {
@@ -1090,6 +1101,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     for (int n = 0; n < ND; ++n) X[n] = f32x4{0.f, 0.f, 0.f, 0.f};
     int cur_slot = 0;
     auto tile = [&](int tau, const bf16x8 (&kh)[KS], const bf16x8 (&kl)[KS]) {
+      // this lane's row (candidate u16) of the tile, for the transposed reads
+      // below; the previous tile's reads have completed (their values fed
+      // that tile's MFMAs)
+#pragma unroll
+      for (int m = 0; m < KS; ++m) {
+        *(bf16x8*)(KTh + u16 * KRP + dslot<D>(kg, m) * 2) = kh[m];
+        *(bf16x8*)(KTl + u16 * KRP + dslot<D>(kg, m) * 2) = kl[m];
+      }
       const int s = wide ? (tau << 4) >> crlg : tau;
       if (s != cur_slot) {  // ascending slots, one step apart
         rot_by_fr<D>(qr, rot_m[0], rot_m[1], kg);
@@ -1131,17 +1150,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
         anyv |= v;
       }
       if (!__any(anyv)) return;
+      wave_sync();  // the rows written above are visible to the whole wave
       // dq = sum_cand dS K~ cancels (sum_cand dS = 0 per head): split both
-      // factors so clustered keys keep their small residual.  The K~^T
-      // loads stay below the score math (keeps the tile within 256 VGPRs).
-      __builtin_amdgcn_sched_barrier(0);
-      const int vn = node0 + (4 * kg < CRU ? 4 * kg : 0);
-      const int64_t tbase = (hrow + (vn & ~15)) / 16 * D * 16 + ((vn & 15) >> 2) * 64 + u16 * 4;
+      // factors so clustered keys keep their small residual.  K~^T comes
+      // from the tile's rows in LDS: one transposing read (ds_read_b64_tr_b16)
+      // gives lane (u16, kg) candidates 4kg..4kg+3 of column d = 16n + u16
+      // (lane i of a 16-lane group addresses row 4kg + i/4, columns
+      // d - i + 4 (i % 4) .. +3).
       s16x4 kt[ND], ktl[ND];
 #pragma unroll
       for (int n = 0; n < ND; ++n) {
-        kt[n] = *(const s16x4*)(P.kt_h + tbase + (int64_t)n * 256);
-        ktl[n] = *(const s16x4*)(P.kt_l + tbase + (int64_t)n * 256);
+        const int off = (4 * kg + (u16 >> 2)) * KRP + (16 * n + 4 * (u16 & 3)) * 2;
+        kt[n] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(__attribute__((address_space(3))) void*)(KTh + off));
+        ktl[n] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(__attribute__((address_space(3))) void*)(KTl + off));
       }
       s16x4 d4h, d4l;
       pack4_split(ds, d4h, d4l);

@@ -208,3 +208,19 @@ def test_backward_reference_default_regime():
     ok, worst = close(dq[rows[:, 0], rows[:, 1]], ref, "float32")
     print("default-regime dq worst", worst, flush=True)
     assert ok
+
+
+@pytest.mark.parametrize("cfg", [(1, 1500, 16, 2, 128, 16, 16, 128, "bfloat16", 61),
+                                 (1, 1100, 8, 1, 128, 32, 8, 256, "float16", 62),
+                                 (1, 900, 8, 2, 64, 8, 16, 128, "float32", 63)],
+                         ids=lambda c: f"D{c[4]}cr{c[5]}{c[8]}")
+def test_backward_recomputed_dq(cfg, monkeypatch):
+    """The dq pass that recomputes the scores (taken when the stored dS
+    would exceed its memory budget, as at BASELINE C4, and for top_k > 64),
+    forced here by a zero budget."""
+    monkeypatch.setenv("HTREE_DS_BUDGET_MB", "0")
+    B, T, H, Hkv, D, CR, TK, MTN, dtype, seed = cfg
+    print(f"case {cfg}", flush=True)
+    q, k, v, dO = inputs(B, T, H, Hkv, D, dtype, seed, dO=True)
+    out, par, gmax, gsum, dq, dk, dv = run(q, k, v, dO, CR, TK, MTN)
+    print(check_backward(q, k, v, dO, CR, TK, MTN, dtype, out, par, gmax, gsum, dq, dk, dv), flush=True)
