@@ -502,22 +502,11 @@ struct Stage {
   static constexpr int SLOTS = BYTES * 2 <= 20 * 1024 ? 2 : 1;  // double-buffer if it fits
 };
 
-typedef __attribute__((address_space(3))) void lds_void;
 
 // byte offset of element e of head row g in a staged block
 template <int D, typename TIn>
 __device__ __forceinline__ int row_off(int g, int e) {
   return g * Stage<D, TIn>::RP + e * (int)sizeof(TIn);
-}
-
-// buffer resource over `bytes` bytes at `base` (raw, byte-addressed); base
-// and bytes are wave-uniform and are moved to scalar registers here
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int bytes) {
-  const uint64_t p = (uint64_t)base;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
-  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0,
-                                           __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
 }
 
 // Asynchronous copies of one entry's inputs into `slot` (buffer loads into

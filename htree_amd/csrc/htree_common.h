@@ -176,6 +176,19 @@ __device__ __forceinline__ bf16x8 pack8(const float (&x)[8]) {
 
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+typedef __attribute__((address_space(3))) void lds_void;
+
+// buffer resource over `bytes` bytes at `base` (raw, byte-addressed); base
+// and bytes are wave-uniform and are moved to scalar registers here
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int bytes) {
+  const uint64_t p = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0,
+                                           __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+
 // Orders LDS traffic between the lanes of one wave (no block barrier: each
 // wave of a block works on its own query group).
 __device__ __forceinline__ void wave_sync() {

@@ -160,13 +160,47 @@ __device__ __forceinline__ void load_kfrag(const uint16_t* __restrict__ row, int
   for (int m = 0; m < D / 32; ++m) f[m] = *(const bf16x8*)(row + dslot<D>(kg, m));
 }
 
+// One tile's inputs staged in LDS: the K~ rows (hi, lo; each row padded by
+// 16 bytes, so that the 16 lanes reading one 16-byte column position of 16
+// rows hit distinct banks) and the tile's 16-node V^T block (hi, lo).
+template <int D, bool PREC>
+struct FwdStage {
+  static constexpr int CPR = D * 2 / 16;          // 16-byte chunks of a K~ row
+  static constexpr int KRP = (CPR + 1) * 16;      // padded row pitch (bytes)
+  static constexpr int NCH = 16 * (CPR + 1);      // chunks of the 16 padded rows
+  static constexpr int OFF_KL = 16 * KRP;
+  static constexpr int VB = 16 * D * 2;           // V^T block of 16 nodes (bf16)
+  static constexpr int OFF_V = 32 * KRP;
+  static constexpr int OFF_VL = OFF_V + VB;
+  static constexpr int BYTES = OFF_V + (PREC ? 2 : 1) * VB;
+};
+
+// Streaming forward for levels of 17..64 candidate tiles (e.g. top_k 32 with
+// CR 32): one wave per query group; upper levels score every tile for the
+// importance, select, then score again for the accumulation.  Each tile's
+// K~ rows (and, for the accumulation, its V^T block) are copied into the
+// wave's LDS slot by buffer loads (range-checked against the level's
+// (b, h_kv) rows) one tile ahead: the copies of tile tau+1 are issued as
+// soon as tile tau's fragments have moved to registers, and land while tile
+// tau is computed.  Tiles run in ascending parent slot and the query turns
+// by R(., -CR) per slot (a table row in LDS), so a tile reads no global
+// memory besides its copies.
 template <int D, bool PREC, typename TIn, int MAXSLOT, bool TRACE>
-__global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fwd_kernel(const FwdArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
+  using St = FwdStage<D, PREC>;
   __shared__ WaveLds<MAXSLOT> lds_all[kWavesPerBlock];
+  __shared__ __attribute__((aligned(16))) char stage_all[kWavesPerBlock][St::BYTES];
+  __shared__ float rot_m[2][HALF];  // cos(CR theta), -sin(CR theta)
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int u16 = lane & 15, kg = lane >> 4;
+  const int G = a.G, CR = a.CR, crlg = a.crlg, TK = a.TK;
+  if (threadIdx.x < HALF) {
+    rot_m[0][threadIdx.x] = a.cosb[(int64_t)CR * HALF + threadIdx.x];
+    rot_m[1][threadIdx.x] = -a.sinb[(int64_t)CR * HALF + threadIdx.x];
+  }
+  __syncthreads();
   // XCD-aware order: hardware deals blocks round-robin over the 8 XCDs; give
   // each XCD a contiguous range of query groups (same (b, h_kv) tree).
   const int bid = blockIdx.x;
@@ -178,21 +212,16 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
   const int h = bh % a.Hkv;
   const int b = bh / a.Hkv;
   WaveLds<MAXSLOT>& W = lds_all[wv];
-  const int G = a.G, CR = a.CR, crlg = a.crlg, TK = a.TK;
+  char* slot = stage_all[wv];
   const int CRU = CR < 16 ? CR : 16;
   const bool wide = CR >= 16;
 
-  // query fragment: lane holds q[g = u16][d-slots of kg], pre-scaled
-  float qf[KS][8];
+  // query fragment (lane: head u16, the lane group's d-slots), kept in its
+  // input type (16-bit types packed)
+  QFrag<D, TIn> qin;
   {
     const bool gv = u16 < G;
-    const TIn* qp = (const TIn*)a.q + (((int64_t)b * a.T + t) * a.H + h * G + (gv ? u16 : 0)) * D;
-#pragma unroll
-    for (int m = 0; m < KS; ++m) {
-      Io<TIn>::ld8(qp + dslot<D>(kg, m), qf[m]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qf[m][e] = gv ? qf[m][e] * a.scale : 0.f;
-    }
+    qin.load((const TIn*)a.q + (((int64_t)b * a.T + t) * a.H + h * G + (gv ? u16 : 0)) * D, kg, gv);
   }
 
   float m_run = -INFINITY, l_part = 0.f;
@@ -220,30 +249,97 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
     if (a.parents && lane < TK)
       a.parents[((((int64_t)l * a.B + b) * a.T + t) * a.Hkv + h) * TK + lane] = pv;
     const int64_t hrow = ((int64_t)b * a.Hkv + h) * P.Np;
-    const uint16_t* KH = P.kh + hrow * D;
-    const uint16_t* KL = P.kl + hrow * D;
-    const uint16_t* VH = P.vh + hrow * D;
-    const uint16_t* VL = PREC ? P.vl + hrow * D : nullptr;
+    const int lvl_bytes = (int)(P.Np * D * 2);  // one (b, h_kv) block of a level array
+    const __amdgpu_buffer_rsrc_t rkh = buf_rsrc(P.kh + hrow * D, lvl_bytes);
+    const __amdgpu_buffer_rsrc_t rkl = buf_rsrc(P.kl + hrow * D, lvl_bytes);
+    const __amdgpu_buffer_rsrc_t rvh = buf_rsrc(P.vh + hrow * D, lvl_bytes);
+    const __amdgpu_buffer_rsrc_t rvl = buf_rsrc(PREC ? P.vl + hrow * D : P.vh + hrow * D, lvl_bytes);
     const bool upper = l > 0;
+    auto slot_of = [&](int tau) { return wide ? (tau << 4) >> crlg : tau; };
+    auto node0_of = [&](int tau) {
+      return (W.par[cur][slot_of(tau)] << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0);
+    };
+    // copies of tile tau's K~ rows (and V^T block) into the slot; rows past
+    // the level's nodes read as zero (never used: their scores are masked)
+    auto issue = [&](int tau, bool with_v) {
+      const int node0 = node0_of(tau);
+      // the lane offsets below are cheap to recompute: keep them out of the
+      // registers held across the tile loop
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+#pragma unroll
+      for (int j = 0; j < (St::NCH + 63) / 64; ++j) {
+        const int pc = j * 64 + ln;
+        const int g = pc / (St::CPR + 1);
+        const int c = pc - g * (St::CPR + 1);
+        const int off = (node0 + g) * (D * 2) + (c < St::CPR ? c : 0) * 16;
+        if ((St::NCH % 64 == 0) || pc < St::NCH) {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rkh, (lds_void*)(slot + j * 1024), 16, off, 0, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rkl, (lds_void*)(slot + St::OFF_KL + j * 1024), 16,
+                                                   off, 0, 0, 0);
+        }
+      }
+      if (with_v) {
+        const int voff = (node0 >> 4) * St::VB;
+#pragma unroll
+        for (int j = 0; j < St::VB / 1024; ++j) {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rvh, (lds_void*)(slot + St::OFF_V + j * 1024), 16,
+                                                   voff + (j * 64 + ln) * 16, 0, 0, 0);
+          if (PREC)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rvl, (lds_void*)(slot + St::OFF_VL + j * 1024),
+                                                     16, voff + (j * 64 + ln) * 16, 0, 0, 0);
+        }
+      }
+    };
+    auto wait_copies = [&]() {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the slot's copies have landed
+      __builtin_amdgcn_wave_barrier();
+    };
+    auto reads_done = [&]() {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slot's reads have completed
+      __builtin_amdgcn_wave_barrier();
+    };
+    auto kread = [&](bf16x8 (&kh)[KS], bf16x8 (&kl)[KS]) {
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const char* row = slot + (ln & 15) * St::KRP;
+#pragma unroll
+      for (int m = 0; m < KS; ++m) {
+        kh[m] = *(const bf16x8*)(row + dslot<D>(ln >> 4, m) * 2);
+        kl[m] = *(const bf16x8*)(row + St::OFF_KL + dslot<D>(ln >> 4, m) * 2);
+      }
+    };
+    // the query turned to a slot: R(q, apos) at slot 0, -CR per slot after
+    float qr[KS][8];
+    int cur_slot = 0;
+    auto frame_start = [&]() {
+      qin.get(qr, a.scale);
+      rope_frag<D>(qr, a.cosb + (int64_t)apos * HALF, a.sinb + (int64_t)apos * HALF, kg, qr);
+      cur_slot = 0;
+    };
+    auto frame_to = [&](int s) {
+      while (cur_slot < s) {
+        rope_frag<D>(qr, rot_m[0], rot_m[1], kg, qr);
+        ++cur_slot;
+      }
+    };
 
     // ------------------------------------------------ selection (upper levels)
     if (upper) {
       float Mrun = -INFINITY;
+      frame_start();
+      issue(0, false);
       for (int tau = 0; tau < nt; ++tau) {
-        const int s = wide ? (tau << 4) >> crlg : tau;
-        const int node0 = (W.par[cur][s] << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0);
-        const int prow = apos - (s << crlg);
-        float qr[KS][8];
-        rot_q<D>(qf, a.cosb + (int64_t)prow * HALF, a.sinb + (int64_t)prow * HALF, kg, qr);
+        frame_to(slot_of(tau));
+        wait_copies();
+        bf16x8 kh[KS], kl[KS];
+        kread(kh, kl);
+        reads_done();
+        if (tau + 1 < nt) issue(tau + 1, false);
         bf16x8 qh[KS], ql[KS];
         to_bf_split<D>(qr, qh, ql);
         const int pos = wide ? (tau << 4) + u16 : (tau << crlg) + u16;
         const bool cv = u16 < CRU && pos < nc;
-        const uint16_t* krow = KH + (int64_t)(node0 + (cv ? u16 : 0)) * D;
-        const uint16_t* klrow = KL + (int64_t)(node0 + (cv ? u16 : 0)) * D;
-        bf16x8 kh[KS], kl[KS];
-        load_kfrag<D>(krow, kg, kh);
-        load_kfrag<D>(klrow, kg, kl);
         f32x4 S = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int m = 0; m < KS; ++m) {
@@ -273,20 +369,25 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
       // key is the float's bit pattern + 1 (0 = no candidate), so unsigned
       // order is importance order and exact ties are resolved by position.
       const int take = TK < nc ? TK : nc;
+      // lane-dependent offsets are recomputed per level rather than hoisted
+      // out of the level loop and held (or spilled) across it
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int su = ln & 15, skg = ln >> 4;
       const int nslot = (nt + 3) >> 2;
       uint32_t key[MAXSLOT];
 #pragma unroll
       for (int sl = 0; sl < MAXSLOT; ++sl) {
         key[sl] = 0u;
         if (sl < nslot) {
-          const int tau = 4 * sl + kg;
-          const int pos = wide ? (tau << 4) + u16 : (tau << crlg) + u16;
-          if (tau < nt && u16 < CRU && pos < nc) {
+          const int tau = 4 * sl + skg;
+          const int pos = wide ? (tau << 4) + su : (tau << crlg) + su;
+          if (tau < nt && su < CRU && pos < nc) {
             float v;
             if (pos == apos) {
               v = 1e6f;  // rightmost candidate always kept (src/naive.py:93)
             } else {
-              v = W.imp[64 * sl + lane];
+              v = W.imp[64 * sl + ln];
               const float mt = W.mt[tau];
               if (mt != Mrun) v *= expf(mt - Mrun);
             }
@@ -318,10 +419,10 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
           const unsigned long long sm = __ballot(sel);
           if (lane == 0) W.selmask[sl] = sm;
           if (sel) {
-            const int tau = 4 * sl + kg;
+            const int tau = 4 * sl + skg;
             const int s = wide ? (tau << 4) >> crlg : tau;
             const int node =
-                (W.par[cur][s] << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0) + u16;
+                (W.par[cur][s] << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0) + su;
             W.par[nxt][sel_before + mbcnt64(sm)] = node;
           }
           eq_before += __popcll(em);
@@ -339,21 +440,27 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
 #pragma unroll
       for (int n = 0; n < ND; ++n) O[n] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    frame_start();
+    issue(0, true);
     for (int tau = 0; tau < nt; ++tau) {
-      const int s = wide ? (tau << 4) >> crlg : tau;
-      const int node0 = (W.par[cur][s] << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0);
-      const int prow = apos - (s << crlg);
+      frame_to(slot_of(tau));
+      const int node0 = node0_of(tau);
       const unsigned long long smask = upper ? W.selmask[tau >> 2] : 0ull;
-      float qr[KS][8];
-      rot_q<D>(qf, a.cosb + (int64_t)prow * HALF, a.sinb + (int64_t)prow * HALF, kg, qr);
+      wait_copies();
+      bf16x8 kh[KS], kl[KS];
+      kread(kh, kl);
+      // V^T fragment: nodes node0 + 4kg + 0..3 of the staged block at d = 16n + u16
+      const int c0 = (node0 & 15) + (4 * kg < CRU ? 4 * kg : 0);
+      s16x4 vh[ND], vl[ND];
+#pragma unroll
+      for (int n = 0; n < ND; ++n) {
+        vh[n] = *(const s16x4*)(slot + St::OFF_V + ((16 * n + u16) * 16 + c0) * 2);
+        if (PREC) vl[n] = *(const s16x4*)(slot + St::OFF_VL + ((16 * n + u16) * 16 + c0) * 2);
+      }
+      reads_done();
+      if (tau + 1 < nt) issue(tau + 1, true);
       bf16x8 qh[KS], ql[KS];
       to_bf_split<D>(qr, qh, ql);
-      const int posk = wide ? (tau << 4) + u16 : (tau << crlg) + u16;
-      const bool cvk = u16 < CRU && posk < nc;
-      const int64_t krow = (int64_t)(node0 + (cvk ? u16 : 0)) * D;
-      bf16x8 kh[KS], kl[KS];
-      load_kfrag<D>(KH + krow, kg, kh);
-      load_kfrag<D>(KL + krow, kg, kl);
       f32x4 S = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int m = 0; m < KS; ++m) {
@@ -391,20 +498,16 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdArgs a) {
         ph[r] = (short)hb;
         pl[r] = PREC ? f_to_bfs(p[r] - bf_to_f(hb)) : (short)0;
       }
-      // V^T fragment: nodes node0 + 4kg + 0..3 at d = 16n + u16
-      const int vn = node0 + (4 * kg < CRU ? 4 * kg : 0);
-      const int64_t vbase = ((int64_t)(vn >> 4) * D + u16) * 16 + (vn & 15);
 #pragma unroll
       for (int n = 0; n < ND; ++n) {
-        const s16x4 vf = *(const s16x4*)(VH + vbase + (int64_t)n * 256);
-        O[n] = mma16(vf, ph, O[n]);
+        O[n] = mma16(vh[n], ph, O[n]);
         if (PREC) {
-          const s16x4 vfl = *(const s16x4*)(VL + vbase + (int64_t)n * 256);
-          O[n] = mma16(vf, pl, O[n]);
-          O[n] = mma16(vfl, ph, O[n]);
+          O[n] = mma16(vh[n], pl, O[n]);
+          O[n] = mma16(vl[n], ph, O[n]);
         }
       }
     }
+    wait_copies();  // no copy into the slot is left in flight past the level
     if (TRACE)
       trace_store<D>(a, l, ((int64_t)b * a.T + t) * a.H + h * G + u16, u16 < G, kg, m_run,
                      l_part, O);
@@ -1212,6 +1315,9 @@ static int forward_impl(const htree_dims* d, float scale, const void* q, const v
   a.TK = d->top_k;
   a.L = P.L;
   a.scale = scale;
+  // the streaming kernel addresses one (b, h_kv) block of a level array
+  // with 32-bit byte offsets
+  if (!P.wide && P.max_tiles > 16 && P.Np[0] * d->D * 2 > 0x7fffffffll) return HTREE_EUNSUPPORTED;
   const int64_t groups = (int64_t)d->B * d->H_kv * d->T;
   // blocks dealt round-robin to the 8 XCDs: XCD x gets blocks x, x+8, ...,
   // which map to a contiguous range of query groups (one tree per XCD's L2)

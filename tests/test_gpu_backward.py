@@ -41,6 +41,7 @@ CASES = [
     (1, 1500, 16, 4, 32, 16, 8, 128, "float16", 9),
     (2, 1000, 8, 2, 32, 8, 16, 64, "bfloat16", 10),
     (1, 2500, 16, 4, 32, 4, 32, 64, "float32", 11),
+    (1, 3000, 8, 1, 128, 32, 32, 256, "bfloat16", 12),  # BASELINE C4's tree shape
 ]
 
 

@@ -44,6 +44,8 @@ SMALL = [
     (1, 1500, 16, 4, 32, 16, 8, 128, "float16", 9),
     (2, 1000, 8, 2, 32, 8, 16, 64, "bfloat16", 10),
     (1, 2500, 16, 4, 32, 4, 32, 64, "float32", 11),    # D = 32, 32 tiles: multi-pass kernel
+    (1, 3000, 8, 1, 128, 32, 32, 256, "bfloat16", 12),  # CR 32, top_k 32 (BASELINE C4's tree): 64 tiles
+    (1, 2200, 8, 2, 64, 16, 32, 256, "float16", 13),    # 32 tiles, fp16 (split V)
 ]
 
 
