@@ -51,7 +51,8 @@ struct BwdPlan {
       off_partial;
   int64_t off_rec[HTREE_MAX_LEVELS];   // per-entry records of each level
   int64_t off_emap[HTREE_MAX_LEVELS];  // (query group, slot) -> {entry, mask}, per level
-  int64_t off_ds[HTREE_MAX_LEVELS];    // dS of every entry tile (bf16 hi, lo), per level
+  int64_t off_ds[HTREE_MAX_LEVELS];    // dS of every entry tile, per level
+  int ds_elems;                        // 16-bit values per stored dS tile (256 or 512)
   bool use_ds;                         // dq from the stored dS (else recomputed)
   int64_t bytes;
 };
@@ -100,9 +101,13 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
   b->off_poff = take((b->max_rows + 1) * 4);
   b->off_npieces = take(4);
   b->off_ptab = take(b->max_pieces * 3 * 4);
-  // dS of every (entry, tile), 1 KB each, kept for the dq pass when the whole
-  // backward's worth fits the budget; otherwise dq recomputes the scores
-  const int64_t ds_level = b->max_entries * b->tpp * 1024;
+  // dS of every (entry, tile), kept for the dq pass when the whole backward's
+  // worth fits the budget; otherwise dq recomputes the scores.  16-bit
+  // inputs: one fp16 value per (head, candidate), 512 B a tile (11 significant
+  // bits, as many as the reference's tf32 dq product carries); fp32 inputs:
+  // bf16 hi + lo, 1 KB a tile.
+  b->ds_elems = P.precise ? 512 : 256;
+  const int64_t ds_level = b->max_entries * b->tpp * b->ds_elems * 2;
   // (wide configurations: dq recomputes, its list per wave lives in LDS).
   // HTREE_DS_BUDGET_MB overrides the budget (read at every plan: keep it
   // fixed between the workspace query and the backward call).
@@ -804,14 +809,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     pack4_split(ds, dh4, dl4);
     pack4_split(pr, ph, plo);
     if (a.ds) {
-      // dS[g][cand] for the dq pass: hi then lo, 16 x 16 each, element
-      // (g, cand) at (cand / 4) * 64 + g * 4 + cand % 4
-      uint16_t* o = a.ds + ((int64_t)(e0 + e) * a.tpp + tile) * 512 + (u16 >> 2) * 64 + 16 * kg +
-                    (u16 & 3);
+      // dS[g][cand] for the dq pass, 16 x 16, element (g, cand) at
+      // (cand / 4) * 64 + g * 4 + cand % 4: fp16 (16-bit inputs), or bf16 hi
+      // then lo (fp32 inputs)
+      uint16_t* o = a.ds + ((int64_t)(e0 + e) * a.tpp + tile) * (PREC ? 512 : 256) + (u16 >> 2) * 64 +
+                    16 * kg + (u16 & 3);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        o[4 * r] = (uint16_t)dh4[r];
-        o[256 + 4 * r] = (uint16_t)dl4[r];
+        if (PREC) {
+          o[4 * r] = (uint16_t)dh4[r];
+          o[256 + 4 * r] = (uint16_t)dl4[r];
+        } else {
+          o[4 * r] = __builtin_bit_cast(uint16_t, (_Float16)ds[r]);
+        }
       }
     }
     f32x4 u[ND];
@@ -1229,11 +1239,11 @@ template <int D>
 struct DqStage {
   static constexpr int KTB = 16 * D * 2;  // one 16-node block of K~^T, bf16
   static constexpr int OFF_KL = KTB;
-  static constexpr int OFF_DS = 2 * KTB;  // dS hi, lo (1 KB)
+  static constexpr int OFF_DS = 2 * KTB;  // dS: fp16 (512 B) or bf16 hi, lo (1 KB)
   static constexpr int BYTES = 2 * KTB + 1024;
 };
 
-template <int D>
+template <int D, bool DS16>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void dq_ds_kernel(const DqDsArgs a) {
   constexpr int ND = D / 16, HALF = D / 2;
   using St = DqStage<D>;
@@ -1297,8 +1307,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void d
         __builtin_amdgcn_global_load_lds(ktl + (j * 64 + lane) * 16,
                                          (lds_void*)(slot + St::OFF_KL + j * 1024), 16, 0, 0);
       }
-      const char* dsp = (const char*)(P.ds + ((int64_t)__builtin_amdgcn_readlane(sr.x, s) * tpp + chunk) * 512);
-      __builtin_amdgcn_global_load_lds(dsp + lane * 16, (lds_void*)(slot + St::OFF_DS), 16, 0, 0);
+      const char* dsp = (const char*)(P.ds + ((int64_t)__builtin_amdgcn_readlane(sr.x, s) * tpp + chunk) *
+                                                 (DS16 ? 256 : 512));
+      if (!DS16 || lane < 32)
+        __builtin_amdgcn_global_load_lds(dsp + lane * 16, (lds_void*)(slot + St::OFF_DS), 16, 0, 0);
     };
     // into the frame of slot 0
     rot_acc<D>(X, a.cosb + (int64_t)apos * HALF, a.sinb + (int64_t)apos * HALF, kg);
@@ -1322,8 +1334,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void d
         kt[n] = *(const s16x4*)(slot + off);
         ktl[n] = *(const s16x4*)(slot + St::OFF_KL + off);
       }
-      const s16x4 dsh = *(const s16x4*)(slot + St::OFF_DS + kg * 128 + u16 * 8);
-      const s16x4 dsl = *(const s16x4*)(slot + St::OFF_DS + 512 + kg * 128 + u16 * 8);
+      s16x4 dsh, dsl;
+      if (DS16) {
+        // fp16 dS as bf16 hi + lo (exact: 11 significant bits)
+        typedef __attribute__((ext_vector_type(4))) _Float16 h16x4;
+        const h16x4 hv = *(const h16x4*)(slot + St::OFF_DS + kg * 128 + u16 * 8);
+        const float f[4] = {(float)hv[0], (float)hv[1], (float)hv[2], (float)hv[3]};
+        pack4_split(f, dsh, dsl);
+      } else {
+        dsh = *(const s16x4*)(slot + St::OFF_DS + kg * 128 + u16 * 8);
+        dsl = *(const s16x4*)(slot + St::OFF_DS + 512 + kg * 128 + u16 * 8);
+      }
       // the slot's reads have landed before the next copies overwrite it
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
       __builtin_amdgcn_wave_barrier();
@@ -1524,7 +1545,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.L = P.L;
     a.tpp = BP.tpp;
     a.scale = scale;
-    hipLaunchKernelGGL((dq_ds_kernel<D>), dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((dq_ds_kernel<D, !PREC>), dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, st, a);
   } else {
     DqArgs a;
     memset(&a, 0, sizeof(a));
