@@ -46,12 +46,14 @@ struct BwdPlan {
   int64_t max_rows, max_entries, piece, max_pieces;
   int64_t off_delta;
   int64_t off_kt[2][HTREE_MAX_LEVELS], off_vr[2][HTREE_MAX_LEVELS];
+  int64_t off_kexp[HTREE_MAX_LEVELS];  // bf16 inputs: exponent of each K~^T block
   int64_t off_dk[HTREE_MAX_LEVELS], off_dv[HTREE_MAX_LEVELS];
   int64_t off_bitmap, off_wpre, off_cnt, off_rowoff, off_pcnt, off_poff, off_npieces, off_ptab,
       off_partial;
   int64_t off_rec[HTREE_MAX_LEVELS];   // per-entry records of each level
   int64_t off_emap[HTREE_MAX_LEVELS];  // (query group, slot) -> {entry, mask}, per level
   int64_t off_ds[HTREE_MAX_LEVELS];    // dS of every entry tile, per level
+  int64_t off_dsexp[HTREE_MAX_LEVELS]; // bf16 inputs: exponent of every stored dS tile
   int ds_elems;                        // 16-bit values per stored dS tile (256 or 512)
   bool use_ds;                         // dq from the stored dS (else recomputed)
   int64_t bytes;
@@ -86,10 +88,14 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
   b->off_delta = take((int64_t)d->B * d->T * d->H * 4);
   for (int l = 0; l < P.L; ++l) {
     const int64_t elems = BH * P.Np[l] * d->D;
+    // K~^T for dq: bf16 hi + lo for fp16 / fp32 inputs (dq = dS K~ cancels:
+    // sum dS = 0); for bf16 inputs fp16 scaled per 16-node block by 2^-kexp
+    // (11 significant bits, the class of the reference's tf32 product)
     for (int s = 0; s < 2; ++s) {
-      b->off_kt[s][l] = take(elems * 2);  // dq = dS K~ cancels (sum dS = 0): split K~
+      b->off_kt[s][l] = (s == 0 || P.precise) ? take(elems * 2) : -1;
       b->off_vr[s][l] = (s == 0 || P.precise) ? take(elems * 2) : -1;
     }
+    b->off_kexp[l] = P.precise ? -1 : take(BH * (P.Np[l] / 16) * 4);
     b->off_dk[l] = l > 0 ? take((int64_t)d->B * P.N[l] * d->H_kv * d->D * 4) : -1;
     b->off_dv[l] = l > 0 ? take((int64_t)d->B * P.N[l] * d->H_kv * d->D * 4) : -1;
   }
@@ -102,10 +108,10 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
   b->off_npieces = take(4);
   b->off_ptab = take(b->max_pieces * 3 * 4);
   // dS of every (entry, tile), kept for the dq pass when the whole backward's
-  // worth fits the budget; otherwise dq recomputes the scores.  16-bit
-  // inputs: one fp16 value per (head, candidate), 512 B a tile (11 significant
-  // bits, as many as the reference's tf32 dq product carries); fp32 inputs:
-  // bf16 hi + lo, 1 KB a tile.
+  // worth fits the budget; otherwise dq recomputes the scores.  bf16
+  // inputs: one fp16 value per (head, candidate) scaled by 2^-e with e per
+  // tile, 512 B a tile (11 significant bits, as many as the reference's tf32
+  // dq product carries); fp16 / fp32 inputs: bf16 hi + lo, 1 KB a tile.
   b->ds_elems = P.precise ? 512 : 256;
   const int64_t ds_level = b->max_entries * b->tpp * b->ds_elems * 2;
   // (wide configurations: dq recomputes, its list per wave lives in LDS).
@@ -118,6 +124,7 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
     b->off_rec[l] = (b->use_ds || l == 0) ? take(b->max_entries * 16) : b->off_rec[0];
     b->off_emap[l] = b->use_ds ? take(b->max_entries * 16) : -1;
     b->off_ds[l] = b->use_ds ? take(ds_level) : -1;
+    b->off_dsexp[l] = (b->use_ds && !P.precise) ? take(b->max_entries * b->tpp * 4) : -1;
   }
   b->off_partial = take(b->max_pieces * b->tpp * 16 * (int64_t)d->D * 2 * 4);
   b->bytes = off;
@@ -260,10 +267,49 @@ __global__ __launch_bounds__(256) void pack_bwd_kernel(
   const int64_t tr = (bh * (Np / 16) + node / 16) * D * 16 + (dd >> 4) * 256 + (c >> 2) * 64 +
                      (dd & 15) * 4 + (c & 3);
   const int64_t vsrc = ((bh * (Np / 16) + node / 16) * D + dd) * 16 + c;
-  kt_h[tr] = kh[idx];
+  if (kt_h) kt_h[tr] = kh[idx];
   if (kt_l) kt_l[tr] = kl[idx];
   vr_h[idx] = vh[vsrc];
   if (vr_l) vr_l[idx] = vl[vsrc];
+}
+
+// Exponent e with |x| 2^-e in [2^14, 2^15) for the largest |x| of a block
+// (0 for an all-zero block): fp16 values scaled by 2^-e keep 11 significant
+// bits for everything within 2^-10 of the block's largest value and cannot
+// overflow.
+__device__ __forceinline__ int fp16_block_exp(float amax) {
+  return amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) - 15 : 0;
+}
+
+// KT16: K~ = hi + lo of one 16-node block, transposed as KT (layout above),
+// as fp16 scaled by 2^-kexp[block].  One wave per (bh, block); lane i writes
+// output elements i, i + 64, ...
+template <int D>
+__global__ __launch_bounds__(256) void pack_kt16_kernel(const uint16_t* __restrict__ kh,
+                                                        const uint16_t* __restrict__ kl, int64_t Np,
+                                                        int64_t nblk, uint16_t* __restrict__ kt,
+                                                        int32_t* __restrict__ kexp) {
+  constexpr int PER = 16 * D / 64;
+  const int lane = threadIdx.x & 63;
+  const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // bh * (Np / 16) + block
+  if (blk >= nblk) return;
+  const int64_t row0 = blk * 16;  // = bh * Np + first node of the block
+  float x[PER];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int o = i * 64 + lane;
+    const int d = (o >> 8) * 16 + ((o & 63) >> 2);
+    const int c = ((o & 255) >> 6) * 4 + (o & 3);
+    const int64_t src = (row0 + c) * D + d;
+    x[i] = bf_to_f(kh[src]) + bf_to_f(kl[src]);
+    amax = fmaxf(amax, fabsf(x[i]));
+  }
+  const int e = fp16_block_exp(wave_max_uniform(amax));
+#pragma unroll
+  for (int i = 0; i < PER; ++i)
+    kt[blk * 16 * D + i * 64 + lane] = __builtin_bit_cast(uint16_t, (_Float16)__builtin_amdgcn_ldexpf(x[i], -e));
+  if (lane == 0) kexp[blk] = e;
 }
 
 // ---------------------------------------------------------------- index
@@ -481,6 +527,7 @@ struct DkvArgs {
   const float *cosb, *sinb;
   float* partial;
   uint16_t* ds;  // nullable: dS per (entry, tile) for the dq pass
+  int32_t* dsexp;  // bf16 inputs: exponent of each stored dS tile
   const uint16_t* sc;  // level's stored scores (fp16 S - m_ref) [groups][max_tiles][256]
   const float* smref;  // level's m_ref [groups][16]
   int64_t N, Np, pw, Pl, BTH;  // BTH = B*T*H (length of gmax / gsum / delta)
@@ -810,18 +857,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     pack4_split(pr, ph, plo);
     if (a.ds) {
       // dS[g][cand] for the dq pass, 16 x 16, element (g, cand) at
-      // (cand / 4) * 64 + g * 4 + cand % 4: fp16 (16-bit inputs), or bf16 hi
-      // then lo (fp32 inputs)
-      uint16_t* o = a.ds + ((int64_t)(e0 + e) * a.tpp + tile) * (PREC ? 512 : 256) + (u16 >> 2) * 64 +
-                    16 * kg + (u16 & 3);
+      // (cand / 4) * 64 + g * 4 + cand % 4: fp16 scaled by 2^-e with e from
+      // the tile's largest |dS| (bf16 inputs), or bf16 hi then lo (fp16 / fp32)
+      const int64_t et = (int64_t)(e0 + e) * a.tpp + tile;
+      uint16_t* o = a.ds + et * (PREC ? 512 : 256) + (u16 >> 2) * 64 + 16 * kg + (u16 & 3);
+      if (PREC) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (PREC) {
+        for (int r = 0; r < 4; ++r) {
           o[4 * r] = (uint16_t)dh4[r];
           o[256 + 4 * r] = (uint16_t)dl4[r];
-        } else {
-          o[4 * r] = __builtin_bit_cast(uint16_t, (_Float16)ds[r]);
         }
+      } else {
+        const float am = fmaxf(fmaxf(fabsf(ds[0]), fabsf(ds[1])), fmaxf(fabsf(ds[2]), fabsf(ds[3])));
+        const int ex = fp16_block_exp(wave_max_uniform(am));
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          o[4 * r] = __builtin_bit_cast(uint16_t, (_Float16)__builtin_amdgcn_ldexpf(ds[r], -ex));
+        if (lane == 0) a.dsexp[et] = ex;
       }
     }
     f32x4 u[ND];
@@ -1220,9 +1272,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
 // turns it by -CR, and R(., -c_t) at the end brings it back, so that
 //   X_end = X_start + sum_s R^-1(dq~_s, a - s CR).
 struct DqDsLevel {
-  const uint16_t *kt_h, *kt_l;  // K~ transposed per 16-node block
+  const uint16_t *kt_h, *kt_l;  // K~ transposed per 16-node block (bf16 hi, lo; or fp16)
+  const int32_t* kexp;          // fp16 form: exponent of each block
   const int4* emap;             // (query group, slot) -> {entry, mask lo, mask hi, 0}
   const uint16_t* ds;
+  const int32_t* dsexp;         // fp16 form: exponent of each dS tile
   int64_t Np, pw;
 };
 
@@ -1235,18 +1289,22 @@ struct DqDsArgs {
   float scale;
 };
 
-template <int D>
+// One tile's staged inputs: K~^T of the 16-node block (bf16 hi and lo, or
+// fp16) and the tile's dS (bf16 hi and lo, 1 KB, or fp16, 512 B).
+template <int D, bool F16>
 struct DqStage {
-  static constexpr int KTB = 16 * D * 2;  // one 16-node block of K~^T, bf16
+  static constexpr int KTB = 16 * D * 2;  // one 16-node block of K~^T, 16-bit
   static constexpr int OFF_KL = KTB;
-  static constexpr int OFF_DS = 2 * KTB;  // dS: fp16 (512 B) or bf16 hi, lo (1 KB)
-  static constexpr int BYTES = 2 * KTB + 1024;
+  static constexpr int OFF_DS = F16 ? KTB : 2 * KTB;
+  static constexpr int BYTES = OFF_DS + (F16 ? 512 : 1024);
 };
 
-template <int D, bool DS16>
+// F16: K~^T and dS in fp16 with power-of-two scales (one MFMA per product,
+// scaled into the fp32 accumulator); else bf16 hi + lo of both (three).
+template <int D, bool F16>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void dq_ds_kernel(const DqDsArgs a) {
   constexpr int ND = D / 16, HALF = D / 2;
-  using St = DqStage<D>;
+  using St = DqStage<D, F16>;
   __shared__ __attribute__((aligned(16))) char stage_all[kWavesPerBlock][St::BYTES];
   __shared__ float rot_m[2][HALF];  // cos(CR theta), -sin(CR theta)
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -1296,27 +1354,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void d
       while (tau < nt && !tmask(tau, s, chunk)) ++tau;
       return tau;
     };
-    auto issue = [&](int s, int chunk) {
+    // copies of a tile's inputs into the slot; for the fp16 form the tile's
+    // scale exponent (block + dS tile) is loaded first, so that the wait for
+    // the copies covers it too
+    auto issue = [&](int s, int chunk, int& ex) {
       const int node0 = (__builtin_amdgcn_readlane(pe, s) << crlg) + (chunk << 4);
       const int64_t blk = (hrow + (node0 & ~15)) / 16;
+      const int64_t et = (int64_t)__builtin_amdgcn_readlane(sr.x, s) * tpp + chunk;
+      if (F16) ex = P.kexp[blk] + P.dsexp[et];
       const char* kth = (const char*)(P.kt_h + blk * D * 16);
-      const char* ktl = (const char*)(P.kt_l + blk * D * 16);
 #pragma unroll
       for (int j = 0; j < St::KTB / 1024; ++j) {
         __builtin_amdgcn_global_load_lds(kth + (j * 64 + lane) * 16, (lds_void*)(slot + j * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(ktl + (j * 64 + lane) * 16,
-                                         (lds_void*)(slot + St::OFF_KL + j * 1024), 16, 0, 0);
+        if (!F16) {
+          const char* ktl = (const char*)(P.kt_l + blk * D * 16);
+          __builtin_amdgcn_global_load_lds(ktl + (j * 64 + lane) * 16,
+                                           (lds_void*)(slot + St::OFF_KL + j * 1024), 16, 0, 0);
+        }
       }
-      const char* dsp = (const char*)(P.ds + ((int64_t)__builtin_amdgcn_readlane(sr.x, s) * tpp + chunk) *
-                                                 (DS16 ? 256 : 512));
-      if (!DS16 || lane < 32)
+      const char* dsp = (const char*)(P.ds + et * (F16 ? 256 : 512));
+      if (!F16 || lane < 32)
         __builtin_amdgcn_global_load_lds(dsp + lane * 16, (lds_void*)(slot + St::OFF_DS), 16, 0, 0);
     };
     // into the frame of slot 0
     rot_acc<D>(X, a.cosb + (int64_t)apos * HALF, a.sinb + (int64_t)apos * HALF, kg);
-    int s = 0, chunk = 0, cur_slot = 0;
+    int s = 0, chunk = 0, cur_slot = 0, ex = 0;
     int tau = next_tile(0, s, chunk);
-    if (tau < nt) issue(s, chunk);
+    if (tau < nt) issue(s, chunk, ex);
     while (tau < nt) {
       int sn = 0, chn = 0;
       const int tn = next_tile(tau + 1, sn, chn);
@@ -1332,28 +1396,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void d
       for (int n = 0; n < ND; ++n) {
         const int off = n * 512 + piece * 128 + u16 * 8;
         kt[n] = *(const s16x4*)(slot + off);
-        ktl[n] = *(const s16x4*)(slot + St::OFF_KL + off);
+        if (!F16) ktl[n] = *(const s16x4*)(slot + St::OFF_KL + off);
       }
-      s16x4 dsh, dsl;
-      if (DS16) {
-        // fp16 dS as bf16 hi + lo (exact: 11 significant bits)
-        typedef __attribute__((ext_vector_type(4))) _Float16 h16x4;
-        const h16x4 hv = *(const h16x4*)(slot + St::OFF_DS + kg * 128 + u16 * 8);
-        const float f[4] = {(float)hv[0], (float)hv[1], (float)hv[2], (float)hv[3]};
-        pack4_split(f, dsh, dsl);
-      } else {
-        dsh = *(const s16x4*)(slot + St::OFF_DS + kg * 128 + u16 * 8);
-        dsl = *(const s16x4*)(slot + St::OFF_DS + 512 + kg * 128 + u16 * 8);
-      }
+      const s16x4 dsh = *(const s16x4*)(slot + St::OFF_DS + kg * 128 + u16 * 8);
+      s16x4 dsl;
+      if (!F16) dsl = *(const s16x4*)(slot + St::OFF_DS + 512 + kg * 128 + u16 * 8);
       // the slot's reads have landed before the next copies overwrite it
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
       __builtin_amdgcn_wave_barrier();
-      if (tn < nt) issue(sn, chn);
+      const int ex_cur = ex;
+      if (tn < nt) issue(sn, chn, ex);
+      if (F16) {
+        typedef __attribute__((ext_vector_type(4))) _Float16 h16x4;
+        const float sc = __builtin_amdgcn_ldexpf(1.f, ex_cur);
 #pragma unroll
-      for (int n = 0; n < ND; ++n) {
-        X[n] = mma16(kt[n], dsh, X[n]);
-        X[n] = mma16(kt[n], dsl, X[n]);
-        X[n] = mma16(ktl[n], dsh, X[n]);
+        for (int n = 0; n < ND; ++n) {
+          const f32x4 y = __builtin_amdgcn_mfma_f32_16x16x16f16(
+              __builtin_bit_cast(h16x4, kt[n]), __builtin_bit_cast(h16x4, dsh), f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          X[n] += sc * y;
+        }
+      } else {
+#pragma unroll
+        for (int n = 0; n < ND; ++n) {
+          X[n] = mma16(kt[n], dsh, X[n]);
+          X[n] = mma16(kt[n], dsl, X[n]);
+          X[n] = mma16(ktl[n], dsh, X[n]);
+        }
       }
       tau = tn;
       s = sn;
@@ -1416,8 +1484,14 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
                        (const uint16_t*)(tws + P.off_kh[l]), (const uint16_t*)(tws + P.off_kl[l]),
                        (const uint16_t*)(tws + P.off_vh[l]),
                        P.off_vl[l] >= 0 ? (const uint16_t*)(tws + P.off_vl[l]) : nullptr, P.Np[l],
-                       d->D, total, U16(BP.off_kt[0][l]), U16(BP.off_kt[1][l]),
+                       d->D, total, PREC ? U16(BP.off_kt[0][l]) : nullptr, U16(BP.off_kt[1][l]),
                        U16(BP.off_vr[0][l]), U16(BP.off_vr[1][l]));
+    if (!PREC && BP.use_ds) {
+      const int64_t nblk = BH * (P.Np[l] / 16);
+      hipLaunchKernelGGL(pack_kt16_kernel<D>, dim3((unsigned)((nblk + 3) / 4)), dim3(256), 0, st,
+                         (const uint16_t*)(tws + P.off_kh[l]), (const uint16_t*)(tws + P.off_kl[l]),
+                         P.Np[l], nblk, U16(BP.off_kt[0][l]), (int32_t*)(ws + BP.off_kexp[l]));
+    }
   }
   uint32_t* bm = (uint32_t*)(ws + BP.off_bitmap);
   int32_t* cnt = (int32_t*)(ws + BP.off_cnt);
@@ -1472,6 +1546,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.sinb = sinb;
     a.partial = partial;
     a.ds = BP.use_ds ? U16(BP.off_ds[l]) : nullptr;
+    a.dsexp = BP.off_dsexp[l] >= 0 ? (int32_t*)(ws + BP.off_dsexp[l]) : nullptr;
     a.N = P.N[l];
     a.Np = P.Np[l];
     a.pw = P.pw[l];
@@ -1525,8 +1600,10 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     for (int l = 0; l < P.L; ++l) {
       a.lv[l].kt_h = U16(BP.off_kt[0][l]);
       a.lv[l].kt_l = U16(BP.off_kt[1][l]);
+      a.lv[l].kexp = BP.off_kexp[l] >= 0 ? (const int32_t*)(ws + BP.off_kexp[l]) : nullptr;
       a.lv[l].emap = (const int4*)(ws + BP.off_emap[l]);
       a.lv[l].ds = U16(BP.off_ds[l]);
+      a.lv[l].dsexp = BP.off_dsexp[l] >= 0 ? (const int32_t*)(ws + BP.off_dsexp[l]) : nullptr;
       a.lv[l].Np = P.Np[l];
       a.lv[l].pw = P.pw[l];
     }

@@ -261,6 +261,36 @@ __device__ __forceinline__ void rope_frag(const float (&x)[D / 32][8], const flo
 
 // sum over the 16 lanes of a DPP row (quad xor 1, quad xor 2, half-row
 // mirror, row mirror); every lane of the row gets the result
+// DPP helpers
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// sum / max over the 16 lanes of a row (quad xor 1, quad xor 2, half-row
+// mirror, row mirror); every lane of the row gets the result
+__device__ __forceinline__ float row_sum16(float x) {
+  x += dpp<0xB1>(x);
+  x += dpp<0x4E>(x);
+  x += dpp<0x141>(x);
+  x += dpp<0x140>(x);
+  return x;
+}
+__device__ __forceinline__ float row_max16(float x) {
+  x = fmaxf(x, dpp<0xB1>(x));
+  x = fmaxf(x, dpp<0x4E>(x));
+  x = fmaxf(x, dpp<0x141>(x));
+  x = fmaxf(x, dpp<0x140>(x));
+  return x;
+}
+__device__ __forceinline__ float wave_max_uniform(float x) {
+  x = row_max16(x);
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
 __device__ __forceinline__ int row_sum16i(int x) {
   x += __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);
   x += __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);

@@ -175,6 +175,74 @@ struct FwdStage {
   static constexpr int BYTES = OFF_V + (PREC ? 2 : 1) * VB;
 };
 
+// Copies of one tile's inputs into a wave's LDS slot (FwdStage layout) by
+// buffer loads over one (b, h_kv) block of the level arrays: offsets past
+// the block read as zero, so rows past the level's nodes are harmless (their
+// scores are masked).  The lane offsets are recomputed per call (an opaque
+// copy of the lane index) instead of being hoisted and held in registers.
+template <int D, bool PREC>
+struct TileStage {
+  using St = FwdStage<D, PREC>;
+  char* slot;
+  __amdgpu_buffer_rsrc_t rkh, rkl, rvh, rvl;
+
+  __device__ __forceinline__ void issue(int node0, bool with_v, int lane) const {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+#pragma unroll
+    for (int j = 0; j < (St::NCH + 63) / 64; ++j) {
+      const int pc = j * 64 + ln;
+      const int g = pc / (St::CPR + 1);
+      const int c = pc - g * (St::CPR + 1);
+      const int off = (node0 + g) * (D * 2) + (c < St::CPR ? c : 0) * 16;
+      if ((St::NCH % 64 == 0) || pc < St::NCH) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rkh, (lds_void*)(slot + j * 1024), 16, off, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rkl, (lds_void*)(slot + St::OFF_KL + j * 1024), 16,
+                                                 off, 0, 0, 0);
+      }
+    }
+    if (with_v) {
+      const int voff = (node0 >> 4) * St::VB;
+#pragma unroll
+      for (int j = 0; j < St::VB / 1024; ++j) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rvh, (lds_void*)(slot + St::OFF_V + j * 1024), 16,
+                                                 voff + (j * 64 + ln) * 16, 0, 0, 0);
+        if (PREC)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rvl, (lds_void*)(slot + St::OFF_VL + j * 1024), 16,
+                                                   voff + (j * 64 + ln) * 16, 0, 0, 0);
+      }
+    }
+  }
+  static __device__ __forceinline__ void wait_copies() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the slot's copies have landed
+    __builtin_amdgcn_wave_barrier();
+  }
+  static __device__ __forceinline__ void reads_done() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slot's reads have completed
+    __builtin_amdgcn_wave_barrier();
+  }
+  // K~ fragments of row (candidate) u16, the lane group's d-slots
+  __device__ __forceinline__ void kread(bf16x8 (&kh)[D / 32], bf16x8 (&kl)[D / 32], int lane) const {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const char* row = slot + (ln & 15) * St::KRP;
+#pragma unroll
+    for (int m = 0; m < D / 32; ++m) {
+      kh[m] = *(const bf16x8*)(row + dslot<D>(ln >> 4, m) * 2);
+      kl[m] = *(const bf16x8*)(row + St::OFF_KL + dslot<D>(ln >> 4, m) * 2);
+    }
+  }
+  // V^T fragments: nodes c0 .. c0+3 of the staged block at d = 16n + u16
+  __device__ __forceinline__ void vread(s16x4 (&vh)[D / 16], s16x4 (&vl)[D / 16], int c0,
+                                        int u16) const {
+#pragma unroll
+    for (int n = 0; n < D / 16; ++n) {
+      vh[n] = *(const s16x4*)(slot + St::OFF_V + ((16 * n + u16) * 16 + c0) * 2);
+      if (PREC) vl[n] = *(const s16x4*)(slot + St::OFF_VL + ((16 * n + u16) * 16 + c0) * 2);
+    }
+  }
+};
+
 // Streaming forward for levels of 17..64 candidate tiles (e.g. top_k 32 with
 // CR 32): one wave per query group; upper levels score every tile for the
 // importance, select, then score again for the accumulation.  Each tile's
@@ -250,65 +318,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       a.parents[((((int64_t)l * a.B + b) * a.T + t) * a.Hkv + h) * TK + lane] = pv;
     const int64_t hrow = ((int64_t)b * a.Hkv + h) * P.Np;
     const int lvl_bytes = (int)(P.Np * D * 2);  // one (b, h_kv) block of a level array
-    const __amdgpu_buffer_rsrc_t rkh = buf_rsrc(P.kh + hrow * D, lvl_bytes);
-    const __amdgpu_buffer_rsrc_t rkl = buf_rsrc(P.kl + hrow * D, lvl_bytes);
-    const __amdgpu_buffer_rsrc_t rvh = buf_rsrc(P.vh + hrow * D, lvl_bytes);
-    const __amdgpu_buffer_rsrc_t rvl = buf_rsrc(PREC ? P.vl + hrow * D : P.vh + hrow * D, lvl_bytes);
+    const TileStage<D, PREC> stg{slot, buf_rsrc(P.kh + hrow * D, lvl_bytes),
+                                 buf_rsrc(P.kl + hrow * D, lvl_bytes),
+                                 buf_rsrc(P.vh + hrow * D, lvl_bytes),
+                                 buf_rsrc((PREC ? P.vl : P.vh) + hrow * D, lvl_bytes)};
     const bool upper = l > 0;
     auto slot_of = [&](int tau) { return wide ? (tau << 4) >> crlg : tau; };
     auto node0_of = [&](int tau) {
       return (W.par[cur][slot_of(tau)] << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0);
     };
-    // copies of tile tau's K~ rows (and V^T block) into the slot; rows past
-    // the level's nodes read as zero (never used: their scores are masked)
-    auto issue = [&](int tau, bool with_v) {
-      const int node0 = node0_of(tau);
-      // the lane offsets below are cheap to recompute: keep them out of the
-      // registers held across the tile loop
-      int ln = lane;
-      asm volatile("" : "+v"(ln));
-#pragma unroll
-      for (int j = 0; j < (St::NCH + 63) / 64; ++j) {
-        const int pc = j * 64 + ln;
-        const int g = pc / (St::CPR + 1);
-        const int c = pc - g * (St::CPR + 1);
-        const int off = (node0 + g) * (D * 2) + (c < St::CPR ? c : 0) * 16;
-        if ((St::NCH % 64 == 0) || pc < St::NCH) {
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rkh, (lds_void*)(slot + j * 1024), 16, off, 0, 0, 0);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rkl, (lds_void*)(slot + St::OFF_KL + j * 1024), 16,
-                                                   off, 0, 0, 0);
-        }
-      }
-      if (with_v) {
-        const int voff = (node0 >> 4) * St::VB;
-#pragma unroll
-        for (int j = 0; j < St::VB / 1024; ++j) {
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rvh, (lds_void*)(slot + St::OFF_V + j * 1024), 16,
-                                                   voff + (j * 64 + ln) * 16, 0, 0, 0);
-          if (PREC)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rvl, (lds_void*)(slot + St::OFF_VL + j * 1024),
-                                                     16, voff + (j * 64 + ln) * 16, 0, 0, 0);
-        }
-      }
-    };
-    auto wait_copies = [&]() {
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the slot's copies have landed
-      __builtin_amdgcn_wave_barrier();
-    };
-    auto reads_done = [&]() {
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slot's reads have completed
-      __builtin_amdgcn_wave_barrier();
-    };
-    auto kread = [&](bf16x8 (&kh)[KS], bf16x8 (&kl)[KS]) {
-      int ln = lane;
-      asm volatile("" : "+v"(ln));
-      const char* row = slot + (ln & 15) * St::KRP;
-#pragma unroll
-      for (int m = 0; m < KS; ++m) {
-        kh[m] = *(const bf16x8*)(row + dslot<D>(ln >> 4, m) * 2);
-        kl[m] = *(const bf16x8*)(row + St::OFF_KL + dslot<D>(ln >> 4, m) * 2);
-      }
-    };
+    auto issue = [&](int tau, bool with_v) { stg.issue(node0_of(tau), with_v, lane); };
+    auto wait_copies = [&]() { stg.wait_copies(); };
+    auto reads_done = [&]() { stg.reads_done(); };
+    auto kread = [&](bf16x8 (&kh)[KS], bf16x8 (&kl)[KS]) { stg.kread(kh, kl, lane); };
     // the query turned to a slot: R(q, apos) at slot 0, -CR per slot after
     float qr[KS][8];
     int cur_slot = 0;
@@ -452,11 +474,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       // V^T fragment: nodes node0 + 4kg + 0..3 of the staged block at d = 16n + u16
       const int c0 = (node0 & 15) + (4 * kg < CRU ? 4 * kg : 0);
       s16x4 vh[ND], vl[ND];
-#pragma unroll
-      for (int n = 0; n < ND; ++n) {
-        vh[n] = *(const s16x4*)(slot + St::OFF_V + ((16 * n + u16) * 16 + c0) * 2);
-        if (PREC) vl[n] = *(const s16x4*)(slot + St::OFF_VL + ((16 * n + u16) * 16 + c0) * 2);
-      }
+      stg.vread(vh, vl, c0, u16);
       reads_done();
       if (tau + 1 < nt) issue(tau + 1, true);
       bf16x8 qh[KS], ql[KS];
@@ -536,36 +554,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   }
 }
 
-
-// ---------------------------------------------------------------- DPP helpers
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
-}
-// sum / max over the 16 lanes of a row (quad xor 1, quad xor 2, half-row
-// mirror, row mirror); every lane of the row gets the result
-__device__ __forceinline__ float row_sum16(float x) {
-  x += dpp<0xB1>(x);
-  x += dpp<0x4E>(x);
-  x += dpp<0x141>(x);
-  x += dpp<0x140>(x);
-  return x;
-}
-__device__ __forceinline__ float row_max16(float x) {
-  x = fmaxf(x, dpp<0xB1>(x));
-  x = fmaxf(x, dpp<0x4E>(x));
-  x = fmaxf(x, dpp<0x141>(x));
-  x = fmaxf(x, dpp<0x140>(x));
-  return x;
-}
-__device__ __forceinline__ float wave_max_uniform(float x) {
-  x = row_max16(x);
-  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
-  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
-  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
-  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
-  return fmaxf(fmaxf(a, b), fmaxf(c, d));
-}
 
 // exp(x) for x <= 0 (x = -inf gives 0) including subnormal results, which
 // torch's CPU exp produces and the selection's exact-tie order depends on;

@@ -225,3 +225,31 @@ def test_backward_recomputed_dq(cfg, monkeypatch):
     q, k, v, dO = inputs(B, T, H, Hkv, D, dtype, seed, dO=True)
     out, par, gmax, gsum, dq, dk, dv = run(q, k, v, dO, CR, TK, MTN)
     print(check_backward(q, k, v, dO, CR, TK, MTN, dtype, out, par, gmax, gsum, dq, dk, dv), flush=True)
+
+
+@pytest.mark.parametrize("cfg", [(1, 2048, 16, 1, 128, 16, 16, 128, 71),
+                                 (1, 1500, 8, 2, 64, 8, 16, 64, 72),
+                                 (1, 1200, 16, 4, 32, 16, 8, 128, 73)],
+                         ids=lambda c: f"D{c[4]}cr{c[5]}")
+def test_backward_power_of_two_scalings(cfg):
+    """bf16 inputs keep the stored dS and the K~ blocks dq reads as fp16
+    with a power-of-two scale per tile / block.  Gradients are linear in dO,
+    and (q 2^-s, k 2^s) leaves every score unchanged while dq scales by 2^s
+    and dk by 2^-s; power-of-two factors commute with every rounding step
+    when nothing overflows or underflows, so the scaled runs reproduce the
+    plain run's gradients exactly.  The factors take |dS| far past fp16's
+    largest value (dO 2^15), deep below its smallest (dO 2^-30) and K~ past
+    it (k 2^16): without the per-tile / per-block scales these runs would
+    give inf, or lose the small values."""
+    B, T, H, Hkv, D, CR, TK, MTN, seed = cfg
+    print(f"case {cfg}", flush=True)
+    q, k, v, dO = inputs(B, T, H, Hkv, D, "bfloat16", seed, dO=True)
+    base = run(q, k, v, dO, CR, TK, MTN)
+    for s_do, s_k in ((15, 0), (-30, 0), (0, 16)):
+        print(f"dO 2^{s_do}, k 2^{s_k}", flush=True)
+        got = run(q * 2.0 ** -s_k, k * 2.0 ** s_k, v, dO * 2.0 ** s_do, CR, TK, MTN)
+        assert np.array_equal(got[1], base[1])  # same selection
+        for name, i, f in (("dq", 4, s_do + s_k), ("dk", 5, s_do - s_k), ("dv", 6, s_do)):
+            g = got[i].astype(np.float64) * 2.0 ** -f
+            assert np.all(np.isfinite(g)), name
+            np.testing.assert_array_equal(g, base[i].astype(np.float64), err_msg=name)
