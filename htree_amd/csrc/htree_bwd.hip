@@ -36,7 +36,10 @@
 
 namespace htree {
 
-constexpr int64_t kDsBudget = 24ll << 30;  // bytes of stored dS before dq recomputes
+// Bytes of stored dS before dq recomputes the scores: a third of the
+// device's memory (96 GB on a 288 GB MI355X), or kDsBudget when the device
+// cannot be queried.
+constexpr int64_t kDsBudget = 24ll << 30;
 
 struct BwdPlan {
   Plan P;
@@ -113,18 +116,31 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
   // tile, 512 B a tile (11 significant bits, as many as the reference's tf32
   // dq product carries); fp16 / fp32 inputs: bf16 hi + lo, 1 KB a tile.
   b->ds_elems = P.precise ? 512 : 256;
-  const int64_t ds_level = b->max_entries * b->tpp * b->ds_elems * 2;
+  // entries of a level: at most min(top_k, parent rows) per query group
+  int64_t ent[HTREE_MAX_LEVELS], ds_total = 0;
+  for (int l = 0; l < P.L; ++l) {
+    const int64_t Pl = (P.N[l] + CR - 1) / CR;
+    ent[l] = BH * d->T * (d->top_k < Pl ? d->top_k : Pl);
+    ds_total += ent[l] * b->tpp * b->ds_elems * 2;
+  }
   // (wide configurations: dq recomputes, its list per wave lives in LDS).
   // HTREE_DS_BUDGET_MB overrides the budget (read at every plan: keep it
-  // fixed between the workspace query and the backward call).
+  // fixed between the workspace query and the backward call, which checks
+  // the workspace it is given against its own plan).
   int64_t budget = kDsBudget;
+  {
+    int dev = 0;
+    size_t total = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceTotalMem(&total, dev) == hipSuccess && total > 0)
+      budget = (int64_t)(total / 3);
+  }
   if (const char* e = getenv("HTREE_DS_BUDGET_MB")) budget = (int64_t)atoll(e) << 20;
-  b->use_ds = !P.wide && ds_level * P.L <= budget;
+  b->use_ds = !P.wide && ds_total <= budget;
   for (int l = 0; l < P.L; ++l) {
-    b->off_rec[l] = (b->use_ds || l == 0) ? take(b->max_entries * 16) : b->off_rec[0];
+    b->off_rec[l] = b->use_ds ? take(ent[l] * 16) : l == 0 ? take(b->max_entries * 16) : b->off_rec[0];
     b->off_emap[l] = b->use_ds ? take(b->max_entries * 16) : -1;
-    b->off_ds[l] = b->use_ds ? take(ds_level) : -1;
-    b->off_dsexp[l] = (b->use_ds && !P.precise) ? take(b->max_entries * b->tpp * 4) : -1;
+    b->off_ds[l] = b->use_ds ? take(ent[l] * b->tpp * b->ds_elems * 2) : -1;
+    b->off_dsexp[l] = (b->use_ds && !P.precise) ? take(ent[l] * b->tpp * 4) : -1;
   }
   b->off_partial = take(b->max_pieces * b->tpp * 16 * (int64_t)d->D * 2 * 4);
   b->bytes = off;
