@@ -556,7 +556,7 @@ struct DkvArgs {
 // delta of the 16 heads.  Head rows are padded by one 16-byte chunk (pitch
 // RP), so that 8 lanes reading one chunk position of 8 heads, and lanes
 // reading one column of 4 heads, hit distinct LDS banks with linear addresses.
-template <int D, typename TIn>
+template <int D, typename TIn, int NT = 1>
 struct Stage {
   static constexpr int CPR = D * (int)sizeof(TIn) / 16;  // chunks per head row
   static constexpr int RP = (CPR + 1) * 16;               // padded row pitch (bytes)
@@ -565,8 +565,8 @@ struct Stage {
   static constexpr int OFF_DO = ROWB;
   static constexpr int OFF_TAB = 2 * ROWB;          // cos [D/2] then sin [D/2]
   static constexpr int OFF_SM = OFF_TAB + D * 4;    // gmax[16], gsum[16], delta[16], m_ref[16]
-  static constexpr int OFF_SC = OFF_SM + 256;       // stored scores of the tile (fp16, 512 B)
-  static constexpr int BYTES = OFF_SC + 512;
+  static constexpr int OFF_SC = OFF_SM + 256;       // stored scores of NT tiles (fp16, 512 B each)
+  static constexpr int BYTES = OFF_SC + 512 * NT;
   static constexpr int SLOTS = BYTES * 2 <= 20 * 1024 ? 2 : 1;  // double-buffer if it fits
 };
 
@@ -579,12 +579,15 @@ __device__ __forceinline__ int row_off(int g, int e) {
 
 // Asynchronous copies of one entry's inputs into `slot` (buffer loads into
 // LDS: the bases live in scalar registers, the lanes hold 32-bit offsets).
-template <int D, typename TIn, bool HAS_S>
+// The copies come in three parts (q rows, dO rows, the rest); wave w of nw
+// waves sharing the slot issues the parts i with i % nw == w.
+template <int D, typename TIn, bool HAS_S, int NT = 1>
 __device__ __forceinline__ void stage_issue(char* slot, const DkvArgs& a, int64_t grp, int rs,
-                                            int tile, int lane) {
+                                            int tile, int lane, int w = 0, int nw = 1) {
+  const bool pq = nw == 1 || w == 0, pd = nw == 1 || w == 1 % nw, pr = nw == 1 || w == 2 % nw;
   const int64_t hq0 = grp * a.G;
   const int rho = rs & 0xffff;
-  using St = Stage<D, TIn>;
+  using St = Stage<D, TIn, NT>;
   constexpr int HALF = D / 2;
   constexpr int ES = (int)sizeof(TIn);
   constexpr int CPR = St::CPR;
@@ -604,11 +607,20 @@ __device__ __forceinline__ void stage_issue(char* slot, const DkvArgs& a, int64_
     int off = (g * CPR + (c < CPR ? c : 0)) * 16;
     off = g < G ? off : 0;  // rows past the group: in-bounds filler, never used
     if ((St::NCH % 64 == 0) || P < St::NCH) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void*)(slot + j * 1024), 16, off, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_void*)(slot + St::OFF_DO + j * 1024), 16,
-                                               off, 0, 0, 0);
+      if (pq) __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void*)(slot + j * 1024), 16, off, 0, 0, 0);
+      if (pd)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_void*)(slot + St::OFF_DO + j * 1024), 16,
+                                                 off, 0, 0, 0);
     }
   }
+  // the stored scores are per tile: every wave copies its own tile's
+  if (HAS_S && lane < 32) {
+    const int tau = (rs >> 16) * a.tpp + tile;  // the forward's tile index
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        buf_rsrc(a.sc + (grp * a.max_tiles + tau) * 256, 512),
+        (lds_void*)(slot + St::OFF_SC + (NT > 1 ? tile : 0) * 512), 16, lane * 16, 0, 0, 0);
+  }
+  if (!pr) return;
   constexpr int CH = HALF / 4;  // 16-byte chunks of one table row
   if (lane < CH) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(a.cosb + (int64_t)rho * HALF, HALF * 4),
@@ -629,12 +641,6 @@ __device__ __forceinline__ void stage_issue(char* slot, const DkvArgs& a, int64_
       __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(a.smref + grp * 16, 64),
                                                (lds_void*)(slot + St::OFF_SM + 192), 4, lane * 4, 0,
                                                0, 0);
-  }
-  if (HAS_S && lane < 32) {
-    const int tau = (rs >> 16) * a.tpp + tile;  // the forward's tile index
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        buf_rsrc(a.sc + (grp * a.max_tiles + tau) * 256, 512), (lds_void*)(slot + St::OFF_SC), 16,
-        lane * 16, 0, 0, 0);
   }
 }
 
@@ -717,17 +723,31 @@ struct DoRow<D, __bf16> {
   }
 };
 
-template <int D, bool PREC, typename TIn, bool HAS_S>
+// PW = 1: blocks of four independent waves, one per (piece, tile).  PW =
+// tiles per parent (2 or 4, CR 32 / 64): one block of PW waves per piece,
+// wave w taking tile w; the waves share one staged copy of each entry (each
+// issues a part of the copies) and meet at a barrier per entry.
+template <int D, bool PREC, typename TIn, bool HAS_S, int PW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void dkv_kernel(const DkvArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
-  using St = Stage<D, TIn>;
-  __shared__ __attribute__((aligned(16))) char stage_a[kWavesPerBlock][St::BYTES];
-  __shared__ __attribute__((aligned(16))) char stage_b[kWavesPerBlock][St::SLOTS == 2 ? St::BYTES : 16];
+  using St = Stage<D, TIn, PW>;
+  constexpr bool TWO = PW > 1 || St::SLOTS == 2;   // two slots per wave (or per shared block)
+  constexpr int NSW = PW > 1 ? 1 : kWavesPerBlock;  // staging areas per block
+  __shared__ __attribute__((aligned(16))) char stage_a[NSW][St::BYTES];
+  __shared__ __attribute__((aligned(16))) char stage_b[NSW][TWO ? St::BYTES : 16];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int u16 = lane & 15, kg = lane >> 4;
-  const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wv;
-  const int64_t pc = gw / a.tpp;
-  const int tile = (int)(gw % a.tpp);
+  const int sw = PW > 1 ? 0 : wv;
+  int64_t pc;
+  int tile;
+  if (PW > 1) {
+    pc = blockIdx.x;
+    tile = wv;
+  } else {
+    const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wv;
+    pc = gw / a.tpp;
+    tile = (int)(gw % a.tpp);
+  }
   if (pc >= *a.npieces) return;
   const int32_t row = a.ptab[3 * pc], e0 = a.ptab[3 * pc + 1], ne = a.ptab[3 * pc + 2];
   const int64_t bh = row / a.Pl;
@@ -738,7 +758,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   const int CRU = CR < 16 ? CR : 16;
   const int coff = CR >= 16 ? tile * 16 : 0;  // first child of the tile
   const int node0 = (p << crlg) + coff;
-  if (node0 >= a.N) return;  // tile past the last node (CR > 16): no children, never read
+  // a tile past the last node (CR > 16) has no children and is never read;
+  // in a shared block its wave still takes part in the staging
+  const bool live = node0 < a.N;
+  if (PW == 1 && !live) return;
   const uint32_t cmask = CR < 16 ? ((1u << CR) - 1u) : 0xffffu;
   auto tile_mask = [&](const int4& rc) {
     const unsigned long long m64 = ((unsigned long long)(uint32_t)rc.w << 32) | (uint32_t)rc.z;
@@ -747,7 +770,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   // stationary K~ / V fragments of the tile's children (lane cand = u16)
   bf16x8 kh[KS], kl[KS], vh[KS], vl[KS];
   {
-    const int64_t r = (bh * a.Np + node0 + (u16 < CRU ? u16 : 0)) * D;
+    const int64_t r = (bh * a.Np + (live ? node0 : 0) + (u16 < CRU ? u16 : 0)) * D;
     if (!HAS_S) {  // K~ only rebuilds the scores
       load_frag<D>(a.kh + r, kg, kh);
       load_frag<D>(a.kl + r, kg, kl);
@@ -762,8 +785,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   auto grp_of = [&](int t) { return (b * a.T + t) * a.Hkv + h; };
 
   // The piece's records are held 64 at a time in the lanes (lane i = entry
-  // base + i) with a ballot of the entries whose tile mask is not empty;
-  // empty entries are skipped without staging.
+  // base + i) with a ballot of the entries whose tile mask (shared block:
+  // the masks of all its tiles) is not empty; empty entries are skipped
+  // without staging.
   int base = -64;
   int4 rb = make_int4(0, 0, 0, 0);
   unsigned long long work = 0ull;
@@ -773,7 +797,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
         base = e & ~63;
         const bool in = base + lane < ne;
         rb = in ? a.rec[e0 + base + lane] : make_int4(0, 0, 0, 0);
-        work = __ballot(in && tile_mask(rb) != 0u);
+        work = __ballot(in && (PW > 1 ? (rb.z | rb.w) != 0 : tile_mask(rb) != 0u));
       }
       const unsigned long long m = work >> (e - base);
       if (m) return e + (int)__builtin_ctzll(m);
@@ -795,7 +819,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   auto step = [&](const char* __restrict__ S0, char* __restrict__ nxt, const int4 rc, const int en,
                   const int4 rn) __attribute__((always_inline)) {
     wait_stage();
-    if (nxt && en < ne) stage_issue<D, TIn, HAS_S>(nxt, a, grp_of(rn.x), rn.y, tile, lane);
+    // shared block: every wave's part of this entry has landed, and every
+    // wave is done reading `nxt` (the previous entry's slot)
+    if (PW > 1) __syncthreads();
+    if (nxt && en < ne) stage_issue<D, TIn, HAS_S, PW>(nxt, a, grp_of(rn.x), rn.y, tile, lane, wv, PW);
     const float* tab = (const float*)(S0 + St::OFF_TAB);  // cos [HALF], sin [HALF]
     const float* sm = (const float*)(S0 + St::OFF_SM);    // gmax, gsum, delta [16 each]
     const bool ok = (tile_mask(rc) >> u16) & 1u;
@@ -807,7 +834,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
       // kg addressing the 8-byte piece i of the group's 128 bytes (heads
       // 4kg..4kg+3, candidates 4 (i % 4)..+3 of head 4kg + i / 4) gives lane
       // m heads 4kg..4kg+3 of candidate m.
-      const char* p = S0 + St::OFF_SC + lane * 8;
+      const char* p = S0 + St::OFF_SC + (PW > 1 ? tile : 0) * 512 + lane * 8;
       const s16x4 sv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
           (__attribute__((address_space(3))) s16x4*)(const __attribute__((address_space(3))) void*)p);
       const float4 mr = *(const float4*)(sm + 48 + 4 * kg);
@@ -921,18 +948,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
       }
     }
   };
-  if (e < ne) stage_issue<D, TIn, HAS_S>(stage_a[wv], a, grp_of(rc.x), rc.y, tile, lane);
-  if constexpr (St::SLOTS == 2) {
+  if (e < ne) stage_issue<D, TIn, HAS_S, PW>(stage_a[sw], a, grp_of(rc.x), rc.y, tile, lane, wv, PW);
+  if constexpr (TWO) {
     while (e < ne) {
       int en = next_work(e + 1);
       int4 rn = en < ne ? rec_of(en) : make_int4(0, 0, 0, 0);
-      step(stage_a[wv], stage_b[wv], rc, en, rn);
+      step(stage_a[sw], stage_b[sw], rc, en, rn);
       e = en;
       rc = rn;
       if (e >= ne) break;
       en = next_work(e + 1);
       rn = en < ne ? rec_of(en) : make_int4(0, 0, 0, 0);
-      step(stage_b[wv], stage_a[wv], rc, en, rn);
+      step(stage_b[sw], stage_a[sw], rc, en, rn);
       e = en;
       rc = rn;
     }
@@ -940,16 +967,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     while (e < ne) {
       const int en = next_work(e + 1);
       const int4 rn = en < ne ? rec_of(en) : make_int4(0, 0, 0, 0);
-      step(stage_a[wv], nullptr, rc, en, rn);
+      step(stage_a[sw], nullptr, rc, en, rn);
       if (en < ne) {
         wave_sync();  // every lane has read the slot
-        stage_issue<D, TIn, HAS_S>(stage_a[wv], a, grp_of(rn.x), rn.y, tile, lane);
+        stage_issue<D, TIn, HAS_S, PW>(stage_a[sw], a, grp_of(rn.x), rn.y, tile, lane);
       }
       e = en;
       rc = rn;
     }
   }
   wait_stage();
+  if (!live) return;
   // dk of the node = scale R^-1(dK~, node mod CR); write this piece's partial
   float* out = a.partial + ((pc * a.tpp + tile) * 16) * (int64_t)D * 2;
 #pragma unroll
@@ -1579,15 +1607,24 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.max_tiles = P.max_tiles;
     a.scale = scale;
     const int64_t waves = BP.max_pieces * BP.tpp;
-    if (!PREC && scores) {
+    const bool has_s = !PREC && scores;
+    if (has_s) {
       a.sc = (const uint16_t*)scores + (int64_t)l * groups * P.max_tiles * 256;
       a.smref = (const float*)(scores + off_mref) + (int64_t)l * groups * 16;
-      hipLaunchKernelGGL((dkv_kernel<D, PREC, T, true>), dim3((unsigned)((waves + 3) / 4)),
-                         dim3(256), 0, st, a);
-    } else {
-      hipLaunchKernelGGL((dkv_kernel<D, PREC, T, false>), dim3((unsigned)((waves + 3) / 4)),
-                         dim3(256), 0, st, a);
     }
+    // tiles of one parent share each entry's staging (one block per piece)
+#define HT_DKV(HS, PW)                                                                          \
+  hipLaunchKernelGGL((dkv_kernel<D, PREC, T, HS, PW>),                                         \
+                     dim3((unsigned)(PW > 1 ? BP.max_pieces : (waves + 3) / 4)), dim3(PW > 1 ? 64 * PW : 256), \
+                     0, st, a)
+    if (BP.tpp == 4) {
+      if (has_s) HT_DKV(true, 4); else HT_DKV(false, 4);
+    } else if (BP.tpp == 2) {
+      if (has_s) HT_DKV(true, 2); else HT_DKV(false, 2);
+    } else {
+      if (has_s) HT_DKV(true, 1); else HT_DKV(false, 1);
+    }
+#undef HT_DKV
     float* dkl = l == 0 ? dk : (float*)(ws + BP.off_dk[l]);
     float* dvl = l == 0 ? dv : (float*)(ws + BP.off_dv[l]);
     const bool top = l == P.L - 1;

@@ -42,6 +42,8 @@ CASES = [
     (2, 1000, 8, 2, 32, 8, 16, 64, "bfloat16", 10),
     (1, 2500, 16, 4, 32, 4, 32, 64, "float32", 11),
     (1, 3000, 8, 1, 128, 32, 32, 256, "bfloat16", 12),  # BASELINE C4's tree shape
+    (1, 2000, 8, 1, 64, 64, 8, 512, "bfloat16", 14),   # CR 64: four tiles per parent
+    (1, 1500, 4, 1, 128, 64, 4, 256, "float32", 15),
 ]
 
 
