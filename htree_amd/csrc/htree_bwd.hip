@@ -78,8 +78,12 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
     if (b->rows[l] > b->max_rows) b->max_rows = b->rows[l];
   }
   b->max_entries = BH * d->T * d->top_k;
-  int64_t piece = 64;
-  while (piece * 8192 < b->max_entries) piece *= 2;
+  // Rows are cut into pieces of 128 entries (one dkv wave each): long rows
+  // of popular parents spread over many waves, and the kernel's tail stays
+  // short.  Beyond 2^20 pieces per level (16 MB of fp32 partials per 1K
+  // pieces and tile) the pieces grow instead.
+  int64_t piece = 128;
+  while (b->max_entries / piece > (1ll << 20)) piece *= 2;
   b->piece = piece;
   b->max_pieces = (b->max_entries + piece - 1) / piece + b->max_rows;
   int64_t off = 0;
