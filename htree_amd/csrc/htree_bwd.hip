@@ -1004,8 +1004,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
 // dK_l / dV_l [B, N, Hkv, D] of one level: the pieces of each tile are summed
 // (pieces k = first + c + LG i by lane group c, the LG sums then added in a
 // fixed order: deterministic), plus the mean-pool backward of the level above,
-// dK_{l+1}[parent] / n_children(parent), when there is one.  A block covers
-// 256 / LG consecutive values of one (row, tile) partial [k|v][child][d]; LG
+// dK_{l+1}[parent] / n_children(parent), when there is one.  A thread takes 4
+// consecutive d of one partial row (16-byte loads and stores); a block covers
+// 1024 / LG consecutive values of one (row, tile) partial [k|v][child][d]; LG
 // follows the level's pieces per row.
 template <int LG>
 __global__ __launch_bounds__(256) void dkv_reduce_kernel(const float* __restrict__ partial,
@@ -1014,12 +1015,12 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(const float* __restrict
                                                          int64_t Pl, const float* __restrict__ upk,
                                                          const float* __restrict__ upv, int64_t Nup,
                                                          float* __restrict__ dk, float* __restrict__ dv) {
-  constexpr int FPB = 256 / LG;  // values per block
-  __shared__ float red[LG][FPB];
-  const int j = threadIdx.x % FPB, c = threadIdx.x / FPB;
-  const int bpt = 32 * D / FPB;  // blocks per (row, tile)
+  constexpr int TPV = 256 / LG;  // threads per lane group
+  __shared__ float4 red[LG][TPV];
+  const int j = threadIdx.x % TPV, c = threadIdx.x / TPV;
+  const int bpt = D * LG / 32;  // blocks per (row, tile): 32 D values, 1024 / LG per block
   const int64_t rt = blockIdx.x / bpt;
-  const int f = (int)(blockIdx.x % bpt) * FPB + j;  // value within the tile's partial
+  const int f = ((int)(blockIdx.x % bpt) * TPV + j) * 4;  // first value within the tile's partial
   const int kv = f / (16 * D);
   const int cand = (f / D) & 15;
   const int dd = f % D;
@@ -1032,24 +1033,39 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(const float* __restrict
   const int cin = (CR >= 16 ? tile * 16 : 0) + cand;
   const int64_t node = (p << crlg) + cin;
   const float* src = partial + f;
-  float acc = 0.f;
-  for (int32_t k = poff[row] + c; k < poff[row + 1]; k += LG)
-    acc += src[((int64_t)k * tpp + tile) * 16 * D * 2];
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int32_t k = poff[row] + c; k < poff[row + 1]; k += LG) {
+    const float4 x = *(const float4*)(src + ((int64_t)k * tpp + tile) * 16 * D * 2);
+    acc.x += x.x;
+    acc.y += x.y;
+    acc.z += x.z;
+    acc.w += x.w;
+  }
   if (LG > 1) {
     red[c][j] = acc;
     __syncthreads();
     if (c != 0) return;
     acc = red[0][j];
 #pragma unroll
-    for (int i = 1; i < LG; ++i) acc += red[i][j];
+    for (int i = 1; i < LG; ++i) {
+      const float4 x = red[i][j];
+      acc.x += x.x;
+      acc.y += x.y;
+      acc.z += x.z;
+      acc.w += x.w;
+    }
   }
   if (cin >= CR || node >= N) return;
   const float* up = kv ? upv : upk;
   if (up) {
-    const int64_t cnt = (p + 1) * CR < N ? CR : N - p * CR;
-    acc += up[((b * Nup + p) * Hkv + h) * D + dd] / (float)cnt;
+    const float cnt = (float)((p + 1) * CR < N ? CR : N - p * CR);
+    const float4 u = *(const float4*)(up + ((b * Nup + p) * Hkv + h) * D + dd);
+    acc.x += u.x / cnt;
+    acc.y += u.y / cnt;
+    acc.z += u.z / cnt;
+    acc.w += u.w / cnt;
   }
-  (kv ? dv : dk)[((b * N + node) * Hkv + h) * D + dd] = acc;
+  *(float4*)((kv ? dv : dk) + ((b * N + node) * Hkv + h) * D + dd) = acc;
 }
 
 // ---------------------------------------------------------------- dq
@@ -1639,7 +1655,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     const int64_t avg = lstride / (BP.piece * BP.rows[l]);
     const int64_t rt = BP.rows[l] * BP.tpp;
 #define HT_RED(LG)                                                                              \
-  hipLaunchKernelGGL(dkv_reduce_kernel<LG>, dim3((unsigned)(rt * 32 * d->D / (256 / LG))),     \
+  hipLaunchKernelGGL(dkv_reduce_kernel<LG>, dim3((unsigned)(rt * d->D * LG / 32)),            \
                      dim3(256), 0, st, partial, poff, P.N[l], d->H_kv, d->D, CR, P.cr_log2,  \
                      BP.tpp, Pl, upk, upv, nup, dkl, dvl)
     if (avg >= 64)
