@@ -570,6 +570,7 @@ struct Stage {
   static constexpr int OFF_TAB = 2 * ROWB;          // cos [D/2] then sin [D/2]
   static constexpr int OFF_SM = OFF_TAB + D * 4;    // gmax[16], gsum[16], delta[16], m_ref[16]
   static constexpr int OFF_SC = OFF_SM + 256;       // stored scores of NT tiles (fp16, 512 B each)
+  static_assert(NT >= 0, "score tiles");
   static constexpr int BYTES = OFF_SC + 512 * NT;
   static constexpr int SLOTS = BYTES * 2 <= 20 * 1024 ? 2 : 1;  // double-buffer if it fits
 };
@@ -734,7 +735,8 @@ struct DoRow<D, __bf16> {
 template <int D, bool PREC, typename TIn, bool HAS_S, int PW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void dkv_kernel(const DkvArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
-  using St = Stage<D, TIn, PW>;
+  constexpr int NT = HAS_S ? PW : 0;  // stored-score tiles per staged entry
+  using St = Stage<D, TIn, NT>;
   constexpr bool TWO = PW > 1 || St::SLOTS == 2;   // two slots per wave (or per shared block)
   constexpr int NSW = PW > 1 ? 1 : kWavesPerBlock;  // staging areas per block
   __shared__ __attribute__((aligned(16))) char stage_a[NSW][St::BYTES];
@@ -826,7 +828,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     // shared block: every wave's part of this entry has landed, and every
     // wave is done reading `nxt` (the previous entry's slot)
     if (PW > 1) __syncthreads();
-    if (nxt && en < ne) stage_issue<D, TIn, HAS_S, PW>(nxt, a, grp_of(rn.x), rn.y, tile, lane, wv, PW);
+    if (nxt && en < ne) stage_issue<D, TIn, HAS_S, NT>(nxt, a, grp_of(rn.x), rn.y, tile, lane, wv, PW);
     const float* tab = (const float*)(S0 + St::OFF_TAB);  // cos [HALF], sin [HALF]
     const float* sm = (const float*)(S0 + St::OFF_SM);    // gmax, gsum, delta [16 each]
     const bool ok = (tile_mask(rc) >> u16) & 1u;
@@ -952,7 +954,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
       }
     }
   };
-  if (e < ne) stage_issue<D, TIn, HAS_S, PW>(stage_a[sw], a, grp_of(rc.x), rc.y, tile, lane, wv, PW);
+  if (e < ne) stage_issue<D, TIn, HAS_S, NT>(stage_a[sw], a, grp_of(rc.x), rc.y, tile, lane, wv, PW);
   if constexpr (TWO) {
     while (e < ne) {
       int en = next_work(e + 1);
@@ -974,7 +976,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
       step(stage_a[sw], nullptr, rc, en, rn);
       if (en < ne) {
         wave_sync();  // every lane has read the slot
-        stage_issue<D, TIn, HAS_S, PW>(stage_a[sw], a, grp_of(rn.x), rn.y, tile, lane);
+        stage_issue<D, TIn, HAS_S, NT>(stage_a[sw], a, grp_of(rn.x), rn.y, tile, lane);
       }
       e = en;
       rc = rn;

@@ -44,6 +44,7 @@ CASES = [
     (1, 3000, 8, 1, 128, 32, 32, 256, "bfloat16", 12),  # BASELINE C4's tree shape
     (1, 2000, 8, 1, 64, 64, 8, 512, "bfloat16", 14),   # CR 64: four tiles per parent
     (1, 1500, 4, 1, 128, 64, 4, 256, "float32", 15),
+    (1, 2500, 16, 2, 128, 64, 4, 256, "bfloat16", 16),  # CR 64 with the stored scores (16 tiles)
 ]
 
 
