@@ -46,7 +46,9 @@ struct BwdPlan {
   int G, tpp;  // tiles per parent
   int64_t W;   // bitmap words per row
   int64_t rows[HTREE_MAX_LEVELS];
-  int64_t max_rows, max_entries, piece, max_pieces;
+  int64_t max_rows, max_entries, max_pieces;
+  int64_t ent[HTREE_MAX_LEVELS];    // entries of a level: at most min(top_k, parent rows) per group
+  int64_t piece[HTREE_MAX_LEVELS];  // entries per piece, per level
   int64_t off_delta;
   int64_t off_kt[2][HTREE_MAX_LEVELS], off_vr[2][HTREE_MAX_LEVELS];
   int64_t off_kexp[HTREE_MAX_LEVELS];  // bf16 inputs: exponent of each K~^T block
@@ -78,14 +80,23 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
     if (b->rows[l] > b->max_rows) b->max_rows = b->rows[l];
   }
   b->max_entries = BH * d->T * d->top_k;
-  // Rows are cut into pieces of 128 entries (one dkv wave each): long rows
-  // of popular parents spread over many waves, and the kernel's tail stays
-  // short.  Beyond 2^20 pieces per level (16 MB of fp32 partials per 1K
-  // pieces and tile) the pieces grow instead.
-  int64_t piece = 128;
-  while (b->max_entries / piece > (1ll << 20)) piece *= 2;
-  b->piece = piece;
-  b->max_pieces = (b->max_entries + piece - 1) / piece + b->max_rows;
+  // Rows are cut into pieces (one dkv wave each) of 32..128 entries: at
+  // least 16K pieces for a level's largest possible entry count, so that a
+  // level's waves fill the GPU's ~2K wave slots many times over and the
+  // kernel's tail stays short, and long rows of popular parents spread over
+  // many waves.  Beyond 2^20 pieces per level (16 MB of fp32 partials per 1K
+  // pieces and tile at D=128) the pieces grow instead.
+  b->max_pieces = 0;
+  for (int l = 0; l < P.L; ++l) {
+    const int64_t Pl = (P.N[l] + CR - 1) / CR;
+    b->ent[l] = BH * d->T * (d->top_k < Pl ? d->top_k : Pl);
+    int64_t piece = 128;
+    while (piece > 32 && b->ent[l] / piece < (1ll << 14)) piece >>= 1;
+    while (b->ent[l] / piece > (1ll << 20)) piece <<= 1;
+    b->piece[l] = piece;
+    const int64_t np = (b->ent[l] + piece - 1) / piece + b->rows[l];
+    if (np > b->max_pieces) b->max_pieces = np;
+  }
   int64_t off = 0;
   auto take = [&](int64_t bytes) {
     int64_t o = off;
@@ -120,13 +131,9 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
   // tile, 512 B a tile (11 significant bits, as many as the reference's tf32
   // dq product carries); fp16 / fp32 inputs: bf16 hi + lo, 1 KB a tile.
   b->ds_elems = P.precise ? 512 : 256;
-  // entries of a level: at most min(top_k, parent rows) per query group
-  int64_t ent[HTREE_MAX_LEVELS], ds_total = 0;
-  for (int l = 0; l < P.L; ++l) {
-    const int64_t Pl = (P.N[l] + CR - 1) / CR;
-    ent[l] = BH * d->T * (d->top_k < Pl ? d->top_k : Pl);
-    ds_total += ent[l] * b->tpp * b->ds_elems * 2;
-  }
+  const int64_t* ent = b->ent;
+  int64_t ds_total = 0;
+  for (int l = 0; l < P.L; ++l) ds_total += ent[l] * b->tpp * b->ds_elems * 2;
   // (wide configurations: dq recomputes, its list per wave lives in LDS).
   // HTREE_DS_BUDGET_MB overrides the budget (read at every plan: keep it
   // fixed between the workspace query and the backward call, which checks
@@ -1568,7 +1575,11 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
   int32_t* ptab = (int32_t*)(ws + BP.off_ptab);
   int32_t* wpre = (int32_t*)(ws + BP.off_wpre);
   float* partial = (float*)(ws + BP.off_partial);
-  for (int l = P.L - 1; l >= 0; --l) {
+  // A top level of <= top_k nodes passes every candidate down and
+  // accumulates none (src/naive.py:97-101): it has no dS and no dK / dV of
+  // its own, so the passes start one level lower.
+  const int Ltop = (P.L > 1 && P.N[P.L - 1] <= d->top_k) ? P.L - 2 : P.L - 1;
+  for (int l = Ltop; l >= 0; --l) {
     const int64_t Pl = (P.N[l] + CR - 1) / CR;
     const int64_t nrows = BP.rows[l];
     const int64_t words = nrows * BP.W;
@@ -1578,11 +1589,11 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     hipLaunchKernelGGL(bitmap_set_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
                        parents + l * lstride, d->T, d->H_kv, d->top_k, Pl, BP.W, ent, bm);
     hipLaunchKernelGGL(row_scan_kernel, dim3((unsigned)nrows), dim3(256), 0, st, bm, BP.W,
-                       (int)BP.piece, wpre, cnt, pcnt);
+                       (int)BP.piece[l], wpre, cnt, pcnt);
     hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, cnt, nrows, rowoff);
     hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, pcnt, nrows, poff);
     hipLaunchKernelGGL(piece_kernel, dim3((unsigned)((nrows + 255) / 256)), dim3(256), 0, st, cnt,
-                       rowoff, poff, nrows, (int)BP.piece, ptab, npieces);
+                       rowoff, poff, nrows, (int)BP.piece[l], ptab, npieces);
     int4* recs = (int4*)(ws + BP.off_rec[l]);
     if (d->top_k > 64)
       hipLaunchKernelGGL(record_wide_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
@@ -1649,12 +1660,12 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
 #undef HT_DKV
     float* dkl = l == 0 ? dk : (float*)(ws + BP.off_dk[l]);
     float* dvl = l == 0 ? dv : (float*)(ws + BP.off_dv[l]);
-    const bool top = l == P.L - 1;
+    const bool top = l == Ltop;
     const float* upk = top ? nullptr : (const float*)(ws + BP.off_dk[l + 1]);
     const float* upv = top ? nullptr : (const float*)(ws + BP.off_dv[l + 1]);
     const int64_t nup = top ? 0 : P.N[l + 1];
     // lane groups per value from the level's mean pieces per row
-    const int64_t avg = lstride / (BP.piece * BP.rows[l]);
+    const int64_t avg = BP.ent[l] / (BP.piece[l] * BP.rows[l]);
     const int64_t rt = BP.rows[l] * BP.tpp;
 #define HT_RED(LG)                                                                              \
   hipLaunchKernelGGL(dkv_reduce_kernel<LG>, dim3((unsigned)(rt * d->D * LG / 32)),            \
@@ -1694,7 +1705,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.CR = CR;
     a.crlg = P.cr_log2;
     a.TK = d->top_k;
-    a.L = P.L;
+    a.L = Ltop + 1;
     a.tpp = BP.tpp;
     a.scale = scale;
     hipLaunchKernelGGL((dq_ds_kernel<D, !PREC>), dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, st, a);
@@ -1728,7 +1739,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.CR = CR;
     a.crlg = P.cr_log2;
     a.TK = d->top_k;
-    a.L = P.L;
+    a.L = Ltop + 1;
     a.scale = scale;
     if (P.wide)
       hipLaunchKernelGGL((dq_kernel<D, PREC, T, kWideMaxTK>), dim3((unsigned)((groups + 3) / 4)),
