@@ -593,7 +593,7 @@ __device__ __forceinline__ int row_off(int g, int e) {
 // LDS: the bases live in scalar registers, the lanes hold 32-bit offsets).
 // The copies come in three parts (q rows, dO rows, the rest); wave w of nw
 // waves sharing the slot issues the parts i with i % nw == w.
-template <int D, typename TIn, bool HAS_S, int NT = 1>
+template <int D, typename TIn, bool HAS_S, int NT = 1, bool OPAQUE = true>
 __device__ __forceinline__ void stage_issue(char* slot, const DkvArgs& a, int64_t grp, int rs,
                                             int tile, int lane, int w = 0, int nw = 1) {
   const bool pq = nw == 1 || w == 0, pd = nw == 1 || w == 1 % nw, pr = nw == 1 || w == 2 % nw;
@@ -604,11 +604,14 @@ __device__ __forceinline__ void stage_issue(char* slot, const DkvArgs& a, int64_
   constexpr int ES = (int)sizeof(TIn);
   constexpr int CPR = St::CPR;
   const int G = a.G;
-  // the lane offsets below are cheap to recompute: keep them out of the
-  // registers held across the entry loop
-  int lane_c = lane;
-  asm volatile("" : "+v"(lane_c));
-  lane = lane_c;
+  // OPAQUE: the lane offsets below are cheap to recompute: keep them out of
+  // the registers held across the entry loop (else the compiler may hoist
+  // them, where it has the registers to spare)
+  if (OPAQUE) {
+    int lane_c = lane;
+    asm volatile("" : "+v"(lane_c));
+    lane = lane_c;
+  }
   const __amdgpu_buffer_rsrc_t rq = buf_rsrc((const char*)a.q + hq0 * D * ES, G * D * ES);
   const __amdgpu_buffer_rsrc_t rd = buf_rsrc((const char*)a.dO + hq0 * D * ES, G * D * ES);
 #pragma unroll
@@ -835,7 +838,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     // shared block: every wave's part of this entry has landed, and every
     // wave is done reading `nxt` (the previous entry's slot)
     if (PW > 1) __syncthreads();
-    if (nxt && en < ne) stage_issue<D, TIn, HAS_S, NT>(nxt, a, grp_of(rn.x), rn.y, tile, lane, wv, PW);
+    if (nxt && en < ne) stage_issue<D, TIn, HAS_S, NT, !HAS_S>(nxt, a, grp_of(rn.x), rn.y, tile, lane, wv, PW);
     const float* tab = (const float*)(S0 + St::OFF_TAB);  // cos [HALF], sin [HALF]
     const float* sm = (const float*)(S0 + St::OFF_SM);    // gmax, gsum, delta [16 each]
     const bool ok = (tile_mask(rc) >> u16) & 1u;
@@ -961,7 +964,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
       }
     }
   };
-  if (e < ne) stage_issue<D, TIn, HAS_S, NT>(stage_a[sw], a, grp_of(rc.x), rc.y, tile, lane, wv, PW);
+  if (e < ne) stage_issue<D, TIn, HAS_S, NT, !HAS_S>(stage_a[sw], a, grp_of(rc.x), rc.y, tile, lane, wv, PW);
   if constexpr (TWO) {
     while (e < ne) {
       int en = next_work(e + 1);
@@ -983,7 +986,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
       step(stage_a[sw], nullptr, rc, en, rn);
       if (en < ne) {
         wave_sync();  // every lane has read the slot
-        stage_issue<D, TIn, HAS_S, NT>(stage_a[sw], a, grp_of(rn.x), rn.y, tile, lane);
+        stage_issue<D, TIn, HAS_S, NT, !HAS_S>(stage_a[sw], a, grp_of(rn.x), rn.y, tile, lane);
       }
       e = en;
       rc = rn;
