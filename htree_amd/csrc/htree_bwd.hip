@@ -751,7 +751,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   constexpr int NSW = PW > 1 ? 1 : kWavesPerBlock;  // staging areas per block
   __shared__ __attribute__((aligned(16))) char stage_a[NSW][St::BYTES];
   __shared__ __attribute__((aligned(16))) char stage_b[NSW][TWO ? St::BYTES : 16];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar
   const int u16 = lane & 15, kg = lane >> 4;
   const int sw = PW > 1 ? 0 : wv;
   int64_t pc;
