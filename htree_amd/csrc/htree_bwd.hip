@@ -251,7 +251,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const T* __restrict__ o, cons
                                                    int64_t ngroups, int H, int G,
                                                    float* __restrict__ delta) {
   constexpr int KS = D / 32;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int u16 = lane & 15, kg = lane >> 4;
   const int64_t grp = (int64_t)blockIdx.x * kWavesPerBlock + wv;
   if (grp >= ngroups) return;
@@ -1139,7 +1139,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   // back transposed for dq~^T = K~^T dS^T (rows padded by 16 bytes)
   constexpr int KRP = 2 * D + 16;
   __shared__ __attribute__((aligned(16))) char ktile[kWavesPerBlock][2][16 * KRP];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int u16 = lane & 15, kg = lane >> 4;
   const int G = a.G, CR = a.CR, crlg = a.crlg, TK = a.TK;
   if (threadIdx.x < HALF) {
@@ -1383,7 +1383,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void d
   using St = DqStage<D, F16>;
   __shared__ __attribute__((aligned(16))) char stage_all[kWavesPerBlock][St::BYTES];
   __shared__ float rot_m[2][HALF];  // cos(CR theta), -sin(CR theta)
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int u16 = lane & 15, kg = lane >> 4;
   const int CR = a.CR, crlg = a.crlg, TK = a.TK, tpp = a.tpp;
   if (threadIdx.x < HALF) {
