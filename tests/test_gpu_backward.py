@@ -45,6 +45,9 @@ CASES = [
     (1, 2000, 8, 1, 64, 64, 8, 512, "bfloat16", 14),   # CR 64: four tiles per parent
     (1, 1500, 4, 1, 128, 64, 4, 256, "float32", 15),
     (1, 2500, 16, 2, 128, 64, 4, 256, "bfloat16", 16),  # CR 64 with the stored scores (16 tiles)
+    (1, 1100, 8, 1, 128, 32, 8, 256, "float16", 17),   # CR 32, fp16 (split dS, shared staging)
+    (1, 4096, 8, 2, 64, 16, 16, 16, "bfloat16", 18),   # 16-node top level: accumulates nothing
+    (2, 3000, 8, 1, 64, 16, 16, 16, "float32", 19),
 ]
 
 
@@ -216,7 +219,8 @@ def test_backward_reference_default_regime():
 
 @pytest.mark.parametrize("cfg", [(1, 1500, 16, 2, 128, 16, 16, 128, "bfloat16", 61),
                                  (1, 1100, 8, 1, 128, 32, 8, 256, "float16", 62),
-                                 (1, 900, 8, 2, 64, 8, 16, 128, "float32", 63)],
+                                 (1, 900, 8, 2, 64, 8, 16, 128, "float32", 63),
+                                 (1, 4096, 8, 2, 64, 16, 16, 16, "bfloat16", 64)],
                          ids=lambda c: f"D{c[4]}cr{c[5]}{c[8]}")
 def test_backward_recomputed_dq(cfg, monkeypatch):
     """The dq pass that recomputes the scores (taken when the stored dS
