@@ -362,6 +362,36 @@ __global__ __launch_bounds__(256) void bitmap_set_kernel(const int32_t* __restri
   atomicOr(&bm[row * W + (t >> 5)], 1u << (t & 31));
 }
 
+// The same bitmap for dense rows (long lists, upper levels): one block per
+// (b, h, 32 consecutive queries) ORs the queries' bits into a column of its
+// rows' words in LDS (chunks of 8192 rows), then writes every word of the
+// column, so no global atomics and no separate clearing are needed.
+__global__ __launch_bounds__(256) void bitmap_cols_kernel(const int32_t* __restrict__ par, int T,
+                                                          int Hkv, int TK, int64_t Pl, int64_t W,
+                                                          uint32_t* __restrict__ bm) {
+  constexpr int CH = 8192;
+  __shared__ uint32_t col[CH];
+  const int64_t w = blockIdx.x % W;
+  const int64_t bh = blockIdx.x / W;
+  const int h = (int)(bh % Hkv);
+  const int64_t b = bh / Hkv;
+  const int t0 = (int)(w * 32);
+  const int nq = T - t0 < 32 ? T - t0 : 32;
+  for (int64_t rc = 0; rc < Pl; rc += CH) {
+    const int nr = (int)(Pl - rc < CH ? Pl - rc : CH);
+    for (int i = threadIdx.x; i < nr; i += 256) col[i] = 0u;
+    __syncthreads();
+    for (int i = threadIdx.x; i < nq * TK; i += 256) {
+      const int q = i / TK, s = i - q * TK;
+      const int p = par[(((int64_t)b * T + t0 + q) * Hkv + h) * TK + s];
+      if (p >= rc && p < rc + nr) atomicOr(&col[p - rc], 1u << q);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < nr; i += 256) bm[(bh * Pl + rc + i) * W + w] = col[i];
+    __syncthreads();
+  }
+}
+
 // One block per row: exclusive prefix of the per-word popcounts of the
 // row's bitmap (wpre), the row's query count and its number of pieces.
 __global__ __launch_bounds__(256) void row_scan_kernel(const uint32_t* __restrict__ bm, int64_t W,
@@ -1586,11 +1616,18 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     const int64_t Pl = (P.N[l] + CR - 1) / CR;
     const int64_t nrows = BP.rows[l];
     const int64_t words = nrows * BP.W;
-    hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st, bm,
-                       words);
     const int64_t ent = lstride;
-    hipLaunchKernelGGL(bitmap_set_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
-                       parents + l * lstride, d->T, d->H_kv, d->top_k, Pl, BP.W, ent, bm);
+    // dense bitmaps (at least one entry per two words: long lists, upper
+    // levels) by columns; sparse ones by global atomics
+    if (2 * BP.ent[l] >= words) {
+      hipLaunchKernelGGL(bitmap_cols_kernel, dim3((unsigned)(BH * BP.W)), dim3(256), 0, st,
+                         parents + l * lstride, d->T, d->H_kv, d->top_k, Pl, BP.W, bm);
+    } else {
+      hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st,
+                         bm, words);
+      hipLaunchKernelGGL(bitmap_set_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
+                         parents + l * lstride, d->T, d->H_kv, d->top_k, Pl, BP.W, ent, bm);
+    }
     hipLaunchKernelGGL(row_scan_kernel, dim3((unsigned)nrows), dim3(256), 0, st, bm, BP.W,
                        (int)BP.piece[l], wpre, cnt, pcnt);
     hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, cnt, nrows, rowoff);
