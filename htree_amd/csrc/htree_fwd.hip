@@ -928,7 +928,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 // 88-105) by an exclusive scan in position order.  The accumulation pass
 // recomputes the scores of the non-selected candidates.
 template <int D, bool PREC, typename TIn, bool TRACE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 ? 3 : 1))) void fwd_wide_kernel(const FwdArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 ? 4 : 1))) void fwd_wide_kernel(const FwdArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2, NW = kWideWaves, C = kWideC;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
