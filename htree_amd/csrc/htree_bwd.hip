@@ -1156,7 +1156,7 @@ __device__ __forceinline__ void rot_acc(f32x4 (&x)[D / 16], const float* c, cons
 //   sum_s R^-1(dq~_s, a - s CR) = R^-1(X, n_c-1 - (np-1) CR) = R(X, -c_t)
 // needs one table rotation per level.
 template <int D, bool PREC, typename TIn, int MAXTK>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void dq_kernel(const DqArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 ? 5 : 2))) void dq_kernel(const DqArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
   // list capacity; selection bits of the 16-candidate tile positions
   // (kMaxTiles or, for MAXTK = kWideMaxTK, kWideMaxPos / 16 tiles)
