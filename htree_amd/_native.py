@@ -28,7 +28,8 @@ DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 # every function the header declares; tests check the library exports them
 EXPORTS = (
     "htree_strerror", "htree_levels", "htree_tree_workspace_bytes", "htree_tree_build",
-    "htree_forward", "htree_backward_workspace_bytes", "htree_backward",
+    "htree_forward", "htree_backward_workspace_bytes", "htree_backward_workspace_min_bytes",
+    "htree_backward",
     "htree_train_scores_bytes", "htree_forward_train", "htree_backward_train",
     "htree_forward_trace", "htree_topk_rows",
 )
@@ -82,6 +83,8 @@ def lib() -> ctypes.CDLL:
     if hasattr(L, "htree_backward"):
         L.htree_backward_workspace_bytes.restype = ctypes.c_int
         L.htree_backward_workspace_bytes.argtypes = [DP, ctypes.POINTER(I64)]
+        L.htree_backward_workspace_min_bytes.restype = ctypes.c_int
+        L.htree_backward_workspace_min_bytes.argtypes = [DP, ctypes.POINTER(I64)]
         L.htree_backward.restype = ctypes.c_int
         L.htree_backward.argtypes = [DP, F, P, P, P, P, P, P, P, I64, P, P, P, P, P, P, I64, P]
     if hasattr(L, "htree_backward_train"):

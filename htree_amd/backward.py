@@ -63,7 +63,13 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
     nb = N.ctypes.c_int64()
     N.check(N.lib().htree_backward_workspace_bytes(N.ctypes.byref(d), N.ctypes.byref(nb)),
             "htree_backward_workspace_bytes")
-    bws = torch.empty(nb.value, dtype=torch.uint8, device=dev)
+    try:
+        bws = torch.empty(nb.value, dtype=torch.uint8, device=dev)
+    except torch.OutOfMemoryError:
+        # no room for the stored dS: the smallest workspace, dq recomputes
+        N.check(N.lib().htree_backward_workspace_min_bytes(N.ctypes.byref(d), N.ctypes.byref(nb)),
+                "htree_backward_workspace_min_bytes")
+        bws = torch.empty(nb.value, dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         if scores is not None:
             rc = N.lib().htree_backward_train(

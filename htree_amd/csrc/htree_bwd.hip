@@ -64,7 +64,9 @@ struct BwdPlan {
   int64_t bytes;
 };
 
-static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
+// allow_ds = false: the plan without the stored dS (dq recomputes the scores),
+// the smallest workspace the backward runs in.
+static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true) {
   memset(b, 0, sizeof(*b));
   int rc = make_plan(d, &b->P);
   if (rc) return rc;
@@ -146,7 +148,7 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b) {
       budget = (int64_t)(total / 3);
   }
   if (const char* e = getenv("HTREE_DS_BUDGET_MB")) budget = (int64_t)atoll(e) << 20;
-  b->use_ds = !P.wide && ds_total <= budget;
+  b->use_ds = allow_ds && !P.wide && ds_total <= budget;
   for (int l = 0; l < P.L; ++l) {
     b->off_rec[l] = b->use_ds ? take(ent[l] * 16) : l == 0 ? take(b->max_entries * 16) : b->off_rec[0];
     b->off_emap[l] = b->use_ds ? take(b->max_entries * 16) : -1;
@@ -1807,6 +1809,15 @@ int htree_backward_workspace_bytes(const htree_dims* d, int64_t* bytes) {
   return HTREE_OK;
 }
 
+int htree_backward_workspace_min_bytes(const htree_dims* d, int64_t* bytes) {
+  BwdPlan BP;
+  int rc = make_bwd_plan(d, &BP, false);
+  if (rc) return rc;
+  if (!bytes) return HTREE_ENULL;
+  *bytes = BP.bytes;
+  return HTREE_OK;
+}
+
 }  // extern "C"
 
 static int backward_impl(const htree_dims* d, float scale, const void* q, const void* out,
@@ -1821,6 +1832,9 @@ static int backward_impl(const htree_dims* d, float scale, const void* q, const 
   if (!q || !out || !dO || !gmax || !gsum || !parents || !tree_ws || !cos_table || !sin_table ||
       !dq || !dk || !dv || !bwd_ws)
     return HTREE_ENULL;
+  // a workspace too small for the stored dS but large enough without it:
+  // dq recomputes the scores
+  if (BP.use_ds && bwd_ws_bytes < BP.bytes) make_bwd_plan(d, &BP, false);
   if (tree_ws_bytes < BP.P.bytes || bwd_ws_bytes < BP.bytes) return HTREE_EWORKSPACE;
   const int64_t sbytes = train_scores_bytes(d, BP.P, nullptr);
   const char* scores = sbytes > 0 ? (const char*)scores_ws : nullptr;

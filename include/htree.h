@@ -110,8 +110,17 @@ int htree_forward_trace(const htree_dims* d, float scale, const void* q, const v
                         void* out, float* gmax, float* gsum, int32_t* parents, float* level_max,
                         float* level_sum, float* level_out, void* stream);
 
-/* Bytes of the backward workspace (host). */
+/* Bytes of the backward workspace (host).  This size lets the backward keep
+ * every (entry, tile)'s dS for its dq pass, when that fits a third of the
+ * current device's memory (HTREE_DS_BUDGET_MB in the environment overrides
+ * the budget); given less, but at least htree_backward_workspace_min_bytes,
+ * the backward recomputes the scores in its dq pass instead. */
 int htree_backward_workspace_bytes(const htree_dims* d, int64_t* bytes);
+
+/* Smallest backward workspace (host): without the stored dS.  No
+ * counterpart in the reference, whose backward allocates its own buffers
+ * (src/backward.py:979-981); for callers short of device memory. */
+int htree_backward_workspace_min_bytes(const htree_dims* d, int64_t* bytes);
 
 /* Backward with the selection held fixed: dq, dk, dv in fp32 (dk, dv after
  * the mean-pool backward onto level 0).  `out` is the forward output handed

@@ -260,3 +260,49 @@ def test_backward_power_of_two_scalings(cfg):
             g = got[i].astype(np.float64) * 2.0 ** -f
             assert np.all(np.isfinite(g)), name
             np.testing.assert_array_equal(g, base[i].astype(np.float64), err_msg=name)
+
+
+def test_backward_min_workspace():
+    """Given the smallest workspace (htree_backward_workspace_min_bytes) the
+    backward recomputes the scores in its dq pass instead of storing dS; the
+    gradients meet the bar against the oracle and agree with the
+    full-workspace run (dk, dv bit-exact: only dq's product changes), and one
+    byte less is rejected before any launch."""
+    import htree_amd
+    from htree_amd import _native as N
+
+    B, T, H, Hkv, D, CR, TK, MTN = 1, 1500, 16, 2, 128, 16, 16, 128
+    q, k, v, dO = inputs(B, T, H, Hkv, D, "bfloat16", 81, dO=True)
+    qd, dOd = q.to(DEV), dO.to(DEV)
+    out, par, gmax, gsum, ctx = htree_amd.htree_forward_parents(qd, k.to(DEV), v.to(DEV), CR, MTN, TK)
+    d = ctx["dims"]
+    nfull, nmin = N.ctypes.c_int64(), N.ctypes.c_int64()
+    N.check(N.lib().htree_backward_workspace_bytes(N.ctypes.byref(d), N.ctypes.byref(nfull)), "ws")
+    N.check(N.lib().htree_backward_workspace_min_bytes(N.ctypes.byref(d), N.ctypes.byref(nmin)), "ws")
+    assert 0 < nmin.value < nfull.value
+    ws, cos, sin = ctx["packed_tree"], ctx["cos_cache"], ctx["sin_cache"]
+
+    def call(nbytes):
+        dq = torch.empty(B, T, H, D, dtype=torch.float32, device=DEV)
+        dk = torch.empty(B, T, Hkv, D, dtype=torch.float32, device=DEV)
+        dv = torch.empty_like(dk)
+        bws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+        rc = N.lib().htree_backward(d, float(ctx["scale"]), N.ptr(qd), N.ptr(out), N.ptr(dOd),
+                                    N.ptr(gmax), N.ptr(gsum), N.ptr(ctx["parents_stacked"]), N.ptr(ws),
+                                    ws.numel(), N.ptr(cos), N.ptr(sin), N.ptr(dq), N.ptr(dk), N.ptr(dv),
+                                    N.ptr(bws), bws.numel(), N.stream_ptr(qd.device))
+        torch.cuda.synchronize()
+        return rc, [x.cpu().numpy() for x in (dq, dk, dv)]
+
+    rc, full = call(nfull.value)
+    N.check(rc, "htree_backward")
+    rc, small = call(nmin.value)
+    N.check(rc, "htree_backward")
+    rc, _ = call(nmin.value - 1)
+    assert rc < 0
+    f = lambda x: x.float().cpu().numpy()
+    print(check_backward(q, k, v, dO, CR, TK, MTN, "bfloat16", f(out), par.cpu().numpy(), f(gmax),
+                         f(gsum), *small), flush=True)
+    assert np.array_equal(small[1], full[1]) and np.array_equal(small[2], full[2])
+    ok, worst = close(small[0], full[0], "bfloat16")
+    assert ok, worst
