@@ -699,13 +699,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   f32x4 O[ND];
 #pragma unroll
   for (int n = 0; n < ND; ++n) O[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int lstart = a.L - 1;
   {
     const int64_t nvp = (t / a.lv[a.L - 1].pw) / CR + 1;
     if (lane < TK) W.par[0][lane] = lane < nvp ? lane : -1;
+    // A top level of <= top_k nodes keeps every candidate and accumulates
+    // none (src/naive.py:97-101): its list is the virtual parents and its
+    // selection every top node up to t's, so the walk starts one level lower.
+    if (!TRACE && a.L > 1 && a.lv[a.L - 1].N <= TK) {
+      if (a.parents && lane < TK)
+        a.parents[((((int64_t)(a.L - 1) * a.B + b) * a.T + t) * a.Hkv + h) * TK + lane] =
+            lane < nvp ? lane : -1;
+      const int64_t ntop = t / a.lv[a.L - 1].pw + 1;
+      if (lane < TK) W.par[0][lane] = lane < ntop ? lane : -1;
+      lstart = a.L - 2;
+    }
   }
   int cur = 0;
 
-  for (int l = a.L - 1; l >= 0; --l) {
+  for (int l = lstart; l >= 0; --l) {
     wave_sync();
     const LevelPtrs P = a.lv[l];
     const int pv = lane < TK ? W.par[cur][lane] : -1;

@@ -46,6 +46,7 @@ SMALL = [
     (1, 2500, 16, 4, 32, 4, 32, 64, "float32", 11),    # D = 32, 32 tiles: multi-pass kernel
     (1, 3000, 8, 1, 128, 32, 32, 256, "bfloat16", 12),  # CR 32, top_k 32 (BASELINE C4's tree): 64 tiles
     (1, 2200, 8, 2, 64, 16, 32, 256, "float16", 13),    # 32 tiles, fp16 (split V)
+    (2, 4096, 16, 2, 128, 16, 16, 16, "bfloat16", 14),  # 16-node top level (keeps every candidate), as C5
 ]
 
 
