@@ -119,7 +119,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported in this build "
-              "(the path shards over (b, h_kv) with no communication; see DESIGN.md)",
+              "(the path shards over (b, h_kv) with no communication between the shards)",
               file=sys.stderr)
         sys.exit(2)
 
@@ -135,7 +135,7 @@ def main():
     torch.cuda.set_device(dev)
     g = torch.Generator().manual_seed(1234)
     if args.workload == "C5":
-        # BASELINE C5: keys from a 64-component Gaussian mixture (means
+        # C5: keys from a 64-component Gaussian mixture (means
         # N(0, 4 I), sigma 0.5), queries around 4 hot components, V and dO iid
         mu = 2.0 * torch.randn(64, D, generator=g)
         hot = torch.randperm(64, generator=g)[:4]

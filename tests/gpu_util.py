@@ -27,7 +27,7 @@ def inputs(B, T, H, Hkv, D, dtype, seed, dO=False):
 
 def skewed_inputs(B, T, H, Hkv, D, dtype, seed, ncomp=64, nhot=4):
     """Keys from a 64-component Gaussian mixture (means N(0,4), sigma 0.5),
-    queries around 4 hot components, V iid N(0,1)."""
+    queries around 4 hot components, V iid N(0,1) (the C5 workload)."""
     g = torch.Generator().manual_seed(seed)
     mu = 2.0 * torch.randn(ncomp, D, generator=g)
     hot = torch.randperm(ncomp, generator=g)[:nhot]

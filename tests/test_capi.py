@@ -51,7 +51,7 @@ def test_levels_follow_reference_rule(T, CR, MTN):
 
 
 def test_baseline_level_counts():
-    # SURVEY: C4 has 3 levels by the reference's rule, C5 has 4
+    # the reference's level rule (src/parallel.py:941-945): C4 has 3 levels, C5 has 4
     assert len(N.levels(dims(T=131072, H=64, H_kv=8, compression_rate=32, top_k=32,
                              max_top_nodes=256, rope_rows=1280))) == 3
     assert len(N.levels(dims(T=65536))) == 4
@@ -112,7 +112,7 @@ def test_python_api_validates_like_reference():
 
 
 def test_work_model_matches_baseline_table():
-    # algorithmic bytes of the gathered-bytes model
+    # published algorithmic bytes (GB) of the gathered-bytes model for the C2, C3, C5 workloads
     w2 = work(1, 32768, 32, 2, 128, 16, 16, 128, 2)
     assert abs(w2.fwd_bytes / 1e9 - 18.36) < 0.01 and abs(w2.bwd_bytes / 1e9 - 18.45) < 0.015
     w3 = work(4, 16384, 32, 4, 128, 16, 16, 128, 2)

@@ -41,7 +41,7 @@ CASES = [
     (1, 1500, 16, 4, 32, 16, 8, 128, "float16", 9),
     (2, 1000, 8, 2, 32, 8, 16, 64, "bfloat16", 10),
     (1, 2500, 16, 4, 32, 4, 32, 64, "float32", 11),
-    (1, 3000, 8, 1, 128, 32, 32, 256, "bfloat16", 12),  # BASELINE C4's tree shape
+    (1, 3000, 8, 1, 128, 32, 32, 256, "bfloat16", 12),  # the C4 workload's tree shape
     (1, 2000, 8, 1, 64, 64, 8, 512, "bfloat16", 14),   # CR 64: four tiles per parent
     (1, 1500, 4, 1, 128, 64, 4, 256, "float32", 15),
     (1, 2500, 16, 2, 128, 64, 4, 256, "bfloat16", 16),  # CR 64 with the stored scores (16 tiles)
@@ -116,7 +116,7 @@ def test_backward_matches_reference_golden(name):
 
 
 def test_backward_training_shape_c3():
-    """BASELINE C3 (B=4, T=16384, Hq=32, Hkv=4, D=128, bf16): dq on sampled
+    """The C3 workload (B=4, T=16384, Hq=32, Hkv=4, D=128, bf16): dq on sampled
     rows vs the oracle; sum over nodes of dv equals sum over the group's
     queries and heads of dO (pooling conserves mass, P sums to 1)."""
     B, T, H, Hkv, D, CR, TK, MTN = 4, 16384, 32, 4, 128, 16, 16, 128
@@ -224,8 +224,8 @@ def test_backward_reference_default_regime():
                          ids=lambda c: f"D{c[4]}cr{c[5]}{c[8]}")
 def test_backward_recomputed_dq(cfg, monkeypatch):
     """The dq pass that recomputes the scores (taken when the stored dS
-    would exceed its memory budget, as at BASELINE C4, and for top_k > 64),
-    forced here by a zero budget."""
+    would exceed its memory budget or the caller's workspace, and for
+    top_k > 64), forced here by a zero budget."""
     monkeypatch.setenv("HTREE_DS_BUDGET_MB", "0")
     B, T, H, Hkv, D, CR, TK, MTN, dtype, seed = cfg
     print(f"case {cfg}", flush=True)

@@ -32,7 +32,7 @@ def run_fwd(q, k, v, CR, TK, MTN):
 
 SMALL = [
     # B, T, H, Hkv, D, CR, TK, MTN, dtype, seed
-    (1, 2048, 4, 1, 64, 16, 8, 64, "float32", 1),      # BASELINE C1 shape
+    (1, 2048, 4, 1, 64, 16, 8, 64, "float32", 1),      # the C1 workload shape
     (1, 2048, 4, 1, 64, 16, 8, 64, "bfloat16", 1),
     (2, 1500, 16, 2, 128, 16, 16, 128, "bfloat16", 2),
     (1, 1100, 8, 1, 128, 16, 16, 128, "float16", 3),
@@ -44,7 +44,7 @@ SMALL = [
     (1, 1500, 16, 4, 32, 16, 8, 128, "float16", 9),
     (2, 1000, 8, 2, 32, 8, 16, 64, "bfloat16", 10),
     (1, 2500, 16, 4, 32, 4, 32, 64, "float32", 11),    # D = 32, 32 tiles: multi-pass kernel
-    (1, 3000, 8, 1, 128, 32, 32, 256, "bfloat16", 12),  # CR 32, top_k 32 (BASELINE C4's tree): 64 tiles
+    (1, 3000, 8, 1, 128, 32, 32, 256, "bfloat16", 12),  # CR 32, top_k 32 (the C4 workload's tree): 64 tiles
     (1, 2200, 8, 2, 64, 16, 32, 256, "float16", 13),    # 32 tiles, fp16 (split V)
     (2, 4096, 16, 2, 128, 16, 16, 16, "bfloat16", 14),  # 16-node top level (keeps every candidate), as C5
 ]
@@ -97,7 +97,7 @@ def test_forward_matches_reference_golden(name):
 
 
 def test_forward_c2_sample():
-    """BASELINE config C2 (T=32768, Hq=32, Hkv=2, D=128, bf16, CR16 MTN128
+    """The C2 workload (T=32768, Hq=32, Hkv=2, D=128, bf16, CR16 MTN128
     TK16): sampled rows against the oracle; every row through invariants."""
     B, T, H, Hkv, D, CR, TK, MTN = 1, 32768, 32, 2, 128, 16, 16, 128
     q, k, v = inputs(B, T, H, Hkv, D, "bfloat16", 2024)
@@ -124,7 +124,7 @@ def test_forward_c2_sample():
 
 
 def test_forward_skewed_sample():
-    """Skewed keys (BASELINE C5 distribution, reduced T): many exact-zero
+    """Skewed keys (the C5 distribution, reduced T): many exact-zero
     importances, ties broken by position."""
     B, T, H, Hkv, D, CR, TK, MTN = 1, 8192, 32, 2, 128, 16, 16, 128
     q, k, v, _ = skewed_inputs(B, T, H, Hkv, D, "bfloat16", 77)
