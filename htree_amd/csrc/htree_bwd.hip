@@ -596,14 +596,25 @@ struct DkvArgs {
 
 // One entry's inputs staged in LDS by asynchronous copies: the 16 query
 // rows and 16 dO rows of the query group, the RoPE row rho, and gmax / gsum /
-// delta of the 16 heads.  Head rows are padded by one 16-byte chunk (pitch
-// RP), so that 8 lanes reading one chunk position of 8 heads, and lanes
-// reading one column of 4 heads, hit distinct LDS banks with linear addresses.
+// delta of the 16 heads.  Two reads meet these rows: 16-byte row reads (lane
+// u16 reads head u16 at one chunk position) and transposing column reads
+// (four lanes read 32 contiguous bytes of one head, a 16-lane group covers
+// heads 4kg..4kg+3).  A padded pitch cannot keep both off each other's LDS
+// banks (the row reads want an odd multiple of 4 dwords, the column reads a
+// multiple of 8), so 2-byte rows of D = 128 (16 chunks) are unpadded with
+// chunk c of head g stored at c ^ swz(g): swz is a bijection of 0..15 whose
+// low 3 bits are distinct over heads 0..7 and 8..15, and whose bits 1..3 are
+// distinct over heads 0..7, 8..15 and (bits 1..2) over each group of four.
+// Other shapes pad each row by one chunk.
+__device__ __forceinline__ int swz(int g) {
+  return 2 * (g & 3) + 8 * ((g >> 2) & 1) + (((g >> 2) ^ (g >> 3)) & 1);
+}
 template <int D, typename TIn, int NT = 1>
 struct Stage {
   static constexpr int CPR = D * (int)sizeof(TIn) / 16;  // chunks per head row
-  static constexpr int RP = (CPR + 1) * 16;               // padded row pitch (bytes)
-  static constexpr int NCH = 16 * (CPR + 1);              // chunks of 16 padded rows
+  static constexpr bool SWZ = CPR == 16;                  // swizzled, unpadded rows
+  static constexpr int RP = (CPR + (SWZ ? 0 : 1)) * 16;   // row pitch (bytes)
+  static constexpr int NCH = 16 * RP / 16;                // chunks of 16 rows
   static constexpr int ROWB = 16 * RP;
   static constexpr int OFF_DO = ROWB;
   static constexpr int OFF_TAB = 2 * ROWB;          // cos [D/2] then sin [D/2]
@@ -618,7 +629,10 @@ struct Stage {
 // byte offset of element e of head row g in a staged block
 template <int D, typename TIn>
 __device__ __forceinline__ int row_off(int g, int e) {
-  return g * Stage<D, TIn>::RP + e * (int)sizeof(TIn);
+  using St = Stage<D, TIn>;
+  const int b = e * (int)sizeof(TIn);
+  if constexpr (St::SWZ) return g * St::RP + ((((b >> 4) ^ swz(g)) << 4) | (b & 15));
+  return g * St::RP + b;
 }
 
 // Asynchronous copies of one entry's inputs into `slot` (buffer loads into
@@ -648,9 +662,15 @@ __device__ __forceinline__ void stage_issue(char* slot, const DkvArgs& a, int64_
   const __amdgpu_buffer_rsrc_t rd = buf_rsrc((const char*)a.dO + hq0 * D * ES, G * D * ES);
 #pragma unroll
   for (int j = 0; j < (St::NCH + 63) / 64; ++j) {
-    const int P = j * 64 + lane;  // LDS chunk: padded row g, chunk c (c == CPR: pad)
-    const int g = P / (CPR + 1);
-    const int c = P - g * (CPR + 1);
+    const int P = j * 64 + lane;  // LDS chunk: row g, chunk c (c == CPR: pad)
+    int g, c;
+    if constexpr (St::SWZ) {
+      g = P >> 4;
+      c = (P & 15) ^ swz(g);
+    } else {
+      g = P / (CPR + 1);
+      c = P - g * (CPR + 1);
+    }
     int off = (g * CPR + (c < CPR ? c : 0)) * 16;
     off = g < G ? off : 0;  // rows past the group: in-bounds filler, never used
     if ((St::NCH % 64 == 0) || P < St::NCH) {
