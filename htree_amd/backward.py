@@ -18,14 +18,39 @@ import torch
 
 from . import _native as N
 from .parallel import build_tree, htree_forward, make_dims
+from .workmodel import level_sizes
 
 
 def _stack_parents(per_layer_parents, L):
     return torch.stack([per_layer_parents[l] for l in range(L)]).contiguous()
 
 
+def _check_parents(parents, B, T, H_kv, TK, CR, MTN, device):
+    """Caller-supplied lists go to the kernels as they are: hold them to what
+    the forward produces (src/naive.py:88-118, :204-207): list l names nodes
+    of level l + 1 (the virtual top parents at the top level), ascending,
+    padded with -1 at the end."""
+    sizes = level_sizes(T, CR, MTN)
+    L = len(sizes)
+    assert parents.shape == (L, B, T, H_kv, TK) and parents.dtype == torch.int32, \
+        f"parent lists must be int32 [{L}, {B}, {T}, {H_kv}, {TK}], got {parents.dtype} {list(parents.shape)}"
+    assert parents.device == device, "parent lists must be on the inputs' device"
+    for l in range(L):
+        p = parents[l]
+        lim = -(-sizes[l] // CR)
+        assert bool(((p >= -1) & (p < lim)).all()), f"level {l}: parent index outside [-1, {lim})"
+        valid = p >= 0
+        assert bool((valid[..., 1:] <= valid[..., :-1]).all()), f"level {l}: -1 padding must come last"
+        assert bool(((p[..., 1:] > p[..., :-1]) | ~valid[..., 1:]).all()), \
+            f"level {l}: parent lists must be ascending"
+
+
 def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_ctx: dict):
-    """Gradients of the htree forward wrt q, k, v (fp32), selection fixed."""
+    """Gradients of the htree forward wrt q, k, v (fp32), selection fixed.
+
+    dO and output are read in q's dtype; the reference upcasts both to fp32
+    (src/backward.py:966-967), so the two agree when dO comes in q's dtype,
+    as autograd hands it."""
     B, T, H, K = q.shape
     layers_k, layers_v = bwd_ctx["layers_k"], bwd_ctx["layers_v"]
     k, v = layers_k[0], layers_v[0]
@@ -43,12 +68,18 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
         rope_base = bwd_ctx.get("rope_base", 10000.0)
         _, _, ws, cos, sin = build_tree(k, v, d, d.rope_rows, rope_base)
     parents = bwd_ctx.get("parents_stacked")
+    plp = bwd_ctx.get("per_layer_parents")
+    # per_layer_parents (what the reference reads) are views of the forward's
+    # stacked lists; a caller that replaced them gets its own lists
+    if parents is not None and plp is not None and any(
+            plp[l].data_ptr() != parents[l].data_ptr() for l in range(L)):
+        parents = None
     # the training forward's stored scores go with its own parent lists
     scores = bwd_ctx.get("train_scores") if parents is not None else None
     if parents is None:
-        plp = bwd_ctx.get("per_layer_parents")
         if plp is not None:
             parents = _stack_parents(plp, L)
+            _check_parents(parents, B, T, k.shape[2], TK, CR, MTN, q.device)
         else:
             _, ctx2 = htree_forward(q, k, v, CR, MTN, TK, scale, bwd_ctx.get("rope_base", 10000.0),
                                     _save_for_backward=True, _save_parents=True)

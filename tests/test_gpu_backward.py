@@ -153,6 +153,27 @@ def test_backward_deterministic():
         assert np.array_equal(x, y)
 
 
+def test_backward_replaced_parent_lists():
+    """A bwd_ctx whose per_layer_parents (the reference's key) were replaced
+    by equal copies runs on the caller's lists: the gradients equal, bitwise,
+    those of the forward's own lists through the same path (no stored
+    scores); a list naming a node past its level is rejected before launch."""
+    import htree_amd
+
+    q, k, v, dO = (x.to(DEV) for x in inputs(1, 1500, 8, 2, 64, "bfloat16", 41, dO=True))
+    out, ctx = htree_amd.htree_forward(q, k, v, 16, 128, 16, _save_for_backward=True)
+    a = htree_amd.htree_backward(dO, q, out, dict(ctx, train_scores=None))
+    plp = {l: t.clone() for l, t in ctx["per_layer_parents"].items()}
+    b = htree_amd.htree_backward(dO, q, out, dict(ctx, per_layer_parents=plp))
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+    bad = {l: t.clone() for l, t in plp.items()}
+    bad[0][0, 1499, 0, 0] = 94  # level 0 lists name level-1 nodes: 94 of them
+    with pytest.raises(AssertionError, match="outside"):
+        htree_amd.htree_backward(dO, q, out, dict(ctx, per_layer_parents=bad))
+
+
 def test_autograd_contract():
     """HTreeTritonFunction: grads in the input dtype, None for non-tensors,
     equal to htree_backward cast to the dtype."""
