@@ -54,6 +54,10 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
     B, T, H, K = q.shape
     layers_k, layers_v = bwd_ctx["layers_k"], bwd_ctx["layers_v"]
     k, v = layers_k[0], layers_v[0]
+    if B == 0 or T == 0:  # empty inputs: empty gradients, no launch
+        f32 = dict(dtype=torch.float32, device=q.device)
+        return (torch.empty(B, T, H, K, **f32), torch.empty(B, T, k.shape[2], K, **f32),
+                torch.empty(B, T, k.shape[2], K, **f32))
     CR = bwd_ctx["compression_rate"]
     TK = bwd_ctx["top_k_per_layer"]
     MTN = bwd_ctx.get("max_top_nodes", TK * CR)

@@ -8,8 +8,10 @@ Differences, all deliberate:
     relies on equality.  The reference's Triton-tiling asserts
     (top_k % 64 == 0, top_k % compression_rate == 0, :923,1019) do not apply.
   * limits of this HIP build (AssertionError): head_dim in {32, 64, 128},
-    H / H_kv <= 16, compression_rate >= 4, top_k_per_layer <= 64 and
-    top_k_per_layer * max(compression_rate, 16) / 16 <= 64.
+    H / H_kv <= 16, 4 <= compression_rate <= 64, top_k_per_layer <= 512 and
+    top_k_per_layer * compression_rate <= 8192 candidates per level.
+  * empty inputs (B == 0 or T == 0) give empty outputs (and a bwd_ctx whose
+    backward gives empty gradients) without a launch.
   * the RoPE tables are built on the host with the reference's recipe
     (src/parallel.py:983-988) and copied to the device.
   * bwd_ctx carries extra keys: `packed_tree` (the MFMA operand copy of the
@@ -62,6 +64,7 @@ def _validate(q, k, v, compression_rate, max_top_nodes, top_k_per_layer):
         f"max_top_nodes ({max_top_nodes}) must be <= top_k_per_layer*compression_rate "
         f"({top_k_per_layer}*{compression_rate}={top_k_per_layer * compression_rate})")
     assert q.is_cuda and k.is_cuda and v.is_cuda, "htree_amd runs on the GPU (no CPU fallback)"
+    assert q.device == k.device == v.device, "q, k, v must be on one device"
 
 
 def make_dims(q, k, compression_rate, max_top_nodes, top_k_per_layer):
@@ -110,8 +113,17 @@ def htree_forward(
         scale = K ** -0.5
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     d, rows = make_dims(q, k, compression_rate, max_top_nodes, top_k_per_layer)
+    empty = B == 0 or T == 0  # nothing to attend: no tree, no launch
     with torch.cuda.device(q.device):
-        layers_k, layers_v, ws, cos, sin = build_tree(k, v, d, rows, rope_base)
+        if empty:
+            # the library's limits still apply: checked on one query
+            N.levels(N.dims(1, 1, H, H_kv, K, compression_rate, top_k_per_layer, max_top_nodes,
+                            q.dtype, rows))
+            layers_k, layers_v = [k], [v]
+            ws = torch.empty(0, dtype=torch.uint8, device=q.device)
+            cos, sin = rope_cache(K, rows, rope_base, q.device)
+        else:
+            layers_k, layers_v, ws, cos, sin = build_tree(k, v, d, rows, rope_base)
         L = len(layers_k)
         out = torch.empty_like(q)
         gmax = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
@@ -119,9 +131,11 @@ def htree_forward(
         save_par = _save_for_backward and _save_parents
         parents = (torch.empty(L, B, T, H_kv, top_k_per_layer, dtype=torch.int32, device=q.device)
                    if save_par else None)
-        nsc = N.train_scores_bytes(d) if save_par else 0
+        nsc = N.train_scores_bytes(d) if save_par and not empty else 0
         scores = torch.empty(nsc, dtype=torch.uint8, device=q.device) if nsc > 0 else None
-        if scores is not None:
+        if empty:
+            pass
+        elif scores is not None:
             rc = N.lib().htree_forward_train(d, float(scale), N.ptr(q), N.ptr(ws), ws.numel(),
                                              N.ptr(cos), N.ptr(sin), N.ptr(out), N.ptr(gmax),
                                              N.ptr(gsum), N.ptr(parents), N.ptr(scores), nsc,

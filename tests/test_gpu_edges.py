@@ -46,3 +46,26 @@ def test_edges_forward_backward(cfg):
                               f(gsum), f(dq), f(dk), f(dv), tree=tree))
     print(rep, flush=True)
     assert dq.dtype == torch.float32 and dq.shape == q.shape and dk.shape == k.shape
+
+
+@pytest.mark.parametrize("B,T", [(0, 300), (2, 0)])
+def test_empty_inputs(B, T):
+    """No batch or no tokens: empty outputs and gradients of the right
+    shapes and dtypes, with no launch; the library's limits still apply."""
+    import htree_amd
+
+    q = torch.randn(B, T, 8, 64, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    k = torch.randn(B, T, 2, 64, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    v = torch.randn(B, T, 2, 64, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    out, ctx = htree_amd.htree_forward(q.detach(), k.detach(), v.detach(), 16, 128, 16,
+                                       _save_for_backward=True)
+    assert out.shape == q.shape and out.dtype == q.dtype
+    dq, dk, dv = htree_amd.htree_backward(torch.zeros_like(out), q.detach(), out, ctx)
+    assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape
+    assert dq.dtype == dk.dtype == dv.dtype == torch.float32
+    o = htree_amd.htree_forward_triton_autograd(q, k, v, 16, 128, 16)
+    o.sum().backward()
+    assert q.grad.shape == q.shape and k.grad.dtype == k.dtype
+    with pytest.raises(AssertionError, match="configuration outside"):
+        htree_amd.htree_forward(q.detach()[..., :48], k.detach()[..., :48], v.detach()[..., :48],
+                                16, 128, 16)
