@@ -126,6 +126,9 @@ int htree_backward_workspace_min_bytes(const htree_dims* d, int64_t* bytes);
  * the mean-pool backward onto level 0).  `out` is the forward output handed
  * to the backward (delta = rowsum(dO * out)); gmax, gsum and parents are
  * what htree_forward wrote; tree_ws is the packed tree of htree_tree_build.
+ * The parent lists are trusted: other lists must keep the forward's form
+ * (indices in [-1, ceil(N_l / CR)), ascending, -1 padding last), else the
+ * kernels read out of bounds.
  * Deterministic: no floating-point atomics.
  * Replaces htree_backward (src/backward.py:941-1119) and its kernels K0
  * (:45-68), K1a/K1b (:119-436), K2 (:75-112), K3/K3u (:443-780),
