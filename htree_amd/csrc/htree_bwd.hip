@@ -460,15 +460,24 @@ __global__ __launch_bounds__(256) void piece_kernel(const int32_t* __restrict__ 
                                                     const int32_t* __restrict__ poff, int64_t nrows,
                                                     int piece, int32_t* __restrict__ ptab,
                                                     int32_t* __restrict__ npieces) {
-  const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (row == 0) *npieces = poff[nrows];
-  if (row >= nrows) return;
-  const int c = cnt[row];
-  for (int i = 0, k = poff[row]; i * piece < c; ++i, ++k) {
-    ptab[3 * k] = (int32_t)row;
-    ptab[3 * k + 1] = rowoff[row] + i * piece;
-    ptab[3 * k + 2] = c - i * piece < piece ? c - i * piece : piece;
+  // one thread per piece k (the grid covers the level's bound on pieces); its
+  // row is the last one whose first piece is <= k (rows without pieces
+  // share their successor's first piece and are passed over)
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int32_t total = poff[nrows];
+  if (k == 0) *npieces = total;
+  if (k >= total) return;
+  int64_t lo = 0, hi = nrows - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) >> 1;
+    if (poff[mid] <= k) lo = mid;
+    else hi = mid - 1;
   }
+  const int i = (int)(k - poff[lo]);
+  const int c = cnt[lo];
+  ptab[3 * k] = (int32_t)lo;
+  ptab[3 * k + 1] = rowoff[lo] + i * piece;
+  ptab[3 * k + 2] = c - i * piece < piece ? c - i * piece : piece;
 }
 
 
@@ -1654,8 +1663,11 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
                        (int)BP.piece[l], wpre, cnt, pcnt);
     hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, cnt, nrows, rowoff);
     hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, pcnt, nrows, poff);
-    hipLaunchKernelGGL(piece_kernel, dim3((unsigned)((nrows + 255) / 256)), dim3(256), 0, st, cnt,
-                       rowoff, poff, nrows, (int)BP.piece[l], ptab, npieces);
+    {
+      const int64_t np = (BP.ent[l] + BP.piece[l] - 1) / BP.piece[l] + BP.rows[l];  // bound
+      hipLaunchKernelGGL(piece_kernel, dim3((unsigned)((np + 255) / 256)), dim3(256), 0, st, cnt,
+                         rowoff, poff, nrows, (int)BP.piece[l], ptab, npieces);
+    }
     int4* recs = (int4*)(ws + BP.off_rec[l]);
     if (d->top_k > 64)
       hipLaunchKernelGGL(record_wide_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
