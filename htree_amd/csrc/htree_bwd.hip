@@ -92,6 +92,7 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true) 
   for (int l = 0; l < P.L; ++l) {
     const int64_t Pl = (P.N[l] + CR - 1) / CR;
     b->ent[l] = BH * d->T * (d->top_k < Pl ? d->top_k : Pl);
+    if (b->ent[l] > INT32_MAX) return HTREE_EUNSUPPORTED;  // entries are indexed in int32
     int64_t piece = 128;
     while (piece > 32 && b->ent[l] / piece < (1ll << 14)) piece >>= 1;
     while (b->ent[l] / piece > (1ll << 20)) piece <<= 1;

@@ -194,7 +194,8 @@ const char* htree_strerror(int status) {
       return "configuration outside this HIP build: needs D in {32,64,128}, H/H_kv <= 16, "
              "4 <= compression_rate <= 64, top_k_per_layer <= 512 and "
              "top_k_per_layer * compression_rate <= 8192 (where top_k_per_layer > 64 or "
-             "top_k_per_layer * max(compression_rate,16) / 16 > 64)";
+             "top_k_per_layer * max(compression_rate,16) / 16 > 64); the backward also needs "
+             "B * T * H_kv * min(top_k_per_layer, parents of a level) < 2^31 per level";
     case HTREE_EWORKSPACE: return "workspace smaller than htree_tree_workspace_bytes()";
     default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown htree status";
   }

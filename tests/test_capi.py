@@ -79,6 +79,20 @@ def test_invalid_configs_raise_assertion(kw, code):
         N.levels(d)
 
 
+def test_backward_entry_count_limit():
+    """The backward indexes a level's entries (query group, parent) in int32:
+    a level with 2^31 or more possible entries is refused by the backward's
+    sizing call, while the forward's plan (no such index) accepts it."""
+    kw = dict(B=8, T=131072, H=64, H_kv=8, D=32, compression_rate=16, top_k=512,
+              max_top_nodes=8192, rope_rows=9216)
+    d = dims(**kw)  # level 0: 8 * 131072 * 8 * 512 = 2^32 entries
+    assert len(N.levels(d)) == 2
+    nb = ctypes.c_int64()
+    assert N.lib().htree_backward_workspace_bytes(ctypes.byref(d), ctypes.byref(nb)) == N.HTREE_EUNSUPPORTED
+    d = dims(**dict(kw, B=1))  # 2^29 entries
+    assert N.lib().htree_backward_workspace_bytes(ctypes.byref(d), ctypes.byref(nb)) == N.HTREE_OK
+
+
 def test_null_pointers_rejected_without_launch():
     d = dims()
     lib = N.lib()
