@@ -430,8 +430,13 @@ __global__ __launch_bounds__(256) void row_scan_kernel(const uint32_t* __restric
 }
 
 // exclusive scan of n ints (one block of 1024 threads); out[n] = total
-__global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ in, int64_t n,
-                                                    int32_t* __restrict__ out) {
+__global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ in0,
+                                                    int32_t* __restrict__ out0,
+                                                    const int32_t* __restrict__ in1,
+                                                    int32_t* __restrict__ out1, int64_t n) {
+  // block b scans (in_b, out_b): two independent scans in one launch
+  const int32_t* __restrict__ in = blockIdx.x ? in1 : in0;
+  int32_t* __restrict__ out = blockIdx.x ? out1 : out0;
   __shared__ int32_t part[1024];
   const int tid = threadIdx.x;
   const int64_t per = (n + 1023) / 1024;
@@ -1662,8 +1667,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     }
     hipLaunchKernelGGL(row_scan_kernel, dim3((unsigned)nrows), dim3(256), 0, st, bm, BP.W,
                        (int)BP.piece[l], wpre, cnt, pcnt);
-    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, cnt, nrows, rowoff);
-    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, st, pcnt, nrows, poff);
+    hipLaunchKernelGGL(scan_kernel, dim3(2), dim3(1024), 0, st, cnt, rowoff, pcnt, poff, nrows);
     {
       const int64_t np = (BP.ent[l] + BP.piece[l] - 1) / BP.piece[l] + BP.rows[l];  // bound
       hipLaunchKernelGGL(piece_kernel, dim3((unsigned)((np + 255) / 256)), dim3(256), 0, st, cnt,
