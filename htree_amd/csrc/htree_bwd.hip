@@ -1654,9 +1654,10 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     const int64_t nrows = BP.rows[l];
     const int64_t words = nrows * BP.W;
     const int64_t ent = lstride;
-    // dense bitmaps (at least one entry per two words: long lists, upper
-    // levels) by columns; sparse ones by global atomics
-    if (2 * BP.ent[l] >= words) {
+    // dense bitmaps (at least one entry per four words: upper levels, and
+    // C2's and C4's level 0) by columns; sparser ones by global atomics
+    // (C5's level 0, one per eight: columns measured +0.6% of its backward)
+    if (4 * BP.ent[l] >= words) {
       hipLaunchKernelGGL(bitmap_cols_kernel, dim3((unsigned)(BH * BP.W)), dim3(256), 0, st,
                          parents + l * lstride, d->T, d->H_kv, d->top_k, Pl, BP.W, bm);
     } else {
