@@ -83,7 +83,7 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true) 
   }
   b->max_entries = BH * d->T * d->top_k;
   // Rows are cut into pieces (one dkv wave each) of 32..128 entries: at
-  // least 16K pieces for a level's largest possible entry count, so that a
+  // least 8K pieces for a level's largest possible entry count, so that a
   // level's waves fill the GPU's ~2K wave slots many times over and the
   // kernel's tail stays short, and long rows of popular parents spread over
   // many waves.  Beyond 2^20 pieces per level (16 MB of fp32 partials per 1K
@@ -94,7 +94,7 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true) 
     b->ent[l] = BH * d->T * (d->top_k < Pl ? d->top_k : Pl);
     if (b->ent[l] > INT32_MAX) return HTREE_EUNSUPPORTED;  // entries are indexed in int32
     int64_t piece = 128;
-    while (piece > 32 && b->ent[l] / piece < (1ll << 14)) piece >>= 1;
+    while (piece > 32 && b->ent[l] / piece < (1ll << 13)) piece >>= 1;
     while (b->ent[l] / piece > (1ll << 20)) piece <<= 1;
     b->piece[l] = piece;
     const int64_t np = (b->ent[l] + piece - 1) / piece + b->rows[l];
