@@ -93,7 +93,8 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true) 
     const int64_t Pl = (P.N[l] + CR - 1) / CR;
     b->ent[l] = BH * d->T * (d->top_k < Pl ? d->top_k : Pl);
     if (b->ent[l] > INT32_MAX) return HTREE_EUNSUPPORTED;  // entries are indexed in int32
-    int64_t piece = 128;
+    // (256-entry pieces only for levels with at least 32K of them: C4)
+    int64_t piece = b->ent[l] / 256 >= (1ll << 15) ? 256 : 128;
     while (piece > 32 && b->ent[l] / piece < (1ll << 13)) piece >>= 1;
     while (b->ent[l] / piece > (1ll << 20)) piece <<= 1;
     b->piece[l] = piece;
