@@ -142,12 +142,13 @@ static float dotf(const float* a, const float* b, int D) {
 }
 
 typedef struct {
-  int B, T, H, Hkv, D, CR, TK, L, G, rope_rows;
+  int B, T, H, Hkv, D, DV, CR, TK, L, G, rope_rows; /* D: q/k head dim, DV: v */
   float scale;
   const float* q;
   const float* lk;
   const float* lv;
-  const int64_t* loff;
+  const int64_t* loff;  /* level offsets of the K levels */
+  const int64_t* vloff; /* level offsets of the V levels */
   const int* ln;
   const float* cosc;
   const float* sinc;
@@ -157,7 +158,7 @@ static const float* krow(const ctx_t* c, int l, int b, int node, int h) {
   return c->lk + c->loff[l] + (((int64_t)b * c->ln[l] + node) * c->Hkv + h) * c->D;
 }
 static const float* vrow(const ctx_t* c, int l, int b, int node, int h) {
-  return c->lv + c->loff[l] + (((int64_t)b * c->ln[l] + node) * c->Hkv + h) * c->D;
+  return c->lv + c->vloff[l] + (((int64_t)b * c->ln[l] + node) * c->Hkv + h) * c->DV;
 }
 
 static int64_t ipow(int b, int e) {
@@ -241,25 +242,26 @@ static void scores_for(const ctx_t* c, int l, int b, int h, int nc,
  *            selection at level l+1 (the accumulated set at level l+1 is then
  *            "candidates not in forced[l]", as naive.py:355-361 does).
  * Outputs (all nullable except out/gmax/gsum):
- *   out      [nrows][H][D] fp32 (before rounding to the output dtype)
+ *   out      [nrows][H][DV] fp32 (before rounding to the output dtype)
  *   gmax/gsum[nrows][H]
  *   par_used [L][nrows][Hkv][TK] parent list used at each level
  *   sel_own  [L][nrows][Hkv][TK] own Top-K result at level l>=1 (ascending, -1 pad)
  *   imp      [L][nrows][Hkv][TK*CR] importance per flat position (forced
  *            rightmost = 1e6), -1 past nc; level 0 rows untouched
- *   lmax/lsum[L][nrows][H], lout [L][nrows][H][D]  per-level trace (naive.py:225-227)
+ *   lmax/lsum[L][nrows][H], lout [L][nrows][H][DV]  per-level trace (naive.py:225-227)
  */
-int orc_forward(const float* q, int B, int T, int H, int Hkv, int D,
+int orc_forward(const float* q, int B, int T, int H, int Hkv, int D, int DV,
                 const float* levels_k, const float* levels_v,
-                const int64_t* level_off, const int* level_n, int L,
+                const int64_t* level_off, const int64_t* vlevel_off,
+                const int* level_n, int L,
                 const float* cosc, const float* sinc, int rope_rows, int CR,
                 int TK, float scale, const int* rows_bt, int nrows,
                 const int* forced, float* out, float* gmax, float* gsum,
                 int* par_used, int* sel_own, float* imp, float* lmax,
                 float* lsum, float* lout) {
   if (H % Hkv != 0 || D % 2 != 0 || L < 1) return ORC_EARG;
-  ctx_t c = {B, T, H, Hkv, D, CR, TK, L, H / Hkv, rope_rows, scale, q,
-             levels_k, levels_v, level_off, level_n, cosc, sinc};
+  ctx_t c = {B, T, H, Hkv, D, DV, CR, TK, L, H / Hkv, rope_rows, scale, q,
+             levels_k, levels_v, level_off, vlevel_off, level_n, cosc, sinc};
   int G = c.G;
   int maxc = TK * CR;
   if (maxc > rope_rows) return ORC_EARG;
@@ -271,10 +273,10 @@ int orc_forward(const float* q, int B, int T, int H, int Hkv, int D,
   unsigned char* acc = (unsigned char*)malloc(maxc);
   int* par = (int*)malloc(sizeof(int) * TK);
   int* nxt = (int*)malloc(sizeof(int) * TK);
-  float* go = (float*)malloc(sizeof(float) * G * D);
+  float* go = (float*)malloc(sizeof(float) * G * DV);
   float* gm = (float*)malloc(sizeof(float) * G);
   float* gs = (float*)malloc(sizeof(float) * G);
-  float* lo = (float*)malloc(sizeof(float) * G * D);
+  float* lo = (float*)malloc(sizeof(float) * G * DV);
   float* lm = (float*)malloc(sizeof(float) * G);
   float* ls = (float*)malloc(sizeof(float) * G);
   int rc = ORC_OK;
@@ -294,7 +296,7 @@ int orc_forward(const float* q, int B, int T, int H, int Hkv, int D,
       for (int g = 0; g < G; ++g) {
         gm[g] = NEG_INF_SENTINEL;
         gs[g] = 0.0f;
-        for (int d = 0; d < D; ++d) go[g * D + d] = 0.0f;
+        for (int d = 0; d < DV; ++d) go[g * DV + d] = 0.0f;
       }
       init_parents(&c, t, par);
       for (int l = L - 1; l >= 0; --l) {
@@ -354,22 +356,22 @@ int orc_forward(const float* q, int B, int T, int H, int Hkv, int D,
           if (!any) {
             lm[g] = NEG_INF_SENTINEL;
             ls[g] = 0.0f;
-            for (int d = 0; d < D; ++d) lo[g * D + d] = 0.0f;
+            for (int d = 0; d < DV; ++d) lo[g * DV + d] = 0.0f;
             continue;
           }
           float nm = tm > NEG_INF_SENTINEL ? tm : NEG_INF_SENTINEL;
           double ssum = 0.0;
-          double* od = (double*)calloc(D, sizeof(double));
+          double* od = (double*)calloc(DV, sizeof(double));
           for (int j = 0; j < nc; ++j)
             if (acc[j]) {
               float p = expf(s[(int64_t)g * nc + j] - nm);
               ssum += p;
               const float* vr = vrow(&c, l, b, nodes[j], h);
-              for (int d = 0; d < D; ++d) od[d] += (double)p * vr[d];
+              for (int d = 0; d < DV; ++d) od[d] += (double)p * vr[d];
             }
           lm[g] = nm;
           ls[g] = (float)ssum;
-          for (int d = 0; d < D; ++d) lo[g * D + d] = (float)od[d];
+          for (int d = 0; d < DV; ++d) lo[g * DV + d] = (float)od[d];
           free(od);
         }
         if (lmax) {
@@ -377,7 +379,7 @@ int orc_forward(const float* q, int B, int T, int H, int Hkv, int D,
             int64_t hi = ((int64_t)l * nrows + r) * H + h * G + g;
             lmax[hi] = lm[g];
             lsum[hi] = ls[g];
-            for (int d = 0; d < D; ++d) lout[hi * D + d] = lo[g * D + d];
+            for (int d = 0; d < DV; ++d) lout[hi * DV + d] = lo[g * DV + d];
           }
         }
         /* merge into the global state with the sum>1e-10 guards (naive.py:215-223) */
@@ -388,9 +390,9 @@ int orc_forward(const float* q, int B, int T, int H, int Hkv, int D,
           float sc = ch ? expf(lm[g] - nm) : 0.0f;
           float ms = gs[g] * sg + ls[g] * sc;
           if (ch) {
-            for (int d = 0; d < D; ++d) {
-              float mo = go[g * D + d] * sg + lo[g * D + d] * sc;
-              go[g * D + d] = gh ? mo : lo[g * D + d];
+            for (int d = 0; d < DV; ++d) {
+              float mo = go[g * DV + d] * sg + lo[g * DV + d] * sc;
+              go[g * DV + d] = gh ? mo : lo[g * DV + d];
             }
             gm[g] = gh ? nm : lm[g];
             gs[g] = gh ? ms : ls[g];
@@ -403,7 +405,7 @@ int orc_forward(const float* q, int B, int T, int H, int Hkv, int D,
         int64_t hi = (int64_t)r * H + h * G + g;
         gmax[hi] = gm[g];
         gsum[hi] = gs[g];
-        for (int d = 0; d < D; ++d) out[hi * D + d] = go[g * D + d] / gs[g];
+        for (int d = 0; d < DV; ++d) out[hi * DV + d] = go[g * DV + d] / gs[g];
       }
     }
   }
@@ -423,7 +425,7 @@ typedef struct {
   const float* gm;    /* global max  [b,t,0]   [H]    */
   const float* gs;    /* global sum  [b,t,0]   [H]    */
   const float* dl;    /* delta       [b,t,0]   [H]    */
-  const float* dOr;   /* dO[b,t,0,0]           [H][D] */
+  const float* dOr;   /* dO[b,t,0,0]           [H][DV] */
 } rowp_t;
 
 typedef struct {
@@ -438,14 +440,14 @@ typedef struct {
   double* dqt;
 } scratch_t;
 
-static int scratch_alloc(scratch_t* w, int G, int D, int maxc) {
+static int scratch_alloc(scratch_t* w, int G, int D, int DV, int maxc) {
   w->nodes = (int*)malloc(sizeof(int) * maxc);
   w->qr = (float*)malloc(sizeof(float) * G * D);
   w->kr = (float*)malloc(sizeof(float) * (int64_t)maxc * D);
   w->s = (float*)malloc(sizeof(float) * (int64_t)G * maxc);
   w->dkt = (double*)malloc(sizeof(double) * D);
   w->dk = (double*)malloc(sizeof(double) * D);
-  w->dv = (double*)malloc(sizeof(double) * D);
+  w->dv = (double*)malloc(sizeof(double) * DV);
   w->tmp = (double*)malloc(sizeof(double) * D);
   w->dqt = (double*)malloc(sizeof(double) * G * D);
   return w->nodes && w->qr && w->kr && w->s && w->dkt && w->dk && w->dv &&
@@ -482,20 +484,21 @@ static int group_bwd(const ctx_t* c, int l, int b, int t, int h,
       if (in) continue;
     }
     const float* vr = vrow(c, l, b, w->nodes[j], h);
-    for (int d = 0; d < D; ++d) w->dkt[d] = w->dv[d] = 0.0;
+    for (int d = 0; d < D; ++d) w->dkt[d] = 0.0;
+    for (int d = 0; d < c->DV; ++d) w->dv[d] = 0.0;
     for (int g = 0; g < G; ++g) {
       int hh = h * G + g;
       float S = w->s[(int64_t)g * nc + j];
       double P = (double)expf(S - rp->gm[hh]) / (double)rp->gs[hh];
-      const float* dOg = rp->dOr + (int64_t)hh * D;
+      const float* dOg = rp->dOr + (int64_t)hh * c->DV;
       double dP = 0.0;
-      for (int d = 0; d < D; ++d) dP += (double)dOg[d] * vr[d];
+      for (int d = 0; d < c->DV; ++d) dP += (double)dOg[d] * vr[d];
       double dS = P * (dP - (double)rp->dl[hh]);
       for (int d = 0; d < D; ++d) {
         w->dqt[g * D + d] += dS * w->kr[(int64_t)j * D + d];
         w->dkt[d] += dS * w->qr[(int64_t)g * D + d];
-        w->dv[d] += P * dOg[d];
       }
+      for (int d = 0; d < c->DV; ++d) w->dv[d] += P * dOg[d];
     }
     rope_inv(w->dkt, c->cosc + (int64_t)j * (D / 2),
              c->sinc + (int64_t)j * (D / 2), D, w->dk);
@@ -511,18 +514,16 @@ static int group_bwd(const ctx_t* c, int l, int b, int t, int h,
 typedef struct {
   double* dk; /* node 0 of one (b,h) slice */
   double* dv;
-  int64_t stride;
-  int D;
+  int64_t stride, vstride;
+  int D, DV;
 } scatter_t;
 
 static void scatter_cb(void* user, int node, const double* dk, const double* dv) {
   scatter_t* sc = (scatter_t*)user;
   double* pk = sc->dk + (int64_t)node * sc->stride;
-  double* pv = sc->dv + (int64_t)node * sc->stride;
-  for (int d = 0; d < sc->D; ++d) {
-    pk[d] += dk[d];
-    pv[d] += dv[d];
-  }
+  double* pv = sc->dv + (int64_t)node * sc->vstride;
+  for (int d = 0; d < sc->D; ++d) pk[d] += dk[d];
+  for (int d = 0; d < sc->DV; ++d) pv[d] += dv[d];
 }
 
 /* delta = rowsum(dO * O) (naive.py:333), double sum of fp32 operands */
@@ -558,46 +559,48 @@ void orc_tree_backward(float* g, int B, int Hkv, int D, const int64_t* level_off
 /*
  * Full backward over all (b,t), given the parent lists used at every level
  * parents [L][B][T][Hkv][TK] (level L-1 holds the initial list).
- *   out (as returned, in fp32), dO [B,T,H,D]; gmax, gsum [B,T,H]
+ *   out (as returned, in fp32), dO [B,T,H,DV]; gmax, gsum [B,T,H]
  * Outputs: dq [B,T,H,D]; dk_lv/dv_lv: per-level gradients concatenated like
  * the tree levels, BEFORE the mean-pool backward.  The caller runs
  * orc_tree_backward on a copy to get the final dk/dv (level 0 slice).
  */
-int orc_backward(const float* q, int B, int T, int H, int Hkv, int D,
+int orc_backward(const float* q, int B, int T, int H, int Hkv, int D, int DV,
                  const float* levels_k, const float* levels_v,
-                 const int64_t* level_off, const int* level_n, int L,
+                 const int64_t* level_off, const int64_t* vlevel_off,
+                 const int* level_n, int L,
                  const float* cosc, const float* sinc, int rope_rows, int CR,
                  int TK, float scale, const int* parents, const float* gmax,
                  const float* gsum, const float* out, const float* dO,
                  float* dq, float* dk_lv, float* dv_lv) {
-  ctx_t c = {B, T, H, Hkv, D, CR, TK, L, H / Hkv, rope_rows, scale, q,
-             levels_k, levels_v, level_off, level_n, cosc, sinc};
+  ctx_t c = {B, T, H, Hkv, D, DV, CR, TK, L, H / Hkv, rope_rows, scale, q,
+             levels_k, levels_v, level_off, vlevel_off, level_n, cosc, sinc};
   int G = c.G, maxc = TK * CR;
   int64_t tot = level_off[L - 1] + (int64_t)B * level_n[L - 1] * Hkv * D;
+  int64_t vtot = vlevel_off[L - 1] + (int64_t)B * level_n[L - 1] * Hkv * DV;
   double* dkd = (double*)calloc(tot, sizeof(double));
-  double* dvd = (double*)calloc(tot, sizeof(double));
+  double* dvd = (double*)calloc(vtot, sizeof(double));
   float* delta = (float*)malloc(sizeof(float) * (int64_t)B * T * H);
   double* dqg = (double*)malloc(sizeof(double) * G * D);
   scratch_t w = {0};
   int rc = ORC_OK;
-  if (!dkd || !dvd || !delta || !dqg || !scratch_alloc(&w, G, D, maxc)) {
+  if (!dkd || !dvd || !delta || !dqg || !scratch_alloc(&w, G, D, DV, maxc)) {
     rc = ORC_ENOMEM;
     goto done;
   }
-  orc_delta(out, dO, (int64_t)B * T * H, D, delta);
+  orc_delta(out, dO, (int64_t)B * T * H, DV, delta);
   for (int b = 0; b < B && rc == ORC_OK; ++b)
     for (int t = 0; t < T && rc == ORC_OK; ++t) {
       int64_t bt = (int64_t)b * T + t;
       rowp_t rp = {q + bt * H * D, gmax + bt * H, gsum + bt * H, delta + bt * H,
-                   dO + bt * H * D};
+                   dO + bt * H * DV};
       for (int h = 0; h < Hkv && rc == ORC_OK; ++h) {
         for (int i = 0; i < G * D; ++i) dqg[i] = 0.0;
         for (int l = L - 1; l >= 0 && rc == ORC_OK; --l) {
           const int* par = parents + (((int64_t)l * B * T + bt) * Hkv + h) * TK;
           const int* nxt = l > 0 ? parents + (((int64_t)(l - 1) * B * T + bt) * Hkv + h) * TK : NULL;
           scatter_t sc = {dkd + level_off[l] + ((int64_t)b * level_n[l] * Hkv + h) * D,
-                          dvd + level_off[l] + ((int64_t)b * level_n[l] * Hkv + h) * D,
-                          (int64_t)Hkv * D, D};
+                          dvd + vlevel_off[l] + ((int64_t)b * level_n[l] * Hkv + h) * DV,
+                          (int64_t)Hkv * D, (int64_t)Hkv * DV, D, DV};
           rc = group_bwd(&c, l, b, t, h, par, nxt, &rp, dqg, scatter_cb, &sc, &w);
         }
         for (int g = 0; g < G; ++g)
@@ -605,11 +608,10 @@ int orc_backward(const float* q, int B, int T, int H, int Hkv, int D,
             dq[(bt * H + h * G + g) * D + d] = (float)dqg[g * D + d];
       }
     }
-  if (rc == ORC_OK)
-    for (int64_t i = 0; i < tot; ++i) {
-      dk_lv[i] = (float)dkd[i];
-      dv_lv[i] = (float)dvd[i];
-    }
+  if (rc == ORC_OK) {
+    for (int64_t i = 0; i < tot; ++i) dk_lv[i] = (float)dkd[i];
+    for (int64_t i = 0; i < vtot; ++i) dv_lv[i] = (float)dvd[i];
+  }
 done:
   free(dkd); free(dvd); free(delta); free(dqg);
   scratch_free(&w);
@@ -619,24 +621,25 @@ done:
 /*
  * Row-subset dq (Q-stationary: needs only the listed rows' own state).
  * parents_rows [L][nrows][Hkv][TK]; gmax/gsum/delta rows [nrows][H];
- * dO_rows [nrows][H][D].  Output dq_rows [nrows][H][D].
+ * dO_rows [nrows][H][DV].  Output dq_rows [nrows][H][D].
  */
 int orc_backward_dq_rows(const float* q, int B, int T, int H, int Hkv, int D,
-                         const float* levels_k, const float* levels_v,
-                         const int64_t* level_off, const int* level_n, int L,
+                         int DV, const float* levels_k, const float* levels_v,
+                         const int64_t* level_off, const int64_t* vlevel_off,
+                         const int* level_n, int L,
                          const float* cosc, const float* sinc, int rope_rows,
                          int CR, int TK, float scale, const int* rows_bt,
                          int nrows, const int* parents_rows,
                          const float* gmax_rows, const float* gsum_rows,
                          const float* delta_rows, const float* dO_rows,
                          float* dq_rows) {
-  ctx_t c = {B, T, H, Hkv, D, CR, TK, L, H / Hkv, rope_rows, scale, q,
-             levels_k, levels_v, level_off, level_n, cosc, sinc};
+  ctx_t c = {B, T, H, Hkv, D, DV, CR, TK, L, H / Hkv, rope_rows, scale, q,
+             levels_k, levels_v, level_off, vlevel_off, level_n, cosc, sinc};
   int G = c.G, maxc = TK * CR;
   double* dqg = (double*)malloc(sizeof(double) * G * D);
   scratch_t w = {0};
   int rc = ORC_OK;
-  if (!dqg || !scratch_alloc(&w, G, D, maxc)) {
+  if (!dqg || !scratch_alloc(&w, G, D, DV, maxc)) {
     rc = ORC_ENOMEM;
     goto done;
   }
@@ -644,7 +647,7 @@ int orc_backward_dq_rows(const float* q, int B, int T, int H, int Hkv, int D,
     int b = rows_bt[2 * r], t = rows_bt[2 * r + 1];
     rowp_t rp = {q + ((int64_t)b * T + t) * H * D, gmax_rows + (int64_t)r * H,
                  gsum_rows + (int64_t)r * H, delta_rows + (int64_t)r * H,
-                 dO_rows + (int64_t)r * H * D};
+                 dO_rows + (int64_t)r * H * DV};
     for (int h = 0; h < Hkv && rc == ORC_OK; ++h) {
       for (int i = 0; i < G * D; ++i) dqg[i] = 0.0;
       for (int l = L - 1; l >= 0 && rc == ORC_OK; --l) {
@@ -664,73 +667,114 @@ done:
 }
 
 /*
- * Node-subset dK/dV at one level, before the mean-pool backward: for each
- * listed (b, h_kv, node) scans every query t of batch b whose level-l parent
- * list holds node/CR and sums that query's contribution to the node.
- * parents [L][B][T][Hkv][TK]; gmax/gsum/delta [B,T,H]; dO [B,T,H,D].
- * Outputs dk_nodes/dv_nodes [n][D].
+ * Node-subset dK/dV, before the mean-pool backward (naive.py:365-386 for
+ * the listed nodes only).  Each target is (level, b, h_kv, node).  A query
+ * group (b, t, h_kv) accumulates the node at that level when its parent
+ * list there holds node/CR in slot s, the node's flat position
+ * j = s*CR + node%CR lies inside the causal candidate count
+ * nc = (n_p-1)*CR + (t/CR^l)%CR + 1 (naive.py:182-190), and, above level 0,
+ * the node is not in the list passed down to level l-1 (naive.py:358-361).
+ * Its contribution is computed from that one candidate's score alone:
+ *   s_g  = scale R(q_g, nc-1) . R(K[node], j)          (naive.py:193-199)
+ *   P_g  = exp(s_g - gmax_g) / gsum_g,  dS_g = P_g (dO_g . V[node] - delta_g)
+ *   dK  += R^-1(sum_g dS_g scale R(q_g, nc-1), j),  dV += sum_g P_g dO_g
+ * with the rotations and sums in double.  This is a different route to the
+ * same numbers as orc_backward (which scores every candidate of the group and
+ * scatters all of them); the tests tie the two together.
+ * parents [L][B][T][Hkv][TK]; gmax/gsum/delta [B,T,H]; dO [B,T,H,DV].
+ * Outputs dk_nodes [n][D], dv_nodes [n][DV].
  */
-typedef struct {
-  int want;
-  double* dk;
-  double* dv;
-  int D;
-} pick_t;
-
-static void pick_cb(void* user, int node, const double* dk, const double* dv) {
-  pick_t* p = (pick_t*)user;
-  if (node != p->want) return;
-  for (int d = 0; d < p->D; ++d) {
-    p->dk[d] += dk[d];
-    p->dv[d] += dv[d];
-  }
-}
-
 int orc_backward_dkv_nodes(const float* q, int B, int T, int H, int Hkv, int D,
-                           const float* levels_k, const float* levels_v,
-                           const int64_t* level_off, const int* level_n, int L,
+                           int DV, const float* levels_k, const float* levels_v,
+                           const int64_t* level_off, const int64_t* vlevel_off,
+                           const int* level_n, int L,
                            const float* cosc, const float* sinc, int rope_rows,
                            int CR, int TK, float scale, const int* parents,
                            const float* gmax, const float* gsum,
-                           const float* delta, const float* dO, int level,
-                           const int* nodes_bhn, int n, float* dk_nodes,
+                           const float* delta, const float* dO,
+                           const int* targets, int n, float* dk_nodes,
                            float* dv_nodes) {
-  ctx_t c = {B, T, H, Hkv, D, CR, TK, L, H / Hkv, rope_rows, scale, q,
-             levels_k, levels_v, level_off, level_n, cosc, sinc};
-  int G = c.G, maxc = TK * CR;
-  double* dqg = (double*)malloc(sizeof(double) * G * D);
+  ctx_t c = {B, T, H, Hkv, D, DV, CR, TK, L, H / Hkv, rope_rows, scale, q,
+             levels_k, levels_v, level_off, vlevel_off, level_n, cosc, sinc};
+  const int G = c.G, hd = D / 2;
+  double* kr = (double*)malloc(sizeof(double) * D);
+  double* qr = (double*)malloc(sizeof(double) * D);
+  double* ut = (double*)malloc(sizeof(double) * D);
   double* ak = (double*)malloc(sizeof(double) * D);
-  double* av = (double*)malloc(sizeof(double) * D);
-  scratch_t w = {0};
+  double* av = (double*)malloc(sizeof(double) * DV);
   int rc = ORC_OK;
-  if (!dqg || !ak || !av || !scratch_alloc(&w, G, D, maxc)) {
+  if (!kr || !qr || !ut || !ak || !av) {
     rc = ORC_ENOMEM;
     goto done;
   }
   for (int i = 0; i < n && rc == ORC_OK; ++i) {
-    int b = nodes_bhn[3 * i], h = nodes_bhn[3 * i + 1], node = nodes_bhn[3 * i + 2];
-    int pnode = node / CR;
-    for (int d = 0; d < D; ++d) ak[d] = av[d] = 0.0;
-    pick_t pk = {node, ak, av, D};
-    for (int t = 0; t < T && rc == ORC_OK; ++t) {
-      int64_t bt = (int64_t)b * T + t;
-      const int* par = parents + (((int64_t)level * B * T + bt) * Hkv + h) * TK;
-      int hit = 0;
-      for (int j = 0; j < TK; ++j)
-        if (par[j] == pnode) hit = 1;
-      if (!hit) continue;
-      const int* nxt = level > 0 ? parents + (((int64_t)(level - 1) * B * T + bt) * Hkv + h) * TK : NULL;
-      rowp_t rp = {q + bt * H * D, gmax + bt * H, gsum + bt * H, delta + bt * H,
-                   dO + bt * H * D};
-      rc = group_bwd(&c, level, b, t, h, par, nxt, &rp, dqg, pick_cb, &pk, &w);
+    const int l = targets[4 * i], b = targets[4 * i + 1], h = targets[4 * i + 2],
+              node = targets[4 * i + 3];
+    if (l < 0 || l >= L || b < 0 || b >= B || h < 0 || h >= Hkv || node < 0 ||
+        node >= level_n[l]) {
+      rc = ORC_EARG;
+      break;
     }
-    for (int d = 0; d < D; ++d) {
-      dk_nodes[(int64_t)i * D + d] = (float)ak[d];
-      dv_nodes[(int64_t)i * D + d] = (float)av[d];
+    const int64_t lp = ipow(CR, l);
+    const int pnode = node / CR, child = node % CR;
+    const float* krw = krow(&c, l, b, node, h);
+    const float* vr = vrow(&c, l, b, node, h);
+    for (int d = 0; d < D; ++d) ak[d] = 0.0;
+    for (int d = 0; d < DV; ++d) av[d] = 0.0;
+    for (int t = 0; t < T; ++t) {
+      if ((int64_t)node > t / lp) continue; /* right of the query's own node */
+      const int64_t bt = (int64_t)b * T + t;
+      const int* par = parents + (((int64_t)l * B * T + bt) * Hkv + h) * TK;
+      int np = 0, slot = -1;
+      for (int k = 0; k < TK; ++k)
+        if (par[k] >= 0) {
+          if (par[k] == pnode) slot = np;
+          ++np;
+        }
+      if (slot < 0) continue;
+      const int j = slot * CR + child;
+      const int nc = (np - 1) * CR + (int)((t / lp) % CR) + 1;
+      if (j >= nc) continue;
+      if (l > 0) {
+        const int* nxt = parents + (((int64_t)(l - 1) * B * T + bt) * Hkv + h) * TK;
+        int in = 0;
+        for (int k = 0; k < TK; ++k) in |= nxt[k] == node;
+        if (in) continue;
+      }
+      const float* ck = cosc + (int64_t)j * hd;
+      const float* sk = sinc + (int64_t)j * hd;
+      const float* cq = cosc + (int64_t)(nc - 1) * hd;
+      const float* sq = sinc + (int64_t)(nc - 1) * hd;
+      for (int d = 0; d < hd; ++d) {
+        kr[d] = (double)krw[d] * ck[d] - (double)krw[d + hd] * sk[d];
+        kr[d + hd] = (double)krw[d] * sk[d] + (double)krw[d + hd] * ck[d];
+      }
+      for (int d = 0; d < D; ++d) ut[d] = 0.0;
+      for (int g = 0; g < G; ++g) {
+        const int hh = h * G + g;
+        const float* qg = q + (bt * H + hh) * D;
+        const float* dOg = dO + (bt * H + hh) * DV;
+        for (int d = 0; d < hd; ++d) {
+          qr[d] = scale * ((double)qg[d] * cq[d] - (double)qg[d + hd] * sq[d]);
+          qr[d + hd] = scale * ((double)qg[d] * sq[d] + (double)qg[d + hd] * cq[d]);
+        }
+        double s = 0.0, dp = 0.0;
+        for (int d = 0; d < D; ++d) s += qr[d] * kr[d];
+        for (int d = 0; d < DV; ++d) dp += (double)dOg[d] * vr[d];
+        const double P = exp(s - (double)gmax[bt * H + hh]) / (double)gsum[bt * H + hh];
+        const double dS = P * (dp - (double)delta[bt * H + hh]);
+        for (int d = 0; d < D; ++d) ut[d] += dS * qr[d];
+        for (int d = 0; d < DV; ++d) av[d] += P * dOg[d];
+      }
+      for (int d = 0; d < hd; ++d) { /* R^-1 at j (naive.py:31-38) */
+        ak[d] += ut[d] * ck[d] + ut[d + hd] * sk[d];
+        ak[d + hd] += -ut[d] * sk[d] + ut[d + hd] * ck[d];
+      }
     }
+    for (int d = 0; d < D; ++d) dk_nodes[(int64_t)i * D + d] = (float)ak[d];
+    for (int d = 0; d < DV; ++d) dv_nodes[(int64_t)i * DV + d] = (float)av[d];
   }
 done:
-  free(dqg); free(ak); free(av);
-  scratch_free(&w);
+  free(kr); free(qr); free(ut); free(ak); free(av);
   return rc;
 }

@@ -17,7 +17,13 @@ Pinning (what each function is checked against, see tests/test_oracle_*.py):
                        closed-form candidate counts
   backward ........... golden fixtures (naive.py HTreeFunction grads);
                        torch float64 autograd of the dense form with the
-                       selection held fixed; finite differences
+                       selection held fixed
+  backward_dq_rows ... the full backward's dq at the same rows
+  backward_dkv_nodes . the full backward's per-level dK/dV at the same nodes
+  final_dkv_level0 ... the full backward's final dk/dv (after the pooling
+                       backward) at the same level-0 nodes
+  forward(forced=) ... dense float64 softmax over the union of the candidates
+                       that perturbed (teacher-forced) lists leave accumulated
 """
 from __future__ import annotations
 
@@ -62,17 +68,16 @@ def lib():
         L.orc_round_array.argtypes = [P, I64, I]
         L.orc_tree_build_level.argtypes = [P, I, I, I, I, I, I, P]
         L.orc_forward.restype = I
-        L.orc_forward.argtypes = [P, I, I, I, I, I, P, P, P, P, I, P, P, I, I, I, F,
-                                  P, I, P, P, P, P, P, P, P, P, P, P]
+        # common prefix: q, B, T, H, Hkv, D, DV, levels k / v, k / v level
+        # offsets, level sizes, L, cos, sin, rope_rows, CR, TK, scale
+        C = [P, I, I, I, I, I, I, P, P, P, P, P, I, P, P, I, I, I, F]
+        L.orc_forward.argtypes = C + [P, I, P, P, P, P, P, P, P, P, P, P]
         L.orc_backward.restype = I
-        L.orc_backward.argtypes = [P, I, I, I, I, I, P, P, P, P, I, P, P, I, I, I, F,
-                                   P, P, P, P, P, P, P, P]
+        L.orc_backward.argtypes = C + [P, P, P, P, P, P, P, P]
         L.orc_backward_dq_rows.restype = I
-        L.orc_backward_dq_rows.argtypes = [P, I, I, I, I, I, P, P, P, P, I, P, P, I, I, I, F,
-                                           P, I, P, P, P, P, P, P]
+        L.orc_backward_dq_rows.argtypes = C + [P, I, P, P, P, P, P, P]
         L.orc_backward_dkv_nodes.restype = I
-        L.orc_backward_dkv_nodes.argtypes = [P, I, I, I, I, I, P, P, P, P, I, P, P, I, I, I, F,
-                                             P, P, P, P, P, I, P, I, P, P]
+        L.orc_backward_dkv_nodes.argtypes = C + [P, P, P, P, P, P, I, P, P]
         L.orc_delta.argtypes = [P, P, I64, I, P]
         L.orc_tree_backward.argtypes = [P, I, I, I, P, P, I, I]
         _lib = L
@@ -149,14 +154,15 @@ def build_tree(k: np.ndarray, v: np.ndarray, compression_rate: int, max_top_node
     k = _f32(k)
     v = _f32(v)
     B, T, Hkv, D = k.shape
+    DV = v.shape[3]
     sizes = level_sizes(T, compression_rate, max_top_nodes)
     lk, lv = [k], [v]
     for n in sizes[1:]:
         pk = np.empty((B, n, Hkv, D), np.float32)
-        pv = np.empty((B, n, Hkv, D), np.float32)
+        pv = np.empty((B, n, Hkv, DV), np.float32)
         lib().orc_tree_build_level(_ptr(lk[-1]), B, lk[-1].shape[1], Hkv, D,
                                    compression_rate, DTYPE_CODE[dtype], _ptr(pk))
-        lib().orc_tree_build_level(_ptr(lv[-1]), B, lv[-1].shape[1], Hkv, D,
+        lib().orc_tree_build_level(_ptr(lv[-1]), B, lv[-1].shape[1], Hkv, DV,
                                    compression_rate, DTYPE_CODE[dtype], _ptr(pv))
         lk.append(pk)
         lv.append(pv)
@@ -175,7 +181,9 @@ def _concat_levels(levels: Sequence[np.ndarray]):
 
 
 class Tree:
-    """Tree levels + RoPE tables shared by the forward/backward calls."""
+    """Tree levels + RoPE tables shared by the forward/backward calls.  The
+    key head dim D (q, k) and the value head dim DV (v) may differ
+    (naive.py:144)."""
 
     def __init__(self, k, v, compression_rate: int, max_top_nodes: int, top_k: int,
                  dtype: str, rope_base: float = 10000.0, levels=None):
@@ -188,17 +196,19 @@ class Tree:
         self.TK = top_k
         self.dtype = dtype
         self.B, self.T, self.Hkv, self.D = self.lk[0].shape
+        self.DV = self.lv[0].shape[3]
         self.L = len(self.lk)
         self.rope_rows = rope_rows_needed(max_top_nodes, top_k, compression_rate)
         self.cos, self.sin = rope_tables(self.D, self.rope_rows, rope_base)
         self.kflat, self.off, self.n = _concat_levels(self.lk)
-        self.vflat, _, _ = _concat_levels(self.lv)
+        self.vflat, self.voff, _ = _concat_levels(self.lv)
 
     def _common(self, q):
         B, T, H, D = q.shape
-        return [_ptr(q), B, T, H, self.Hkv, D, _ptr(self.kflat), _ptr(self.vflat),
-                _ptr(self.off), _ptr(self.n), self.L, _ptr(self.cos), _ptr(self.sin),
-                self.rope_rows, self.CR, self.TK]
+        assert D == self.D, f"q head dim {D} != k head dim {self.D}"
+        return [_ptr(q), B, T, H, self.Hkv, D, self.DV, _ptr(self.kflat), _ptr(self.vflat),
+                _ptr(self.off), _ptr(self.voff), _ptr(self.n), self.L, _ptr(self.cos),
+                _ptr(self.sin), self.rope_rows, self.CR, self.TK]
 
 
 def all_rows(B: int, T: int) -> np.ndarray:
@@ -219,8 +229,8 @@ def forward(q, tree: Tree, scale: float, rows: Optional[np.ndarray] = None,
         rows = all_rows(B, T)
     rows = np.ascontiguousarray(rows, np.int32)
     n = rows.shape[0]
-    L, Hkv, TK, CR = tree.L, tree.Hkv, tree.TK, tree.CR
-    out = np.zeros((n, H, D), np.float32)
+    L, Hkv, TK, CR, DV = tree.L, tree.Hkv, tree.TK, tree.CR, tree.DV
+    out = np.zeros((n, H, DV), np.float32)
     gmax = np.zeros((n, H), np.float32)
     gsum = np.zeros((n, H), np.float32)
     par = np.full((L, n, Hkv, TK), -1, np.int32)
@@ -230,7 +240,7 @@ def forward(q, tree: Tree, scale: float, rows: Optional[np.ndarray] = None,
     if trace:
         lmax = np.zeros((L, n, H), np.float32)
         lsum = np.zeros((L, n, H), np.float32)
-        lout = np.zeros((L, n, H, D), np.float32)
+        lout = np.zeros((L, n, H, DV), np.float32)
     if forced is not None:
         forced = np.ascontiguousarray(forced, np.int32)
         assert forced.shape == (L, n, Hkv, TK)
@@ -263,16 +273,19 @@ def backward(q, tree: Tree, scale: float, parents: np.ndarray, gmax, gsum, out, 
     dk_fin = dk_lv.copy()
     dv_fin = dv_lv.copy()
     lib().orc_tree_backward(_ptr(dk_fin), B, tree.Hkv, D, _ptr(tree.off), _ptr(tree.n), tree.L, tree.CR)
-    lib().orc_tree_backward(_ptr(dv_fin), B, tree.Hkv, D, _ptr(tree.off), _ptr(tree.n), tree.L, tree.CR)
-    split = lambda flat: [flat[tree.off[i]:tree.off[i] + tree.lk[i].size].reshape(tree.lk[i].shape)
-                          for i in range(tree.L)]
-    return dict(dq=dq, dk_levels=split(dk_lv), dv_levels=split(dv_lv),
-                dk=split(dk_fin)[0].copy(), dv=split(dv_fin)[0].copy())
+    lib().orc_tree_backward(_ptr(dv_fin), B, tree.Hkv, tree.DV, _ptr(tree.voff), _ptr(tree.n), tree.L,
+                            tree.CR)
+    split = lambda flat, lv, off: [flat[off[i]:off[i] + lv[i].size].reshape(lv[i].shape)
+                                   for i in range(tree.L)]
+    return dict(dq=dq, dk_levels=split(dk_lv, tree.lk, tree.off),
+                dv_levels=split(dv_lv, tree.lv, tree.voff),
+                dk=split(dk_fin, tree.lk, tree.off)[0].copy(),
+                dv=split(dv_fin, tree.lv, tree.voff)[0].copy())
 
 
 def delta(out, dO) -> np.ndarray:
     out, dO = _f32(out), _f32(dO)
-    D = out.shape[-1]
+    D = out.shape[-1]  # the value head dim
     res = np.zeros(out.shape[:-1], np.float32)
     lib().orc_delta(_ptr(out), _ptr(dO), res.size, D, _ptr(res))
     return res
@@ -295,20 +308,82 @@ def backward_dq_rows(q, tree: Tree, scale: float, rows, parents_rows, gmax_rows,
 
 
 def backward_dkv_nodes(q, tree: Tree, scale: float, parents, gmax, gsum, delta_, dO,
-                       level: int, nodes_bhn) -> Tuple[np.ndarray, np.ndarray]:
-    """Per-level dK/dV (before the mean-pool backward) for listed (b,h_kv,node)."""
+                       targets, threads: int = 0) -> Tuple[np.ndarray, np.ndarray]:
+    """Per-level dK/dV (before the mean-pool backward) at listed nodes.
+
+    targets [n, 4] of (level, b, h_kv, node).  Each node's contribution is
+    computed from its own score in every query group that accumulates it
+    (naive.py:365-386 restricted to one node), so the cost is one scan of the
+    parent lists plus O(G*D) per accumulating query: usable at full workload
+    sizes.  parents [L,B,T,Hkv,TK]; gmax, gsum, delta_ [B,T,H]; dO [B,T,H,D].
+    The targets are split over `threads` host threads (0: all cores)."""
+    from concurrent.futures import ThreadPoolExecutor
+
     q = _f32(q)
-    nodes_bhn = np.ascontiguousarray(nodes_bhn, np.int32)
-    n = nodes_bhn.shape[0]
     D = q.shape[-1]
+    targets = np.ascontiguousarray(targets, np.int32).reshape(-1, 4)
+    n = targets.shape[0]
     dk = np.zeros((n, D), np.float32)
-    dv = np.zeros((n, D), np.float32)
+    dv = np.zeros((n, tree.DV), np.float32)
     args = [np.ascontiguousarray(parents, np.int32), _f32(gmax), _f32(gsum), _f32(delta_), _f32(dO)]
-    rc = lib().orc_backward_dkv_nodes(*tree._common(q), ctypes.c_float(scale),
-                                      *[_ptr(a) for a in args], level, _ptr(nodes_bhn), n,
-                                      _ptr(dk), _ptr(dv))
-    _check(rc, "oracle dkv nodes")
+    common = tree._common(q)
+    nt = max(1, min(n, threads or min(16, os.cpu_count() or 1)))
+    cuts = np.linspace(0, n, nt + 1).astype(int)
+
+    def part(i):
+        a, b = cuts[i], cuts[i + 1]
+        if a == b:
+            return 0
+        return lib().orc_backward_dkv_nodes(*common, ctypes.c_float(scale), *[_ptr(x) for x in args],
+                                            _ptr(targets[a:]), int(b - a), _ptr(dk[a:]), _ptr(dv[a:]))
+
+    lib()
+    with ThreadPoolExecutor(nt) as ex:
+        for rc in ex.map(part, range(nt)):
+            _check(rc, "oracle dkv nodes")
     return dk, dv
+
+
+def level0_ancestors(tree: Tree, node: int) -> List[Tuple[int, int, int]]:
+    """(level, ancestor, children of that ancestor) for level-0 `node`, level
+    1 upwards: the factors of the mean-pool backward (naive.py:388-394)."""
+    out = []
+    a = node
+    for l in range(1, tree.L):
+        a //= tree.CR
+        cnt = min(tree.CR, int(tree.n[l - 1]) - a * tree.CR)
+        out.append((l, a, cnt))
+    return out
+
+
+def final_dkv_level0(q, tree: Tree, scale: float, parents, gmax, gsum, delta_, dO, nodes_bhn,
+                     threads: int = 0) -> Tuple[np.ndarray, np.ndarray]:
+    """Final dk / dv (after the mean-pool backward, naive.py:388-394) at
+    level-0 nodes nodes_bhn [n, 3] of (b, h_kv, node), from the per-level
+    terms of every ancestor: g_0[x] = dK_0[x] + g_1[x/CR] / |Ch(x/CR)|,
+    g_l[p] = dK_l[p] + g_{l+1}[p/CR] / |Ch(p/CR)|.  Returns float64 [n, D]."""
+    nodes_bhn = np.asarray(nodes_bhn, np.int64).reshape(-1, 3)
+    want = {}
+    for b, h, x in nodes_bhn:
+        want[(0, b, h, x)] = None
+        for l, a, _ in level0_ancestors(tree, int(x)):
+            want[(l, b, h, a)] = None
+    keys = list(want)
+    dk, dv = backward_dkv_nodes(q, tree, scale, parents, gmax, gsum, delta_, dO,
+                                np.array(keys, np.int32), threads)
+    term = {key: (dk[i].astype(np.float64), dv[i].astype(np.float64)) for i, key in enumerate(keys)}
+    D, DV = dk.shape[1], dv.shape[1]
+    rk = np.zeros((len(nodes_bhn), D))
+    rv = np.zeros((len(nodes_bhn), DV))
+    for i, (b, h, x) in enumerate(nodes_bhn):
+        anc = level0_ancestors(tree, int(x))
+        gk, gv = np.zeros(D), np.zeros(DV)
+        for (l, a, cnt) in reversed(anc):  # top-down
+            gk = (gk + term[(l, b, h, a)][0]) / cnt
+            gv = (gv + term[(l, b, h, a)][1]) / cnt
+        rk[i] = gk + term[(0, b, h, x)][0]
+        rv[i] = gv + term[(0, b, h, x)][1]
+    return rk, rv
 
 
 def initial_parents(B: int, T: int, Hkv: int, TK: int, CR: int, L: int) -> np.ndarray:

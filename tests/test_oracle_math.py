@@ -237,3 +237,217 @@ def test_backward_is_autograd_of_dense_form(run):
         ref = ref.numpy()
         err = np.abs(got - ref).max() / np.abs(ref).max()
         assert err < 1e-5, f"{name}: rel err {err:.2e}"
+
+
+# ------------------------------------------------------------ subset checkers
+# The full-size GPU tests check the device against row- and node-subset forms
+# of the oracle (backward_dq_rows, backward_dkv_nodes, final_dkv_level0) and
+# against the forward teacher-forced on the device's lists.  These tie each of
+# them to the full backward (itself pinned by the reference's gradients and by
+# float64 autograd above) and to the dense softmax.
+
+def full_backward(r):
+    B, T, H, Hkv, D, TK, L = r["B"], r["T"], r["H"], r["Hkv"], r["D"], r["TK"], r["tree"].L
+    fw = r["fw"]
+    par = fw["parents"].reshape(L, B, T, Hkv, TK)
+    gm, gs = fw["gmax"].reshape(B, T, H), fw["gsum"].reshape(B, T, H)
+    out = fw["out"].reshape(B, T, H, D)
+    bw = orc.backward(r["q"], r["tree"], D ** -0.5, par, gm, gs, out, r["dO"])
+    return bw, par, gm, gs, orc.delta(out, r["dO"])
+
+
+def sample_nodes(r, rng, per_level=12):
+    """(level, b, h, node) targets: random nodes of every level plus each
+    level's first and last node (the last parent's partial tail)."""
+    tree = r["tree"]
+    out = []
+    for l in range(tree.L):
+        n = int(tree.n[l])
+        for b in range(r["B"]):
+            for h in range(r["Hkv"]):
+                picks = set(rng.choice(n, min(n, per_level), replace=False).tolist()) | {0, n - 1}
+                out += [(l, b, h, x) for x in sorted(picks)]
+    return np.array(out, np.int32)
+
+
+def test_dq_rows_matches_full_backward(run):
+    bw, par, gm, gs, dl = full_backward(run)
+    B, T, H, D = run["B"], run["T"], run["H"], run["D"]
+    rows = orc.all_rows(B, T)[::7]
+    rows = np.concatenate([rows, [[B - 1, T - 1]]]).astype(np.int32)
+    b, t = rows[:, 0], rows[:, 1]
+    got = orc.backward_dq_rows(run["q"], run["tree"], D ** -0.5, rows, par[:, b, t], gm[b, t], gs[b, t],
+                               dl[b, t], run["dO"][b, t])
+    # same per-group routine on the same inputs: identical values
+    np.testing.assert_array_equal(got, bw["dq"][b, t])
+
+
+def test_dkv_nodes_matches_full_backward(run):
+    """Per-level dK/dV from each node's own scores (a different route from
+    the full backward, which scores whole groups and scatters)."""
+    bw, par, gm, gs, dl = full_backward(run)
+    tg = sample_nodes(run, np.random.default_rng(1))
+    dk, dv = orc.backward_dkv_nodes(run["q"], run["tree"], run["D"] ** -0.5, par, gm, gs, dl,
+                                    run["dO"], tg, threads=4)
+    ref_k = np.stack([bw["dk_levels"][l][b, x, h] for l, b, h, x in tg])
+    ref_v = np.stack([bw["dv_levels"][l][b, x, h] for l, b, h, x in tg])
+    for got, ref in ((dk, ref_k), (dv, ref_v)):
+        scl = np.abs(ref).max()
+        assert scl > 0
+        np.testing.assert_allclose(got, ref, rtol=1e-4, atol=2e-6 * scl)
+    # nodes that nothing accumulates (e.g. a level's nodes that every query
+    # passes down) come out exactly zero in both
+    zero = np.all(ref_k == 0, axis=1)
+    assert np.all(dk[zero] == 0)
+
+
+def test_final_dkv_level0_matches_full_backward(run):
+    bw, par, gm, gs, dl = full_backward(run)
+    rng = np.random.default_rng(2)
+    T = run["T"]
+    nodes = [(b, h, x) for b in range(run["B"]) for h in range(run["Hkv"])
+             for x in set(rng.choice(T, 10, replace=False).tolist()) | {0, T - 1}]
+    nodes = np.array(nodes, np.int32)
+    dk, dv = orc.final_dkv_level0(run["q"], run["tree"], run["D"] ** -0.5, par, gm, gs, dl, run["dO"],
+                                  nodes, threads=4)
+    ref_k = np.stack([bw["dk"][b, x, h] for b, h, x in nodes])
+    ref_v = np.stack([bw["dv"][b, x, h] for b, h, x in nodes])
+    for got, ref in ((dk, ref_k), (dv, ref_v)):
+        np.testing.assert_allclose(got, ref, rtol=1e-4, atol=2e-6 * np.abs(ref).max())
+
+
+def test_subset_backward_matches_autograd():
+    """dq rows and final dk/dv at level-0 nodes straight against float64
+    autograd of the dense form (the first, small fp32 case)."""
+    B, T, H, Hkv, D, CR, TK, MTN, dtype = CASES[0]
+    q, k, v, dO = make_inputs(B, T, H, Hkv, D, dtype)
+    tree = orc.Tree(k, v, CR, MTN, TK, dtype)
+    fw = orc.forward(q, tree, D ** -0.5, trace=True)
+    r = dict(B=B, T=T, H=H, Hkv=Hkv, D=D, CR=CR, TK=TK, MTN=MTN, dtype=dtype, q=q, k=k, v=v, dO=dO,
+             tree=tree, fw=fw)
+    L = tree.L
+    qt = torch.from_numpy(q).double().requires_grad_(True)
+    kt = torch.from_numpy(k).double().requires_grad_(True)
+    vt = torch.from_numpy(v).double().requires_grad_(True)
+    rows_all = [(b, t) for b in range(B) for t in range(T)]
+    o = dense_torch_forward(r, qt, kt, vt, rows_all).reshape(B, T, H, D)
+    o.backward(torch.from_numpy(dO).double())
+    par = fw["parents"].reshape(L, B, T, Hkv, TK)
+    gm, gs = fw["gmax"].reshape(B, T, H), fw["gsum"].reshape(B, T, H)
+    dl = orc.delta(fw["out"].reshape(B, T, H, D), dO)
+    rows = np.array([(0, t) for t in (0, 5, 77, 150, 299)], np.int32)
+    b, t = rows[:, 0], rows[:, 1]
+    dq = orc.backward_dq_rows(q, tree, D ** -0.5, rows, par[:, b, t], gm[b, t], gs[b, t], dl[b, t], dO[b, t])
+    ref = qt.grad.numpy()[b, t]
+    assert np.abs(dq - ref).max() < 1e-5 * np.abs(qt.grad.numpy()).max()
+    nodes = np.array([(0, 0, x) for x in (0, 3, 64, 150, 298, 299)], np.int32)
+    dk, dv = orc.final_dkv_level0(q, tree, D ** -0.5, par, gm, gs, dl, dO, nodes, threads=2)
+    for got, ref in ((dk, kt.grad.numpy()[0, nodes[:, 2], 0]), (dv, vt.grad.numpy()[0, nodes[:, 2], 0])):
+        assert np.abs(got - ref).max() < 1e-5 * np.abs(ref).max()
+
+
+def perturbed_lists(r, rng, frac=0.5):
+    """Parent lists [L, n, Hkv, TK] that differ from the oracle's own
+    selection: level by level from the top, each list is the oracle's own
+    Top-K from the (already perturbed) list above, and in about `frac` of the
+    rows one selected node other than the rightmost is swapped for a
+    candidate that was not selected.  Lists stay ascending, -1 padded, with
+    the rightmost node kept, like every list the device writes."""
+    tree, CR, TK, q, D = r["tree"], r["CR"], r["TK"], r["q"], r["D"]
+    L = tree.L
+    rows = orc.all_rows(r["B"], r["T"])
+    forced = orc.forward(q, tree, D ** -0.5, rows=rows)["parents"].copy()
+    swapped = 0
+    for l in range(L - 1, 0, -1):
+        fw = orc.forward(q, tree, D ** -0.5, rows=rows, forced=forced)
+        sel = fw["sel"][l].copy()  # own Top-K at level l from the list used there
+        for i in range(sel.shape[0]):
+            t = int(rows[i, 1])
+            for h in range(sel.shape[1]):
+                if rng.random() >= frac:
+                    continue
+                vp = [int(x) for x in forced[l, i, h] if x >= 0]
+                nc = (len(vp) - 1) * CR + (t // CR ** l) % CR + 1
+                cand = [vp[j // CR] * CR + j % CR for j in range(nc)]
+                cur = [int(x) for x in sel[i, h] if x >= 0]
+                right = t // CR ** l
+                out_ = [x for x in cand if x not in cur]
+                inn = [x for x in cur if x != right]
+                if not out_ or not inn:
+                    continue
+                cur.remove(inn[rng.integers(len(inn))])
+                cur.append(out_[rng.integers(len(out_))])
+                cur.sort()
+                sel[i, h] = cur + [-1] * (TK - len(cur))
+                swapped += 1
+        forced[l - 1] = sel
+    return forced, swapped
+
+
+@pytest.mark.parametrize("case", CASES[:2], ids=lambda c: f"T{c[1]}cr{c[5]}tk{c[6]}")
+def test_forced_forward_is_dense_softmax(case):
+    """Teacher forcing with lists that are not the oracle's own choice: the
+    output is one softmax over the candidates those lists leave accumulated,
+    and gmax its max."""
+    B, T, H, Hkv, D, CR, TK, MTN, dtype = case
+    q, k, v, dO = make_inputs(B, T, H, Hkv, D, dtype, seed=5)
+    tree = orc.Tree(k, v, CR, MTN, TK, dtype)
+    r = dict(B=B, T=T, H=H, Hkv=Hkv, D=D, CR=CR, TK=TK, MTN=MTN, dtype=dtype, q=q, tree=tree)
+    forced, swapped = perturbed_lists(r, np.random.default_rng(7))
+    assert swapped > 50
+    fw = orc.forward(q, tree, D ** -0.5, rows=orc.all_rows(B, T), forced=forced)
+    assert np.array_equal(fw["parents"][:-1], forced[:-1])
+    own = orc.forward(q, tree, D ** -0.5)
+    assert not np.allclose(fw["out_f32"], own["out_f32"])  # the lists matter
+    r["fw"] = fw
+    test_output_is_dense_softmax_over_accumulated(r)
+
+
+# ------------------------------------------------------------ K != V
+# The reference carries the value head dim apart from the key head dim
+# (src/naive.py:144 v_dim = v.shape[-1]).  The oracle restates that directly;
+# pinned here by the dense softmax and float64 autograd of the dense form.
+
+@pytest.mark.parametrize("kv", [(32, 16), (16, 32)], ids=lambda x: f"K{x[0]}V{x[1]}")
+def test_oracle_separate_value_dim(kv):
+    K, V = kv
+    B, T, H, Hkv, CR, TK, MTN, dtype = 1, 260, 4, 2, 4, 8, 32, "float32"
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(B, T, H, K, generator=g).numpy()
+    k = torch.randn(B, T, Hkv, K, generator=g).numpy()
+    v = torch.randn(B, T, Hkv, V, generator=g).numpy()
+    dO = torch.randn(B, T, H, V, generator=g).numpy()
+    tree = orc.Tree(k, v, CR, MTN, TK, dtype)
+    assert tree.DV == V and tree.lv[1].shape[-1] == V
+    fw = orc.forward(q, tree, K ** -0.5, trace=True)
+    assert fw["out"].shape == (B * T, H, V)
+    r = dict(B=B, T=T, H=H, Hkv=Hkv, D=K, CR=CR, TK=TK, MTN=MTN, dtype=dtype, q=q, k=k, v=v, dO=dO,
+             tree=tree, fw=fw)
+    test_output_is_dense_softmax_over_accumulated(r)
+    L = tree.L
+    par = fw["parents"].reshape(L, B, T, Hkv, TK)
+    gm, gs = fw["gmax"].reshape(B, T, H), fw["gsum"].reshape(B, T, H)
+    out = fw["out"].reshape(B, T, H, V)
+    bw = orc.backward(q, tree, K ** -0.5, par, gm, gs, out, dO)
+    assert bw["dq"].shape == q.shape and bw["dk"].shape == k.shape and bw["dv"].shape == v.shape
+    qt = torch.from_numpy(q).double().requires_grad_(True)
+    kt = torch.from_numpy(k).double().requires_grad_(True)
+    vt = torch.from_numpy(v).double().requires_grad_(True)
+    o = dense_torch_forward(r, qt, kt, vt, [(b, t) for b in range(B) for t in range(T)])
+    o.reshape(B, T, H, V).backward(torch.from_numpy(dO).double())
+    for name, got, ref in (("dq", bw["dq"], qt.grad), ("dk", bw["dk"], kt.grad), ("dv", bw["dv"], vt.grad)):
+        ref = ref.numpy()
+        err = np.abs(got - ref).max() / np.abs(ref).max()
+        assert err < 1e-5, f"{name}: rel err {err:.2e}"
+    # the subset forms at K != V
+    dl = orc.delta(out, dO)
+    nodes = np.array([(0, h, x) for h in range(Hkv) for x in (0, 7, 130, 259)], np.int32)
+    dk, dv = orc.final_dkv_level0(q, tree, K ** -0.5, par, gm, gs, dl, dO, nodes, threads=2)
+    np.testing.assert_allclose(dk, bw["dk"][0, nodes[:, 2], nodes[:, 1]], rtol=1e-4,
+                               atol=1e-6 * np.abs(bw["dk"]).max())
+    np.testing.assert_allclose(dv, bw["dv"][0, nodes[:, 2], nodes[:, 1]], rtol=1e-4,
+                               atol=1e-6 * np.abs(bw["dv"]).max())
+    rows = np.array([(0, t) for t in (3, 100, 259)], np.int32)
+    b, t = rows[:, 0], rows[:, 1]
+    dq = orc.backward_dq_rows(q, tree, K ** -0.5, rows, par[:, b, t], gm[b, t], gs[b, t], dl[b, t], dO[b, t])
+    np.testing.assert_array_equal(dq, bw["dq"][b, t])
