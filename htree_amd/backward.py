@@ -4,11 +4,23 @@
 
 `htree_backward(dO, q, output, bwd_ctx) -> (dq, dk, dv)` in fp32, reading
 the reference's bwd_ctx keys.  The selection is taken from
-`per_layer_parents` (saved by the forward); when the context holds none
-(the reference's autograd path saves none, src/backward.py:1138) the
-forward's selection is replayed once to recover them.  The autograd
-Function saves the parent lists (B*T*H_kv*TK int32 per level) instead of
-recomputing them.
+`per_layer_parents` when the context holds them; otherwise (the reference's
+own autograd path saves none, src/backward.py:1138) the forward's selection
+is replayed once, with the context's own RoPE tables (`cos_cache`,
+`sin_cache`), as the reference's `_recompute_parents` does
+(src/backward.py:881-934,1163-1171).  A context without `packed_tree` gets
+its operand tree rebuilt from `layers_k[0]` / `layers_v[0]` with those same
+tables (src/backward.py:848-878).
+
+Two autograd modes:
+  * default: the Function saves the parent lists, the packed tree and (bf16
+    configurations with <= 16 candidate tiles per level) the candidate
+    scores, so the backward replays nothing;
+  * `_save_parents=False` (htree_forward_triton_autograd): the Function
+    saves only the reference's eight tensors (q, k, v, out, global max / sum,
+    cos / sin, src/backward.py:1141-1145); the backward rebuilds the tree and
+    replays the forward once (keeping its scores for the duration of the
+    backward only).
 """
 from __future__ import annotations
 
@@ -17,7 +29,8 @@ from typing import Optional
 import torch
 
 from . import _native as N
-from .parallel import build_tree, htree_forward, make_dims
+from .parallel import (HeadFrame, build_tree, check_tables, forward_frame, htree_forward,
+                       make_dims)
 from .workmodel import level_sizes
 
 
@@ -45,6 +58,18 @@ def _check_parents(parents, B, T, H_kv, TK, CR, MTN, device):
             f"level {l}: parent lists must be ascending"
 
 
+def infer_max_top_nodes(T: int, CR: int, TK: int, L: int) -> int:
+    """A max_top_nodes that gives the context's level count L (for a context
+    without the key): the smallest power of two >= the top level's size is
+    below the level under it, so the level rule stops at the same level."""
+    n = T
+    for _ in range(L - 1):
+        n = -(-n // CR)
+    if L == 1:
+        return TK * CR
+    return 1 << max(0, (n - 1).bit_length())
+
+
 def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_ctx: dict):
     """Gradients of the htree forward wrt q, k, v (fp32), selection fixed.
 
@@ -54,23 +79,30 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
     B, T, H, K = q.shape
     layers_k, layers_v = bwd_ctx["layers_k"], bwd_ctx["layers_v"]
     k, v = layers_k[0], layers_v[0]
+    H_kv, V = k.shape[2], v.shape[3]
+    dev = q.device
+    f32 = dict(dtype=torch.float32, device=dev)
     if B == 0 or T == 0:  # empty inputs: empty gradients, no launch
-        f32 = dict(dtype=torch.float32, device=q.device)
-        return (torch.empty(B, T, H, K, **f32), torch.empty(B, T, k.shape[2], K, **f32),
-                torch.empty(B, T, k.shape[2], K, **f32))
+        return (torch.empty(B, T, H, K, **f32), torch.empty(B, T, H_kv, K, **f32),
+                torch.empty(B, T, H_kv, V, **f32))
+    hf = bwd_ctx.get("head_frame") or HeadFrame(K, V)
     CR = bwd_ctx["compression_rate"]
     TK = bwd_ctx["top_k_per_layer"]
-    MTN = bwd_ctx.get("max_top_nodes", TK * CR)
-    scale = bwd_ctx["scale"]
     L = bwd_ctx["num_layers"]
-    d = bwd_ctx.get("dims")
-    if d is None:
-        d, _ = make_dims(q, k, CR, MTN, TK)
-    ws = bwd_ctx.get("packed_tree")
+    MTN = bwd_ctx.get("max_top_nodes") or infer_max_top_nodes(T, CR, TK, L)
+    scale = bwd_ctx["scale"]
     cos, sin = bwd_ctx["cos_cache"], bwd_ctx["sin_cache"]
-    if ws is None:
-        rope_base = bwd_ctx.get("rope_base", 10000.0)
-        _, _, ws, cos, sin = build_tree(k, v, d, d.rope_rows, rope_base)
+    ws = bwd_ctx.get("packed_tree")
+    d = bwd_ctx.get("dims")
+    if ws is None or d is None:
+        # a context of the reference's keys: the kernels run with its own tables
+        check_tables(cos, sin, K // 2, TK * CR, dev)
+        d = make_dims(B, T, H, H_kv, hf.D, CR, MTN, TK, q.dtype, cos.shape[0])
+        assert len(N.levels(d)) == L, f"num_layers {L} does not match T={T}, CR={CR}, MTN={MTN}"
+        ws = None
+    cos_k, sin_k = hf.tables(cos, sin)
+    q = q.contiguous()
+    qf = hf.pad_qk(q)
     parents = bwd_ctx.get("parents_stacked")
     plp = bwd_ctx.get("per_layer_parents")
     # per_layer_parents (what the reference reads) are views of the forward's
@@ -80,20 +112,21 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
         parents = None
     # the training forward's stored scores go with its own parent lists
     scores = bwd_ctx.get("train_scores") if parents is not None else None
+    if parents is None and plp is not None:
+        parents = _stack_parents(plp, L)
+        _check_parents(parents, B, T, H_kv, TK, CR, MTN, dev)
     if parents is None:
-        if plp is not None:
-            parents = _stack_parents(plp, L)
-            _check_parents(parents, B, T, k.shape[2], TK, CR, MTN, q.device)
-        else:
-            _, ctx2 = htree_forward(q, k, v, CR, MTN, TK, scale, bwd_ctx.get("rope_base", 10000.0),
-                                    _save_for_backward=True, _save_parents=True)
-            parents = ctx2["parents_stacked"]
-    q = q.contiguous()
-    dO = dO.contiguous().to(q.dtype)
-    output = output.contiguous().to(q.dtype)
-    dev = q.device
-    dq = torch.empty(B, T, H, K, dtype=torch.float32, device=dev)
-    dk = torch.empty(B, T, k.shape[2], K, dtype=torch.float32, device=dev)
+        # replay the selection (and keep the replay's scores for this backward)
+        _, _, _, parents, _, _, ws, scores = forward_frame(
+            qf, hf.pad_qk(k.contiguous()), hf.pad_v(v.contiguous()), d, cos_k, sin_k, scale,
+            True, True)
+    elif ws is None:
+        _, _, ws = build_tree(hf.pad_qk(k.contiguous()), hf.pad_v(v.contiguous()), d, cos_k, sin_k)
+    dOf = hf.pad_v(dO.contiguous().to(q.dtype))
+    outf = hf.pad_v(output.contiguous().to(q.dtype))
+    D = hf.D
+    dq = torch.empty(B, T, H, D, **f32)
+    dk = torch.empty(B, T, H_kv, D, **f32)
     dv = torch.empty_like(dk)
     nb = N.ctypes.c_int64()
     N.check(N.lib().htree_backward_workspace_bytes(N.ctypes.byref(d), N.ctypes.byref(nb)),
@@ -108,24 +141,30 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
     with torch.cuda.device(dev):
         if scores is not None:
             rc = N.lib().htree_backward_train(
-                d, float(scale), N.ptr(q), N.ptr(output), N.ptr(dO), N.ptr(bwd_ctx["global_max"]),
-                N.ptr(bwd_ctx["global_sum"]), N.ptr(parents), N.ptr(ws), ws.numel(), N.ptr(cos),
-                N.ptr(sin), N.ptr(scores), scores.numel(), N.ptr(dq), N.ptr(dk), N.ptr(dv),
+                d, float(scale), N.ptr(qf), N.ptr(outf), N.ptr(dOf), N.ptr(bwd_ctx["global_max"]),
+                N.ptr(bwd_ctx["global_sum"]), N.ptr(parents), N.ptr(ws), ws.numel(), N.ptr(cos_k),
+                N.ptr(sin_k), N.ptr(scores), scores.numel(), N.ptr(dq), N.ptr(dk), N.ptr(dv),
                 N.ptr(bws), bws.numel(), N.stream_ptr(dev))
             N.check(rc, "htree_backward_train")
         else:
             rc = N.lib().htree_backward(
-                d, float(scale), N.ptr(q), N.ptr(output), N.ptr(dO), N.ptr(bwd_ctx["global_max"]),
-                N.ptr(bwd_ctx["global_sum"]), N.ptr(parents), N.ptr(ws), ws.numel(), N.ptr(cos),
-                N.ptr(sin), N.ptr(dq), N.ptr(dk), N.ptr(dv), N.ptr(bws), bws.numel(),
+                d, float(scale), N.ptr(qf), N.ptr(outf), N.ptr(dOf), N.ptr(bwd_ctx["global_max"]),
+                N.ptr(bwd_ctx["global_sum"]), N.ptr(parents), N.ptr(ws), ws.numel(), N.ptr(cos_k),
+                N.ptr(sin_k), N.ptr(dq), N.ptr(dk), N.ptr(dv), N.ptr(bws), bws.numel(),
                 N.stream_ptr(dev))
             N.check(rc, "htree_backward")
-    return dq, dk, dv
+    return hf.unpad_qk(dq), hf.unpad_qk(dk), hf.unpad_v(dv)
+
+
+_REF_META = ("num_layers", "compression_rate", "top_k_per_layer", "max_top_nodes", "scale",
+             "rope_base", "NUM_GROUPS", "G_PAD", "TILE_P", "DROP_BLOCK")
 
 
 class HTreeTritonFunction(torch.autograd.Function):
     """Autograd contract of the reference (src/backward.py:1126-1193): grads
-    in the input dtypes and None for the five non-tensor arguments."""
+    in the input dtypes and None for the five non-tensor arguments.  Saves
+    the parent lists, the packed tree and the candidate scores, so that the
+    backward replays nothing."""
 
     @staticmethod
     def forward(ctx, q, k, v, compression_rate, max_top_nodes, top_k_per_layer, scale, rope_base):
@@ -137,17 +176,42 @@ class HTreeTritonFunction(torch.autograd.Function):
                               bwd_ctx["cos_cache"], bwd_ctx["sin_cache"],
                               bwd_ctx["parents_stacked"], bwd_ctx["packed_tree"],
                               bwd_ctx["train_scores"])
-        ctx.meta = dict(num_layers=bwd_ctx["num_layers"], compression_rate=compression_rate,
-                        top_k_per_layer=top_k_per_layer, max_top_nodes=max_top_nodes,
-                        scale=bwd_ctx["scale"], dims=bwd_ctx["dims"], rope_base=rope_base)
+        ctx.meta = {key: bwd_ctx[key] for key in _REF_META}
+        ctx.meta.update(dims=bwd_ctx["dims"], head_frame=bwd_ctx["head_frame"])
         return out
 
     @staticmethod
     def backward(ctx, dO):
         q, k, v, out, gmax, gsum, cos, sin, parents, ws, scores = ctx.saved_tensors
         bwd_ctx = dict(ctx.meta, global_max=gmax, global_sum=gsum, layers_k=[k], layers_v=[v],
-                       cos_cache=cos, sin_cache=sin, parents_stacked=parents, packed_tree=ws,
-                       train_scores=scores)
+                       cos_cache=cos, sin_cache=sin, parents_stacked=parents,
+                       per_layer_parents=None, packed_tree=ws, train_scores=scores)
+        dq, dk, dv = htree_backward(dO, q, out, bwd_ctx)
+        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None
+
+
+class HTreeLeanFunction(torch.autograd.Function):
+    """The reference's memory trade-off (src/backward.py:1130-1171): saves
+    only q, k, v, out, global max / sum and the RoPE tables; the backward
+    rebuilds the tree and replays the selection.  Same contract as
+    HTreeTritonFunction."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, compression_rate, max_top_nodes, top_k_per_layer, scale, rope_base):
+        out, bwd_ctx = htree_forward(q, k, v, compression_rate=compression_rate,
+                                     max_top_nodes=max_top_nodes, top_k_per_layer=top_k_per_layer,
+                                     scale=scale, rope_base=rope_base, _save_for_backward=True,
+                                     _save_parents=False)
+        ctx.save_for_backward(q, k, v, out, bwd_ctx["global_max"], bwd_ctx["global_sum"],
+                              bwd_ctx["cos_cache"], bwd_ctx["sin_cache"])
+        ctx.meta = {key: bwd_ctx[key] for key in _REF_META}
+        return out
+
+    @staticmethod
+    def backward(ctx, dO):
+        q, k, v, out, gmax, gsum, cos, sin = ctx.saved_tensors
+        bwd_ctx = dict(ctx.meta, global_max=gmax, global_sum=gsum, layers_k=[k], layers_v=[v],
+                       cos_cache=cos, sin_cache=sin, per_layer_parents=None)
         dq, dk, dv = htree_backward(dO, q, out, bwd_ctx)
         return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None
 
@@ -158,14 +222,17 @@ HTreeFunction = HTreeTritonFunction
 def htree_forward_triton_autograd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                   compression_rate: int = 16, max_top_nodes: int = 8192,
                                   top_k_per_layer: int = 512, scale: Optional[float] = None,
-                                  rope_base: float = 10000.0) -> torch.Tensor:
+                                  rope_base: float = 10000.0, _save_parents: bool = True
+                                  ) -> torch.Tensor:
     """Differentiable htree forward (name of src/backward.py:1196 kept for
-    drop-in use; the kernels are the HIP ones)."""
+    drop-in use; the kernels are the HIP ones).  `_save_parents=False`
+    selects the lean mode (HTreeLeanFunction): only the reference's eight
+    tensors are kept between forward and backward."""
     if scale is None:
         scale = q.shape[-1] ** -0.5
-    return HTreeTritonFunction.apply(q.contiguous(), k.contiguous(), v.contiguous(),
-                                     compression_rate, max_top_nodes, top_k_per_layer, scale,
-                                     rope_base)
+    fn = HTreeTritonFunction if _save_parents else HTreeLeanFunction
+    return fn.apply(q.contiguous(), k.contiguous(), v.contiguous(), compression_rate, max_top_nodes,
+                    top_k_per_layer, scale, rope_base)
 
 
 htree_forward_autograd = htree_forward_triton_autograd

@@ -28,7 +28,10 @@ __global__ __launch_bounds__(256) void topk_rows_kernel(const float* __restrict_
   const int64_t row = blockIdx.x;
   const float* xr = x + row * n;
   uint32_t key[C];
-  if (tid * C + C <= n) {
+  // 16-byte loads only where the row starts 16-byte aligned (n % 4 == 0 on
+  // an aligned base): rows of other lengths are read element by element
+  const bool vec_ok = ((uintptr_t)xr & 15u) == 0u;
+  if (vec_ok && tid * C + C <= n) {
 #pragma unroll
     for (int i = 0; i < C; i += 4) {
       const float4 f = *(const float4*)(xr + tid * C + i);

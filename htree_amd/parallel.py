@@ -7,18 +7,27 @@ Differences, all deliberate:
     reference asserts equality, src/parallel.py:917); the algorithm never
     relies on equality.  The reference's Triton-tiling asserts
     (top_k % 64 == 0, top_k % compression_rate == 0, :923,1019) do not apply.
-  * limits of this HIP build (AssertionError): head_dim in {32, 64, 128},
-    H / H_kv <= 16, 4 <= compression_rate <= 64, top_k_per_layer <= 512 and
-    top_k_per_layer * compression_rate <= 8192 candidates per level.
+  * limits of this HIP build (AssertionError): max(K, V) in {32, 64, 128}
+    (K even), H / H_kv <= 16, 4 <= compression_rate <= 64,
+    top_k_per_layer <= 512 and top_k_per_layer * compression_rate <= 8192
+    candidates per level.
+  * K != V (the reference carries V = v.shape[-1] apart from K,
+    src/parallel.py:904) runs the kernels at one head dim D = max(K, V):
+    V is zero-padded to D (zero columns add nothing to P.V and come out
+    zero), and for K < V the query / key halves of each RoPE pair are placed
+    at [0, K/2) and [D/2, D/2 + K/2) with zeros between, rotated by tables
+    whose first K/2 columns are the K-dim tables (the zero columns stay zero
+    under any rotation), so every score is the K-dim score.
   * empty inputs (B == 0 or T == 0) give empty outputs (and a bwd_ctx whose
     backward gives empty gradients) without a launch.
   * the RoPE tables are built on the host with the reference's recipe
     (src/parallel.py:983-988) and copied to the device.
-  * bwd_ctx carries extra keys: `packed_tree` (the MFMA operand copy of the
-    tree, reused by the backward), `dims`, `parents_stacked` and
+  * bwd_ctx carries extra keys: `rope_base`, `packed_tree` (the MFMA operand
+    copy of the tree, reused by the backward), `dims`, `parents_stacked`,
     `train_scores` (every candidate tile's scores, fp16 relative to the
     head's running max, so that the backward does not rebuild them; None
-    where the configuration rebuilds them).
+    where the configuration rebuilds them) and `head_frame` (how K and V
+    map onto the kernels' head dim).
 """
 from __future__ import annotations
 
@@ -30,6 +39,8 @@ from . import _native as N
 
 HTREE_SCORE_NEG_INF = -1.0e10            # src/parallel.py:75
 HTREE_SCORE_VALID_THRESHOLD = HTREE_SCORE_NEG_INF * 0.9  # :81
+
+KERNEL_HEAD_DIMS = (32, 64, 128)
 
 _rope_cache: Dict[Tuple, Tuple[torch.Tensor, torch.Tensor]] = {}
 
@@ -48,6 +59,51 @@ def rope_cache(head_dim: int, rows: int, rope_base: float, device) -> Tuple[torc
     return hit
 
 
+class HeadFrame:
+    """Maps the caller's head dims (K for q/k, V for v) onto the kernels' one
+    head dim D = max(K, V).  With K == V every method returns its argument."""
+
+    def __init__(self, K: int, V: int):
+        self.K, self.V = K, V
+        self.D = max(K, V)
+        self.same = K == V
+
+    def pad_qk(self, x: torch.Tensor) -> torch.Tensor:
+        """[..., K] -> [..., D]: RoPE pair halves at [0, K/2) and [D/2, D/2 + K/2)."""
+        if self.K == self.D:
+            return x
+        h, H = self.K // 2, self.D // 2
+        y = x.new_zeros(*x.shape[:-1], self.D)
+        y[..., :h] = x[..., :h]
+        y[..., H:H + h] = x[..., h:]
+        return y
+
+    def unpad_qk(self, x: torch.Tensor) -> torch.Tensor:
+        if self.K == self.D:
+            return x
+        h, H = self.K // 2, self.D // 2
+        return torch.cat([x[..., :h], x[..., H:H + h]], -1)
+
+    def pad_v(self, x: torch.Tensor) -> torch.Tensor:
+        if self.V == self.D:
+            return x
+        return torch.nn.functional.pad(x, (0, self.D - self.V))
+
+    def unpad_v(self, x: torch.Tensor) -> torch.Tensor:
+        if self.V == self.D:
+            return x
+        return x[..., :self.V].contiguous()
+
+    def tables(self, cos: torch.Tensor, sin: torch.Tensor):
+        """K-dim tables [rows, K/2] -> kernel tables [rows, D/2] (identity
+        rotation on the padding columns, which only ever meet zeros)."""
+        if self.K == self.D:
+            return cos, sin
+        pad = self.D // 2 - self.K // 2
+        return (torch.nn.functional.pad(cos, (0, pad), value=1.0).contiguous(),
+                torch.nn.functional.pad(sin, (0, pad), value=0.0).contiguous())
+
+
 def _validate(q, k, v, compression_rate, max_top_nodes, top_k_per_layer):
     assert q.dim() == 4 and k.dim() == 4 and v.dim() == 4, "q/k/v must be rank-4 tensors"
     B, T, H, K = q.shape
@@ -55,7 +111,12 @@ def _validate(q, k, v, compression_rate, max_top_nodes, top_k_per_layer):
     assert H % H_kv == 0, f"H ({H}) must be divisible by H_kv ({H_kv})"
     assert k.shape[2] == v.shape[2], "K and V must have same number of heads"
     assert k.shape[:2] == (B, T) and v.shape[:2] == (B, T), "q/k/v batch and length must match"
-    assert k.shape[3] == K and v.shape[3] == K, "this implementation needs K == V == head_dim"
+    assert k.shape[3] == K, f"q and k must share the head dim K ({K} vs {k.shape[3]})"
+    V = v.shape[3]
+    assert K % 2 == 0 and K > 0 and V > 0, "head dims must be positive, K even (RoPE pairs)"
+    assert max(K, V) in KERNEL_HEAD_DIMS, (
+        f"configuration outside this HIP build: needs max(K, V) in {KERNEL_HEAD_DIMS}, "
+        f"got K={K}, V={V}")
     assert q.dtype == k.dtype == v.dtype, "q, k, v must share one dtype"
     assert (top_k_per_layer & (top_k_per_layer - 1)) == 0, "top_k_per_layer (TOP_K) must be a power of 2"
     assert (compression_rate & (compression_rate - 1)) == 0, "compression_rate must be a power of 2"
@@ -67,29 +128,87 @@ def _validate(q, k, v, compression_rate, max_top_nodes, top_k_per_layer):
     assert q.device == k.device == v.device, "q, k, v must be on one device"
 
 
-def make_dims(q, k, compression_rate, max_top_nodes, top_k_per_layer):
-    B, T, H, K = q.shape
-    rows = max(max_top_nodes + 1024, top_k_per_layer * compression_rate)
-    return N.dims(B, T, H, k.shape[2], K, compression_rate, top_k_per_layer, max_top_nodes,
-                  q.dtype, rows), rows
+def rope_rows_for(max_top_nodes: int, top_k_per_layer: int, compression_rate: int) -> int:
+    """Rows of the RoPE tables: the reference's max_top_nodes + 1024
+    (src/parallel.py:983), and at least every candidate position."""
+    return max(max_top_nodes + 1024, top_k_per_layer * compression_rate)
 
 
-def build_tree(k, v, d, rows, rope_base):
-    """Levels 1..L-1 (input dtype) and the packed operand tree."""
-    B, T, H_kv, K = k.shape
+def make_dims(B, T, H, H_kv, D, compression_rate, max_top_nodes, top_k_per_layer, dtype, rope_rows):
+    return N.dims(B, T, H, H_kv, D, compression_rate, top_k_per_layer, max_top_nodes, dtype,
+                  rope_rows)
+
+
+def check_tables(cos, sin, half: int, rows_min: int, device):
+    """RoPE tables handed in by a caller (a bwd_ctx's cos_cache / sin_cache)
+    go to the kernels as they are: fp32 [rows, half], rows >= rows_min."""
+    for name, t in (("cos_cache", cos), ("sin_cache", sin)):
+        assert t.dtype == torch.float32 and t.dim() == 2 and t.shape[1] == half, \
+            f"{name} must be fp32 [rows, {half}], got {t.dtype} {list(t.shape)}"
+        assert t.shape[0] >= rows_min, \
+            f"{name} has {t.shape[0]} rows; every candidate position needs {rows_min}"
+        assert t.device == device, f"{name} must be on the inputs' device"
+    assert cos.shape == sin.shape, "cos_cache and sin_cache must have one shape"
+
+
+def build_tree(k, v, d, cos, sin):
+    """Levels 1..L-1 (input dtype) and the packed operand tree, with K
+    pre-rotated by the given kernel-frame tables.  k, v are in the kernel
+    frame ([B,T,H_kv,D])."""
+    B, T, H_kv, D = k.shape
     sizes = N.levels(d)
     layers_k, layers_v = [k], [v]
     for n in sizes[1:]:
-        layers_k.append(torch.empty(B, n, H_kv, K, dtype=k.dtype, device=k.device))
-        layers_v.append(torch.empty(B, n, H_kv, K, dtype=v.dtype, device=v.device))
-    cos, sin = rope_cache(K, rows, rope_base, k.device)
+        layers_k.append(torch.empty(B, n, H_kv, D, dtype=k.dtype, device=k.device))
+        layers_v.append(torch.empty(B, n, H_kv, D, dtype=v.dtype, device=v.device))
     ws = torch.empty(N.tree_workspace_bytes(d), dtype=torch.uint8, device=k.device)
     rc = N.lib().htree_tree_build(
         d, N.ptr(k), N.ptr(v), N.ptr_array([None] + layers_k[1:]),
         N.ptr_array([None] + layers_v[1:]), N.ptr(cos), N.ptr(sin), N.ptr(ws), ws.numel(),
         N.stream_ptr(k.device))
     N.check(rc, "htree_tree_build")
-    return layers_k, layers_v, ws, cos, sin
+    return layers_k, layers_v, ws
+
+
+def forward_frame(qf, kf, vf, d, cos_k, sin_k, scale, save_parents, keep_scores):
+    """The HIP forward on kernel-frame tensors.  cos_k / sin_k: the kernel
+    frame's tables.  Returns (out, gmax, gsum, parents | None, layers_k,
+    layers_v, packed tree, scores | None)."""
+    B, T, H, D = qf.shape
+    H_kv = kf.shape[2]
+    dev = qf.device
+    empty = B == 0 or T == 0  # nothing to attend: no tree, no launch
+    with torch.cuda.device(dev):
+        if empty:
+            # the library's limits still apply: checked on one query
+            N.levels(make_dims(1, 1, H, H_kv, D, d.compression_rate, d.max_top_nodes, d.top_k,
+                               qf.dtype, d.rope_rows))
+            layers_k, layers_v = [kf], [vf]
+            ws = torch.empty(0, dtype=torch.uint8, device=dev)
+        else:
+            layers_k, layers_v, ws = build_tree(kf, vf, d, cos_k, sin_k)
+        L = len(layers_k)
+        out = torch.empty_like(qf)
+        gmax = torch.empty(B, T, H, dtype=torch.float32, device=dev)
+        gsum = torch.empty(B, T, H, dtype=torch.float32, device=dev)
+        parents = (torch.empty(L, B, T, H_kv, d.top_k, dtype=torch.int32, device=dev)
+                   if save_parents else None)
+        nsc = N.train_scores_bytes(d) if save_parents and keep_scores and not empty else 0
+        scores = torch.empty(nsc, dtype=torch.uint8, device=dev) if nsc > 0 else None
+        if empty:
+            pass
+        elif scores is not None:
+            rc = N.lib().htree_forward_train(d, float(scale), N.ptr(qf), N.ptr(ws), ws.numel(),
+                                             N.ptr(cos_k), N.ptr(sin_k), N.ptr(out), N.ptr(gmax),
+                                             N.ptr(gsum), N.ptr(parents), N.ptr(scores), nsc,
+                                             N.stream_ptr(dev))
+            N.check(rc, "htree_forward_train")
+        else:
+            rc = N.lib().htree_forward(d, float(scale), N.ptr(qf), N.ptr(ws), ws.numel(),
+                                       N.ptr(cos_k), N.ptr(sin_k), N.ptr(out), N.ptr(gmax),
+                                       N.ptr(gsum), N.ptr(parents), N.stream_ptr(dev))
+            N.check(rc, "htree_forward")
+    return out, gmax, gsum, parents, layers_k, layers_v, ws, scores
 
 
 def htree_forward(
@@ -104,57 +223,39 @@ def htree_forward(
     _save_for_backward: bool = False,
     _save_parents: bool = True,
 ):
-    """htree forward.  q [B,T,H,K], k/v [B,T,H_kv,K] -> output [B,T,H,K]
-    (q.dtype); with _save_for_backward also the bwd_ctx dict."""
+    """htree forward.  q [B,T,H,K], k [B,T,H_kv,K], v [B,T,H_kv,V] ->
+    output [B,T,H,V] (q.dtype); with _save_for_backward also the bwd_ctx dict.
+    With _save_parents (the default, as in the reference) the context holds
+    every level's parent lists and, where the configuration keeps them, the
+    candidate scores for the backward; without it the backward replays the
+    selection (src/backward.py:881-934)."""
     _validate(q, k, v, compression_rate, max_top_nodes, top_k_per_layer)
     B, T, H, K = q.shape
     H_kv = k.shape[2]
+    hf = HeadFrame(K, v.shape[3])
     if scale is None:
         scale = K ** -0.5
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-    d, rows = make_dims(q, k, compression_rate, max_top_nodes, top_k_per_layer)
-    empty = B == 0 or T == 0  # nothing to attend: no tree, no launch
-    with torch.cuda.device(q.device):
-        if empty:
-            # the library's limits still apply: checked on one query
-            N.levels(N.dims(1, 1, H, H_kv, K, compression_rate, top_k_per_layer, max_top_nodes,
-                            q.dtype, rows))
-            layers_k, layers_v = [k], [v]
-            ws = torch.empty(0, dtype=torch.uint8, device=q.device)
-            cos, sin = rope_cache(K, rows, rope_base, q.device)
-        else:
-            layers_k, layers_v, ws, cos, sin = build_tree(k, v, d, rows, rope_base)
-        L = len(layers_k)
-        out = torch.empty_like(q)
-        gmax = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
-        gsum = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
-        save_par = _save_for_backward and _save_parents
-        parents = (torch.empty(L, B, T, H_kv, top_k_per_layer, dtype=torch.int32, device=q.device)
-                   if save_par else None)
-        nsc = N.train_scores_bytes(d) if save_par and not empty else 0
-        scores = torch.empty(nsc, dtype=torch.uint8, device=q.device) if nsc > 0 else None
-        if empty:
-            pass
-        elif scores is not None:
-            rc = N.lib().htree_forward_train(d, float(scale), N.ptr(q), N.ptr(ws), ws.numel(),
-                                             N.ptr(cos), N.ptr(sin), N.ptr(out), N.ptr(gmax),
-                                             N.ptr(gsum), N.ptr(parents), N.ptr(scores), nsc,
-                                             N.stream_ptr(q.device))
-            N.check(rc, "htree_forward_train")
-        else:
-            rc = N.lib().htree_forward(d, float(scale), N.ptr(q), N.ptr(ws), ws.numel(),
-                                       N.ptr(cos), N.ptr(sin), N.ptr(out), N.ptr(gmax),
-                                       N.ptr(gsum), N.ptr(parents), N.stream_ptr(q.device))
-            N.check(rc, "htree_forward")
+    rows = rope_rows_for(max_top_nodes, top_k_per_layer, compression_rate)
+    d = make_dims(B, T, H, H_kv, hf.D, compression_rate, max_top_nodes, top_k_per_layer, q.dtype,
+                  rows)
+    cos, sin = rope_cache(K, rows, rope_base, q.device)
+    cos_k, sin_k = hf.tables(cos, sin)
+    save_par = _save_for_backward and _save_parents
+    out_f, gmax, gsum, parents, lk, lv, ws, scores = forward_frame(
+        hf.pad_qk(q), hf.pad_qk(k), hf.pad_v(v), d, cos_k, sin_k, scale, save_par, True)
+    out = hf.unpad_v(out_f)
     if not _save_for_backward:
         return out
+    L = len(lk)
     G = H // H_kv
     bwd_ctx = dict(
         global_max=gmax,
         global_sum=gsum,
         per_layer_parents={l: parents[l] for l in range(L)} if save_par else None,
-        layers_k=layers_k,
-        layers_v=layers_v,
+        # the caller's frame: layers_k[0] is k (src/parallel.py:949)
+        layers_k=[k] + [hf.unpad_qk(x) for x in lk[1:]] if not hf.same else lk,
+        layers_v=[v] + [hf.unpad_v(x) for x in lv[1:]] if not hf.same else lv,
         cos_cache=cos,
         sin_cache=sin,
         num_layers=L,
@@ -166,10 +267,12 @@ def htree_forward(
         G_PAD=max(1 << (G - 1).bit_length(), 16),
         TILE_P=4,
         DROP_BLOCK=64,
+        rope_base=rope_base,
         packed_tree=ws,
         dims=d,
         parents_stacked=parents,
         train_scores=scores,
+        head_frame=hf,
     )
     return out, bwd_ctx
 

@@ -11,7 +11,7 @@ level.  The trace dict has the reference's layout:
   {"num_layers": L, "num_groups": G, "layers": {l: LayerTrace}}
 with, per level l: the parent list the level selected for level l-1
 ([B,T,H_kv,TK] int32, ascending, -1 padded; None at the bottom), and the
-level's own max / sum [B,T,H] and unnormalised output [B,T,H,D] in fp32
+level's own max / sum [B,T,H] and unnormalised output [B,T,H,V] in fp32
 (-1e10 / 0 / 0 where the level accumulated nothing).
 """
 from __future__ import annotations
@@ -22,7 +22,7 @@ from typing import Dict, List, Optional, Tuple
 import torch
 
 from . import _native as N
-from .parallel import _validate, build_tree, make_dims
+from .parallel import (HeadFrame, _validate, build_tree, make_dims, rope_cache, rope_rows_for)
 
 
 @dataclass
@@ -44,32 +44,38 @@ def run_parallel_with_trace(
     scale: Optional[float],
     rope_base: float,
 ) -> Tuple[torch.Tensor, Dict]:
-    """Forward with the per-level trace.  Returns (output [B,T,H,D] in
+    """Forward with the per-level trace.  Returns (output [B,T,H,V] in
     q.dtype, trace dict); output, global max and sum are the merge of the
     traced level states (src/naive.py:215-231)."""
     _validate(q, k, v, compression_rate, max_top_nodes, top_k_per_layer)
     B, T, H, K = q.shape
     H_kv = k.shape[2]
+    hf = HeadFrame(K, v.shape[3])
     if scale is None:
         scale = K ** -0.5
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-    d, rows = make_dims(q, k, compression_rate, max_top_nodes, top_k_per_layer)
+    rows = rope_rows_for(max_top_nodes, top_k_per_layer, compression_rate)
+    d = make_dims(B, T, H, H_kv, hf.D, compression_rate, max_top_nodes, top_k_per_layer, q.dtype,
+                  rows)
     dev = q.device
     with torch.cuda.device(dev):
-        layers_k, layers_v, ws, cos, sin = build_tree(k, v, d, rows, rope_base)
+        cos, sin = hf.tables(*rope_cache(K, rows, rope_base, dev))
+        qf = hf.pad_qk(q)
+        layers_k, layers_v, ws = build_tree(hf.pad_qk(k), hf.pad_v(v), d, cos, sin)
         L = len(layers_k)
-        out = torch.empty_like(q)
+        out = torch.empty_like(qf)
         gmax = torch.empty(B, T, H, dtype=torch.float32, device=dev)
         gsum = torch.empty(B, T, H, dtype=torch.float32, device=dev)
         parents = torch.empty(L, B, T, H_kv, top_k_per_layer, dtype=torch.int32, device=dev)
         lmax = torch.empty(L, B, T, H, dtype=torch.float32, device=dev)
         lsum = torch.empty(L, B, T, H, dtype=torch.float32, device=dev)
-        lout = torch.empty(L, B, T, H, K, dtype=torch.float32, device=dev)
-        rc = N.lib().htree_forward_trace(d, float(scale), N.ptr(q), N.ptr(ws), ws.numel(),
+        lout = torch.empty(L, B, T, H, hf.D, dtype=torch.float32, device=dev)
+        rc = N.lib().htree_forward_trace(d, float(scale), N.ptr(qf), N.ptr(ws), ws.numel(),
                                          N.ptr(cos), N.ptr(sin), N.ptr(out), N.ptr(gmax),
                                          N.ptr(gsum), N.ptr(parents), N.ptr(lmax), N.ptr(lsum),
                                          N.ptr(lout), N.stream_ptr(dev))
         N.check(rc, "htree_forward_trace")
+        out, lout = hf.unpad_v(out), hf.unpad_v(lout)
     layers = {
         l: LayerTrace(layer_idx=l,
                       selected_parents=parents[l - 1] if l > 0 else None,

@@ -42,9 +42,12 @@ enum htree_status {
                               algorithm's rules (powers of two,
                               max_top_nodes <= top_k * compression_rate) */
   HTREE_EUNSUPPORTED = -4, /* legal for the reference, outside this build:
-                              D not in {64,128}, G = H/H_kv > 16,
+                              D not in {32, 64, 128}, G = H/H_kv > 16,
                               compression_rate outside [4, 64],
-                              top_k * max(CR,16) / 16 > 64 */
+                              top_k > 512, top_k * compression_rate > 8192,
+                              more than HTREE_MAX_LEVELS levels, or a
+                              backward level of 2^31 or more entries
+                              (B * T * H_kv * min(top_k, parents)) */
   HTREE_EWORKSPACE = -5    /* workspace too small */
 };
 

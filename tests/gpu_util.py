@@ -48,7 +48,7 @@ def close(a: np.ndarray, b: np.ndarray, dtype: str):
 
 
 def check_forward(q, k, v, CR, TK, MTN, dtype, rows=None, out_dev=None, parents_dev=None,
-                  tree=None):
+                  tree=None, gmax_dev=None, gsum_dev=None):
     """Checks a device forward (out [B,T,H,D], parents [L,B,T,Hkv,TK]) against
     the oracle on `rows` ([n,2] of (b,t); default all), teacher-forced on the
     device's parent lists.  Returns a report dict; raises AssertionError on a
@@ -75,6 +75,27 @@ def check_forward(q, k, v, CR, TK, MTN, dtype, rows=None, out_dev=None, parents_
     ok, worst = close(got, fw["out"], dtype)
     rep["out_worst"] = worst
     assert ok, f"output outside tolerance: worst {worst:.3f} of the bar"
+    if gmax_dev is not None:
+        rep.update(check_state(gmax_dev[rows[:, 0], rows[:, 1]], gsum_dev[rows[:, 0], rows[:, 1]],
+                               fw["gmax"], fw["gsum"], dtype))
+    return rep
+
+
+# online-softmax state bars: the max is one score, |err| <= atol + rtol |max|
+# (16-bit inputs: the split-bf16 score product); the sum's relative error
+# follows the scores' (exp(s - max) moves by the score error)
+STATE_TOL = {"bfloat16": (2e-3, 1e-3, 3e-3), "float16": (2e-3, 1e-3, 3e-3),
+             "float32": (1e-4, 1e-4, 2e-4)}
+
+
+def check_state(gmax, gsum, ref_max, ref_sum, dtype):
+    """gmax / gsum [n, H] of the device against the oracle's: the max over
+    the accumulated candidates and the sum of exp(s - max) over them."""
+    atol, rtol, srtol = STATE_TOL[dtype]
+    gm = np.abs(gmax.astype(np.float64) - ref_max) / (atol + rtol * np.abs(ref_max))
+    gs = np.abs(gsum.astype(np.float64) - ref_sum) / (srtol * np.abs(ref_sum))
+    rep = dict(gmax_worst=float(gm.max()), gsum_worst=float(gs.max()))
+    assert rep["gmax_worst"] <= 1 and rep["gsum_worst"] <= 1, rep
     return rep
 
 
@@ -94,13 +115,15 @@ def oracle_grads(q, k, v, dO, CR, TK, MTN, dtype, parents_dev, out_dev, tree=Non
     par = np.ascontiguousarray(parents_dev.reshape(L, B * T, *parents_dev.shape[3:]))
     fw = orc.forward(q.float().numpy(), tree, D ** -0.5, rows=rows, forced=par)
     bw = orc.backward(q.float().numpy(), tree, D ** -0.5, parents_dev, fw["gmax"].reshape(B, T, H),
-                      fw["gsum"].reshape(B, T, H), out_dev.reshape(B, T, H, D), dO.float().numpy())
+                      fw["gsum"].reshape(B, T, H), out_dev.reshape(B, T, H, -1), dO.float().numpy())
     return bw, fw
 
 
 def check_backward(q, k, v, dO, CR, TK, MTN, dtype, out_dev, parents_dev, gmax_dev, gsum_dev,
-                   dq, dk, dv, tree=None):
+                   dq, dk, dv, tree=None, rope_base=10000.0):
     """Device grads (fp32 numpy) vs the oracle's, same selection; bar as TOL."""
+    if tree is None:
+        tree = orc.Tree(k.float().numpy(), v.float().numpy(), CR, MTN, TK, dtype, rope_base)
     bw, _ = oracle_grads(q, k, v, dO, CR, TK, MTN, dtype, parents_dev, out_dev, tree)
     rep = {}
     for name, got, ref in (("dq", dq, bw["dq"]), ("dk", dk, bw["dk"]), ("dv", dv, bw["dv"])):
@@ -108,4 +131,71 @@ def check_backward(q, k, v, dO, CR, TK, MTN, dtype, out_dev, parents_dev, gmax_d
         rep[name] = worst
         assert np.all(np.isfinite(got)), f"{name} not finite"
         assert ok, f"{name} outside tolerance: worst {worst:.3f} of the bar"
+    return rep
+
+
+def dkv_nodes_for_pair(tree, par_bh, T, CR, rng, n_random=8):
+    """Level-0 nodes to check in one (b, h_kv): the children (up to 16,
+    always the last) of a random level-1 parent and of the last one, plus
+    random nodes; level-1 is the pooled parent of CR level-0 nodes."""
+    L = tree.L
+    nodes = set(rng.choice(T, min(T, n_random), replace=False).tolist())
+    if L > 1:
+        P0 = -(-T // CR)
+        for p in (int(rng.integers(0, max(1, P0 - 1))), P0 - 1):
+            kids = list(range(p * CR, min(p * CR + CR, T)))
+            pick = kids if len(kids) <= 16 else sorted(
+                set(rng.choice(kids[:-1], 15, replace=False).tolist()) | {kids[-1]})
+            nodes |= set(pick)
+    nodes |= {0, T - 1}
+    return np.array(sorted(nodes), np.int64)
+
+
+def check_dkv_sampled(q, dO, out, k, v, parents, gmax, gsum, dk, dv, CR, TK, MTN, dtype, pairs,
+                      seed, scale=None):
+    """Final dk / dv of the device at sampled level-0 nodes of the (b, h_kv)
+    pairs listed, against the oracle's per-level terms combined with the
+    mean-pool factors (src/naive.py:365-394), at the bar of `dtype`.
+
+    The backward is a function of (q, k, v, dO, out, gmax, gsum, parents)
+    (src/backward.py:941-1119): the oracle gets the device's forward state for
+    those, so this checks the backward kernels alone; the forward state is
+    checked against the oracle separately.  Arguments may be device tensors
+    or host arrays ([B,T,H,D], [B,T,Hkv,D], [L,B,T,Hkv,TK], [B,T,H])."""
+    tnp = lambda x, *ix: (x[ix].float().cpu().numpy() if hasattr(x, "cpu")
+                          else np.asarray(x[ix], np.float32))
+    B, T, H, D = q.shape
+    Hkv = k.shape[2]
+    G = H // Hkv
+    if scale is None:
+        scale = D ** -0.5
+    rng = np.random.default_rng(seed)
+    rep = {}
+    for (b, h) in pairs:
+        hs = slice(h * G, (h + 1) * G)
+        qs = tnp(q, slice(b, b + 1), slice(None), hs)
+        dOs = tnp(dO, slice(b, b + 1), slice(None), hs)
+        os_ = tnp(out, slice(b, b + 1), slice(None), hs)
+        dl = (os_.astype(np.float64) * dOs).sum(-1).astype(np.float32)
+        gm = tnp(gmax, slice(b, b + 1), slice(None), hs)
+        gs = tnp(gsum, slice(b, b + 1), slice(None), hs)
+        ks = tnp(k, slice(b, b + 1), slice(None), slice(h, h + 1))
+        vs = tnp(v, slice(b, b + 1), slice(None), slice(h, h + 1))
+        ps = parents[:, b:b + 1, :, h:h + 1]
+        ps = np.ascontiguousarray(ps.cpu().numpy() if hasattr(ps, "cpu") else ps, np.int32)
+        tree = orc.Tree(ks, vs, CR, MTN, TK, dtype)
+        nodes = dkv_nodes_for_pair(tree, ps, T, CR, rng)
+        tg = np.stack([np.zeros_like(nodes), np.zeros_like(nodes), nodes], 1)
+        rk, rv = orc.final_dkv_level0(qs, tree, scale, ps, gm, gs, dl, dOs, tg)
+        ix = torch.from_numpy(nodes) if hasattr(dk, "cpu") else nodes
+        gk = dk[b, ix.to(dk.device) if hasattr(dk, "cpu") else ix, h]
+        gv = dv[b, ix.to(dv.device) if hasattr(dv, "cpu") else ix, h]
+        gk = gk.float().cpu().numpy() if hasattr(gk, "cpu") else np.asarray(gk)
+        gv = gv.float().cpu().numpy() if hasattr(gv, "cpu") else np.asarray(gv)
+        okk, wk = close(gk, rk, dtype)
+        okv, wv = close(gv, rv, dtype)
+        rep[(b, h)] = dict(nodes=len(nodes), dk=wk, dv=wv)
+        assert np.abs(rk).max() > 0 and np.abs(rv).max() > 0
+        assert okk, f"dk at ({b}, {h}) outside tolerance: worst {wk:.3f} of the bar"
+        assert okv, f"dv at ({b}, {h}) outside tolerance: worst {wv:.3f} of the bar"
     return rep

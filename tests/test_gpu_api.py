@@ -1,0 +1,148 @@
+"""GPU parity of the drop-in's other entry paths, against the CPU oracle:
+
+* a bwd_ctx holding exactly the reference's keys (src/parallel.py:1139-1158),
+  made at a non-default rope_base: the backward rebuilds the operand tree and
+  (without per_layer_parents) replays the selection with the context's own
+  RoPE tables, as src/backward.py:848-934 does;
+* the lean autograd mode (only the reference's eight saved tensors,
+  src/backward.py:1141-1145): the same gradients as the default mode;
+* K != V head dims (src/parallel.py:904, src/naive.py:144): forward and
+  backward against the oracle's native two-dim restatement."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from tests.gpu_util import DT, check_backward, check_forward, close
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+REF_KEYS = ("global_max", "global_sum", "per_layer_parents", "layers_k", "layers_v", "cos_cache",
+            "sin_cache", "num_layers", "compression_rate", "top_k_per_layer", "max_top_nodes",
+            "scale", "NUM_GROUPS", "G_PAD", "TILE_P", "DROP_BLOCK")
+
+
+def seeded(B, T, H, Hkv, K, V, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=g).to(DT[dtype])
+    return r(B, T, H, K), r(B, T, Hkv, K), r(B, T, Hkv, V), r(B, T, H, V)
+
+
+@pytest.mark.parametrize("with_parents", [True, False], ids=["parents", "replay"])
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+def test_reference_keys_context(with_parents, dtype):
+    import htree_amd
+
+    B, T, H, Hkv, D, CR, TK, MTN, base = 1, 2000, 16, 2, 64, 16, 16, 128, 500.0
+    print(f"case ref-keys ctx {dtype} parents={with_parents}", flush=True)
+    q, k, v, dO = seeded(B, T, H, Hkv, D, D, dtype, 51)
+    qd, kd, vd, dOd = (x.to(DEV) for x in (q, k, v, dO))
+    out, ctx = htree_amd.htree_forward(qd, kd, vd, CR, MTN, TK, rope_base=base,
+                                       _save_for_backward=True)
+    full = htree_amd.htree_backward(dOd, qd, out, ctx)
+    ref_ctx = {key: ctx[key] for key in REF_KEYS}
+    if not with_parents:
+        ref_ctx["per_layer_parents"] = None
+    got = htree_amd.htree_backward(dOd, qd, out, ref_ctx)
+    torch.cuda.synchronize()
+    par = ctx["parents_stacked"].cpu().numpy()
+    f = lambda x: x.float().cpu().numpy()
+    tree = orc.Tree(k.float().numpy(), v.float().numpy(), CR, MTN, TK, dtype, base)
+    rep = check_backward(q, k, v, dO, CR, TK, MTN, dtype, f(out), par, f(ctx["global_max"]),
+                         f(ctx["global_sum"]), *[f(x) for x in got], tree=tree)
+    print(rep, flush=True)
+    if not with_parents:
+        # the replay selects the same lists (and keeps the same scores)
+        for a, b in zip(got, full):
+            assert torch.equal(a, b)
+    # the forward at this base is the oracle's at this base, not at 10000
+    rows = orc.all_rows(B, T)[::3]
+    check_forward(q, k, v, CR, TK, MTN, dtype, rows=rows, out_dev=f(out), parents_dev=par, tree=tree,
+                  gmax_dev=f(ctx["global_max"]), gsum_dev=f(ctx["global_sum"]))
+    tree0 = orc.Tree(k.float().numpy(), v.float().numpy(), CR, MTN, TK, dtype)
+    with pytest.raises(AssertionError):
+        check_forward(q, k, v, CR, TK, MTN, dtype, rows=rows, out_dev=f(out), parents_dev=par,
+                      tree=tree0)
+
+
+def test_reference_keys_context_without_max_top_nodes():
+    """A context without max_top_nodes (it is not among the keys the
+    reference's backward reads) still resolves the tree's levels."""
+    import htree_amd
+
+    B, T, H, Hkv, D, CR, TK, MTN = 1, 3000, 8, 1, 64, 8, 16, 64
+    q, k, v, dO = (x.to(DEV) for x in seeded(B, T, H, Hkv, D, D, "bfloat16", 52))
+    out, ctx = htree_amd.htree_forward(q, k, v, CR, MTN, TK, _save_for_backward=True)
+    a = htree_amd.htree_backward(dO, q, out, dict(ctx, train_scores=None))
+    ref_ctx = {key: ctx[key] for key in REF_KEYS if key != "max_top_nodes"}
+    b = htree_amd.htree_backward(dO, q, out, ref_ctx)
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_lean_autograd_mode(dtype):
+    """_save_parents=False keeps the reference's eight tensors and replays
+    the selection in the backward: bitwise the default mode's gradients."""
+    import htree_amd
+
+    B, T, H, Hkv, D, CR, TK, MTN = 1, 2500, 16, 2, 128, 16, 16, 128
+    q, k, v, dO = seeded(B, T, H, Hkv, D, D, dtype, 53)
+    grads = []
+    for save in (True, False):
+        qg, kg, vg = (x.to(DEV).requires_grad_(True) for x in (q, k, v))
+        out = htree_amd.htree_forward_triton_autograd(qg, kg, vg, CR, MTN, TK, rope_base=2000.0,
+                                                      _save_parents=save)
+        n_saved = len(out.grad_fn.saved_tensors)
+        assert n_saved == (11 if save else 8), n_saved
+        out.backward(dO.to(DEV))
+        torch.cuda.synchronize()
+        grads.append((out.detach(), qg.grad, kg.grad, vg.grad))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
+
+
+KV_CASES = [
+    # B, T, H, Hkv, K, V, CR, TK, MTN, dtype, seed
+    (1, 2000, 16, 2, 128, 64, 16, 16, 128, "bfloat16", 61),
+    (1, 1500, 8, 1, 64, 128, 16, 8, 128, "bfloat16", 62),
+    (1, 1200, 8, 2, 32, 64, 8, 16, 128, "float32", 63),
+    (2, 900, 4, 1, 64, 32, 4, 32, 64, "float16", 64),
+]
+
+
+@pytest.mark.parametrize("cfg", KV_CASES, ids=lambda c: f"K{c[4]}V{c[5]}cr{c[6]}{c[9]}")
+def test_separate_value_dim(cfg):
+    import htree_amd
+
+    B, T, H, Hkv, K, V, CR, TK, MTN, dtype, seed = cfg
+    print(f"case {cfg}", flush=True)
+    q, k, v, dO = seeded(B, T, H, Hkv, K, V, dtype, seed)
+    qd, kd, vd = (x.to(DEV) for x in (q, k, v))
+    out, par, gmax, gsum, ctx = htree_amd.htree_forward_parents(qd, kd, vd, CR, MTN, TK)
+    assert out.shape == (B, T, H, V) and out.dtype == q.dtype
+    assert ctx["layers_k"][0] is kd and ctx["layers_v"][0] is vd
+    assert all(x.shape[-1] == K for x in ctx["layers_k"]) and all(x.shape[-1] == V for x in ctx["layers_v"])
+    dq, dk, dv = htree_amd.htree_backward(dO.to(DEV), qd, out, ctx)
+    torch.cuda.synchronize()
+    assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape
+    f = lambda x: x.float().cpu().numpy()
+    tree = orc.Tree(k.float().numpy(), v.float().numpy(), CR, MTN, TK, dtype)
+    for l in range(1, tree.L):  # the caller-frame levels are the oracle's, bit for bit
+        assert np.array_equal(f(ctx["layers_k"][l]), tree.lk[l]) and np.array_equal(f(ctx["layers_v"][l]), tree.lv[l])
+    par = par.cpu().numpy()
+    rep = check_forward(q, k, v, CR, TK, MTN, dtype, out_dev=f(out), parents_dev=par, tree=tree,
+                        gmax_dev=f(gmax), gsum_dev=f(gsum))
+    rep.update(check_backward(q, k, v, dO, CR, TK, MTN, dtype, f(out), par, f(gmax), f(gsum), f(dq),
+                              f(dk), f(dv), tree=tree))
+    print(rep, flush=True)
+    # the autograd path at K != V, lean and default: same gradients
+    for save in (True, False):
+        qg, kg, vg = (x.clone().requires_grad_(True) for x in (qd, kd, vd))
+        o = htree_amd.htree_forward_triton_autograd(qg, kg, vg, CR, MTN, TK, _save_parents=save)
+        o.backward(dO.to(DEV))
+        for got, ref in ((qg.grad, dq), (kg.grad, dk), (vg.grad, dv)):
+            ok, w = close(f(got), f(ref.to(got.dtype)), dtype)
+            assert ok, w

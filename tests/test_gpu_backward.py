@@ -9,7 +9,8 @@ import pytest
 import torch
 
 from oracle import oracle as orc
-from tests.gpu_util import check_backward, close, inputs, skewed_inputs
+from tests.gpu_util import (check_backward, check_dkv_sampled, check_forward, close, inputs,
+                            skewed_inputs)
 from tests.helpers import load_golden
 
 pytestmark = pytest.mark.gpu
@@ -48,6 +49,9 @@ CASES = [
     (1, 1100, 8, 1, 128, 32, 8, 256, "float16", 17),   # CR 32, fp16 (split dS, shared staging)
     (1, 4096, 8, 2, 64, 16, 16, 16, "bfloat16", 18),   # 16-node top level: accumulates nothing
     (2, 3000, 8, 1, 64, 16, 16, 16, "float32", 19),
+    # 750 level-0 parents > 128 * top_k: a sparse level, whose bitmap is set
+    # by atomics (bitmap_set_kernel); five levels
+    (1, 3000, 8, 1, 64, 4, 4, 16, "bfloat16", 20),
 ]
 
 
@@ -116,12 +120,15 @@ def test_backward_matches_reference_golden(name):
 
 
 def test_backward_training_shape_c3():
-    """The C3 workload (B=4, T=16384, Hq=32, Hkv=4, D=128, bf16): dq on sampled
-    rows vs the oracle; sum over nodes of dv equals sum over the group's
-    queries and heads of dO (pooling conserves mass, P sums to 1)."""
+    """The C3 workload (B=4, T=16384, Hq=32, Hkv=4, D=128, bf16): the forward
+    (selection, output, gmax, gsum) and dq on sampled rows vs the oracle,
+    final dk / dv at sampled level-0 nodes of two (b, h_kv) pairs; sum over
+    nodes of dv equals sum over the group's queries and heads of dO (pooling
+    conserves mass, P sums to 1)."""
     B, T, H, Hkv, D, CR, TK, MTN = 4, 16384, 32, 4, 128, 16, 16, 128
     q, k, v, dO = inputs(B, T, H, Hkv, D, "bfloat16", 31, dO=True)
     out, par, gmax, gsum, dq, dk, dv = run(q, k, v, dO, CR, TK, MTN)
+    print("device forward + backward done", flush=True)
     assert np.all(np.isfinite(dq)) and np.all(np.isfinite(dk)) and np.all(np.isfinite(dv))
     G = H // Hkv
     dOf = dO.float().numpy().reshape(B, T, Hkv, G, D).astype(np.float64)
@@ -143,6 +150,13 @@ def test_backward_training_shape_c3():
     ok, worst = close(dq[rows[:, 0], rows[:, 1]], ref, "bfloat16")
     print("c3 dq worst", worst, flush=True)
     assert ok
+    rep = check_forward(q, k, v, CR, TK, MTN, "bfloat16", rows=rows, out_dev=out, parents_dev=par,
+                        tree=tree, gmax_dev=gmax, gsum_dev=gsum)
+    print("c3 forward", rep, flush=True)
+    rep = check_dkv_sampled(q.float().numpy(), dO.float().numpy(), out, k.float().numpy(),
+                            v.float().numpy(), par, gmax, gsum, dk, dv, CR, TK, MTN, "bfloat16",
+                            [(0, 0), (B - 1, Hkv - 1)], 33)
+    print("c3 dk/dv at sampled nodes", rep, flush=True)
 
 
 def test_backward_deterministic():
@@ -209,7 +223,8 @@ def test_backward_wide_matches_oracle(cfg):
 
 def test_backward_reference_default_regime():
     """correctness_test_bwd.py defaults (T=12000, Hq=16, Hkv=4, K=V=32, fp32,
-    CR=16, top_k=512, MTN=8192): dq on sampled rows vs the oracle; the sum
+    CR=16, top_k=512, MTN=8192): dq on sampled rows and final dk / dv at
+    sampled level-0 nodes vs the oracle; the sum
     of dv over the nodes equals the sum of dO over the group's queries and
     heads (every head's probabilities sum to 1, the pooling backward keeps
     sums)."""
@@ -236,6 +251,10 @@ def test_backward_reference_default_regime():
     ok, worst = close(dq[rows[:, 0], rows[:, 1]], ref, "float32")
     print("default-regime dq worst", worst, flush=True)
     assert ok
+    rep = check_dkv_sampled(q.float().numpy(), dO.float().numpy(), out, k.float().numpy(),
+                            v.float().numpy(), par, gmax, gsum, dk, dv, CR, TK, MTN, "float32",
+                            [(0, 0), (0, Hkv - 1)], 44)
+    print("default-regime dk/dv at sampled nodes", rep, flush=True)
 
 
 @pytest.mark.parametrize("cfg", [(1, 1500, 16, 2, 128, 16, 16, 128, "bfloat16", 61),

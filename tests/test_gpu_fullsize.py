@@ -5,7 +5,9 @@ oracle, teacher-forced on the device's parent lists, plus size-independent
 properties over every row: the parent lists' closed-form lengths, ascending
 order and forced rightmost child, and the mass of dV (pooling conserves it and
 every P row sums to 1, so the sum of dV over all nodes equals the sum of dO
-over the group's queries and heads).
+over the group's queries and heads); and final dK / dV at sampled level-0
+nodes of two (b, h_kv) pairs (every query that accumulates them or their
+ancestors), against the oracle's per-level terms and the pooling factors.
 
 Inputs are drawn on the device (seeded) so that a test fits its time limit;
 the oracle gets K and V whole and Q/dO only at the sampled rows (it reads no
@@ -15,7 +17,7 @@ import pytest
 import torch
 
 from oracle import oracle as orc
-from tests.gpu_util import DT, check_forward, close
+from tests.gpu_util import DT, check_dkv_sampled, check_forward, close
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -80,11 +82,16 @@ def run_case(q, k, v, dO, CR, TK, MTN, nrows, seed):
     want = dO.reshape(B, T, Hkv, H // Hkv, D).to(torch.float64).sum(dim=(1, 3)).cpu().numpy()
     got = dv.to(torch.float64).sum(dim=1).cpu().numpy()
     np.testing.assert_allclose(got, want, rtol=1e-3, atol=1e-3 * np.sqrt(T * H / Hkv))
-    del dk, dv, ctx
+    del ctx
     torch.cuda.empty_cache()
     par = par.cpu().numpy()
     lists_invariants(par, T, CR, TK)
     print("parent-list invariants hold", flush=True)
+    rep = check_dkv_sampled(q, dO, out, k, v, par, gmax, gsum, dk, dv, CR, TK, MTN, "bfloat16",
+                            [(0, 0), (B - 1, Hkv - 1)], seed)
+    print("dk/dv at sampled level-0 nodes:", rep, flush=True)
+    del dk, dv
+    torch.cuda.empty_cache()
     rng = np.random.default_rng(seed)
     rows = np.stack([rng.integers(0, B, nrows), np.sort(rng.choice(T, nrows, replace=False))],
                     1).astype(np.int32)
@@ -100,8 +107,13 @@ def run_case(q, k, v, dO, CR, TK, MTN, nrows, seed):
     # hold those rows in place
     out_s = np.zeros((B, T, H, D), np.float32)
     out_s[rows[:, 0], rows[:, 1]] = out_r
+    gm_s = np.zeros((B, T, H), np.float32)
+    gs_s = np.ones((B, T, H), np.float32)
+    gm_s[rows[:, 0], rows[:, 1]] = gmax[idx[:, 0], idx[:, 1]].cpu().numpy()
+    gs_s[rows[:, 0], rows[:, 1]] = gsum[idx[:, 0], idx[:, 1]].cpu().numpy()
     rep = check_forward(torch.from_numpy(qn), k[:, :1, :, :1], None, CR, TK, MTN, "bfloat16",
-                        rows=rows, out_dev=out_s, parents_dev=par, tree=tree)
+                        rows=rows, out_dev=out_s, parents_dev=par, tree=tree, gmax_dev=gm_s,
+                        gsum_dev=gs_s)
     pr = par[:, rows[:, 0], rows[:, 1]]
     fw = orc.forward(qn, tree, D ** -0.5, rows=rows, forced=pr)
     d = dOn[rows[:, 0], rows[:, 1]]
