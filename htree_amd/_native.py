@@ -22,6 +22,7 @@ HTREE_ESHAPE = -2
 HTREE_ECONFIG = -3
 HTREE_EUNSUPPORTED = -4
 HTREE_EWORKSPACE = -5
+HTREE_ESCRATCH = -6
 
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
@@ -31,7 +32,8 @@ EXPORTS = (
     "htree_forward", "htree_backward_workspace_bytes", "htree_backward_workspace_min_bytes",
     "htree_backward",
     "htree_train_scores_bytes", "htree_forward_train", "htree_backward_train",
-    "htree_forward_trace", "htree_topk_rows",
+    "htree_forward_trace", "htree_topk_rows", "htree_backward_noalloc_bytes",
+    "htree_backward_noalloc",
 )
 
 
@@ -87,6 +89,12 @@ def lib() -> ctypes.CDLL:
         L.htree_backward_workspace_min_bytes.argtypes = [DP, ctypes.POINTER(I64)]
         L.htree_backward.restype = ctypes.c_int
         L.htree_backward.argtypes = [DP, F, P, P, P, P, P, P, P, I64, P, P, P, P, P, P, I64, P]
+    if hasattr(L, "htree_backward_noalloc"):
+        L.htree_backward_noalloc_bytes.restype = ctypes.c_int
+        L.htree_backward_noalloc_bytes.argtypes = [DP, ctypes.POINTER(I64)]
+        L.htree_backward_noalloc.restype = ctypes.c_int
+        L.htree_backward_noalloc.argtypes = [DP, F, P, P, P, P, P, P, P, I64, P, P, P, I64, P, P,
+                                             P, P]
     if hasattr(L, "htree_backward_train"):
         L.htree_backward_train.restype = ctypes.c_int
         L.htree_backward_train.argtypes = [DP, F, P, P, P, P, P, P, P, I64, P, P, P, I64, P, P, P,

@@ -32,6 +32,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "htree_common.h"
 
 namespace htree {
@@ -1920,6 +1922,74 @@ int htree_backward_train(const htree_dims* d, float scale, const void* q, const 
   return backward_impl(d, scale, q, out, dO, gmax, gsum, parents, tree_ws, tree_ws_bytes,
                        cos_table, sin_table, scores, scores_bytes, dq, dk, dv, bwd_ws,
                        bwd_ws_bytes, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- no-alloc
+// Backward scratch for callers that cannot allocate device memory (code under
+// graph capture, serving loops, harnesses that forbid hipMalloc): a
+// file-scope device array, one copy per GPU, held until the process ends.
+// Every call on a GPU reuses that GPU's copy; the backward writes every word
+// of its workspace it later reads (no part of it needs to start at zero), so
+// no clearing is needed, and two calls that overlap on one GPU race.
+static __device__ __align__(256) char scratch[HTREE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch_ptr[kMaxDevices] = {};  // device address of `scratch`, per device
+
+// Device address of the current device's `scratch` (the array's name in host
+// code is a host-side stand-in, not a device address).
+int scratch_for_current_device(char** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return HTREE_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return HTREE_ENULL;
+    g_scratch_ptr[dev] = (char*)p;
+  }
+  *out = g_scratch_ptr[dev];
+  return HTREE_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int htree_backward_noalloc_bytes(const htree_dims* d, int64_t* bytes) {
+  BwdPlan BP;
+  int rc = make_bwd_plan(d, &BP);
+  if (rc) return rc;
+  if (!bytes) return HTREE_ENULL;
+  if (BP.bytes > HTREE_NOALLOC_SCRATCH_BYTES) {
+    rc = make_bwd_plan(d, &BP, false);
+    if (rc) return rc;
+  }
+  *bytes = BP.bytes;
+  return BP.bytes > HTREE_NOALLOC_SCRATCH_BYTES ? HTREE_ESCRATCH : HTREE_OK;
+}
+
+int htree_backward_noalloc(const htree_dims* d, float scale, const void* q, const void* out,
+                           const void* dO, const float* gmax, const float* gsum,
+                           const int32_t* parents, const void* tree_ws, int64_t tree_ws_bytes,
+                           const float* cos_table, const float* sin_table, const void* scores,
+                           int64_t scores_bytes, float* dq, float* dk, float* dv, void* stream) {
+  int64_t need = 0;
+  int rc = htree_backward_noalloc_bytes(d, &need);
+  if (rc) return rc;  // HTREE_ESCRATCH: the problem's backward needs more than the array holds
+  char* ws = nullptr;
+  rc = scratch_for_current_device(&ws);
+  if (rc) return rc;
+  // the stored-dS plan when its workspace fits the array, else the smallest
+  // (backward_impl takes the smaller plan for a workspace below the full one)
+  return backward_impl(d, scale, q, out, dO, gmax, gsum, parents, tree_ws, tree_ws_bytes,
+                       cos_table, sin_table, scores, scores_bytes, dq, dk, dv, ws, need, stream);
 }
 
 }  // extern "C"

@@ -197,6 +197,9 @@ const char* htree_strerror(int status) {
              "top_k_per_layer * max(compression_rate,16) / 16 > 64); the backward also needs "
              "B * T * H_kv * min(top_k_per_layer, parents of a level) < 2^31 per level";
     case HTREE_EWORKSPACE: return "workspace smaller than htree_tree_workspace_bytes()";
+    case HTREE_ESCRATCH:
+      return "backward needs more scratch than htree_backward_noalloc's device array "
+             "(HTREE_NOALLOC_SCRATCH_BYTES) holds: use htree_backward with a workspace";
     default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown htree status";
   }
 }

@@ -48,8 +48,13 @@ enum htree_status {
                               more than HTREE_MAX_LEVELS levels, or a
                               backward level of 2^31 or more entries
                               (B * T * H_kv * min(top_k, parents)) */
-  HTREE_EWORKSPACE = -5    /* workspace too small */
+  HTREE_EWORKSPACE = -5,   /* workspace too small */
+  HTREE_ESCRATCH = -6      /* htree_backward_noalloc: the problem's backward
+                              needs more than HTREE_NOALLOC_SCRATCH_BYTES */
 };
+
+/* Size of the device array htree_backward_noalloc works in (one per GPU). */
+#define HTREE_NOALLOC_SCRATCH_BYTES (128ll << 20)
 
 /* Problem description shared by every entry point (host struct). */
 typedef struct htree_dims {
@@ -172,6 +177,27 @@ int htree_backward_train(const htree_dims* d, float scale, const void* q, const 
                          const float* cos_table, const float* sin_table, const void* scores,
                          int64_t scores_bytes, float* dq, float* dk, float* dv, void* bwd_ws,
                          int64_t bwd_ws_bytes, void* stream);
+
+/* Backward workspace bytes htree_backward_noalloc would use for `d`
+ * (host): the stored-dS plan when it fits HTREE_NOALLOC_SCRATCH_BYTES, else
+ * the smallest plan; HTREE_ESCRATCH (with *bytes set) when even that does
+ * not fit.  No counterpart in the reference. */
+int htree_backward_noalloc_bytes(const htree_dims* d, int64_t* bytes);
+
+/* htree_backward_train that allocates nothing and takes no workspace: the
+ * backward works in a file-scope device array of
+ * HTREE_NOALLOC_SCRATCH_BYTES bytes (one per GPU, held until the process
+ * ends).  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  Problems whose backward needs more
+ * scratch get HTREE_ESCRATCH before any launch.  `scores` may be NULL (as
+ * for htree_backward).  Calls share their GPU's array: two calls that
+ * overlap on one GPU (different streams, or threads) race. */
+int htree_backward_noalloc(const htree_dims* d, float scale, const void* q, const void* out,
+                           const void* dO, const float* gmax, const float* gsum,
+                           const int32_t* parents, const void* tree_ws, int64_t tree_ws_bytes,
+                           const float* cos_table, const float* sin_table, const void* scores,
+                           int64_t scores_bytes, float* dq, float* dk, float* dv, void* stream);
 
 /* Row-wise Top-K (the selection of the forward's wide kernel, on its own):
  * for each of `rows` rows of n fp32 values (n <= 8192, 1 <= k <= n), the k

@@ -29,7 +29,7 @@ def test_header_and_exports_agree():
 
 def test_strerror_covers_codes():
     for rc in (N.HTREE_OK, N.HTREE_ENULL, N.HTREE_ESHAPE, N.HTREE_ECONFIG, N.HTREE_EUNSUPPORTED,
-               N.HTREE_EWORKSPACE):
+               N.HTREE_EWORKSPACE, N.HTREE_ESCRATCH):
         assert len(N.strerror(rc)) > 0
     assert N.strerror(-99) == "unknown htree status"
 
