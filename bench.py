@@ -16,9 +16,10 @@ backward (`htree_backward` from the saved context) when the backward is
 built; `value` = B*T / step time (tokens/s).  The roofline object is for the
 dominant kernel (the fused forward), timed with HIP events on the stream it
 runs on, against the gathered-bytes model in htree_amd/workmodel.py.
-The CPU baseline times the CPU restatement of src/naive.py (oracle/,
-single-threaded C) on a bounded random sample of the same workload's query
-rows; it is a reported baseline only.
+The CPU baseline times the CPU restatement of src/naive.py (oracle/, C on
+every host core up to 16) on a bounded random sample of the same workload's
+query rows, and, as cpu_baseline.c1, on the whole of the CPU config C1
+(forward and backward, median of 3); it is a reported baseline only.
 """
 from __future__ import annotations
 
@@ -72,28 +73,36 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(q, k, v, dO, out, gmax, gsum, parents, CR, TK, MTN, dtype, budget_s=12.0):
-    """Oracle (CPU restatement of src/naive.py, one thread) on random query
-    rows of the workload until `budget_s` seconds of forward work have run,
-    then the same rows through the backward's per-row work."""
+def host_threads() -> int:
+    """Host threads for the CPU legs: every core os.cpu_count() reports, at
+    most the 16 a one-GPU box's share holds."""
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def cpu_baseline(q, k, v, dO, out, gmax, gsum, parents, CR, TK, MTN, dtype, budget_s=10.0):
+    """Oracle (CPU restatement of src/naive.py, C, on host_threads() threads)
+    on random query rows of the workload until `budget_s` seconds of forward
+    work have run, then the same rows through the backward's per-row (dq)
+    work."""
     import numpy as np
 
     from oracle import oracle as orc
 
     B, T, H, D = q.shape
+    th = host_threads()
     qn = q.float().cpu().numpy()
     tree = orc.Tree(k.float().cpu().numpy(), v.float().cpu().numpy(), CR, MTN, TK, dtype)
     rng = np.random.default_rng(0)
     done, t_fwd, rows_all = 0, 0.0, []
     while t_fwd < budget_s and done < B * T:
-        rows = np.stack([rng.integers(0, B, 64), rng.integers(0, T, 64)], 1).astype(np.int32)
+        rows = np.stack([rng.integers(0, B, 32 * th), rng.integers(0, T, 32 * th)], 1).astype(np.int32)
         t0 = time.perf_counter()
-        orc.forward(qn, tree, D ** -0.5, rows=rows)
+        orc.forward_threaded(qn, tree, D ** -0.5, th, rows=rows)
         t_fwd += time.perf_counter() - t0
         done += len(rows)
         rows_all.append(rows)
     rows = np.concatenate(rows_all)
-    res = dict(fwd_tok_s=done / t_fwd, fwd_rows=done, fwd_s=t_fwd)
+    res = dict(fwd_tok_s=done / t_fwd, fwd_rows=done, fwd_s=t_fwd, threads=th)
     if parents is not None:
         par = parents.cpu().numpy()[:, rows[:, 0], rows[:, 1]]
         gm = gmax.cpu().numpy()[rows[:, 0], rows[:, 1]]
@@ -101,11 +110,52 @@ def cpu_baseline(q, k, v, dO, out, gmax, gsum, parents, CR, TK, MTN, dtype, budg
         o = out.float().cpu().numpy()[rows[:, 0], rows[:, 1]]
         d = dO.float().cpu().numpy()[rows[:, 0], rows[:, 1]]
         delta = (o.astype(np.float64) * d).sum(-1).astype(np.float32)
+        from concurrent.futures import ThreadPoolExecutor
+
+        parts = orc.split_rows(np.arange(len(rows)), th)
         t0 = time.perf_counter()
-        orc.backward_dq_rows(qn, tree, D ** -0.5, rows, par, gm, gs, delta, d)
+        with ThreadPoolExecutor(len(parts)) as ex:
+            list(ex.map(lambda i: orc.backward_dq_rows(qn, tree, D ** -0.5, rows[i], par[:, i], gm[i],
+                                                       gs[i], delta[i], d[i]), parts))
         t_bwd = time.perf_counter() - t0
         res.update(bwd_tok_s=len(rows) / t_bwd, bwd_s=t_bwd)
     return res
+
+
+def cpu_leg_c1(iters: int = 3):
+    """The CPU baseline planned for the BASELINE.json CPU config C1 (B=1,
+    T=2048, Hq=4, Hkv=1, D=64, fp32, CR=16, MTN=64, TK=8; q/k/v/dO iid N(0,1)
+    from a fixed seed): the oracle's whole forward (tree build included) and
+    whole analytical backward (src/naive.py:133-396 restated) on
+    host_threads() threads, one warm-up and `iters` timed runs, median."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as orc
+
+    B, T, H, Hkv, D, CR, TK, MTN = 1, 2048, 4, 1, 64, 16, 8, 64
+    g = torch.Generator().manual_seed(7)
+    q, k, v, dO = (torch.randn(*s, generator=g).numpy()
+                   for s in ((B, T, H, D), (B, T, Hkv, D), (B, T, Hkv, D), (B, T, H, D)))
+    th = host_threads()
+    tf, tb = [], []
+    for _ in range(1 + iters):
+        t0 = time.perf_counter()
+        tree = orc.Tree(k, v, CR, MTN, TK, "float32")
+        fw = orc.forward_threaded(q, tree, D ** -0.5, th)
+        t1 = time.perf_counter()
+        L = tree.L
+        orc.backward_threaded(q, tree, D ** -0.5, fw["parents"].reshape(L, B, T, Hkv, TK),
+                              fw["gmax"].reshape(B, T, H), fw["gsum"].reshape(B, T, H),
+                              fw["out"].reshape(B, T, H, D), dO, th)
+        t2 = time.perf_counter()
+        tf.append(t1 - t0)
+        tb.append(t2 - t1)
+    f, b = float(np.median(tf[1:])), float(np.median(tb[1:]))
+    return {"config": f"C1: B={B} T={T} Hq={H} Hkv={Hkv} D={D} f32 CR={CR} MTN={MTN} TK={TK}",
+            "threads": th, "fwd_s": f, "bwd_s": b, "fwd_tokens_per_s": B * T / f,
+            "bwd_tokens_per_s": B * T / b, "tokens_per_s": B * T / (f + b),
+            "timing": f"1 warm-up + {iters} runs, median wall-clock"}
 
 
 def main():
@@ -272,13 +322,15 @@ def main():
                           CR, TK, MTN, dtype)
         tot = 1.0 / (1.0 / cb["fwd_tok_s"] + (1.0 / cb["bwd_tok_s"] if has_bwd and "bwd_tok_s" in cb else 0.0))
         res["cpu_baseline"] = {
-            "value": tot, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "value": tot, "unit": "tokens/s", "cores": cb["threads"], "kind": "port",
             "sample": f"{cb['fwd_rows']} random query rows (b,t) of {args.workload} through the "
                       f"oracle's forward ({cb['fwd_s']:.1f} s)"
-                      + (f" and backward per-row work ({cb['bwd_s']:.1f} s)" if "bwd_s" in cb else "")
-                      + f"; host CPU: {cpu_model()}, os.cpu_count()={os.cpu_count()}",
+                      + (f" and backward per-row (dq) work ({cb['bwd_s']:.1f} s)" if "bwd_s" in cb else "")
+                      + f", {cb['threads']} host threads; host CPU: {cpu_model()}, "
+                      f"os.cpu_count()={os.cpu_count()}",
             "fwd_tokens_per_s": cb["fwd_tok_s"],
             "bwd_tokens_per_s": cb.get("bwd_tok_s"),
+            "c1": cpu_leg_c1(),
         }
     else:
         res["cpu_baseline"] = None

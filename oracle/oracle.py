@@ -386,6 +386,65 @@ def final_dkv_level0(q, tree: Tree, scale: float, parents, gmax, gsum, delta_, d
     return rk, rv
 
 
+def split_rows(rows: np.ndarray, parts: int) -> List[np.ndarray]:
+    cuts = np.linspace(0, len(rows), max(1, parts) + 1).astype(int)
+    return [rows[a:b] for a, b in zip(cuts[:-1], cuts[1:]) if b > a]
+
+
+def forward_threaded(q, tree: Tree, scale: float, threads: int, rows: Optional[np.ndarray] = None):
+    """forward() over row chunks on `threads` host threads (the C calls
+    release the GIL); out, out_f32, gmax, gsum, parents for `rows` in order."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    q = _f32(q)
+    if rows is None:
+        rows = all_rows(q.shape[0], q.shape[1])
+    chunks = split_rows(np.ascontiguousarray(rows, np.int32), threads)
+    with ThreadPoolExecutor(len(chunks)) as ex:
+        parts = list(ex.map(lambda r: forward(q, tree, scale, rows=r), chunks))
+    cat = lambda key, ax=0: np.concatenate([p[key] for p in parts], ax)
+    return dict(out=cat("out"), out_f32=cat("out_f32"), gmax=cat("gmax"), gsum=cat("gsum"),
+                parents=cat("parents", 1), rows=rows)
+
+
+def backward_threaded(q, tree: Tree, scale: float, parents, gmax, gsum, out, dO, threads: int):
+    """The full backward (as backward()) on `threads` host threads: dq by row
+    chunks (backward_dq_rows), every level's dK / dV by node chunks
+    (backward_dkv_nodes), then the mean-pool backward (naive.py:388-394).
+    Returns dq, dk, dv (final, level 0)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    q = _f32(q)
+    B, T, H, D = q.shape
+    parents = np.ascontiguousarray(parents, np.int32)
+    gmax, gsum, out, dO = _f32(gmax), _f32(gsum), _f32(out), _f32(dO)
+    dl = delta(out, dO)
+    rows = all_rows(B, T)
+    chunks = split_rows(rows, threads)
+
+    def dq_part(r):
+        b, t = r[:, 0], r[:, 1]
+        return backward_dq_rows(q, tree, scale, r, parents[:, b, t], gmax[b, t], gsum[b, t], dl[b, t],
+                                dO[b, t])
+
+    with ThreadPoolExecutor(len(chunks)) as ex:
+        dq = np.concatenate(list(ex.map(dq_part, chunks))).reshape(B, T, H, D)
+    tg = np.array([(l, b, h, x) for l in range(tree.L) for b in range(B) for h in range(tree.Hkv)
+                   for x in range(int(tree.n[l]))], np.int32)
+    dk_n, dv_n = backward_dkv_nodes(q, tree, scale, parents, gmax, gsum, dl, dO, tg, threads)
+    dk_lv = np.zeros_like(tree.kflat)
+    dv_lv = np.zeros_like(tree.vflat)
+    for i, (l, b, h, x) in enumerate(tg):
+        dk_lv[tree.off[l] + ((b * tree.n[l] + x) * tree.Hkv + h) * D:][:D] = dk_n[i]
+        dv_lv[tree.voff[l] + ((b * tree.n[l] + x) * tree.Hkv + h) * tree.DV:][:tree.DV] = dv_n[i]
+    lib().orc_tree_backward(_ptr(dk_lv), B, tree.Hkv, D, _ptr(tree.off), _ptr(tree.n), tree.L, tree.CR)
+    lib().orc_tree_backward(_ptr(dv_lv), B, tree.Hkv, tree.DV, _ptr(tree.voff), _ptr(tree.n), tree.L,
+                            tree.CR)
+    dk = dk_lv[:tree.lk[0].size].reshape(tree.lk[0].shape)
+    dv = dv_lv[:tree.lv[0].size].reshape(tree.lv[0].shape)
+    return dq, dk, dv
+
+
 def initial_parents(B: int, T: int, Hkv: int, TK: int, CR: int, L: int) -> np.ndarray:
     """naive.py:108-118"""
     tlp = CR ** (L - 1)

@@ -451,3 +451,18 @@ def test_oracle_separate_value_dim(kv):
     b, t = rows[:, 0], rows[:, 1]
     dq = orc.backward_dq_rows(q, tree, K ** -0.5, rows, par[:, b, t], gm[b, t], gs[b, t], dl[b, t], dO[b, t])
     np.testing.assert_array_equal(dq, bw["dq"][b, t])
+
+
+def test_threaded_forms_match(run):
+    """forward_threaded / backward_threaded (the CPU baseline's multi-core
+    forms) against the single-threaded forward and full backward."""
+    B, T, H, D = run["B"], run["T"], run["H"], run["D"]
+    fw = orc.forward_threaded(run["q"], run["tree"], D ** -0.5, threads=3)
+    for key in ("out", "gmax", "gsum", "parents"):
+        np.testing.assert_array_equal(fw[key], run["fw"][key])
+    bw, par, gm, gs, _ = full_backward(run)
+    dq, dk, dv = orc.backward_threaded(run["q"], run["tree"], D ** -0.5, par, gm, gs,
+                                       run["fw"]["out"].reshape(B, T, H, D), run["dO"], threads=3)
+    np.testing.assert_array_equal(dq, bw["dq"])
+    for got, ref in ((dk, bw["dk"]), (dv, bw["dv"])):
+        np.testing.assert_allclose(got, ref, rtol=1e-4, atol=2e-6 * np.abs(ref).max())
