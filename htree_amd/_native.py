@@ -40,7 +40,7 @@ EXPORTS = (
 class HtreeDims(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in (
         "B", "T", "H", "H_kv", "D", "compression_rate", "top_k", "max_top_nodes", "dtype",
-        "rope_rows")]
+        "rope_rows", "kv_share")]
 
 
 class HtreeError(RuntimeError):
@@ -119,11 +119,12 @@ def check(rc: int, what: str) -> None:
     raise HtreeError(msg)
 
 
-def dims(B, T, H, H_kv, D, compression_rate, top_k, max_top_nodes, dtype, rope_rows) -> HtreeDims:
+def dims(B, T, H, H_kv, D, compression_rate, top_k, max_top_nodes, dtype, rope_rows,
+         kv_share=1) -> HtreeDims:
     if dtype not in DTYPE_CODE:
         raise AssertionError(f"unsupported dtype {dtype}: expected float32, bfloat16 or float16")
     return HtreeDims(B, T, H, H_kv, D, compression_rate, top_k, max_top_nodes,
-                     DTYPE_CODE[dtype], rope_rows)
+                     DTYPE_CODE[dtype], rope_rows, kv_share)
 
 
 def levels(d: HtreeDims):

@@ -85,7 +85,7 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
     if B == 0 or T == 0:  # empty inputs: empty gradients, no launch
         return (torch.empty(B, T, H, K, **f32), torch.empty(B, T, H_kv, K, **f32),
                 torch.empty(B, T, H_kv, V, **f32))
-    hf = bwd_ctx.get("head_frame") or HeadFrame(K, V)
+    hf = bwd_ctx.get("head_frame") or HeadFrame(K, V, H // H_kv)
     CR = bwd_ctx["compression_rate"]
     TK = bwd_ctx["top_k_per_layer"]
     L = bwd_ctx["num_layers"]
@@ -97,7 +97,7 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
     if ws is None or d is None:
         # a context of the reference's keys: the kernels run with its own tables
         check_tables(cos, sin, K // 2, TK * CR, dev)
-        d = make_dims(B, T, H, H_kv, hf.D, CR, MTN, TK, q.dtype, cos.shape[0])
+        d = make_dims(B, T, H, H_kv, hf.D, CR, MTN, TK, q.dtype, cos.shape[0], hf.share)
         assert len(N.levels(d)) == L, f"num_layers {L} does not match T={T}, CR={CR}, MTN={MTN}"
         ws = None
     cos_k, sin_k = hf.tables(cos, sin)
@@ -115,18 +115,19 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
     if parents is None and plp is not None:
         parents = _stack_parents(plp, L)
         _check_parents(parents, B, T, H_kv, TK, CR, MTN, dev)
+        parents = hf.dup(parents, 3)
     if parents is None:
         # replay the selection (and keep the replay's scores for this backward)
         _, _, _, parents, _, _, ws, scores = forward_frame(
-            qf, hf.pad_qk(k.contiguous()), hf.pad_v(v.contiguous()), d, cos_k, sin_k, scale,
-            True, True)
+            qf, hf.kv_k(k.contiguous()), hf.kv_v(v.contiguous()), d, cos_k, sin_k, scale, True,
+            True)
     elif ws is None:
-        _, _, ws = build_tree(hf.pad_qk(k.contiguous()), hf.pad_v(v.contiguous()), d, cos_k, sin_k)
+        _, _, ws = build_tree(hf.kv_k(k.contiguous()), hf.kv_v(v.contiguous()), d, cos_k, sin_k)
     dOf = hf.pad_v(dO.contiguous().to(q.dtype))
     outf = hf.pad_v(output.contiguous().to(q.dtype))
     D = hf.D
     dq = torch.empty(B, T, H, D, **f32)
-    dk = torch.empty(B, T, H_kv, D, **f32)
+    dk = torch.empty(B, T, H_kv * hf.share, D, **f32)
     dv = torch.empty_like(dk)
     nb = N.ctypes.c_int64()
     N.check(N.lib().htree_backward_workspace_bytes(N.ctypes.byref(d), N.ctypes.byref(nb)),
@@ -153,7 +154,7 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
                 N.ptr(sin_k), N.ptr(dq), N.ptr(dk), N.ptr(dv), N.ptr(bws), bws.numel(),
                 N.stream_ptr(dev))
             N.check(rc, "htree_backward")
-    return hf.unpad_qk(dq), hf.unpad_qk(dk), hf.unpad_v(dv)
+    return hf.unpad_qk(dq), hf.unpad_qk(hf.pair_sum(dk)), hf.unpad_v(hf.pair_sum(dv))
 
 
 _REF_META = ("num_layers", "compression_rate", "top_k_per_layer", "max_top_nodes", "scale",

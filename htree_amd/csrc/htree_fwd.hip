@@ -57,6 +57,7 @@ struct FwdArgs {
   int32_t B, T, H, Hkv, G, CR, crlg, TK, L, max_tiles;
   float scale;
   int32_t per_xcd;
+  int32_t kv_share;  // 2: KV heads 2i, 2i+1 share one selection (register forward)
 };
 
 template <int MAXSLOT>
@@ -575,12 +576,18 @@ __device__ __forceinline__ float exp_sel(float x) {
 // (stable descending sort).  Writes the selected nodes in ascending order
 // (= ascending position) to par_next, -1 padded to TK, and one selection
 // bitmask per slot to selmask.
+// With imp2 (a pair of KV heads sharing the selection), the importance of
+// position j is imp[j] f1 + imp2[j] f2: each array is relative to its own
+// half's level max, f = exp(m_half - m_pair); both waves of the pair pass
+// the arrays in the same order, so both select the same nodes.
 template <int MAXSLOT>
 __device__ __forceinline__ void select_topk(const float* __restrict__ imp, const float* mt,
                                             float Mrun, int nt, int nc, int apos, int TK,
                                             bool wide, int crlg, int CR, int CRU,
                                             const int32_t* par_cur, int32_t* par_next,
-                                            unsigned long long* selmask, int lane) {
+                                            unsigned long long* selmask, int lane,
+                                            const float* __restrict__ imp2 = nullptr,
+                                            float f1 = 1.f, float f2 = 0.f) {
   const int u16 = lane & 15, kg = lane >> 4;
   const int take = TK < nc ? TK : nc;
   const int nslot = (nt + 3) >> 2;
@@ -596,7 +603,7 @@ __device__ __forceinline__ void select_topk(const float* __restrict__ imp, const
         if (pos == apos) {
           v = 1e6f;  // rightmost candidate always kept (src/naive.py:93)
         } else {
-          v = imp[64 * sl + lane];
+          v = imp2 ? imp[64 * sl + lane] * f1 + imp2[64 * sl + lane] * f2 : imp[64 * sl + lane];
           if (mt) {
             const float m = mt[tau];
             if (m != Mrun) v *= expf(m - Mrun);
@@ -656,6 +663,7 @@ struct WaveLdsR {
   float imp[256];
   float xrow[64];
   unsigned long long selmask[4];
+  float lvl_max;     // the level's max score of this wave's heads (KV-head pairs)
 };
 
 template <int D>
@@ -681,11 +689,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   const int bid = blockIdx.x;
   const int64_t lb = (int64_t)(bid & 7) * a.per_xcd + (bid >> 3);
   const int64_t grp = lb * kWavesPerBlock + wv;
-  if (grp >= (int64_t)a.B * a.Hkv * a.T) return;
-  const int t = (int)(grp % a.T);
-  const int bh = (int)(grp / a.T);
-  const int h = bh % a.Hkv;
-  const int b = bh / a.Hkv;
+  // A top level of <= top_k nodes keeps every candidate and accumulates
+  // none (src/naive.py:97-101): its list is the virtual parents and its
+  // selection every top node up to t's, so the walk starts one level lower.
+  const bool skip_top = !TRACE && a.L > 1 && a.lv[a.L - 1].N <= TK;
+  const int lstart = skip_top ? a.L - 2 : a.L - 1;
+  // KV-head pairs (kv_share 2): waves 2i and 2i+1 of a block take KV heads
+  // 2h, 2h+1 of one query and meet at two block barriers per upper level to
+  // combine their importances.  Pairs never straddle blocks (the group count
+  // is even), and the waves of an empty pair still pass every barrier.
+  const bool pair = a.kv_share == 2;
+  if (grp >= (int64_t)a.B * a.Hkv * a.T) {
+    if (pair)
+      for (int l = lstart; l >= 1; --l) {
+        __syncthreads();
+        __syncthreads();
+      }
+    return;
+  }
+  int t, h, b;
+  if (pair) {
+    const int Hr = a.Hkv >> 1;
+    const int64_t pq = grp >> 1;
+    t = (int)(pq % a.T);
+    const int64_t bhr = pq / a.T;
+    h = 2 * (int)(bhr % Hr) + (int)(grp & 1);
+    b = (int)(bhr / Hr);
+  } else {
+    t = (int)(grp % a.T);
+    const int bh = (int)(grp / a.T);
+    h = bh % a.Hkv;
+    b = bh / a.Hkv;
+  }
   WaveLdsR& W = lds_all[wv];
   const int CRU = CR < 16 ? CR : 16;
   const bool wide = CR >= 16;
@@ -699,20 +734,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   f32x4 O[ND];
 #pragma unroll
   for (int n = 0; n < ND; ++n) O[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  int lstart = a.L - 1;
   {
     const int64_t nvp = (t / a.lv[a.L - 1].pw) / CR + 1;
     if (lane < TK) W.par[0][lane] = lane < nvp ? lane : -1;
-    // A top level of <= top_k nodes keeps every candidate and accumulates
-    // none (src/naive.py:97-101): its list is the virtual parents and its
-    // selection every top node up to t's, so the walk starts one level lower.
-    if (!TRACE && a.L > 1 && a.lv[a.L - 1].N <= TK) {
+    if (skip_top) {
       if (a.parents && lane < TK)
         a.parents[((((int64_t)(a.L - 1) * a.B + b) * a.T + t) * a.Hkv + h) * TK + lane] =
             lane < nvp ? lane : -1;
       const int64_t ntop = t / a.lv[a.L - 1].pw + 1;
       if (lane < TK) W.par[0][lane] = lane < ntop ? lane : -1;
-      lstart = a.L - 2;
     }
   }
   int cur = 0;
@@ -795,10 +825,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
         const float mine = u16 == 0 ? e[0] : u16 == 1 ? e[1] : u16 == 2 ? e[2] : e[3];
         if (u16 < 4) W.imp[(tau << 4) + 4 * kg + u16] = mine;
       }
-      wave_sync();
-      select_topk<4>(W.imp, nullptr, M, nt, nc, apos, TK, wide, crlg, CR, CRU, W.par[cur],
-                     W.par[cur ^ 1], W.selmask, lane);
-      wave_sync();
+      if (pair) {
+        // the pair's importance: both halves' sums taken to the pair's max
+        // (the group-shared sum of src/naive.py:204-205 over all G heads)
+        if (lane == 0) W.lvl_max = M;
+        __syncthreads();
+        const WaveLdsR& W0 = lds_all[wv & ~1];
+        const WaveLdsR& W1 = lds_all[wv | 1];
+        const float m0 = W0.lvl_max, m1 = W1.lvl_max, mp = fmaxf(m0, m1);
+        select_topk<4>(W0.imp, nullptr, mp, nt, nc, apos, TK, wide, crlg, CR, CRU, W.par[cur],
+                       W.par[cur ^ 1], W.selmask, lane, W1.imp, expf(m0 - mp), expf(m1 - mp));
+        __syncthreads();  // the partner has read this wave's importances
+      } else {
+        wave_sync();
+        select_topk<4>(W.imp, nullptr, M, nt, nc, apos, TK, wide, crlg, CR, CRU, W.par[cur],
+                       W.par[cur ^ 1], W.selmask, lane);
+        wave_sync();
+      }
     }
 
     // ---- per-head max over the accumulated candidates (rows kg via LDS)
@@ -1315,6 +1358,7 @@ static int forward_impl(const htree_dims* d, float scale, const void* q, const v
   a.TK = d->top_k;
   a.L = P.L;
   a.scale = scale;
+  a.kv_share = d->kv_share == 2 ? 2 : 1;
   // the streaming kernel addresses one (b, h_kv) block of a level array
   // with 32-bit byte offsets
   if (!P.wide && P.max_tiles > 16 && P.Np[0] * d->D * 2 > 0x7fffffffll) return HTREE_EUNSUPPORTED;

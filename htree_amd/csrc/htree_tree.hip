@@ -25,12 +25,16 @@ int make_plan(const htree_dims* d, Plan* p) {
     return HTREE_ECONFIG;
   if ((int64_t)d->rope_rows < (int64_t)d->top_k * d->compression_rate)
     return HTREE_ECONFIG;
+  if (d->kv_share < 0 || d->kv_share > 2 || (d->kv_share == 2 && d->H_kv % 2 != 0))
+    return HTREE_ESHAPE;
   const int CR = d->compression_rate;
   const int64_t max_tiles = (int64_t)d->top_k * (CR > 16 ? CR : 16) / 16;
   const bool wide = max_tiles > kMaxTiles || d->top_k > kMaxTK;
   if ((d->D != 32 && d->D != 64 && d->D != 128) || d->H / d->H_kv > 16 || CR < 4 || CR > 64 ||
       (wide && (d->top_k > kWideMaxTK || (int64_t)d->top_k * CR > kWideMaxPos)))
     return HTREE_EUNSUPPORTED;
+  // shared selections over KV-head pairs: the register forward's paired waves
+  if (d->kv_share == 2 && (wide || max_tiles > 16)) return HTREE_EUNSUPPORTED;
 
   memset(p, 0, sizeof(*p));
   p->precise = d->dtype != HTREE_BF16;
@@ -185,13 +189,16 @@ const char* htree_strerror(int status) {
   switch (status) {
     case HTREE_OK: return "ok";
     case HTREE_ENULL: return "a required pointer argument is NULL";
-    case HTREE_ESHAPE: return "invalid shape: need B,T,H,H_kv,D > 0, even D, H % H_kv == 0, dtype in {f32,bf16,f16}";
+    case HTREE_ESHAPE:
+      return "invalid shape: need B,T,H,H_kv,D > 0, even D, H % H_kv == 0, dtype in {f32,bf16,f16}, "
+             "kv_share in {0,1,2} (2: H_kv even)";
     case HTREE_ECONFIG:
       return "invalid tree configuration: compression_rate, top_k_per_layer and max_top_nodes "
              "must be powers of two with max_top_nodes <= top_k_per_layer * compression_rate "
              "and rope_rows >= top_k_per_layer * compression_rate";
     case HTREE_EUNSUPPORTED:
-      return "configuration outside this HIP build: needs D in {32,64,128}, H/H_kv <= 16, "
+      return "configuration outside this HIP build: needs D in {32,64,128}, H/H_kv <= 16 "
+             "(up to 32 with kv_share 2, where top_k_per_layer * max(compression_rate,16) <= 256), "
              "4 <= compression_rate <= 64, top_k_per_layer <= 512 and "
              "top_k_per_layer * compression_rate <= 8192 (where top_k_per_layer > 64 or "
              "top_k_per_layer * max(compression_rate,16) / 16 > 64); the backward also needs "

@@ -8,9 +8,14 @@ Differences, all deliberate:
     relies on equality.  The reference's Triton-tiling asserts
     (top_k % 64 == 0, top_k % compression_rate == 0, :923,1019) do not apply.
   * limits of this HIP build (AssertionError): max(K, V) in {32, 64, 128}
-    (K even), H / H_kv <= 16, 4 <= compression_rate <= 64,
-    top_k_per_layer <= 512 and top_k_per_layer * compression_rate <= 8192
-    candidates per level.
+    (K even), H / H_kv <= 16 (or even and <= 32 where
+    top_k_per_layer * max(compression_rate, 16) <= 256), 4 <= compression_rate
+    <= 64, top_k_per_layer <= 512 and top_k_per_layer * compression_rate <=
+    8192 candidates per level.
+  * a query group of G > 16 heads (the reference pads it to G_PAD,
+    src/parallel.py:1023) runs as two groups of G/2 heads over duplicated KV
+    heads that share one selection (the kernels' kv_share mode); each KV
+    head's dk / dv is the sum of its two copies'.
   * K != V (the reference carries V = v.shape[-1] apart from K,
     src/parallel.py:904) runs the kernels at one head dim D = max(K, V):
     V is zero-padded to D (zero columns add nothing to P.V and come out
@@ -60,13 +65,45 @@ def rope_cache(head_dim: int, rows: int, rope_base: float, device) -> Tuple[torc
 
 
 class HeadFrame:
-    """Maps the caller's head dims (K for q/k, V for v) onto the kernels' one
-    head dim D = max(K, V).  With K == V every method returns its argument."""
+    """Maps the caller's heads onto the kernels': the head dims (K for q/k, V
+    for v) onto one head dim D = max(K, V), and a query group of G > 16 heads
+    onto two groups of G/2 over KV heads duplicated in place (KV head h
+    becomes kernel KV heads 2h, 2h+1: query head h*G + g is then kernel
+    group 2h + g // (G/2), so q keeps its layout).  With K == V and G <= 16
+    every method returns its argument."""
 
-    def __init__(self, K: int, V: int):
+    def __init__(self, K: int, V: int, G: int = 1):
         self.K, self.V = K, V
         self.D = max(K, V)
         self.same = K == V
+        self.share = 2 if G > 16 else 1
+        self.plain = self.same and self.share == 1
+
+    def kv_k(self, k: torch.Tensor) -> torch.Tensor:
+        """Caller k [B,T,H_kv,K] -> kernel k [B,T,share*H_kv,D]."""
+        return self.dup(self.pad_qk(k), 2)
+
+    def kv_v(self, v: torch.Tensor) -> torch.Tensor:
+        return self.dup(self.pad_v(v), 2)
+
+    def dup(self, x: torch.Tensor, dim: int) -> torch.Tensor:
+        return x if self.share == 1 else x.repeat_interleave(self.share, dim).contiguous()
+
+    def pick(self, x: torch.Tensor, dim: int) -> torch.Tensor:
+        """Kernel KV heads -> caller KV heads (the first of each copy: the
+        copies agree on everything but their own dk / dv)."""
+        if self.share == 1:
+            return x
+        idx = [slice(None)] * x.dim()
+        idx[dim] = slice(0, None, self.share)
+        return x[tuple(idx)]
+
+    def pair_sum(self, x: torch.Tensor) -> torch.Tensor:
+        """Kernel dk / dv [B,T,share*H_kv,D] -> caller [B,T,H_kv,D]."""
+        if self.share == 1:
+            return x
+        B, T, Hs, D = x.shape
+        return x.view(B, T, Hs // self.share, self.share, D).sum(3)
 
     def pad_qk(self, x: torch.Tensor) -> torch.Tensor:
         """[..., K] -> [..., D]: RoPE pair halves at [0, K/2) and [D/2, D/2 + K/2)."""
@@ -113,6 +150,10 @@ def _validate(q, k, v, compression_rate, max_top_nodes, top_k_per_layer):
     assert k.shape[:2] == (B, T) and v.shape[:2] == (B, T), "q/k/v batch and length must match"
     assert k.shape[3] == K, f"q and k must share the head dim K ({K} vs {k.shape[3]})"
     V = v.shape[3]
+    G = H // H_kv
+    assert G <= 16 or (G <= 32 and G % 2 == 0), (
+        f"configuration outside this HIP build: query groups of up to 16 heads, or an even "
+        f"number up to 32, got H/H_kv = {G}")
     assert K % 2 == 0 and K > 0 and V > 0, "head dims must be positive, K even (RoPE pairs)"
     assert max(K, V) in KERNEL_HEAD_DIMS, (
         f"configuration outside this HIP build: needs max(K, V) in {KERNEL_HEAD_DIMS}, "
@@ -134,9 +175,12 @@ def rope_rows_for(max_top_nodes: int, top_k_per_layer: int, compression_rate: in
     return max(max_top_nodes + 1024, top_k_per_layer * compression_rate)
 
 
-def make_dims(B, T, H, H_kv, D, compression_rate, max_top_nodes, top_k_per_layer, dtype, rope_rows):
-    return N.dims(B, T, H, H_kv, D, compression_rate, top_k_per_layer, max_top_nodes, dtype,
-                  rope_rows)
+def make_dims(B, T, H, H_kv, D, compression_rate, max_top_nodes, top_k_per_layer, dtype, rope_rows,
+              share=1):
+    """Kernel dims; H_kv counts the caller's KV heads, the kernels see
+    share * H_kv of them."""
+    return N.dims(B, T, H, H_kv * share, D, compression_rate, top_k_per_layer, max_top_nodes, dtype,
+                  rope_rows, share)
 
 
 def check_tables(cos, sin, half: int, rows_min: int, device):
@@ -181,8 +225,8 @@ def forward_frame(qf, kf, vf, d, cos_k, sin_k, scale, save_parents, keep_scores)
     with torch.cuda.device(dev):
         if empty:
             # the library's limits still apply: checked on one query
-            N.levels(make_dims(1, 1, H, H_kv, D, d.compression_rate, d.max_top_nodes, d.top_k,
-                               qf.dtype, d.rope_rows))
+            N.levels(N.dims(1, 1, H, H_kv, D, d.compression_rate, d.top_k, d.max_top_nodes,
+                            qf.dtype, d.rope_rows, d.kv_share))
             layers_k, layers_v = [kf], [vf]
             ws = torch.empty(0, dtype=torch.uint8, device=dev)
         else:
@@ -232,30 +276,32 @@ def htree_forward(
     _validate(q, k, v, compression_rate, max_top_nodes, top_k_per_layer)
     B, T, H, K = q.shape
     H_kv = k.shape[2]
-    hf = HeadFrame(K, v.shape[3])
+    G = H // H_kv
+    hf = HeadFrame(K, v.shape[3], G)
     if scale is None:
         scale = K ** -0.5
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     rows = rope_rows_for(max_top_nodes, top_k_per_layer, compression_rate)
     d = make_dims(B, T, H, H_kv, hf.D, compression_rate, max_top_nodes, top_k_per_layer, q.dtype,
-                  rows)
+                  rows, hf.share)
     cos, sin = rope_cache(K, rows, rope_base, q.device)
     cos_k, sin_k = hf.tables(cos, sin)
     save_par = _save_for_backward and _save_parents
     out_f, gmax, gsum, parents, lk, lv, ws, scores = forward_frame(
-        hf.pad_qk(q), hf.pad_qk(k), hf.pad_v(v), d, cos_k, sin_k, scale, save_par, True)
+        hf.pad_qk(q), hf.kv_k(k), hf.kv_v(v), d, cos_k, sin_k, scale, save_par, True)
     out = hf.unpad_v(out_f)
     if not _save_for_backward:
         return out
     L = len(lk)
-    G = H // H_kv
     bwd_ctx = dict(
         global_max=gmax,
         global_sum=gsum,
-        per_layer_parents={l: parents[l] for l in range(L)} if save_par else None,
+        per_layer_parents={l: hf.pick(parents[l], 2) for l in range(L)} if save_par else None,
         # the caller's frame: layers_k[0] is k (src/parallel.py:949)
-        layers_k=[k] + [hf.unpad_qk(x) for x in lk[1:]] if not hf.same else lk,
-        layers_v=[v] + [hf.unpad_v(x) for x in lv[1:]] if not hf.same else lv,
+        layers_k=[k] + [hf.unpad_qk(hf.pick(x, 2)).contiguous() for x in lk[1:]]
+        if not hf.plain else lk,
+        layers_v=[v] + [hf.unpad_v(hf.pick(x, 2)).contiguous() for x in lv[1:]]
+        if not hf.plain else lv,
         cos_cache=cos,
         sin_cache=sin,
         num_layers=L,
@@ -284,4 +330,5 @@ def htree_forward_parents(q, k, v, compression_rate=16, max_top_nodes=8192, top_
     each level's selection), gmax and gsum.  Used by the trace tests."""
     out, ctx = htree_forward(q, k, v, compression_rate, max_top_nodes, top_k_per_layer, scale,
                              rope_base, _save_for_backward=True, _save_parents=True)
-    return out, ctx["parents_stacked"], ctx["global_max"], ctx["global_sum"], ctx
+    par = ctx["head_frame"].pick(ctx["parents_stacked"], 3)
+    return out, par, ctx["global_max"], ctx["global_sum"], ctx

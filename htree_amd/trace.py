@@ -50,23 +50,24 @@ def run_parallel_with_trace(
     _validate(q, k, v, compression_rate, max_top_nodes, top_k_per_layer)
     B, T, H, K = q.shape
     H_kv = k.shape[2]
-    hf = HeadFrame(K, v.shape[3])
+    hf = HeadFrame(K, v.shape[3], H // H_kv)
     if scale is None:
         scale = K ** -0.5
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     rows = rope_rows_for(max_top_nodes, top_k_per_layer, compression_rate)
     d = make_dims(B, T, H, H_kv, hf.D, compression_rate, max_top_nodes, top_k_per_layer, q.dtype,
-                  rows)
+                  rows, hf.share)
     dev = q.device
     with torch.cuda.device(dev):
         cos, sin = hf.tables(*rope_cache(K, rows, rope_base, dev))
         qf = hf.pad_qk(q)
-        layers_k, layers_v, ws = build_tree(hf.pad_qk(k), hf.pad_v(v), d, cos, sin)
+        layers_k, layers_v, ws = build_tree(hf.kv_k(k), hf.kv_v(v), d, cos, sin)
         L = len(layers_k)
         out = torch.empty_like(qf)
         gmax = torch.empty(B, T, H, dtype=torch.float32, device=dev)
         gsum = torch.empty(B, T, H, dtype=torch.float32, device=dev)
-        parents = torch.empty(L, B, T, H_kv, top_k_per_layer, dtype=torch.int32, device=dev)
+        parents = torch.empty(L, B, T, H_kv * hf.share, top_k_per_layer, dtype=torch.int32,
+                              device=dev)
         lmax = torch.empty(L, B, T, H, dtype=torch.float32, device=dev)
         lsum = torch.empty(L, B, T, H, dtype=torch.float32, device=dev)
         lout = torch.empty(L, B, T, H, hf.D, dtype=torch.float32, device=dev)
@@ -76,6 +77,7 @@ def run_parallel_with_trace(
                                          N.ptr(lout), N.stream_ptr(dev))
         N.check(rc, "htree_forward_trace")
         out, lout = hf.unpad_v(out), hf.unpad_v(lout)
+        parents = hf.pick(parents, 3)
     layers = {
         l: LayerTrace(layer_idx=l,
                       selected_parents=parents[l - 1] if l > 0 else None,

@@ -42,7 +42,8 @@ enum htree_status {
                               algorithm's rules (powers of two,
                               max_top_nodes <= top_k * compression_rate) */
   HTREE_EUNSUPPORTED = -4, /* legal for the reference, outside this build:
-                              D not in {32, 64, 128}, G = H/H_kv > 16,
+                              D not in {32, 64, 128}, G = H/H_kv > 16
+                              (see kv_share for G <= 32),
                               compression_rate outside [4, 64],
                               top_k > 512, top_k * compression_rate > 8192,
                               more than HTREE_MAX_LEVELS levels, or a
@@ -64,6 +65,17 @@ typedef struct htree_dims {
   int32_t max_top_nodes;    /* MTN: build levels while N_l > MTN            */
   int32_t dtype;            /* enum htree_dtype of q, k, v, out             */
   int32_t rope_rows;        /* rows of the cos/sin tables (>= top_k * CR)   */
+  int32_t kv_share;         /* 0 or 1: every KV head selects on its own.
+                               2: KV heads 2i and 2i+1 hold the same keys and
+                               values and share one Top-K selection (their
+                               query heads' importances are summed): a query
+                               group of G heads, 16 < G <= 32, G even, runs
+                               as two groups of G/2 heads over duplicated KV
+                               heads (H_kv here counts the duplicates).  The
+                               backward needs nothing more: each KV head of a
+                               pair gets its half's dk / dv, the caller adds
+                               the pair.  Register forward only
+                               (top_k * max(CR, 16) <= 256). */
 } htree_dims;
 
 /* Static description of a status code (host). */

@@ -36,10 +36,11 @@ def test_strerror_covers_codes():
 
 def dims(**kw):
     base = dict(B=1, T=32768, H=32, H_kv=2, D=128, compression_rate=16, top_k=16,
-                max_top_nodes=128, dtype=torch.bfloat16, rope_rows=1152)
+                max_top_nodes=128, dtype=torch.bfloat16, rope_rows=1152, kv_share=1)
     base.update(kw)
     return N.dims(base["B"], base["T"], base["H"], base["H_kv"], base["D"], base["compression_rate"],
-                  base["top_k"], base["max_top_nodes"], base["dtype"], base["rope_rows"])
+                  base["top_k"], base["max_top_nodes"], base["dtype"], base["rope_rows"],
+                  base["kv_share"])
 
 
 @pytest.mark.parametrize("T,CR,MTN", [(32768, 16, 128), (131072, 32, 256), (65536, 16, 128),
@@ -57,6 +58,11 @@ def test_baseline_level_counts():
     assert len(N.levels(dims(T=65536))) == 4
 
 
+def test_shared_kv_heads_accepted():
+    # a group of 32 query heads as two groups of 16 over duplicated KV heads
+    assert len(N.levels(dims(H=64, H_kv=4, kv_share=2))) == 3
+
+
 @pytest.mark.parametrize("kw,code", [
     (dict(H=30, H_kv=4), N.HTREE_ESHAPE),
     (dict(T=0), N.HTREE_ESHAPE),
@@ -65,7 +71,12 @@ def test_baseline_level_counts():
     (dict(max_top_nodes=512), N.HTREE_ECONFIG),        # > top_k * CR
     (dict(rope_rows=100), N.HTREE_ECONFIG),
     (dict(D=96), N.HTREE_EUNSUPPORTED),
-    (dict(H=64, H_kv=2), N.HTREE_EUNSUPPORTED),        # group of 32
+    (dict(H=64, H_kv=2), N.HTREE_EUNSUPPORTED),        # group of 32 without kv_share
+    (dict(H=96, H_kv=2, kv_share=2), N.HTREE_EUNSUPPORTED),  # 48 heads per kernel group
+    (dict(H=32, H_kv=3, kv_share=2), N.HTREE_ESHAPE),  # kv_share 2 needs an even H_kv
+    (dict(kv_share=3), N.HTREE_ESHAPE),
+    (dict(H=64, H_kv=4, kv_share=2, compression_rate=32, top_k=32, max_top_nodes=256,
+          rope_rows=1280), N.HTREE_EUNSUPPORTED),      # shared selection: register forward only
     (dict(D=16), N.HTREE_EUNSUPPORTED),
     (dict(top_k=1024, max_top_nodes=128, rope_rows=16384), N.HTREE_EUNSUPPORTED),  # top_k > 512
     (dict(top_k=512, compression_rate=32, max_top_nodes=128, rope_rows=16384),

@@ -146,3 +146,53 @@ def test_separate_value_dim(cfg):
         for got, ref in ((qg.grad, dq), (kg.grad, dk), (vg.grad, dv)):
             ok, w = close(f(got), f(ref.to(got.dtype)), dtype)
             assert ok, w
+
+
+G_CASES = [
+    # B, T, H, Hkv, D, CR, TK, MTN, dtype, seed
+    (1, 1501, 32, 1, 128, 16, 16, 128, "bfloat16", 71),  # G = 32; 1501 pairs: a last block half empty
+    (1, 1500, 48, 2, 64, 8, 16, 128, "float32", 72),      # G = 24
+    (2, 900, 64, 2, 32, 16, 8, 128, "float16", 73),       # G = 32, two batches, two KV heads
+]
+
+
+@pytest.mark.parametrize("cfg", G_CASES, ids=lambda c: f"G{c[2] // c[3]}D{c[4]}cr{c[5]}{c[8]}")
+def test_query_groups_over_16_heads(cfg):
+    """Groups of 17..32 query heads (the reference pads them to G_PAD,
+    src/parallel.py:1023): forward, backward, trace and both autograd modes
+    against the oracle, which restates any group size directly."""
+    import htree_amd
+
+    B, T, H, Hkv, D, CR, TK, MTN, dtype, seed = cfg
+    print(f"case {cfg}", flush=True)
+    q, k, v, dO = seeded(B, T, H, Hkv, D, D, dtype, seed)
+    qd, kd, vd, dOd = (x.to(DEV) for x in (q, k, v, dO))
+    out, par, gmax, gsum, ctx = htree_amd.htree_forward_parents(qd, kd, vd, CR, MTN, TK)
+    assert par.shape == (ctx["num_layers"], B, T, Hkv, TK)
+    assert ctx["per_layer_parents"][0].shape == (B, T, Hkv, TK)
+    dq, dk, dv = htree_amd.htree_backward(dOd, qd, out, ctx)
+    torch.cuda.synchronize()
+    assert dk.shape == k.shape and dv.shape == v.shape
+    f = lambda x: x.float().cpu().numpy()
+    tree = orc.Tree(k.float().numpy(), v.float().numpy(), CR, MTN, TK, dtype)
+    for l in range(1, tree.L):
+        assert np.array_equal(f(ctx["layers_k"][l]), tree.lk[l])
+    parn = par.cpu().numpy()
+    rep = check_forward(q, k, v, CR, TK, MTN, dtype, out_dev=f(out), parents_dev=parn, tree=tree,
+                        gmax_dev=f(gmax), gsum_dev=f(gsum))
+    rep.update(check_backward(q, k, v, dO, CR, TK, MTN, dtype, f(out), parn, f(gmax), f(gsum), f(dq),
+                              f(dk), f(dv), tree=tree))
+    print(rep, flush=True)
+    tout, tr = htree_amd.run_parallel_with_trace(qd, kd, vd, CR, MTN, TK, None, 10000.0)
+    torch.cuda.synchronize()
+    for l in range(1, tr["num_layers"]):
+        assert torch.equal(tr["layers"][l].selected_parents, par[l - 1]), l
+    ok, w = close(f(tout), f(out), dtype)
+    assert ok, w
+    for save in (True, False):
+        qg, kg, vg = (x.clone().requires_grad_(True) for x in (qd, kd, vd))
+        o = htree_amd.htree_forward_triton_autograd(qg, kg, vg, CR, MTN, TK, _save_parents=save)
+        o.backward(dOd)
+        for got, ref in ((qg.grad, dq), (kg.grad, dk), (vg.grad, dv)):
+            ok, w = close(f(got), f(ref.to(got.dtype)), dtype)
+            assert ok, w
