@@ -283,8 +283,8 @@ __global__ __launch_bounds__(256) void prep_kernel(const T* __restrict__ o, cons
 // ---------------------------------------------------------------- pack
 // KT: K~ transposed per 16-node block, element (d, c) of block blk at
 // blk*16D + (d/16)*256 + (c/4)*64 + (d%16)*4 + c%4, so that the 4-node pieces
-// one MFMA operand read takes lie contiguous; the V source VH[blk][d][c] is
-// written back as rows VR[node][d].  One thread per (bh, node, d).
+// one MFMA operand read takes lie contiguous; the V source
+// VH[blk][c/4][d][c%4] is written back as rows VR[node][d].  One thread per (bh, node, d).
 __global__ __launch_bounds__(256) void pack_bwd_kernel(
     const uint16_t* __restrict__ kh, const uint16_t* __restrict__ kl,
     const uint16_t* __restrict__ vh, const uint16_t* __restrict__ vl, int64_t Np, int D,
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(256) void pack_bwd_kernel(
   const int c = (int)(node & 15);
   const int64_t tr = (bh * (Np / 16) + node / 16) * D * 16 + (dd >> 4) * 256 + (c >> 2) * 64 +
                      (dd & 15) * 4 + (c & 3);
-  const int64_t vsrc = ((bh * (Np / 16) + node / 16) * D + dd) * 16 + c;
+  const int64_t vsrc = (bh * (Np / 16) + node / 16) * D * 16 + (c >> 2) * 4 * D + dd * 4 + (c & 3);
   if (kt_h) kt_h[tr] = kh[idx];
   if (kt_l) kt_l[tr] = kl[idx];
   vr_h[idx] = vh[vsrc];

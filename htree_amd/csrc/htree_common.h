@@ -28,7 +28,9 @@ constexpr int kWideMaxTK = 512;
 // ---------------------------------------------------------------- plan
 // Packed operand tree, per level l (all bf16, Np = N rounded up to 16):
 //   KH/KL [B][H_kv][Np][D]      hi / lo bf16 split of R(K_l[node], node mod CR)
-//   VH/VL [B][H_kv][Np/16][D][16]  V_l transposed in blocks of 16 nodes
+//   VH/VL [B][H_kv][Np/16][4][D][4]  V_l transposed in blocks of 16 nodes,
+//                               each block as four quads of 4 nodes
+//                               (element (d, c) at (c/4)*4D + d*4 + c%4)
 // Scores always use the split product (plain bf16 scores err by ~2e-2 when
 // |q||k| is large, e.g. clustered keys); VL exists for fp32/fp16 inputs only
 // (bf16 V is exact in VH).

@@ -233,13 +233,16 @@ struct TileStage {
       kl[m] = *(const bf16x8*)(row + St::OFF_KL + dslot<D>(ln >> 4, m) * 2);
     }
   }
-  // V^T fragments: nodes c0 .. c0+3 of the staged block at d = 16n + u16
+  // V^T fragments: nodes c0 .. c0+3 (one quad, c0 % 4 == 0) of the staged
+  // block at d = 16n + u16: the 16 lanes of a lane group read 128
+  // contiguous bytes (no bank conflicts)
   __device__ __forceinline__ void vread(s16x4 (&vh)[D / 16], s16x4 (&vl)[D / 16], int c0,
                                         int u16) const {
 #pragma unroll
     for (int n = 0; n < D / 16; ++n) {
-      vh[n] = *(const s16x4*)(slot + St::OFF_V + ((16 * n + u16) * 16 + c0) * 2);
-      if (PREC) vl[n] = *(const s16x4*)(slot + St::OFF_VL + ((16 * n + u16) * 16 + c0) * 2);
+      const int e = (c0 >> 2) * 4 * D + (16 * n + u16) * 4;
+      vh[n] = *(const s16x4*)(slot + St::OFF_V + e * 2);
+      if (PREC) vl[n] = *(const s16x4*)(slot + St::OFF_VL + e * 2);
     }
   }
 };
@@ -900,11 +903,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     // ---- O^T += V^T P^T over the tiles, V double-buffered
     auto vload = [&](int tau, s16x4 (&vh)[ND], s16x4 (&vl)[ND]) {
       const int vn = node0_of(tau) + (4 * kg < CRU ? 4 * kg : 0);
-      const int64_t vbase = ((int64_t)(vn >> 4) * D + u16) * 16 + (vn & 15);
+      const int64_t vbase = (int64_t)(vn >> 4) * 16 * D + ((vn & 15) >> 2) * 4 * D + u16 * 4;
 #pragma unroll
       for (int n = 0; n < ND; ++n) {
-        vh[n] = *(const s16x4*)(VH + vbase + (int64_t)n * 256);
-        if (PREC) vl[n] = *(const s16x4*)(VL + vbase + (int64_t)n * 256);
+        vh[n] = *(const s16x4*)(VH + vbase + (int64_t)n * 64);
+        if (PREC) vl[n] = *(const s16x4*)(VL + vbase + (int64_t)n * 64);
       }
     };
     auto pv_tile = [&](int tau, const s16x4 (&vh)[ND], const s16x4 (&vl)[ND]) {
@@ -1229,13 +1232,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 ? 4
         pl[r] = PREC ? f_to_bfs(p[r] - bf_to_f(hb)) : (short)0;
       }
       const int vn = node0 + (4 * kg < CRU ? 4 * kg : 0);
-      const int64_t vbase = ((int64_t)(vn >> 4) * D + u16) * 16 + (vn & 15);
+      const int64_t vbase = (int64_t)(vn >> 4) * 16 * D + ((vn & 15) >> 2) * 4 * D + u16 * 4;
 #pragma unroll
       for (int n = 0; n < ND; ++n) {
-        const s16x4 vf = *(const s16x4*)(VH + vbase + (int64_t)n * 256);
+        const s16x4 vf = *(const s16x4*)(VH + vbase + (int64_t)n * 64);
         O[n] = mma16(vf, ph, O[n]);
         if (PREC) {
-          const s16x4 vfl = *(const s16x4*)(VL + vbase + (int64_t)n * 256);
+          const s16x4 vfl = *(const s16x4*)(VL + vbase + (int64_t)n * 64);
           O[n] = mma16(vf, pl, O[n]);
           O[n] = mma16(vfl, ph, O[n]);
         }

@@ -98,7 +98,9 @@ __global__ __launch_bounds__(256) void pool_kernel(const T* __restrict__ src,
 }
 
 // Packs one level: K rotated by its node's child index (node mod CR) and
-// split into bf16 hi/lo; V transposed per 16-node block.  One thread per
+// split into bf16 hi/lo; V transposed per 16-node block, in 4-node quads
+// (a lane's MFMA piece, 4 nodes at one d, is 8 contiguous bytes, and the 16
+// lanes reading 16 consecutive d of one quad read 128 contiguous bytes).  One thread per
 // (b, h, node, i < D/2), handling the RoPE pair (i, i + D/2).
 template <typename T>
 __global__ __launch_bounds__(256) void pack_kernel(
@@ -135,13 +137,15 @@ __global__ __launch_bounds__(256) void pack_kernel(
   split_bf(r1, hi, lo);
   kh[krow + i + half] = hi;
   if (kl) kl[krow + i + half] = lo;
-  const int64_t vb = (bh * (Np / 16) + node / 16) * D * 16 + (node & 15);
+  // V^T block of 16 nodes as four 4-node quads: element (d, c) at
+  // (c / 4) * 4D + d * 4 + c % 4
+  const int64_t vb = (bh * (Np / 16) + node / 16) * D * 16 + ((node & 15) >> 2) * 4 * D + (node & 3);
   split_bf(v0, hi, lo);
-  vh[vb + (int64_t)i * 16] = hi;
-  if (vl) vl[vb + (int64_t)i * 16] = lo;
+  vh[vb + (int64_t)i * 4] = hi;
+  if (vl) vl[vb + (int64_t)i * 4] = lo;
   split_bf(v1, hi, lo);
-  vh[vb + (int64_t)(i + half) * 16] = hi;
-  if (vl) vl[vb + (int64_t)(i + half) * 16] = lo;
+  vh[vb + (int64_t)(i + half) * 4] = hi;
+  if (vl) vl[vb + (int64_t)(i + half) * 4] = lo;
 }
 
 template <typename T>
