@@ -42,7 +42,10 @@ def _check_parents(parents, B, T, H_kv, TK, CR, MTN, device):
     """Caller-supplied lists go to the kernels as they are: hold them to what
     the forward produces (src/naive.py:88-118, :204-207): list l names nodes
     of level l + 1 (the virtual top parents at the top level), ascending,
-    padded with -1 at the end."""
+    padded with -1 at the end.  The list of the highest level that
+    accumulates is fixed by the algorithm, whatever the data: the virtual
+    parents 0 .. (t / CR^l) / CR (src/naive.py:108-118), which is also every
+    top node up to t's when a top level of <= top_k nodes keeps them all."""
     sizes = level_sizes(T, CR, MTN)
     L = len(sizes)
     assert parents.shape == (L, B, T, H_kv, TK) and parents.dtype == torch.int32, \
@@ -56,6 +59,13 @@ def _check_parents(parents, B, T, H_kv, TK, CR, MTN, device):
         assert bool((valid[..., 1:] <= valid[..., :-1]).all()), f"level {l}: -1 padding must come last"
         assert bool(((p[..., 1:] > p[..., :-1]) | ~valid[..., 1:]).all()), \
             f"level {l}: parent lists must be ascending"
+    ltop = L - 2 if L > 1 and sizes[-1] <= TK else L - 1
+    t = torch.arange(T, device=device)
+    nvp = (t // CR ** ltop) // CR + 1
+    slot = torch.arange(TK, device=device)
+    fixed = torch.where(slot[None, :] < nvp[:, None], slot[None, :], -1).to(torch.int32)
+    assert bool((parents[ltop] == fixed[None, :, None, :]).all()), \
+        f"level {ltop}: the top list must be the virtual parents 0 .. (t / CR^{ltop}) / CR"
 
 
 def infer_max_top_nodes(T: int, CR: int, TK: int, L: int) -> int:

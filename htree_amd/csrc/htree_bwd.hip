@@ -63,12 +63,24 @@ struct BwdPlan {
   int64_t off_dsexp[HTREE_MAX_LEVELS]; // bf16 inputs: exponent of every stored dS tile
   int ds_elems;                        // 16-bit values per stored dS tile (256 or 512)
   bool use_ds;                         // dq from the stored dS (else recomputed)
+  // Rows of a level are its parents (vcr = CR children each) except at the
+  // merged level `vlevel` (-1: none): a top level whose lists are the
+  // data-independent prefix [0, t's parent] (the initial virtual parents,
+  // or every top node up to t's when the top level keeps all of them) is
+  // viewed with 64-child parents (vcr = 64, four 16-child tiles, vm real
+  // parents each), so each query is staged once per 64 children instead of
+  // once per CR.  Used with the training forward's stored scores.
+  int vcr[HTREE_MAX_LEVELS], vlg[HTREE_MAX_LEVELS], vtpp[HTREE_MAX_LEVELS], vm[HTREE_MAX_LEVELS];
+  int vlevel;
+  int64_t off_vlist;                   // the merged level's lists [B,T,H_kv,TK]
+  int64_t max_ptiles;                  // pieces x tiles per piece, largest level
   int64_t bytes;
 };
 
 // allow_ds = false: the plan without the stored dS (dq recomputes the scores),
-// the smallest workspace the backward runs in.
-static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true) {
+// the smallest workspace the backward runs in.  view = true: the merged
+// top level where it applies (stored scores and stored dS required).
+static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true, bool view = false) {
   memset(b, 0, sizeof(*b));
   int rc = make_plan(d, &b->P);
   if (rc) return rc;
@@ -77,31 +89,78 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true) 
   b->G = d->H / d->H_kv;
   b->tpp = CR > 16 ? CR / 16 : 1;
   b->W = (d->T + 31) / 32;
+  b->vlevel = -1;
   const int64_t BH = (int64_t)d->B * d->H_kv;
-  b->max_rows = 0;
   for (int l = 0; l < P.L; ++l) {
-    b->rows[l] = BH * ((P.N[l] + CR - 1) / CR);
-    if (b->rows[l] > b->max_rows) b->max_rows = b->rows[l];
+    b->vcr[l] = CR;
+    b->vlg[l] = P.cr_log2;
+    b->vtpp[l] = b->tpp;
+    b->vm[l] = 1;
   }
-  b->max_entries = BH * d->T * d->top_k;
   // Rows are cut into pieces (one dkv wave each) of 32..128 entries: at
   // least 8K pieces for a level's largest possible entry count, so that a
   // level's waves fill the GPU's ~2K wave slots many times over and the
   // kernel's tail stays short, and long rows of popular parents spread over
   // many waves.  Beyond 2^20 pieces per level (16 MB of fp32 partials per 1K
   // pieces and tile at D=128) the pieces grow instead.
-  b->max_pieces = 0;
-  for (int l = 0; l < P.L; ++l) {
-    const int64_t Pl = (P.N[l] + CR - 1) / CR;
-    b->ent[l] = BH * d->T * (d->top_k < Pl ? d->top_k : Pl);
-    if (b->ent[l] > INT32_MAX) return HTREE_EUNSUPPORTED;  // entries are indexed in int32
-    // (256-entry pieces only for levels with at least 32K of them: C4)
-    int64_t piece = b->ent[l] / 256 >= (1ll << 15) ? 256 : 128;
-    while (piece > 32 && b->ent[l] / piece < (1ll << 13)) piece >>= 1;
-    while (b->ent[l] / piece > (1ll << 20)) piece <<= 1;
-    b->piece[l] = piece;
-    const int64_t np = (b->ent[l] + piece - 1) / piece + b->rows[l];
-    if (np > b->max_pieces) b->max_pieces = np;
+  auto size_levels = [&]() -> int {
+    b->max_rows = 0;
+    b->max_pieces = 0;
+    b->max_ptiles = 0;
+    for (int l = 0; l < P.L; ++l) {
+      const int64_t Pl = (P.N[l] + b->vcr[l] - 1) / b->vcr[l];
+      b->rows[l] = BH * Pl;
+      if (b->rows[l] > b->max_rows) b->max_rows = b->rows[l];
+      b->ent[l] = BH * d->T * (d->top_k < Pl ? d->top_k : Pl);
+      if (b->ent[l] > INT32_MAX) return HTREE_EUNSUPPORTED;  // entries are indexed in int32
+      // (256-entry pieces only for levels with at least 32K of them: C4)
+      int64_t piece = b->ent[l] / 256 >= (1ll << 15) ? 256 : 128;
+      while (piece > 32 && b->ent[l] / piece < (1ll << 13)) piece >>= 1;
+      while (b->ent[l] / piece > (1ll << 20)) piece <<= 1;
+      b->piece[l] = piece;
+      const int64_t np = (b->ent[l] + piece - 1) / piece + b->rows[l];
+      if (np > b->max_pieces) b->max_pieces = np;
+      if (np * b->vtpp[l] > b->max_ptiles) b->max_ptiles = np * b->vtpp[l];
+    }
+    return HTREE_OK;
+  };
+  rc = size_levels();
+  if (rc) return rc;
+  b->max_entries = BH * d->T * d->top_k;
+  // dS of every (entry, tile), kept for the dq pass when the whole backward's
+  // worth fits the budget; otherwise dq recomputes the scores.  bf16
+  // inputs: one fp16 value per (head, candidate) scaled by 2^-e with e per
+  // tile, 512 B a tile (11 significant bits, as many as the reference's tf32
+  // dq product carries); fp16 / fp32 inputs: bf16 hi + lo, 1 KB a tile.
+  b->ds_elems = P.precise ? 512 : 256;
+  int64_t ds_total = 0;
+  for (int l = 0; l < P.L; ++l) ds_total += b->ent[l] * b->tpp * b->ds_elems * 2;
+  // (wide configurations: dq recomputes, its list per wave lives in LDS).
+  // HTREE_DS_BUDGET_MB overrides the budget (read at every plan: keep it
+  // fixed between the workspace query and the backward call, which checks
+  // the workspace it is given against its own plan).
+  int64_t budget = kDsBudget;
+  {
+    int dev = 0;
+    size_t total = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceTotalMem(&total, dev) == hipSuccess && total > 0)
+      budget = (int64_t)(total / 3);
+  }
+  if (const char* e = getenv("HTREE_DS_BUDGET_MB")) budget = (int64_t)atoll(e) << 20;
+  b->use_ds = allow_ds && !P.wide && ds_total <= budget;
+  // the merged top level (stored scores: bf16, <= 16 tiles per level)
+  const int Ltop = (P.L > 1 && P.N[P.L - 1] <= d->top_k) ? P.L - 2 : P.L - 1;
+  // (a merged entry's four tiles index the stored scores of tiles 4 s' .. 4 s' + 3
+  // of the query: they must lie within the query's max_tiles)
+  if (view && b->use_ds && !P.precise && P.max_tiles <= 16 && (CR == 16 || CR == 32) &&
+      P.N[Ltop] > CR && 4 * ((P.N[Ltop] + 63) / 64) <= P.max_tiles) {
+    b->vlevel = Ltop;
+    b->vcr[Ltop] = 64;
+    b->vlg[Ltop] = 6;
+    b->vtpp[Ltop] = 4;
+    b->vm[Ltop] = 64 / CR;
+    rc = size_levels();
+    if (rc) return rc;
   }
   int64_t off = 0;
   auto take = [&](int64_t bytes) {
@@ -131,36 +190,28 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true) 
   b->off_poff = take((b->max_rows + 1) * 4);
   b->off_npieces = take(4);
   b->off_ptab = take(b->max_pieces * 3 * 4);
-  // dS of every (entry, tile), kept for the dq pass when the whole backward's
-  // worth fits the budget; otherwise dq recomputes the scores.  bf16
-  // inputs: one fp16 value per (head, candidate) scaled by 2^-e with e per
-  // tile, 512 B a tile (11 significant bits, as many as the reference's tf32
-  // dq product carries); fp16 / fp32 inputs: bf16 hi + lo, 1 KB a tile.
-  b->ds_elems = P.precise ? 512 : 256;
+  b->off_vlist = b->vlevel >= 0 ? take(b->max_entries * 4) : -1;
   const int64_t* ent = b->ent;
-  int64_t ds_total = 0;
-  for (int l = 0; l < P.L; ++l) ds_total += ent[l] * b->tpp * b->ds_elems * 2;
-  // (wide configurations: dq recomputes, its list per wave lives in LDS).
-  // HTREE_DS_BUDGET_MB overrides the budget (read at every plan: keep it
-  // fixed between the workspace query and the backward call, which checks
-  // the workspace it is given against its own plan).
-  int64_t budget = kDsBudget;
-  {
-    int dev = 0;
-    size_t total = 0;
-    if (hipGetDevice(&dev) == hipSuccess && hipDeviceTotalMem(&total, dev) == hipSuccess && total > 0)
-      budget = (int64_t)(total / 3);
-  }
-  if (const char* e = getenv("HTREE_DS_BUDGET_MB")) budget = (int64_t)atoll(e) << 20;
-  b->use_ds = allow_ds && !P.wide && ds_total <= budget;
   for (int l = 0; l < P.L; ++l) {
     b->off_rec[l] = b->use_ds ? take(ent[l] * 16) : l == 0 ? take(b->max_entries * 16) : b->off_rec[0];
     b->off_emap[l] = b->use_ds ? take(b->max_entries * 16) : -1;
-    b->off_ds[l] = b->use_ds ? take(ent[l] * b->tpp * b->ds_elems * 2) : -1;
-    b->off_dsexp[l] = (b->use_ds && !P.precise) ? take(ent[l] * b->tpp * 4) : -1;
+    b->off_ds[l] = b->use_ds ? take(ent[l] * b->vtpp[l] * b->ds_elems * 2) : -1;
+    b->off_dsexp[l] = (b->use_ds && !P.precise) ? take(ent[l] * b->vtpp[l] * 4) : -1;
   }
-  b->off_partial = take(b->max_pieces * b->tpp * 16 * (int64_t)d->D * 2 * 4);
+  b->off_partial = take(b->max_ptiles * 16 * (int64_t)d->D * 2 * 4);
   b->bytes = off;
+  return HTREE_OK;
+}
+
+// Workspace for the stored-dS backward, with or without the merged top
+// level (the call takes the merged plan when it gets stored scores).
+static int bwd_full_bytes(const htree_dims* d, int64_t* bytes) {
+  BwdPlan a, m;
+  int rc = make_bwd_plan(d, &a, true, false);
+  if (rc) return rc;
+  rc = make_bwd_plan(d, &m, true, true);
+  if (rc) return rc;
+  *bytes = a.bytes > m.bytes ? a.bytes : m.bytes;
   return HTREE_OK;
 }
 
@@ -489,6 +540,20 @@ __global__ __launch_bounds__(256) void piece_kernel(const int32_t* __restrict__ 
   ptab[3 * k + 2] = c - i * piece < piece ? c - i * piece : piece;
 }
 
+
+// Lists of the merged top level (64-child parents): a query group whose node
+// at the level is r lists 64-child parents 0 .. r / 64, -1 padded to TK.
+__global__ __launch_bounds__(256) void prefix_list_kernel(int T, int Hkv, int TK, int64_t pw,
+                                                          int lg, int64_t total,
+                                                          int32_t* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int s = (int)(idx % TK);
+  const int64_t grp = idx / TK;
+  const int t = (int)((grp / Hkv) % T);
+  const int64_t np = ((t / pw) >> lg) + 1;
+  out[idx] = s < np ? s : -1;
+}
 
 // One lane per (query group, slot s): the entry of (parent p's row, t) is
 // found from the row bitmap's word prefix, and gets the rotation row
@@ -1424,6 +1489,10 @@ struct DqDsLevel {
   const uint16_t* ds;
   const int32_t* dsexp;         // fp16 form: exponent of each dS tile
   int64_t Np, pw;
+  // the merged top level: real slot s is slot s >> vshift of the records,
+  // its tiles are tiles (s & (2^vshift - 1)) * tiles-per-parent + chunk of
+  // that entry, which holds tppl tiles (0 / the level's own elsewhere)
+  int vshift, tppl;
 };
 
 struct DqDsArgs {
@@ -1482,7 +1551,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void d
     const int pe = lane < TK ? a.parents[l * lstride + grp * TK + lane] : -1;
     const int np = __popcll(__ballot(pe >= 0));
     if (np <= 0) continue;
-    const int4 sr = pe >= 0 ? P.emap[grp * TK + lane] : make_int4(0, 0, 0, 0);
+    const int4 sr = pe >= 0 ? P.emap[grp * TK + (lane >> P.vshift)] : make_int4(0, 0, 0, 0);
+    const int rtpp = CR > 16 ? CR >> 4 : 1;  // tiles per real parent
+    const int vmask = (1 << P.vshift) - 1;
     const int ct = (int)((t / P.pw) & (CR - 1));
     const int apos = ((np - 1) << crlg) + ct;
     const int nt = wide ? ((apos + 16) >> 4) : np;
@@ -1494,7 +1565,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void d
       const uint32_t mlo = (uint32_t)__builtin_amdgcn_readlane(sr.y, s);
       const uint32_t mhi = (uint32_t)__builtin_amdgcn_readlane(sr.z, s);
       const unsigned long long m64 = ((unsigned long long)mhi << 32) | mlo;
-      return (uint32_t)(m64 >> (chunk << 4)) & cmask;
+      const int vt = (s & vmask) * rtpp + chunk;  // tile within the record's entry
+      return (uint32_t)(m64 >> (vt << 4)) & cmask;
     };
     auto next_tile = [&](int tau, int& s, int& chunk) {
       while (tau < nt && !tmask(tau, s, chunk)) ++tau;
@@ -1506,7 +1578,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void d
     auto issue = [&](int s, int chunk, int& ex) {
       const int node0 = (__builtin_amdgcn_readlane(pe, s) << crlg) + (chunk << 4);
       const int64_t blk = (hrow + (node0 & ~15)) / 16;
-      const int64_t et = (int64_t)__builtin_amdgcn_readlane(sr.x, s) * tpp + chunk;
+      const int64_t et =
+          (int64_t)__builtin_amdgcn_readlane(sr.x, s) * P.tppl + (s & vmask) * rtpp + chunk;
       if (F16) ex = P.kexp[blk] + P.dsexp[et];
       const char* kth = (const char*)(P.kt_h + blk * D * 16);
 #pragma unroll
@@ -1653,21 +1726,31 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
   // its own, so the passes start one level lower.
   const int Ltop = (P.L > 1 && P.N[P.L - 1] <= d->top_k) ? P.L - 2 : P.L - 1;
   for (int l = Ltop; l >= 0; --l) {
-    const int64_t Pl = (P.N[l] + CR - 1) / CR;
+    // the level's rows: parents of vcr children (64 at the merged level)
+    const int CRl = BP.vcr[l], lgl = BP.vlg[l], tppl = BP.vtpp[l];
+    const int64_t Pl = (P.N[l] + CRl - 1) / CRl;
     const int64_t nrows = BP.rows[l];
     const int64_t words = nrows * BP.W;
     const int64_t ent = lstride;
+    const int32_t* parl = parents + l * lstride;
+    if (l == BP.vlevel) {
+      // the merged level's lists: 64-child parents 0 .. (t's node) / 64
+      int32_t* vl = (int32_t*)(ws + BP.off_vlist);
+      hipLaunchKernelGGL(prefix_list_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
+                         d->T, d->H_kv, d->top_k, P.pw[l], lgl, ent, vl);
+      parl = vl;
+    }
     // dense bitmaps (at least one entry per four words: upper levels, and
     // C2's and C4's level 0) by columns; sparser ones by global atomics
     // (C5's level 0, one per eight: columns measured +0.6% of its backward)
     if (4 * BP.ent[l] >= words) {
       hipLaunchKernelGGL(bitmap_cols_kernel, dim3((unsigned)(BH * BP.W)), dim3(256), 0, st,
-                         parents + l * lstride, d->T, d->H_kv, d->top_k, Pl, BP.W, bm);
+                         parl, d->T, d->H_kv, d->top_k, Pl, BP.W, bm);
     } else {
       hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st,
                          bm, words);
       hipLaunchKernelGGL(bitmap_set_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
-                         parents + l * lstride, d->T, d->H_kv, d->top_k, Pl, BP.W, ent, bm);
+                         parl, d->T, d->H_kv, d->top_k, Pl, BP.W, ent, bm);
     }
     hipLaunchKernelGGL(row_scan_kernel, dim3((unsigned)nrows), dim3(256), 0, st, bm, BP.W,
                        (int)BP.piece[l], wpre, cnt, pcnt);
@@ -1685,9 +1768,9 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
                          ent, recs);
     else
       hipLaunchKernelGGL(record_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
-                         parents + l * lstride, l > 0 ? parents + (l - 1) * lstride : nullptr, bm,
-                         wpre, rowoff, d->T, d->H_kv, d->top_k, Pl, BP.W, P.pw[l], CR, P.cr_log2,
-                         ent, recs, BP.use_ds ? (int4*)(ws + BP.off_emap[l]) : nullptr);
+                         parl, l > 0 ? parents + (l - 1) * lstride : nullptr, bm, wpre, rowoff,
+                         d->T, d->H_kv, d->top_k, Pl, BP.W, P.pw[l], CRl, lgl, ent, recs,
+                         BP.use_ds ? (int4*)(ws + BP.off_emap[l]) : nullptr);
     DkvArgs a;
     memset(&a, 0, sizeof(a));
     a.kh = (const uint16_t*)(tws + P.off_kh[l]);
@@ -1716,13 +1799,13 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.H = d->H;
     a.Hkv = d->H_kv;
     a.G = G;
-    a.CR = CR;
-    a.crlg = P.cr_log2;
+    a.CR = CRl;
+    a.crlg = lgl;
     a.TK = d->top_k;
-    a.tpp = BP.tpp;
-    a.max_tiles = P.max_tiles;
+    a.tpp = tppl;
+    a.max_tiles = P.max_tiles;  // the forward's tiles per level (stored-score index)
     a.scale = scale;
-    const int64_t waves = BP.max_pieces * BP.tpp;
+    const int64_t waves = BP.max_pieces * tppl;
     const bool has_s = !PREC && scores;
     if (has_s) {
       a.sc = (const uint16_t*)scores + (int64_t)l * groups * P.max_tiles * 256;
@@ -1733,9 +1816,9 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
   hipLaunchKernelGGL((dkv_kernel<D, PREC, T, HS, PW>),                                         \
                      dim3((unsigned)(PW > 1 ? BP.max_pieces : (waves + 3) / 4)), dim3(PW > 1 ? 64 * PW : 256), \
                      0, st, a)
-    if (BP.tpp == 4) {
+    if (tppl == 4) {
       if (has_s) HT_DKV(true, 4); else HT_DKV(false, 4);
-    } else if (BP.tpp == 2) {
+    } else if (tppl == 2) {
       if (has_s) HT_DKV(true, 2); else HT_DKV(false, 2);
     } else {
       if (has_s) HT_DKV(true, 1); else HT_DKV(false, 1);
@@ -1749,11 +1832,11 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     const int64_t nup = top ? 0 : P.N[l + 1];
     // lane groups per value from the level's mean pieces per row
     const int64_t avg = BP.ent[l] / (BP.piece[l] * BP.rows[l]);
-    const int64_t rt = BP.rows[l] * BP.tpp;
+    const int64_t rt = BP.rows[l] * tppl;
 #define HT_RED(LG)                                                                              \
   hipLaunchKernelGGL(dkv_reduce_kernel<LG>, dim3((unsigned)(rt * d->D * LG / 32)),            \
-                     dim3(256), 0, st, partial, poff, P.N[l], d->H_kv, d->D, CR, P.cr_log2,  \
-                     BP.tpp, Pl, upk, upv, nup, dkl, dvl)
+                     dim3(256), 0, st, partial, poff, P.N[l], d->H_kv, d->D, CRl, lgl, tppl,  \
+                     Pl, upk, upv, nup, dkl, dvl)
     if (avg >= 64)
       HT_RED(16);
     else if (avg >= 8)
@@ -1775,6 +1858,8 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
       a.lv[l].dsexp = BP.off_dsexp[l] >= 0 ? (const int32_t*)(ws + BP.off_dsexp[l]) : nullptr;
       a.lv[l].Np = P.Np[l];
       a.lv[l].pw = P.pw[l];
+      a.lv[l].vshift = BP.vm[l] == 4 ? 2 : BP.vm[l] == 2 ? 1 : 0;
+      a.lv[l].tppl = BP.vtpp[l];
     }
     a.parents = parents;
     a.cosb = cosb;
@@ -1842,11 +1927,11 @@ using namespace htree;
 extern "C" {
 
 int htree_backward_workspace_bytes(const htree_dims* d, int64_t* bytes) {
-  BwdPlan BP;
-  int rc = make_bwd_plan(d, &BP);
+  int64_t n = 0;
+  int rc = bwd_full_bytes(d, &n);
   if (rc) return rc;
   if (!bytes) return HTREE_ENULL;
-  *bytes = BP.bytes;
+  *bytes = n;
   return HTREE_OK;
 }
 
@@ -1873,13 +1958,19 @@ static int backward_impl(const htree_dims* d, float scale, const void* q, const 
   if (!q || !out || !dO || !gmax || !gsum || !parents || !tree_ws || !cos_table || !sin_table ||
       !dq || !dk || !dv || !bwd_ws)
     return HTREE_ENULL;
+  const int64_t sbytes = train_scores_bytes(d, BP.P, nullptr);
+  const char* scores = sbytes > 0 ? (const char*)scores_ws : nullptr;
+  if (scores && scores_bytes < sbytes) return HTREE_EWORKSPACE;
+  // with stored scores, the plan with the merged top level when it fits
+  if (scores) {
+    BwdPlan M;
+    if (make_bwd_plan(d, &M, true, true) == HTREE_OK && M.vlevel >= 0 && bwd_ws_bytes >= M.bytes)
+      BP = M;
+  }
   // a workspace too small for the stored dS but large enough without it:
   // dq recomputes the scores
   if (BP.use_ds && bwd_ws_bytes < BP.bytes) make_bwd_plan(d, &BP, false);
   if (tree_ws_bytes < BP.P.bytes || bwd_ws_bytes < BP.bytes) return HTREE_EWORKSPACE;
-  const int64_t sbytes = train_scores_bytes(d, BP.P, nullptr);
-  const char* scores = sbytes > 0 ? (const char*)scores_ws : nullptr;
-  if (scores && scores_bytes < sbytes) return HTREE_EWORKSPACE;
   hipStream_t st = (hipStream_t)stream;
   const char* tws = (const char*)tree_ws;
   char* ws = (char*)bwd_ws;
@@ -1963,16 +2054,18 @@ int scratch_for_current_device(char** out) {
 extern "C" {
 
 int htree_backward_noalloc_bytes(const htree_dims* d, int64_t* bytes) {
-  BwdPlan BP;
-  int rc = make_bwd_plan(d, &BP);
+  int64_t n = 0;
+  int rc = bwd_full_bytes(d, &n);
   if (rc) return rc;
   if (!bytes) return HTREE_ENULL;
-  if (BP.bytes > HTREE_NOALLOC_SCRATCH_BYTES) {
+  if (n > HTREE_NOALLOC_SCRATCH_BYTES) {
+    BwdPlan BP;
     rc = make_bwd_plan(d, &BP, false);
     if (rc) return rc;
+    n = BP.bytes;
   }
-  *bytes = BP.bytes;
-  return BP.bytes > HTREE_NOALLOC_SCRATCH_BYTES ? HTREE_ESCRATCH : HTREE_OK;
+  *bytes = n;
+  return n > HTREE_NOALLOC_SCRATCH_BYTES ? HTREE_ESCRATCH : HTREE_OK;
 }
 
 int htree_backward_noalloc(const htree_dims* d, float scale, const void* q, const void* out,

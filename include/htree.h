@@ -148,7 +148,9 @@ int htree_backward_workspace_min_bytes(const htree_dims* d, int64_t* bytes);
  * what htree_forward wrote; tree_ws is the packed tree of htree_tree_build.
  * The parent lists are trusted: other lists must keep the forward's form
  * (indices in [-1, ceil(N_l / CR)), ascending, -1 padding last), else the
- * kernels read out of bounds.
+ * kernels read out of bounds; the list of the highest level that
+ * accumulates must be the forward's fixed one (virtual parents
+ * 0 .. (t / CR^l) / CR).
  * Deterministic: no floating-point atomics.
  * Replaces htree_backward (src/backward.py:941-1119) and its kernels K0
  * (:45-68), K1a/K1b (:119-436), K2 (:75-112), K3/K3u (:443-780),

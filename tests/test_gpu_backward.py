@@ -52,6 +52,9 @@ CASES = [
     # 750 level-0 parents > 128 * top_k: a sparse level, whose bitmap is set
     # by atomics (bitmap_set_kernel); five levels
     (1, 3000, 8, 1, 64, 4, 4, 16, "bfloat16", 20),
+    # CR 32 with stored scores: the top level (125 nodes) merged into 64-child
+    # parents of two real ones, the last one partial
+    (1, 4000, 8, 1, 64, 32, 8, 256, "bfloat16", 21),
 ]
 
 

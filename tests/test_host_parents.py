@@ -67,3 +67,18 @@ def test_shape_and_dtype(lists):
         check(lists.to(torch.int64))
     with pytest.raises(AssertionError, match="int32"):
         check(lists[:, :, :-1])
+
+
+def test_top_list_is_fixed(lists):
+    """The highest accumulating level's list is the algorithm's fixed one
+    (the virtual parents); a caller list that drops one of its parents is
+    refused before any launch."""
+    bad = lists.clone()
+    L = bad.shape[0]
+    row = bad[L - 1, 0, -1, 0]
+    n = int((row >= 0).sum())
+    assert n >= 2
+    row[n - 2] = row[n - 1]  # drop the second-to-last virtual parent (keeps ascending)
+    row[n - 1] = -1
+    with pytest.raises(AssertionError, match="top list"):
+        check(bad)
