@@ -66,6 +66,7 @@ struct WaveLds {
   float imp[MAXSLOT * 64];
   float mt[MAXSLOT * 4];
   unsigned long long selmask[MAXSLOT];
+  float lvl_max;  // the level's final running max (KV-head pairs)
 };
 
 
@@ -278,11 +279,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   const int bid = blockIdx.x;
   const int64_t lb = (int64_t)(bid & 7) * a.per_xcd + (bid >> 3);
   const int64_t grp = lb * kWavesPerBlock + wv;
-  if (grp >= (int64_t)a.B * a.Hkv * a.T) return;
-  const int t = (int)(grp % a.T);
-  const int bh = (int)(grp / a.T);
-  const int h = bh % a.Hkv;
-  const int b = bh / a.Hkv;
+  // KV-head pairs (kv_share 2): as in fwd_reg_kernel, waves 2i and 2i+1 take
+  // KV heads 2h, 2h+1 of one query and meet at two block barriers per upper
+  // level; the waves of an empty pair pass the same barriers
+  const bool pair = a.kv_share == 2;
+  if (grp >= (int64_t)a.B * a.Hkv * a.T) {
+    if (pair)
+      for (int l = a.L - 1; l >= 1; --l) {
+        __syncthreads();
+        __syncthreads();
+      }
+    return;
+  }
+  int t, h, b;
+  if (pair) {
+    const int Hr = a.Hkv >> 1;
+    const int64_t pq = grp >> 1;
+    t = (int)(pq % a.T);
+    const int64_t bhr = pq / a.T;
+    h = 2 * (int)(bhr % Hr) + (int)(grp & 1);
+    b = (int)(bhr / Hr);
+  } else {
+    t = (int)(grp % a.T);
+    const int bh = (int)(grp / a.T);
+    h = bh % a.Hkv;
+    b = bh / a.Hkv;
+  }
   WaveLds<MAXSLOT>& W = lds_all[wv];
   char* slot = stage_all[wv];
   const int CRU = CR < 16 ? CR : 16;
@@ -389,7 +411,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
         if (kg == 0) W.imp[(tau << 4) + u16] = e;
         if (lane == 0) W.mt[tau] = Mrun;
       }
-      wave_sync();
+      // a pair's importance: both halves' sums, each from its tile's running
+      // max, taken to the pair's max (the group-shared sum of
+      // src/naive.py:204-205 over all G heads), in a fixed order
+      const WaveLds<MAXSLOT>& W0 = lds_all[wv & ~1];
+      const WaveLds<MAXSLOT>& W1 = lds_all[wv | 1];
+      float Mp = Mrun;
+      if (pair) {
+        if (lane == 0) W.lvl_max = Mrun;
+        __syncthreads();
+        Mp = fmaxf(W0.lvl_max, W1.lvl_max);
+      } else {
+        wave_sync();
+      }
 
       // importance of position j lives in lane j % 64 of slot j / 64; the
       // key is the float's bit pattern + 1 (0 = no candidate), so unsigned
@@ -412,6 +446,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
             float v;
             if (pos == apos) {
               v = 1e6f;  // rightmost candidate always kept (src/naive.py:93)
+            } else if (pair) {
+              v = W0.imp[64 * sl + ln] * expf(W0.mt[tau] - Mp) +
+                  W1.imp[64 * sl + ln] * expf(W1.mt[tau] - Mp);
             } else {
               v = W.imp[64 * sl + ln];
               const float mt = W.mt[tau];
@@ -421,6 +458,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
           }
         }
       }
+      if (pair) __syncthreads();  // the partner has read this wave's importances
       uint32_t thr = 0u;
       for (int bit = 30; bit >= 0; --bit) {
         const uint32_t c = thr | (1u << bit);

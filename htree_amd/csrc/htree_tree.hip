@@ -33,8 +33,9 @@ int make_plan(const htree_dims* d, Plan* p) {
   if ((d->D != 32 && d->D != 64 && d->D != 128) || d->H / d->H_kv > 16 || CR < 4 || CR > 64 ||
       (wide && (d->top_k > kWideMaxTK || (int64_t)d->top_k * CR > kWideMaxPos)))
     return HTREE_EUNSUPPORTED;
-  // shared selections over KV-head pairs: the register forward's paired waves
-  if (d->kv_share == 2 && (wide || max_tiles > 16)) return HTREE_EUNSUPPORTED;
+  // shared selections over KV-head pairs: the paired waves of the
+  // one-wave-per-group forwards (not the block-per-group wide forward)
+  if (d->kv_share == 2 && wide) return HTREE_EUNSUPPORTED;
 
   memset(p, 0, sizeof(*p));
   p->precise = d->dtype != HTREE_BF16;
@@ -202,7 +203,8 @@ const char* htree_strerror(int status) {
              "and rope_rows >= top_k_per_layer * compression_rate";
     case HTREE_EUNSUPPORTED:
       return "configuration outside this HIP build: needs D in {32,64,128}, H/H_kv <= 16 "
-             "(up to 32 with kv_share 2, where top_k_per_layer * max(compression_rate,16) <= 256), "
+             "(up to 32 with kv_share 2, where top_k_per_layer <= 64 and "
+             "top_k_per_layer * max(compression_rate,16) <= 1024), "
              "4 <= compression_rate <= 64, top_k_per_layer <= 512 and "
              "top_k_per_layer * compression_rate <= 8192 (where top_k_per_layer > 64 or "
              "top_k_per_layer * max(compression_rate,16) / 16 > 64); the backward also needs "

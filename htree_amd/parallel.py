@@ -8,8 +8,8 @@ Differences, all deliberate:
     relies on equality.  The reference's Triton-tiling asserts
     (top_k % 64 == 0, top_k % compression_rate == 0, :923,1019) do not apply.
   * limits of this HIP build (AssertionError): max(K, V) in {32, 64, 128}
-    (K even), H / H_kv <= 16 (or even and <= 32 where
-    top_k_per_layer * max(compression_rate, 16) <= 256), 4 <= compression_rate
+    (K even), H / H_kv <= 16 (or even and <= 32 where top_k_per_layer <= 64
+    and top_k_per_layer * max(compression_rate, 16) <= 1024), 4 <= compression_rate
     <= 64, top_k_per_layer <= 512 and top_k_per_layer * compression_rate <=
     8192 candidates per level.
   * a query group of G > 16 heads (the reference pads it to G_PAD,

@@ -74,8 +74,9 @@ typedef struct htree_dims {
                                heads (H_kv here counts the duplicates).  The
                                backward needs nothing more: each KV head of a
                                pair gets its half's dk / dv, the caller adds
-                               the pair.  Register forward only
-                               (top_k * max(CR, 16) <= 256). */
+                               the pair.  Register and streaming forwards
+                               (top_k <= 64, top_k * max(CR, 16) <= 1024),
+                               not the wide one. */
 } htree_dims;
 
 /* Static description of a status code (host). */

@@ -59,8 +59,11 @@ def test_baseline_level_counts():
 
 
 def test_shared_kv_heads_accepted():
-    # a group of 32 query heads as two groups of 16 over duplicated KV heads
+    # a group of 32 query heads as two groups of 16 over duplicated KV heads,
+    # in the register forward (16 tiles per level) and the streaming one (32)
     assert len(N.levels(dims(H=64, H_kv=4, kv_share=2))) == 3
+    assert len(N.levels(dims(T=131072, H=64, H_kv=4, kv_share=2, compression_rate=32, top_k=32,
+                             max_top_nodes=256, rope_rows=1280))) == 3
 
 
 @pytest.mark.parametrize("kw,code", [
@@ -75,8 +78,8 @@ def test_shared_kv_heads_accepted():
     (dict(H=96, H_kv=2, kv_share=2), N.HTREE_EUNSUPPORTED),  # 48 heads per kernel group
     (dict(H=32, H_kv=3, kv_share=2), N.HTREE_ESHAPE),  # kv_share 2 needs an even H_kv
     (dict(kv_share=3), N.HTREE_ESHAPE),
-    (dict(H=64, H_kv=4, kv_share=2, compression_rate=32, top_k=32, max_top_nodes=256,
-          rope_rows=1280), N.HTREE_EUNSUPPORTED),      # shared selection: register forward only
+    (dict(H=64, H_kv=4, kv_share=2, top_k=128, max_top_nodes=128, rope_rows=2048),
+     N.HTREE_EUNSUPPORTED),                            # shared selection: not the wide forward
     (dict(D=16), N.HTREE_EUNSUPPORTED),
     (dict(top_k=1024, max_top_nodes=128, rope_rows=16384), N.HTREE_EUNSUPPORTED),  # top_k > 512
     (dict(top_k=512, compression_rate=32, max_top_nodes=128, rope_rows=16384),

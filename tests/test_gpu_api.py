@@ -153,6 +153,9 @@ G_CASES = [
     (1, 1501, 32, 1, 128, 16, 16, 128, "bfloat16", 71),  # G = 32; 1501 pairs: a last block half empty
     (1, 1500, 48, 2, 64, 8, 16, 128, "float32", 72),      # G = 24
     (2, 900, 64, 2, 32, 16, 8, 128, "float16", 73),       # G = 32, two batches, two KV heads
+    # 64 candidate tiles per level: the streaming forward's paired waves
+    (1, 3001, 32, 1, 128, 32, 32, 256, "bfloat16", 74),  # G = 32, C4's CR / top_k
+    (1, 2500, 48, 2, 32, 8, 64, 256, "float16", 75),      # G = 24, top_k 64, three levels
 ]
 
 
