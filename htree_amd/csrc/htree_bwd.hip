@@ -174,9 +174,10 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true, 
     // K~^T for dq: bf16 hi + lo for fp16 / fp32 inputs (dq = dS K~ cancels:
     // sum dS = 0); for bf16 inputs fp16 scaled per 16-node block by 2^-kexp
     // (11 significant bits, the class of the reference's tf32 product)
+    // V rows for dq_kernel (the stored-dS path reads V from the tree's V^T)
     for (int s = 0; s < 2; ++s) {
       b->off_kt[s][l] = (s == 0 || P.precise) ? take(elems * 2) : -1;
-      b->off_vr[s][l] = (s == 0 || P.precise) ? take(elems * 2) : -1;
+      b->off_vr[s][l] = (!b->use_ds && (s == 0 || P.precise)) ? take(elems * 2) : -1;
     }
     b->off_kexp[l] = P.precise ? -1 : take(BH * (P.Np[l] / 16) * 4);
     b->off_dk[l] = l > 0 ? take((int64_t)d->B * P.N[l] * d->H_kv * d->D * 4) : -1;
@@ -248,6 +249,25 @@ __device__ __forceinline__ void load_frag(const uint16_t* __restrict__ row, int 
                                           bf16x8 (&f)[D / 32]) {
 #pragma unroll
   for (int m = 0; m < D / 32; ++m) f[m] = *(const bf16x8*)(row + dslot<D>(kg, m));
+}
+
+// The same fragment of node `node`'s V row, read from the level's V^T
+// blocks (16-node blocks of 4-node quads, element (d, c) at
+// (c / 4) * 4D + d * 4 + c % 4): 2-byte reads 8 bytes apart.
+template <int D>
+__device__ __forceinline__ void load_frag_vt(const uint16_t* __restrict__ vt, int64_t bh, int64_t Np,
+                                             int64_t node, int kg, bf16x8 (&f)[D / 32]) {
+  const uint16_t* base =
+      vt + (bh * (Np / 16) + node / 16) * 16 * D + ((node & 15) >> 2) * 4 * D + (node & 3);
+#pragma unroll
+  for (int m = 0; m < D / 32; ++m) {
+    const int d0 = dslot<D>(kg, m);
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = (uint32_t)base[(d0 + 2 * e) * 4] | ((uint32_t)base[(d0 + 2 * e + 1) * 4] << 16);
+    f[m] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
+  }
 }
 
 __device__ __forceinline__ int wave_sum_i(int v) {
@@ -353,7 +373,7 @@ __global__ __launch_bounds__(256) void pack_bwd_kernel(
   const int64_t vsrc = (bh * (Np / 16) + node / 16) * D * 16 + (c >> 2) * 4 * D + dd * 4 + (c & 3);
   if (kt_h) kt_h[tr] = kh[idx];
   if (kt_l) kt_l[tr] = kl[idx];
-  vr_h[idx] = vh[vsrc];
+  if (vr_h) vr_h[idx] = vh[vsrc];
   if (vr_l) vr_l[idx] = vl[vsrc];
 }
 
@@ -660,7 +680,7 @@ __global__ __launch_bounds__(256) void record_wide_kernel(
 // ---------------------------------------------------------------- dkv
 struct DkvArgs {
   const uint16_t *kh, *kl;      // K~ rows (hi/lo), [B][Hkv][Np][D]
-  const uint16_t *vr_h, *vr_l;  // V rows
+  const uint16_t *vt_h, *vt_l;  // the tree's V^T blocks (hi / lo) of the level
   const void* q;
   const void* dO;
   const float *gmax, *gsum, *delta;
@@ -926,8 +946,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
       load_frag<D>(a.kh + r, kg, kh);
       load_frag<D>(a.kl + r, kg, kl);
     }
-    load_frag<D>(a.vr_h + r, kg, vh);
-    if (PREC) load_frag<D>(a.vr_l + r, kg, vl);
+    const int64_t vnode = (live ? node0 : 0) + (u16 < CRU ? u16 : 0);
+    load_frag_vt<D>(a.vt_h, bh, a.Np, vnode, kg, vh);
+    if (PREC) load_frag_vt<D>(a.vt_l, bh, a.Np, vnode, kg, vl);
   }
   f32x4 dv[ND], dk[ND];
 #pragma unroll
@@ -1699,7 +1720,9 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
                      (const T*)out, (const T*)dO, groups, d->H, G, delta);
   for (int l = 0; l < P.L; ++l) {
     const int64_t total = BH * P.Np[l] * d->D;
-    hipLaunchKernelGGL(pack_bwd_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
+    // transposed K~ (fp16 / fp32 inputs) and V rows (dq_kernel)
+    if (PREC || !BP.use_ds)
+      hipLaunchKernelGGL(pack_bwd_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
                        (const uint16_t*)(tws + P.off_kh[l]), (const uint16_t*)(tws + P.off_kl[l]),
                        (const uint16_t*)(tws + P.off_vh[l]),
                        P.off_vl[l] >= 0 ? (const uint16_t*)(tws + P.off_vl[l]) : nullptr, P.Np[l],
@@ -1775,8 +1798,8 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     memset(&a, 0, sizeof(a));
     a.kh = (const uint16_t*)(tws + P.off_kh[l]);
     a.kl = (const uint16_t*)(tws + P.off_kl[l]);
-    a.vr_h = U16(BP.off_vr[0][l]);
-    a.vr_l = U16(BP.off_vr[1][l]);
+    a.vt_h = (const uint16_t*)(tws + P.off_vh[l]);
+    a.vt_l = P.off_vl[l] >= 0 ? (const uint16_t*)(tws + P.off_vl[l]) : nullptr;
     a.q = q;
     a.dO = dO;
     a.gmax = gmax;

@@ -75,110 +75,308 @@ int make_plan(const htree_dims* d, Plan* p) {
 }
 
 // ---------------------------------------------------------------- kernels
-// Mean of the <= CR children of each parent, summed in child order in fp32,
-// divided once, rounded to the level dtype (src/naive.py:53-57: upper levels
-// are stored in the input dtype and the next level pools the rounded values).
-template <typename T>
-__global__ __launch_bounds__(256) void pool_kernel(const T* __restrict__ src,
-                                                   T* __restrict__ dst, int64_t Nc,
-                                                   int64_t Np, int Hkv, int D, int CR,
-                                                   int64_t total) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= total) return;
-  const int dd = (int)(idx % D);
-  int64_t r = idx / D;
-  const int h = (int)(r % Hkv);
-  r /= Hkv;
-  const int64_t p = r % Np;
-  const int64_t b = r / Np;
-  const int64_t s0 = p * CR;
-  const int64_t e = s0 + CR < Nc ? s0 + CR : Nc;
-  float acc = 0.f;
-  for (int64_t c = s0; c < e; ++c) acc += Io<T>::ld(src + ((b * Nc + c) * Hkv + h) * D + dd);
-  Io<T>::st(dst + ((b * Np + p) * Hkv + h) * D + dd, acc / (float)(e - s0));
+// The tree in one pass over the leaves: one block per span of kSpan
+// consecutive leaves of one (b, h_kv) stages the span's K rows, then its V
+// rows, in LDS, packs them, and pools every level whose nodes lie inside the
+// span (CR^l <= kSpan), writing and packing those nodes too.  Each higher
+// level (CR^l > kSpan: nodes covering more than one span) is one more launch
+// over its nodes, pooled from the level below.  Pooling follows src/naive.py:53-57: the <= CR children of
+// a parent summed in child order in fp32, divided once, rounded to the level
+// dtype, and the next level pools the rounded values.
+constexpr int kSpan = 64;
+constexpr int kBuildMaxD = 128;
+// nodes above the leaves a span holds: kSpan/CR + kSpan/CR^2 + ... <= 21 (CR 4)
+constexpr int kSpanUpper = 32;
+
+struct BuildArgs {
+  const void* x0[2];                    // leaves: k, v [B][N_0][Hkv][D]
+  void* lx[2][HTREE_MAX_LEVELS];        // levels l >= 1: [B][N_l][Hkv][D]
+  uint16_t* kh[HTREE_MAX_LEVELS];
+  uint16_t* kl[HTREE_MAX_LEVELS];
+  uint16_t* vh[HTREE_MAX_LEVELS];
+  uint16_t* vl[HTREE_MAX_LEVELS];       // nullptr for bf16 inputs
+  int64_t N[HTREE_MAX_LEVELS], Np[HTREE_MAX_LEVELS], pw[HTREE_MAX_LEVELS];
+  const float *cosb, *sinb;
+  int64_t chunks;                       // spans per (b, h_kv)
+  int Hkv, D, CR, L, lspan;             // levels 0 .. lspan-1 come from the span launch
+};
+
+// K~ of nodes nf .. nf+cnt-1 of level l: R(K, node mod CR) split into bf16
+// hi / lo; val(j, e) is element e of node nf + j.  A thread takes 4
+// consecutive RoPE pairs (i, i + D/2) of one node (8-byte stores).
+template <typename F>
+__device__ __forceinline__ void pack_k(const BuildArgs& a, int l, int64_t bh, int64_t nf, int cnt,
+                                       F val) {
+  const int D = a.D, HALF = D / 2, Q = D / 8;
+  uint16_t* kh = a.kh[l];
+  uint16_t* kl = a.kl[l];
+  for (int it = threadIdx.x; it < cnt * Q; it += blockDim.x) {
+    const int j = it / Q, i0 = (it - j * Q) * 4;
+    const int64_t node = nf + j;
+    const int c = (int)(node & (a.CR - 1));
+    const float* cr = a.cosb + (int64_t)c * HALF + i0;
+    const float* sr = a.sinb + (int64_t)c * HALF + i0;
+    float r0[4], r1[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float k0 = val(j, i0 + q), k1 = val(j, i0 + q + HALF);
+      const float cs = cr[q], sn = sr[q];
+      r0[q] = k0 * cs - k1 * sn;  // R(x,p)_lo = x_lo cos - x_hi sin (naive.py:22-28)
+      r1[q] = k0 * sn + k1 * cs;  // R(x,p)_hi = x_lo sin + x_hi cos
+    }
+    uint32_t h0[2], l0[2], h1[2], l1[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      h0[q] = cvt_pk_bf16(r0[2 * q], r0[2 * q + 1]);
+      l0[q] = cvt_pk_bf16(r0[2 * q] - __uint_as_float(h0[q] << 16),
+                          r0[2 * q + 1] - __uint_as_float(h0[q] & 0xffff0000u));
+      h1[q] = cvt_pk_bf16(r1[2 * q], r1[2 * q + 1]);
+      l1[q] = cvt_pk_bf16(r1[2 * q] - __uint_as_float(h1[q] << 16),
+                          r1[2 * q + 1] - __uint_as_float(h1[q] & 0xffff0000u));
+    }
+    const int64_t row = (bh * a.Np[l] + node) * D;
+    *(uint2*)(kh + row + i0) = make_uint2(h0[0], h0[1]);
+    *(uint2*)(kh + row + HALF + i0) = make_uint2(h1[0], h1[1]);
+    *(uint2*)(kl + row + i0) = make_uint2(l0[0], l0[1]);
+    *(uint2*)(kl + row + HALF + i0) = make_uint2(l1[0], l1[1]);
+  }
 }
 
-// Packs one level: K rotated by its node's child index (node mod CR) and
-// split into bf16 hi/lo; V transposed per 16-node block, in 4-node quads
-// (a lane's MFMA piece, 4 nodes at one d, is 8 contiguous bytes, and the 16
-// lanes reading 16 consecutive d of one quad read 128 contiguous bytes).  One thread per
-// (b, h, node, i < D/2), handling the RoPE pair (i, i + D/2).
+// element (d, node) of the level's V^T blocks: 16-node blocks of four
+// 4-node quads, (d, c) at (c / 4) * 4D + d * 4 + c % 4
+__device__ __forceinline__ int64_t vt_index(const BuildArgs& a, int l, int64_t bh, int64_t node,
+                                            int d) {
+  return (bh * (a.Np[l] / 16) + node / 16) * a.D * 16 + ((node & 15) >> 2) * 4 * a.D +
+         (int64_t)d * 4 + (node & 3);
+}
+
+// V^T of nodes nf .. nf+cnt-1 of level l (bf16 hi, and lo for fp32 / fp16).
+// Whole quads (nf, cnt multiples of 4): a thread takes one quad at one d
+// (8-byte stores, 16 threads cover 128 contiguous bytes); else one element.
+template <typename F>
+__device__ __forceinline__ void pack_v(const BuildArgs& a, int l, int64_t bh, int64_t nf, int cnt,
+                                       F val) {
+  const int D = a.D;
+  uint16_t* vh = a.vh[l];
+  uint16_t* vl = a.vl[l];
+  if ((nf & 3) == 0 && (cnt & 3) == 0) {
+    for (int it = threadIdx.x; it < (cnt / 4) * D; it += blockDim.x) {
+      const int qd = it / D, d = it - qd * D;
+      float x[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) x[c] = val(4 * qd + c, d);
+      const uint32_t h01 = cvt_pk_bf16(x[0], x[1]), h23 = cvt_pk_bf16(x[2], x[3]);
+      const int64_t o = vt_index(a, l, bh, nf + 4 * qd, d);
+      *(uint2*)(vh + o) = make_uint2(h01, h23);
+      if (vl) {
+        const uint32_t l01 = cvt_pk_bf16(x[0] - __uint_as_float(h01 << 16),
+                                         x[1] - __uint_as_float(h01 & 0xffff0000u));
+        const uint32_t l23 = cvt_pk_bf16(x[2] - __uint_as_float(h23 << 16),
+                                         x[3] - __uint_as_float(h23 & 0xffff0000u));
+        *(uint2*)(vl + o) = make_uint2(l01, l23);
+      }
+    }
+  } else {
+    for (int it = threadIdx.x; it < cnt * D; it += blockDim.x) {
+      const int j = it / D, d = it - j * D;
+      uint16_t hi, lo;
+      split_bf(val(j, d), hi, lo);
+      const int64_t o = vt_index(a, l, bh, nf + j, d);
+      vh[o] = hi;
+      if (vl) vl[o] = lo;
+    }
+  }
+}
+
+// Zero rows N_l .. Np_l - 1 of every level's packed arrays for one (b, h_kv)
+// (the kernels read whole 16-node blocks).
+__device__ __forceinline__ void zero_padding(const BuildArgs& a, int64_t bh) {
+  const int D = a.D;
+  for (int l = 0; l < a.L; ++l) {
+    const int np = (int)(a.Np[l] - a.N[l]);
+    for (int it = threadIdx.x; it < np * D; it += blockDim.x) {
+      const int j = it / D, d = it - j * D;
+      const int64_t node = a.N[l] + j;
+      const int64_t row = (bh * a.Np[l] + node) * D;
+      a.kh[l][row + d] = 0;
+      a.kl[l][row + d] = 0;
+      const int64_t o = vt_index(a, l, bh, node, d);
+      a.vh[l][o] = 0;
+      if (a.vl[l]) a.vl[l][o] = 0;
+    }
+  }
+}
+
 template <typename T>
-__global__ __launch_bounds__(256) void pack_kernel(
-    const T* __restrict__ ksrc, const T* __restrict__ vsrc, int64_t N, int64_t Np,
-    int Hkv, int D, int CR, const float* __restrict__ cosb, const float* __restrict__ sinb,
-    uint16_t* __restrict__ kh, uint16_t* __restrict__ kl, uint16_t* __restrict__ vh,
-    uint16_t* __restrict__ vl, int64_t total) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= total) return;
-  const int half = D / 2;
-  const int i = (int)(idx % half);
-  int64_t r = idx / half;
-  const int64_t node = r % Np;
-  const int64_t bh = r / Np;
+__global__ __launch_bounds__(256) void build_span_kernel(const BuildArgs a) {
+  __shared__ __attribute__((aligned(16))) T xs[kSpan * kBuildMaxD];       // the span's leaves
+  __shared__ __attribute__((aligned(16))) T us[kSpanUpper * kBuildMaxD];  // its upper nodes
+  const int D = a.D, CR = a.CR, Hkv = a.Hkv;
+  const int64_t bh = blockIdx.x / a.chunks;
+  const int64_t n0 = (blockIdx.x - bh * a.chunks) * kSpan;
   const int h = (int)(bh % Hkv);
   const int64_t b = bh / Hkv;
-  float k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
-  if (node < N) {
-    const int64_t base = ((b * N + node) * Hkv + h) * D;
-    k0 = Io<T>::ld(ksrc + base + i);
-    k1 = Io<T>::ld(ksrc + base + i + half);
-    v0 = Io<T>::ld(vsrc + base + i);
-    v1 = Io<T>::ld(vsrc + base + i + half);
+  const int64_t N0 = a.N[0];
+  const int nl = (int)(N0 - n0 < kSpan ? N0 - n0 : kSpan);  // leaves of the span (>= 1)
+  if (n0 == 0) zero_padding(a, bh);
+  constexpr int PER = 16 / (int)sizeof(T);  // elements per 16-byte chunk
+  constexpr int MAXC = kSpan * kBuildMaxD / PER / 256;  // chunks per thread
+  const int cpr = D / PER;
+  // a thread's chunks of the span's rows (zero past N_0), held in registers
+  // so that V's loads are in flight while K is packed
+  uint4 rows[MAXC];
+  auto load_rows = [&](const T* src) {
+#pragma unroll
+    for (int k = 0; k < MAXC; ++k) {
+      const int it = threadIdx.x + 256 * k;
+      const int n = it / cpr, c = it - n * cpr;
+      rows[k] = make_uint4(0u, 0u, 0u, 0u);
+      if (n < nl && it < kSpan * cpr)
+        rows[k] = *(const uint4*)(src + ((b * N0 + n0 + n) * Hkv + h) * D + c * PER);
+    }
+  };
+  load_rows((const T*)a.x0[0]);
+  for (int x = 0; x < 2; ++x) {
+    __syncthreads();  // the previous tensor's reads of xs / us are done
+#pragma unroll
+    for (int k = 0; k < MAXC; ++k) {
+      const int it = threadIdx.x + 256 * k;
+      const int n = it / cpr, c = it - n * cpr;
+      if (it < kSpan * cpr) *(uint4*)(xs + n * D + c * PER) = rows[k];
+    }
+    __syncthreads();
+    if (x == 0) load_rows((const T*)a.x0[1]);
+    auto leaf = [&](int j, int e) { return (float)xs[j * D + e]; };
+    if (x == 0) {
+      pack_k(a, 0, bh, n0, nl, leaf);
+    } else {
+      // whole quads up to the padded end Np_0 (a multiple of 16): rows past
+      // N_0 are staged as zero
+      const int64_t np0 = a.Np[0] - n0;
+      pack_v(a, 0, bh, n0, (int)(np0 < kSpan ? np0 : kSpan), leaf);
+    }
+    // the levels inside the span
+    const T* prev = xs;
+    int64_t pf = n0;  // first node of the previous level held in prev
+    int uo = 0;
+    for (int l = 1; l < a.lspan; ++l) {
+      const int64_t nf = n0 / a.pw[l];
+      if (nf >= a.N[l]) break;
+      const int64_t cap = kSpan / a.pw[l];
+      const int cnt = (int)(a.N[l] - nf < cap ? a.N[l] - nf : cap);
+      const int64_t Nc = a.N[l - 1];
+      T* cur = us + uo * D;
+      T* dst = (T*)a.lx[x][l];
+      for (int it = threadIdx.x; it < cnt * D; it += blockDim.x) {
+        const int j = it / D, d = it - j * D;
+        const int64_t s0 = (nf + j) * CR;
+        const int64_t e = s0 + CR < Nc ? s0 + CR : Nc;
+        float acc = 0.f;
+        for (int64_t c = s0; c < e; ++c) acc += (float)prev[(c - pf) * D + d];
+        const T v = (T)(acc / (float)(e - s0));
+        cur[j * D + d] = v;
+        dst[((b * a.N[l] + nf + j) * Hkv + h) * D + d] = v;
+      }
+      __syncthreads();
+      auto node = [&](int j, int e) { return (float)cur[j * D + e]; };
+      if (x == 0)
+        pack_k(a, l, bh, nf, cnt, node);
+      else
+        pack_v(a, l, bh, nf, cnt, node);
+      prev = cur;
+      pf = nf;
+      uo += cnt;
+    }
   }
-  const int c = (int)(node & (CR - 1));
-  const float cs = cosb[c * half + i], sn = sinb[c * half + i];
-  const float r0 = k0 * cs - k1 * sn;  // R(x,p)_lo = x_lo cos - x_hi sin (naive.py:22-28)
-  const float r1 = k0 * sn + k1 * cs;  // R(x,p)_hi = x_lo sin + x_hi cos
-  const int64_t krow = (bh * Np + node) * D;
-  uint16_t hi, lo;
-  split_bf(r0, hi, lo);
-  kh[krow + i] = hi;
-  if (kl) kl[krow + i] = lo;
-  split_bf(r1, hi, lo);
-  kh[krow + i + half] = hi;
-  if (kl) kl[krow + i + half] = lo;
-  // V^T block of 16 nodes as four 4-node quads: element (d, c) at
-  // (c / 4) * 4D + d * 4 + c % 4
-  const int64_t vb = (bh * (Np / 16) + node / 16) * D * 16 + ((node & 15) >> 2) * 4 * D + (node & 3);
-  split_bf(v0, hi, lo);
-  vh[vb + (int64_t)i * 4] = hi;
-  if (vl) vl[vb + (int64_t)i * 4] = lo;
-  split_bf(v1, hi, lo);
-  vh[vb + (int64_t)(i + half) * 4] = hi;
-  if (vl) vl[vb + (int64_t)(i + half) * 4] = lo;
+}
+
+// Level l >= lspan (nodes covering more than one span), from the level
+// below: kLevelNodes consecutive nodes of one (b, h_kv) per one-wave block,
+// one launch per level.  A thread pools 8 consecutive elements of one node,
+// loading up to 8 children at a time before adding them in child order.
+constexpr int kLevelNodes = 2;
+
+template <typename T>
+__global__ __launch_bounds__(64) void build_level_kernel(const BuildArgs a, int l) {
+  __shared__ __attribute__((aligned(16))) T ns[2][kLevelNodes * kBuildMaxD];
+  const int D = a.D, CR = a.CR, Hkv = a.Hkv, Q = D / 8;
+  const int64_t Nl = a.N[l], Nc = a.N[l - 1];
+  const int64_t per = (Nl + kLevelNodes - 1) / kLevelNodes;  // blocks per (b, h_kv)
+  const int64_t bh = blockIdx.x / per;
+  const int64_t nf = (blockIdx.x - bh * per) * kLevelNodes;
+  const int cnt = (int)(Nl - nf < kLevelNodes ? Nl - nf : kLevelNodes);
+  const int h = (int)(bh % Hkv);
+  const int64_t b = bh / Hkv;
+  const int64_t rs = (int64_t)Hkv * D;  // child row stride
+  for (int it = threadIdx.x; it < 2 * cnt * Q; it += blockDim.x) {
+    const int x = it / (cnt * Q);
+    const int r = it - x * cnt * Q;
+    const int j = r / Q, d0 = (r - j * Q) * 8;
+    const T* src = (const T*)a.lx[x][l - 1] + (b * Nc * Hkv + h) * D + d0;
+    const int64_t s0 = (nf + j) * CR;
+    const int64_t e = s0 + CR < Nc ? s0 + CR : Nc;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int64_t c0 = s0; c0 < e; c0 += 8) {
+      float w[8][8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (c0 + u < e) Io<T>::ld8(src + (c0 + u) * rs, w[u]);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (c0 + u < e)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] += w[u][i];
+    }
+    T* dst = (T*)a.lx[x][l] + ((b * Nl + nf + j) * Hkv + h) * D + d0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const T v = (T)(acc[i] / (float)(e - s0));
+      ns[x][j * D + d0 + i] = v;
+      dst[i] = v;
+    }
+  }
+  __syncthreads();
+  pack_k(a, l, bh, nf, cnt, [&](int j, int e) { return (float)ns[0][j * D + e]; });
+  pack_v(a, l, bh, nf, cnt, [&](int j, int e) { return (float)ns[1][j * D + e]; });
 }
 
 template <typename T>
 static int tree_build_t(const htree_dims* d, const Plan& P, const void* k, const void* v,
                         void* const* level_k, void* const* level_v, const float* cosb,
                         const float* sinb, void* ws, hipStream_t st) {
-  const T* ck = (const T*)k;
-  const T* cv = (const T*)v;
+  BuildArgs a;
+  memset(&a, 0, sizeof(a));
   char* base = (char*)ws;
+  a.x0[0] = k;
+  a.x0[1] = v;
   for (int l = 0; l < P.L; ++l) {
-    {
-      const int64_t total = (int64_t)d->B * d->H_kv * P.Np[l] * (d->D / 2);
-      const int64_t grid = (total + 255) / 256;
-      hipLaunchKernelGGL(pack_kernel<T>, dim3((unsigned)grid), dim3(256), 0, st, ck, cv,
-                         P.N[l], P.Np[l], d->H_kv, d->D, d->compression_rate, cosb, sinb,
-                         (uint16_t*)(base + P.off_kh[l]),
-                         P.off_kl[l] >= 0 ? (uint16_t*)(base + P.off_kl[l]) : nullptr,
-                         (uint16_t*)(base + P.off_vh[l]),
-                         P.off_vl[l] >= 0 ? (uint16_t*)(base + P.off_vl[l]) : nullptr, total);
+    if (l > 0) {
+      a.lx[0][l] = level_k[l];
+      a.lx[1][l] = level_v[l];
     }
-    if (l + 1 < P.L) {
-      T* nk = (T*)level_k[l + 1];
-      T* nv = (T*)level_v[l + 1];
-      const int64_t total = (int64_t)d->B * P.N[l + 1] * d->H_kv * d->D;
-      const int64_t grid = (total + 255) / 256;
-      hipLaunchKernelGGL(pool_kernel<T>, dim3((unsigned)grid), dim3(256), 0, st, ck, nk,
-                         P.N[l], P.N[l + 1], d->H_kv, d->D, d->compression_rate, total);
-      hipLaunchKernelGGL(pool_kernel<T>, dim3((unsigned)grid), dim3(256), 0, st, cv, nv,
-                         P.N[l], P.N[l + 1], d->H_kv, d->D, d->compression_rate, total);
-      ck = nk;
-      cv = nv;
-    }
+    a.kh[l] = (uint16_t*)(base + P.off_kh[l]);
+    a.kl[l] = (uint16_t*)(base + P.off_kl[l]);
+    a.vh[l] = (uint16_t*)(base + P.off_vh[l]);
+    a.vl[l] = P.off_vl[l] >= 0 ? (uint16_t*)(base + P.off_vl[l]) : nullptr;
+    a.N[l] = P.N[l];
+    a.Np[l] = P.Np[l];
+    a.pw[l] = P.pw[l];
+  }
+  a.cosb = cosb;
+  a.sinb = sinb;
+  a.Hkv = d->H_kv;
+  a.D = d->D;
+  a.CR = d->compression_rate;
+  a.L = P.L;
+  int ls = 1;
+  while (ls < P.L && P.pw[ls] <= kSpan) ++ls;
+  a.lspan = ls;
+  const int64_t BH = (int64_t)d->B * d->H_kv;
+  a.chunks = (P.N[0] + kSpan - 1) / kSpan;
+  hipLaunchKernelGGL(build_span_kernel<T>, dim3((unsigned)(BH * a.chunks)), dim3(256), 0, st, a);
+  for (int l = ls; l < P.L; ++l) {
+    const int64_t per = (P.N[l] + kLevelNodes - 1) / kLevelNodes;
+    hipLaunchKernelGGL(build_level_kernel<T>, dim3((unsigned)(BH * per)), dim3(64), 0, st, a, l);
   }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? HTREE_OK : (int)e;

@@ -94,7 +94,8 @@ int htree_tree_workspace_bytes(const htree_dims* d, int64_t* bytes);
 /* Tree build: writes levels 1..L-1 of K and V in the input dtype (mean of
  * <= CR children, rounded to the dtype per level) into level_k[l] /
  * level_v[l] (level_k[0] / level_v[0] are ignored: level 0 is k / v), and
- * the packed operand tree into tree_ws.
+ * the packed operand tree into tree_ws, in one pass over the leaves (one
+ * launch, plus one per level whose nodes cover more than 64 leaves).
  * Replaces htree_build_kernel (src/parallel.py:87-181) and its host loop
  * (src/parallel.py:947-978, src/backward.py:848-878).
  * level_k, level_v: HOST arrays of HTREE_MAX_LEVELS device pointers. */
