@@ -20,6 +20,11 @@ The CPU baseline times the CPU restatement of src/naive.py (oracle/, C on
 every host core up to 16) on a bounded random sample of the same workload's
 query rows, and, as cpu_baseline.c1, on the whole of the CPU config C1
 (forward and backward, median of 3); it is a reported baseline only.
+
+After those, the default C2 run measures C3, C4, C5 and REF_BWD briefly
+(inputs drawn on the GPU, 2 warm-up + 3 timed steps, forward / backward /
+bare-kernel times with HIP events) into `other_workloads` of the same line;
+`--also ''` skips them.
 """
 from __future__ import annotations
 
@@ -158,53 +163,52 @@ def cpu_leg_c1(iters: int = 3):
             "timing": f"1 warm-up + {iters} runs, median wall-clock"}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="C2", choices=sorted(WORKLOADS))
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--kernel-iters", type=int, default=20)
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported in this build "
-              "(the path shards over (b, h_kv) with no communication between the shards)",
-              file=sys.stderr)
-        sys.exit(2)
+def make_inputs(workload, dev, on_gpu=False):
+    """Seeded synthetic q, k, v, dO of a workload in HBM (drawn on the host
+    for the headline run, on the GPU for the short extra runs)."""
+    import torch
 
+    (B, T, H, Hkv, D, CR, TK, MTN), dtype, _ = WORKLOADS[workload]
+    tdt = getattr(torch, dtype)
+    gdev = dev if on_gpu else torch.device("cpu")
+    g = torch.Generator(device=gdev).manual_seed(1234)
+    rn = lambda *shape: torch.randn(*shape, generator=g, device=gdev)
+    where = "the GPU" if on_gpu else "the host"
+    if workload == "C5":
+        # C5: keys from a 64-component Gaussian mixture (means
+        # N(0, 4 I), sigma 0.5), queries around 4 hot components, V and dO iid
+        mu = 2.0 * rn(64, D)
+        hot = torch.randperm(64, generator=g, device=gdev)[:4]
+        k = mu[torch.randint(0, 64, (B, T, Hkv), generator=g, device=gdev)] + 0.5 * rn(B, T, Hkv, D)
+        q = mu[hot[torch.randint(0, 4, (B, T, H), generator=g, device=gdev)]] + 0.5 * rn(B, T, H, D)
+        v = rn(B, T, Hkv, D)
+        dO = rn(B, T, H, D)
+        q, k, v, dO = (x.to(tdt).to(dev) for x in (q, k, v, dO))
+        data = (f"synthetic: C5 skewed keys/queries (64-component mixture, 4 hot), v,dO iid N(0,1), "
+                f"seed 1234 on {where}")
+    else:
+        q = rn(B, T, H, D).to(tdt).to(dev)
+        k = rn(B, T, Hkv, D).to(tdt).to(dev)
+        v = rn(B, T, Hkv, D).to(tdt).to(dev)
+        dO = rn(B, T, H, D).to(tdt).to(dev)
+        data = f"synthetic: q,k,v,dO iid N(0,1) from torch.Generator seed 1234 on {where}"
+    return q, k, v, dO, data
+
+
+def measure(workload, q, k, v, dO, steps, warmup, kernel_iters):
+    """Times `steps` steps (wall clock, after `warmup`), then the forward and
+    backward apart and `kernel_iters` bare launches of the fused forward
+    kernel with HIP events on their stream.  Returns the figures and the last
+    forward's output and context."""
     import torch
 
     import htree_amd
     from htree_amd import _native as N
     from htree_amd.workmodel import work
 
-    (B, T, H, Hkv, D, CR, TK, MTN), dtype, with_bwd = WORKLOADS[args.workload]
-    tdt = getattr(torch, dtype)
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    g = torch.Generator().manual_seed(1234)
-    if args.workload == "C5":
-        # C5: keys from a 64-component Gaussian mixture (means
-        # N(0, 4 I), sigma 0.5), queries around 4 hot components, V and dO iid
-        mu = 2.0 * torch.randn(64, D, generator=g)
-        hot = torch.randperm(64, generator=g)[:4]
-        k = mu[torch.randint(0, 64, (B, T, Hkv), generator=g)] + 0.5 * torch.randn(B, T, Hkv, D, generator=g)
-        q = mu[hot[torch.randint(0, 4, (B, T, H), generator=g)]] + 0.5 * torch.randn(B, T, H, D, generator=g)
-        v = torch.randn(B, T, Hkv, D, generator=g)
-        dO = torch.randn(B, T, H, D, generator=g)
-        q, k, v, dO = (x.to(tdt).to(dev) for x in (q, k, v, dO))
-        data = "synthetic: C5 skewed keys/queries (64-component mixture, 4 hot), v,dO iid N(0,1), seed 1234"
-    else:
-        q = torch.randn(B, T, H, D, generator=g).to(tdt).to(dev)
-        k = torch.randn(B, T, Hkv, D, generator=g).to(tdt).to(dev)
-        v = torch.randn(B, T, Hkv, D, generator=g).to(tdt).to(dev)
-        dO = torch.randn(B, T, H, D, generator=g).to(tdt).to(dev)
-        data = "synthetic: q,k,v,dO iid N(0,1) from torch.Generator seed 1234"
+    (B, T, H, Hkv, D, CR, TK, MTN), dtype, with_bwd = WORKLOADS[workload]
+    dev = q.device
     has_bwd = with_bwd and hasattr(htree_amd, "htree_backward")
-    torch.cuda.synchronize()
-    print(f"# workload {args.workload} B={B} T={T} H={H} Hkv={Hkv} D={D} {dtype} CR={CR} TK={TK} "
-          f"MTN={MTN} backward={'yes' if has_bwd else 'no'}", file=sys.stderr, flush=True)
 
     def step():
         if not has_bwd:  # forward only (speed_test.py): nothing kept for a backward
@@ -213,34 +217,34 @@ def main():
         htree_amd.htree_backward(dO, q, out, ctx)
         return out
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     torch.cuda.synchronize()
-    step_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    print(f"# timed {args.steps} steps: {step_ms:.3f} ms/step", file=sys.stderr, flush=True)
+    step_ms = (time.perf_counter() - t0) * 1e3 / steps
+    print(f"# {workload}: timed {steps} steps: {step_ms:.3f} ms/step", file=sys.stderr, flush=True)
 
     # fwd / bwd split and the fused forward kernel alone, with HIP events
     stream = torch.cuda.current_stream(dev)
     ev = lambda: torch.cuda.Event(enable_timing=True)
     e0, e1, e2 = ev(), ev(), ev()
     e0.record(stream)
-    for _ in range(args.steps):
+    for _ in range(steps):
         if has_bwd:
             out, ctx = htree_amd.htree_forward(q, k, v, CR, MTN, TK, _save_for_backward=True)
         else:
             out = htree_amd.htree_forward(q, k, v, CR, MTN, TK)
     e1.record(stream)
     if has_bwd:
-        for _ in range(args.steps):
+        for _ in range(steps):
             htree_amd.htree_backward(dO, q, out, ctx)
     e2.record(stream)
     torch.cuda.synchronize()
-    fwd_ms = e0.elapsed_time(e1) / args.steps
-    bwd_ms = e1.elapsed_time(e2) / args.steps if has_bwd else None
+    fwd_ms = e0.elapsed_time(e1) / steps
+    bwd_ms = e1.elapsed_time(e2) / steps if has_bwd else None
     if not has_bwd:
         out, ctx = htree_amd.htree_forward(q, k, v, CR, MTN, TK, _save_for_backward=True)
 
@@ -253,13 +257,53 @@ def main():
     sp = N.stream_ptr(dev)
     k0, k1 = ev(), ev()
     k0.record(stream)
-    for _ in range(args.kernel_iters):
+    for _ in range(kernel_iters):
         rc = lib.htree_forward(d, scale, N.ptr(q), N.ptr(ws), ws.numel(), N.ptr(cos), N.ptr(sin),
                                N.ptr(out), N.ptr(gmax), N.ptr(gsum), None, sp)
         N.check(rc, "htree_forward")
     k1.record(stream)
     torch.cuda.synchronize()
-    kern_ms = k0.elapsed_time(k1) / args.kernel_iters
+    kern_ms = k0.elapsed_time(k1) / kernel_iters
+    w = work(B, T, H, Hkv, D, CR, TK, MTN, getattr(torch, dtype).itemsize)
+    return dict(has_bwd=has_bwd, step_ms=step_ms, fwd_ms=fwd_ms, bwd_ms=bwd_ms, kern_ms=kern_ms,
+                work=w, out=out, ctx=ctx)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="C2", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--kernel-iters", type=int, default=20)
+    ap.add_argument("--also", default=None,
+                    help="comma-separated workloads measured briefly after the main one "
+                         "(3 steps each; default for C2: C3,C4,C5,REF_BWD; '' for none)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported in this build "
+              "(the path shards over (b, h_kv) with no communication between the shards)",
+              file=sys.stderr)
+        sys.exit(2)
+    also = args.also if args.also is not None else ("C3,C4,C5,REF_BWD" if args.workload == "C2" else "")
+    also = [w for w in also.split(",") if w]
+    for w in also:
+        if w not in WORKLOADS:
+            ap.error(f"--also: unknown workload {w}")
+
+    import torch
+
+    (B, T, H, Hkv, D, CR, TK, MTN), dtype, with_bwd = WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    q, k, v, dO, data = make_inputs(args.workload, dev)
+    torch.cuda.synchronize()
+    print(f"# workload {args.workload} B={B} T={T} H={H} Hkv={Hkv} D={D} {dtype} CR={CR} TK={TK} "
+          f"MTN={MTN}", file=sys.stderr, flush=True)
+    m = measure(args.workload, q, k, v, dO, args.steps, args.warmup, args.kernel_iters)
+    has_bwd, fwd_ms, bwd_ms, kern_ms, w = m["has_bwd"], m["fwd_ms"], m["bwd_ms"], m["kern_ms"], m["work"]
+    out, ctx = m["out"], m["ctx"]
 
     # Calibration copy for the PMC traffic measurement (outside every timed
     # region): 256 MiB read + 256 MiB written by torch's copy kernel, so that a
@@ -271,7 +315,6 @@ def main():
     torch.cuda.synchronize()
     del cal_src, cal_dst
 
-    w = work(B, T, H, Hkv, D, CR, TK, MTN, tdt.itemsize)
     traffic = measured_traffic(args.workload)
     achieved = w.fwd_kernel_bytes / (kern_ms * 1e-3)
     fwd_tok = B * T / (fwd_ms * 1e-3)
@@ -302,7 +345,7 @@ def main():
             "ms": bwd_ms, "tokens_per_s": B * T / (bwd_ms * 1e-3),
             "hbm_roofline_frac": w.bwd_bytes / (bwd_ms * 1e-3) / HBM_PEAK,
             "algorithmic_bytes": w.bwd_bytes},
-        "wall_ms_per_step": step_ms,
+        "wall_ms_per_step": m["step_ms"],
         "roofline": {
             "kernel": ("htree::fwd_wide_kernel" if ctx["dims"].top_k > 64 else "htree::fwd_reg_kernel")
                       + " (fused forward, all levels)",
@@ -318,8 +361,8 @@ def main():
         },
     }
     if not args.no_cpu:
-        cb = cpu_baseline(q, k, v, dO, out, gmax, gsum, ctx.get("parents_stacked") if has_bwd else None,
-                          CR, TK, MTN, dtype)
+        cb = cpu_baseline(q, k, v, dO, out, ctx["global_max"], ctx["global_sum"],
+                          ctx.get("parents_stacked") if has_bwd else None, CR, TK, MTN, dtype)
         tot = 1.0 / (1.0 / cb["fwd_tok_s"] + (1.0 / cb["bwd_tok_s"] if has_bwd and "bwd_tok_s" in cb else 0.0))
         res["cpu_baseline"] = {
             "value": tot, "unit": "tokens/s", "cores": cb["threads"], "kind": "port",
@@ -334,6 +377,34 @@ def main():
         }
     else:
         res["cpu_baseline"] = None
+
+    # the other BASELINE workloads, briefly (after every timed region above)
+    if also:
+        del q, k, v, dO, out, ctx, m
+        torch.cuda.empty_cache()
+        res["other_workloads"] = {}
+    for wl in also:
+        (B2, T2, H2, Hkv2, D2, CR2, TK2, MTN2), dt2, _ = WORKLOADS[wl]
+        q2, k2, v2, dO2, data2 = make_inputs(wl, dev, on_gpu=True)
+        m2 = measure(wl, q2, k2, v2, dO2, steps=3, warmup=2, kernel_iters=3)
+        w2 = m2["work"]
+        res["other_workloads"][wl] = {
+            "config": f"B={B2} T={T2} Hq={H2} Hkv={Hkv2} D={D2} {DT_SHORT[dt2]} CR={CR2} MTN={MTN2} "
+                      f"TK={TK2}",
+            "data": data2,
+            "steps": 3, "warmup": 2,
+            "tokens_per_s": B2 * T2 / ((m2["fwd_ms"] + (m2["bwd_ms"] or 0.0)) * 1e-3),
+            "fwd_ms": m2["fwd_ms"],
+            "fwd_hbm_roofline_frac": w2.fwd_bytes / (m2["fwd_ms"] * 1e-3) / HBM_PEAK,
+            "bwd_ms": m2["bwd_ms"],
+            "bwd_hbm_roofline_frac": (w2.bwd_bytes / (m2["bwd_ms"] * 1e-3) / HBM_PEAK
+                                      if m2["bwd_ms"] else None),
+            "kernel_ms": m2["kern_ms"],
+            "kernel_hbm_roofline_frac": w2.fwd_kernel_bytes / (m2["kern_ms"] * 1e-3) / HBM_PEAK,
+            "wall_ms_per_step": m2["step_ms"],
+        }
+        del q2, k2, v2, dO2, m2
+        torch.cuda.empty_cache()
     print(json.dumps(res), flush=True)
 
 
