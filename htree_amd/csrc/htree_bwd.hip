@@ -1281,12 +1281,11 @@ __device__ __forceinline__ void rot_acc(f32x4 (&x)[D / 16], const float* c, cons
 // a frame that turns with it, X <- R(X, -CR) + dq~_tile, so that
 //   sum_s R^-1(dq~_s, a - s CR) = R^-1(X, n_c-1 - (np-1) CR) = R(X, -c_t)
 // needs one table rotation per level.
-template <int D, bool PREC, typename TIn, int MAXTK>
+template <int D, bool PREC, typename TIn, int MAXTK, int MAXPOS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 ? 5 : 2))) void dq_kernel(const DqArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
-  // list capacity; selection bits of the 16-candidate tile positions
-  // (kMaxTiles or, for MAXTK = kWideMaxTK, kWideMaxPos / 16 tiles)
-  constexpr int SWW = MAXTK > kMaxTK ? kWideMaxPos / 32 : kMaxTiles / 2;
+  // list capacity; selection bits of the candidate positions (MAXPOS)
+  constexpr int SWW = MAXPOS / 32;
   __shared__ int32_t lst[kWavesPerBlock][MAXTK];
   __shared__ uint32_t selw[kWavesPerBlock][SWW];
   __shared__ float rot_m[2][HALF];  // cos(CR theta), -sin(CR theta)
@@ -1932,12 +1931,16 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.TK = d->top_k;
     a.L = Ltop + 1;
     a.scale = scale;
-    if (P.wide)
-      hipLaunchKernelGGL((dq_kernel<D, PREC, T, kWideMaxTK>), dim3((unsigned)((groups + 3) / 4)),
-                         dim3(256), 0, st, a);
+    // LDS sized for the lists and positions: one-wave-per-group forwards
+    // (64, 64 tiles), the reference's default regime (512, 8192), beyond
+    // (1024, 16384)
+    const dim3 grid((unsigned)((groups + 3) / 4));
+    if (!P.wide)
+      hipLaunchKernelGGL((dq_kernel<D, PREC, T, kMaxTK, kMaxTiles * 16>), grid, dim3(256), 0, st, a);
+    else if (d->top_k <= 512 && ((int64_t)d->top_k << P.cr_log2) <= kWideMidPos)
+      hipLaunchKernelGGL((dq_kernel<D, PREC, T, 512, kWideMidPos>), grid, dim3(256), 0, st, a);
     else
-      hipLaunchKernelGGL((dq_kernel<D, PREC, T, kMaxTK>), dim3((unsigned)((groups + 3) / 4)),
-                         dim3(256), 0, st, a);
+      hipLaunchKernelGGL((dq_kernel<D, PREC, T, kWideMaxTK, kWideMaxPos>), grid, dim3(256), 0, st, a);
   }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? HTREE_OK : (int)e;

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "htree.h"
 
 namespace htree {
@@ -19,11 +21,13 @@ constexpr int kMaxTK = 64;       // parent lists of the one-wave-per-group kerne
 constexpr int kMaxTiles = 64;    // candidate tiles per level of those kernels
 // Wide configurations (top_k > kMaxTK or more than kMaxTiles tiles, e.g. the
 // reference's default top_k = 512, CR = 16): one block of kWideWaves waves per
-// query group, kWideC candidate positions per thread in the selection.
+// query group, kWideC candidate positions per thread in the selection (twice
+// that above kWideC * 256 positions).
 constexpr int kWideWaves = 4;
 constexpr int kWideC = 32;
-constexpr int kWideMaxPos = 64 * kWideWaves * kWideC;  // top_k * CR <= 8192
-constexpr int kWideMaxTK = 512;
+constexpr int kWideMidPos = 64 * kWideWaves * kWideC;  // 8192: kWideC keys per thread
+constexpr int kWideMaxPos = 2 * kWideMidPos;           // top_k * CR <= 16384
+constexpr int kWideMaxTK = 1024;
 
 // ---------------------------------------------------------------- plan
 // Packed operand tree, per level l (all bf16, Np = N rounded up to 16):
@@ -311,10 +315,15 @@ __device__ __forceinline__ int row_sum16i(int x) {
 // order of a stable descending sort) by an exclusive scan in position order,
 // and returns this thread's selection bits; `before` receives the number of
 // selected positions below this thread's first (their rank in ascending
-// position order).  `red` is 32 ints of LDS.
+// position order).  `red` is 32 ints of LDS.  C = 32 or 64 (the selection
+// bits are one 32- or 64-bit word per thread).
 template <int C>
 struct BlockSelect {
-  static_assert(C <= 32, "selection bits are one 32-bit word per thread");
+  static_assert(C == 32 || C == 64, "selection bits are one 32- or 64-bit word per thread");
+  typedef typename std::conditional<C == 32, uint32_t, unsigned long long>::type Mask;
+  static __device__ __forceinline__ int popc(Mask m) {
+    if constexpr (C == 32) return __popc(m); else return __popcll(m);
+  }
   int32_t* red;
   int lane, wv;
   int rc = 0, rs = 0;
@@ -354,8 +363,8 @@ struct BlockSelect {
     for (int w = 0; w < wv; ++w) base += r[w];
     return base + x - v;
   }
-  __device__ __forceinline__ uint32_t select(const uint32_t (&key)[C], int take, int top_bit,
-                                             int& before) {
+  __device__ __forceinline__ Mask select(const uint32_t (&key)[C], int take, int top_bit,
+                                         int& before) {
     uint32_t thr = 0u;
 #pragma unroll 1
     for (int bit = top_bit; bit >= 0; --bit) {
@@ -363,17 +372,17 @@ struct BlockSelect {
       if (count(key, c, false) >= take) thr = c;
     }
     const int need = take - count(key, thr, true);
-    uint32_t gtb = 0u, eqb = 0u;  // this thread's positions above / at the threshold
+    Mask gtb = 0, eqb = 0;  // this thread's positions above / at the threshold
 #pragma unroll
     for (int i = 0; i < C; ++i) {
-      gtb |= (uint32_t)(key[i] > thr) << i;
-      eqb |= (uint32_t)(key[i] == thr) << i;
+      gtb |= (Mask)(key[i] > thr) << i;
+      eqb |= (Mask)(key[i] == thr) << i;
       if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);
     }
-    int allow = need - scan(__popc(eqb));
-    uint32_t bits = gtb;
-    for (uint32_t e = eqb; e != 0u && allow > 0; e &= e - 1u, --allow) bits |= e & (0u - e);
-    before = scan(__popc(bits));
+    int allow = need - scan(popc(eqb));
+    Mask bits = gtb;
+    for (Mask e = eqb; e != 0 && allow > 0; e &= e - 1, --allow) bits |= e & (0 - e);
+    before = scan(popc(bits));
     return bits;
   }
 };

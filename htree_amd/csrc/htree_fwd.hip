@@ -1019,13 +1019,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 // candidates).  Upper levels score every tile once for the importance
 // (relative to the wave's running max, rescaled to the level max afterwards)
 // and select with a block-wide radix select over the float bits: thread i
-// holds candidate positions 32i .. 32i+31 in registers, so ties at the
+// holds candidate positions Ci .. Ci+C-1 in registers (C = 32, or 64 above
+// 8192 positions), so ties at the
 // threshold go to the lowest positions (stable descending sort, src/naive.py:
 // 88-105) by an exclusive scan in position order.  The accumulation pass
 // recomputes the scores of the non-selected candidates.
-template <int D, bool PREC, typename TIn, bool TRACE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 ? 4 : 1))) void fwd_wide_kernel(const FwdArgs a) {
-  constexpr int KS = D / 32, ND = D / 16, HALF = D / 2, NW = kWideWaves, C = kWideC;
+template <int D, bool PREC, typename TIn, bool TRACE, int C>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && C == 32 ? 4 : 1))) void fwd_wide_kernel(const FwdArgs a) {
+  constexpr int KS = D / 32, ND = D / 16, HALF = D / 2, NW = kWideWaves;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int u16 = lane & 15, kg = lane >> 4;
@@ -1200,13 +1201,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 ? 4
       }
       // ---- the take-th largest key, bit by bit from the top (keys < 2^31)
       int idx;
-      const uint32_t bits = bsel.select(key, take, 30, idx);
+      const auto bits = bsel.select(key, take, 30, idx);
       int32_t* pn = par + (cur ^ 1) * TK;
-      for (uint32_t bb = bits; bb != 0u; bb &= bb - 1u) {
-        const int pos = tid * C + (__builtin_ffs((int)bb) - 1);
+      for (auto bb = bits; bb != 0; bb &= bb - 1) {
+        const int pos = tid * C + __builtin_ctzll((unsigned long long)bb);
         pn[idx++] = (pc[pos >> crlg] << crlg) + (pos & (CR - 1));
       }
-      if (tid * C < (TK << crlg)) selw[tid] = bits;
+      if (tid * C < (TK << crlg)) {
+        selw[tid * (C / 32)] = (uint32_t)bits;
+        if constexpr (C == 64) selw[tid * 2 + 1] = (uint32_t)((unsigned long long)bits >> 32);
+      }
       for (int i = take + tid; i < TK; i += 256) pn[i] = -1;
       __syncthreads();
     }
@@ -1319,10 +1323,18 @@ static void launch_fwd(const FwdArgs& a, const Plan& P, dim3 grid, hipStream_t s
   const int max_tiles = P.max_tiles;
   if (P.wide) {  // one block per query group
     const unsigned lds = (unsigned)wide_lds(a.TK, a.TK << a.crlg, max_tiles, D).bytes;
-    if (trace)
-      hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, true>), grid, dim3(256), lds, st, a);
-    else
-      hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, false>), grid, dim3(256), lds, st, a);
+    const bool c64 = (a.TK << a.crlg) > kWideMidPos;  // 64 keys per thread
+    if (trace) {
+      if (c64)
+        hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, true, 64>), grid, dim3(256), lds, st, a);
+      else
+        hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, true, 32>), grid, dim3(256), lds, st, a);
+    } else {
+      if (c64)
+        hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, false, 64>), grid, dim3(256), lds, st, a);
+      else
+        hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, false, 32>), grid, dim3(256), lds, st, a);
+    }
   } else if (max_tiles <= 16) {
     if (trace)
       hipLaunchKernelGGL((fwd_reg_kernel<D, PREC, TIn, true>), grid, dim3(256), 0, st, a);

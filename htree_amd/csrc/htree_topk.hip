@@ -71,7 +71,7 @@ extern "C" int htree_topk_rows(const float* values, int64_t rows, int32_t n, int
                                int32_t* out_index, int32_t* out_payload, void* stream) {
   if (!values || !out_values || !out_index) return HTREE_ENULL;
   if (rows < 0 || n <= 0 || k <= 0 || k > n || rows > 0x7fffffff) return HTREE_ESHAPE;
-  if (n > kWideMaxPos) return HTREE_EUNSUPPORTED;
+  if (n > kWideMidPos) return HTREE_EUNSUPPORTED;
   if (n_payload != 0 && n_payload != 1 && n_payload != 8) return HTREE_EUNSUPPORTED;
   if (n_payload && (!payload || !out_payload)) return HTREE_ENULL;
   if (rows == 0) return HTREE_OK;

@@ -403,8 +403,8 @@ const char* htree_strerror(int status) {
       return "configuration outside this HIP build: needs D in {32,64,128}, H/H_kv <= 16 "
              "(up to 32 with kv_share 2, where top_k_per_layer <= 64 and "
              "top_k_per_layer * max(compression_rate,16) <= 1024), "
-             "4 <= compression_rate <= 64, top_k_per_layer <= 512 and "
-             "top_k_per_layer * compression_rate <= 8192 (where top_k_per_layer > 64 or "
+             "4 <= compression_rate <= 64, top_k_per_layer <= 1024 and "
+             "top_k_per_layer * compression_rate <= 16384 (where top_k_per_layer > 64 or "
              "top_k_per_layer * max(compression_rate,16) / 16 > 64); the backward also needs "
              "B * T * H_kv * min(top_k_per_layer, parents of a level) < 2^31 per level";
     case HTREE_EWORKSPACE: return "workspace smaller than htree_tree_workspace_bytes()";

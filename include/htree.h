@@ -45,7 +45,7 @@ enum htree_status {
                               D not in {32, 64, 128}, G = H/H_kv > 16
                               (see kv_share for G <= 32),
                               compression_rate outside [4, 64],
-                              top_k > 512, top_k * compression_rate > 8192,
+                              top_k > 1024, top_k * compression_rate > 16384,
                               more than HTREE_MAX_LEVELS levels, or a
                               backward level of 2^31 or more entries
                               (B * T * H_kv * min(top_k, parents)) */

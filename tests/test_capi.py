@@ -58,6 +58,13 @@ def test_baseline_level_counts():
     assert len(N.levels(dims(T=65536))) == 4
 
 
+def test_largest_candidate_sets_accepted():
+    # 16384 candidates per level: top_k 1024 at CR 16, top_k 512 at CR 32
+    assert len(N.levels(dims(T=20000, H=8, top_k=1024, max_top_nodes=16384, rope_rows=17408))) == 2
+    assert len(N.levels(dims(T=20000, H=8, compression_rate=32, top_k=512, max_top_nodes=512,
+                             rope_rows=16384))) == 3
+
+
 def test_shared_kv_heads_accepted():
     # a group of 32 query heads as two groups of 16 over duplicated KV heads,
     # in the register forward (16 tiles per level) and the streaming one (32)
@@ -81,9 +88,10 @@ def test_shared_kv_heads_accepted():
     (dict(H=64, H_kv=4, kv_share=2, top_k=128, max_top_nodes=128, rope_rows=2048),
      N.HTREE_EUNSUPPORTED),                            # shared selection: not the wide forward
     (dict(D=16), N.HTREE_EUNSUPPORTED),
-    (dict(top_k=1024, max_top_nodes=128, rope_rows=16384), N.HTREE_EUNSUPPORTED),  # top_k > 512
-    (dict(top_k=512, compression_rate=32, max_top_nodes=128, rope_rows=16384),
-     N.HTREE_EUNSUPPORTED),                            # 16384 candidates per level
+    (dict(top_k=2048, compression_rate=4, max_top_nodes=128, rope_rows=16384),
+     N.HTREE_EUNSUPPORTED),                            # top_k > 1024
+    (dict(top_k=512, compression_rate=64, max_top_nodes=128, rope_rows=32768),
+     N.HTREE_EUNSUPPORTED),                            # 32768 candidates per level
 ])
 def test_invalid_configs_raise_assertion(kw, code):
     d = dims(**kw)

@@ -151,14 +151,18 @@ WIDE = [
     (1, 5000, 8, 2, 64, 4, 256, 1024, "bfloat16", 23, False),     # CR < 16: one tile per parent
     (1, 6000, 8, 1, 128, 32, 128, 4096, "bfloat16", 24, False),   # CR > 16
     (1, 8192, 16, 2, 64, 16, 256, 4096, "bfloat16", 25, True),    # many exact-zero importances
+    # 16384 candidates per level (64 keys per thread in the selection)
+    (1, 20000, 8, 2, 32, 16, 1024, 16384, "float32", 26, False),  # top_k 1024
+    (1, 20000, 8, 2, 64, 32, 512, 512, "bfloat16", 27, False),    # top_k 512 at CR 32, 3 levels
 ]
 
 
 @pytest.mark.parametrize("cfg", WIDE, ids=lambda c: f"T{c[1]}D{c[4]}cr{c[5]}tk{c[6]}{c[8]}{'skew' if c[10] else ''}")
 def test_forward_wide_matches_oracle(cfg):
-    """The reference's default regime (top_k up to 512, up to 8192 candidates
-    per level): sampled rows against the oracle, teacher-forced on the
-    device's lists; every row through the list invariants."""
+    """The reference's default regime and beyond (top_k up to 1024, up to
+    16384 candidates per level): sampled rows against the oracle,
+    teacher-forced on the device's lists; every row through the list
+    invariants."""
     B, T, H, Hkv, D, CR, TK, MTN, dtype, seed, skewed = cfg
     print(f"case {cfg}", flush=True)
     if skewed:

@@ -2,7 +2,8 @@
 // against the layout the launch allocates (wide_lds() of htree_common.h, the
 // same function the kernel and its launch call).  For every configuration
 // the library accepts on the wide path (top_k > 64 or more than 64 candidate
-// tiles; top_k <= 512, top_k * CR <= 8192, CR in [4, 64], D in {32, 64, 128})
+// tiles; top_k <= 1024, top_k * CR <= 16384, CR in [4, 64], D in {32, 64, 128};
+// 32 selection keys per thread up to 8192 positions, 64 above)
 // and every level shape (np parents, child index ct of the query), each LDS
 // index the kernel forms is checked to lie inside its region, and the
 // regions to lie inside the allocation without overlapping.  Test
@@ -37,12 +38,15 @@ static void check_config(int TK, int CR, int D) {
   const int max_tiles = TK * (CR > 16 ? CR : 16) / 16;  // make_plan
   const int maxpos = TK << crlg;                        // launch: TK << crlg
   const WideLds w = wide_lds(TK, maxpos, max_tiles, D);
-  const int NW = kWideWaves, C = kWideC;
+  const int NW = kWideWaves;
+  const int C = maxpos > kWideMidPos ? 2 * kWideC : kWideC;  // the launch's choice
+  const int WPT = C / 32;                                    // selection words per thread
+  CHECK(256 * C >= maxpos, "TK %d CR %d: %d keys per thread cover %d positions", TK, CR, C, maxpos);
   const bool wide = CR >= 16;
   const int CRU = CR < 16 ? CR : 16;
   // regions as the kernel reads them
   const Region par{w.par, (long)w.par + 2L * TK * 4};
-  const Region selw{w.selw, (long)w.selw + 256L * 4};   // selw[tid], tid < 256
+  const Region selw{w.selw, (long)w.selw + 256L * WPT * 4};  // selw[tid * WPT + j]
   const Region mt{w.mt, (long)w.mt + (long)max_tiles * 4};
   const Region red{w.red, (long)w.red + 36L * 4};       // counts, scans, maxima
   const long imp_floats = (w.bytes - w.imp) / 4;
@@ -55,7 +59,9 @@ static void check_config(int TK, int CR, int D) {
   CHECK(w.imp % 16 == 0 && w.mt % 4 == 0 && w.red % 4 == 0, "alignment");
   // selection bits are written by threads with tid * C < maxpos only
   for (int tid = 0; tid < 256; ++tid)
-    if (tid * C < maxpos) CHECK(w.selw + tid * 4 + 4 <= (long)w.selw + (maxpos + 31) / 32 * 4, "selw[%d]", tid);
+    if (tid * C < maxpos)
+      CHECK(w.selw + (tid + 1) * WPT * 4 <= (long)w.selw + (maxpos + 31) / 32 * 4, "selw[%d]", tid);
+  (void)selw;
   // every level shape: np valid parents, the query's child index ct
   for (int np = 1; np <= TK; ++np)
     for (int ct = 0; ct < CR; ++ct) {
@@ -71,7 +77,7 @@ static void check_config(int TK, int CR, int D) {
           const int pos = wide ? (tau << 4) + u : (tau << crlg) + u;
           if (!(u < CRU && pos < nc)) continue;
           CHECK(pos < imp_floats, "imp[%d] of %ld", pos, imp_floats);
-          CHECK((pos >> 5) < 256 && (pos >> 5) * 4 + 4 <= (maxpos + 31) / 32 * 4, "selw word of %d", pos);
+          CHECK((pos >> 5) < 256 * WPT && (pos >> 5) * 4 + 4 <= (maxpos + 31) / 32 * 4, "selw word of %d", pos);
           const int mtile = wide ? pos >> 4 : pos >> crlg;
           CHECK(mtile == tau && mtile < max_tiles, "mt index %d for tile %d", mtile, tau);
         }
