@@ -106,7 +106,7 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
     d = bwd_ctx.get("dims")
     if ws is None or d is None:
         # a context of the reference's keys: the kernels run with its own tables
-        check_tables(cos, sin, K // 2, TK * CR, dev)
+        check_tables(cos, sin, K // 2, max(TK * CR, CR + 1), dev)
         d = make_dims(B, T, H, H_kv, hf.D, CR, MTN, TK, q.dtype, cos.shape[0], hf.share)
         assert len(N.levels(d)) == L, f"num_layers {L} does not match T={T}, CR={CR}, MTN={MTN}"
         ws = None

@@ -58,6 +58,7 @@ struct BwdPlan {
   int64_t off_bitmap, off_wpre, off_cnt, off_rowoff, off_pcnt, off_poff, off_npieces, off_ptab,
       off_partial;
   int64_t off_rec[HTREE_MAX_LEVELS];   // per-entry records of each level
+  int64_t off_rech;                    // CR 128: masks of children 64..127 per entry (or -1)
   int64_t off_emap[HTREE_MAX_LEVELS];  // (query group, slot) -> {entry, mask}, per level
   int64_t off_ds[HTREE_MAX_LEVELS];    // dS of every entry tile, per level
   int64_t off_dsexp[HTREE_MAX_LEVELS]; // bf16 inputs: exponent of every stored dS tile
@@ -147,7 +148,8 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true, 
       budget = (int64_t)(total / 3);
   }
   if (const char* e = getenv("HTREE_DS_BUDGET_MB")) budget = (int64_t)atoll(e) << 20;
-  b->use_ds = allow_ds && !P.wide && ds_total <= budget;
+  // (CR 128: the per-entry maps carry 64 children, so dq recomputes)
+  b->use_ds = allow_ds && !P.wide && CR <= 64 && ds_total <= budget;
   // the merged top level (stored scores: bf16, <= 16 tiles per level)
   const int Ltop = (P.L > 1 && P.N[P.L - 1] <= d->top_k) ? P.L - 2 : P.L - 1;
   // (a merged entry's four tiles index the stored scores of tiles 4 s' .. 4 s' + 3
@@ -192,6 +194,7 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true, 
   b->off_npieces = take(4);
   b->off_ptab = take(b->max_pieces * 3 * 4);
   b->off_vlist = b->vlevel >= 0 ? take(b->max_entries * 4) : -1;
+  b->off_rech = CR > 64 ? take(b->max_entries * 8) : -1;
   const int64_t* ent = b->ent;
   for (int l = 0; l < P.L; ++l) {
     b->off_rec[l] = b->use_ds ? take(ent[l] * 16) : l == 0 ? take(b->max_entries * 16) : b->off_rec[0];
@@ -581,6 +584,22 @@ __global__ __launch_bounds__(256) void prefix_list_kernel(int T, int Hkv, int TK
 // this level (valid positions, not passed to level l-1).  A query group's
 // TK slots are TK consecutive lanes of one wave; its next-level list is read
 // by shuffles.  emap (nullable) maps (query group, slot) to {entry, mask}.
+// Accumulate mask of p's children in one entry: the nvalid candidates (>= 1)
+// minus the children passed to the next level (drop), CR bits as two 64-bit
+// halves (the second only for CR 128).
+__device__ __forceinline__ void child_masks(int nvalid, int CR, unsigned long long drop_lo,
+                                            unsigned long long drop_hi, unsigned long long& lo,
+                                            unsigned long long& hi) {
+  lo = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
+  hi = nvalid >= 128 ? ~0ull : nvalid > 64 ? ((1ull << (nvalid - 64)) - 1ull) : 0ull;
+  if (CR < 64) lo &= (1ull << CR) - 1ull;
+  if (CR <= 64) hi = 0ull;
+  lo &= ~drop_lo;
+  hi &= ~drop_hi;
+}
+__device__ __forceinline__ void drop_child(int c, unsigned long long& lo, unsigned long long& hi) {
+  if (c < 64) lo |= 1ull << c; else hi |= 1ull << (c - 64);
+}
 __global__ __launch_bounds__(256) void record_kernel(const int32_t* __restrict__ par,
                                                      const int32_t* __restrict__ par_next,
                                                      const uint32_t* __restrict__ bm,
@@ -588,7 +607,7 @@ __global__ __launch_bounds__(256) void record_kernel(const int32_t* __restrict__
                                                      const int32_t* __restrict__ rowoff, int T,
                                                      int Hkv, int TK, int64_t Pl, int64_t W,
                                                      int64_t pw, int CR, int crlg, int64_t total,
-                                                     int4* __restrict__ rec,
+                                                     int4* __restrict__ rec, int2* __restrict__ rech,
                                                      int4* __restrict__ emap) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const bool in = idx < total;
@@ -598,10 +617,10 @@ __global__ __launch_bounds__(256) void record_kernel(const int32_t* __restrict__
   const unsigned long long gmask = (TK >= 64 ? ~0ull : ((1ull << TK) - 1ull)) << base;
   const int np = __popcll(__ballot(p >= 0) & gmask);
   const int vn = (in && par_next) ? par_next[idx] : -1;
-  unsigned long long drop = 0ull;  // children of p passed to level l-1
+  unsigned long long drop = 0ull, drop_hi = 0ull;  // children of p passed to level l-1
   for (int i = 0; i < TK; ++i) {
     const int v = __shfl(vn, base + i);
-    if (v >= 0 && (v >> crlg) == p) drop |= 1ull << (v & (CR - 1));
+    if (v >= 0 && (v >> crlg) == p) drop_child(v & (CR - 1), drop, drop_hi);
   }
   if (p < 0) return;
   const int64_t grp = idx / TK;
@@ -613,13 +632,13 @@ __global__ __launch_bounds__(256) void record_kernel(const int32_t* __restrict__
   const int ct = (int)((t / pw) & (CR - 1));
   const int nc = ((np - 1) << crlg) + ct + 1;
   const int nvalid = nc - (s << crlg);  // children of p that are candidates
-  unsigned long long m = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
-  if (CR < 64) m &= (1ull << CR) - 1ull;
-  m &= ~drop;
+  unsigned long long m, mh;
+  child_masks(nvalid, CR, drop, drop_hi, m, mh);
   const int64_t row = (b * Hkv + h) * Pl + p;
   const int64_t wi = row * W + (t >> 5);
   const int e = rowoff[row] + wpre[wi] + __popc(bm[wi] & ((1u << (t & 31)) - 1u));
   rec[e] = make_int4(t, (nc - 1 - (s << crlg)) | (s << 16), (int)(uint32_t)m, (int)(uint32_t)(m >> 32));
+  if (rech) rech[e] = make_int2((int)(uint32_t)mh, (int)(uint32_t)(mh >> 32));
   if (emap) emap[idx] = make_int4(e, (int)(uint32_t)m, (int)(uint32_t)(m >> 32), 0);
 }
 
@@ -631,7 +650,7 @@ __global__ __launch_bounds__(256) void record_wide_kernel(
     const int32_t* __restrict__ par, const int32_t* __restrict__ par_next,
     const uint32_t* __restrict__ bm, const int32_t* __restrict__ wpre,
     const int32_t* __restrict__ rowoff, int T, int Hkv, int TK, int64_t Pl, int64_t W, int64_t pw,
-    int CR, int crlg, int64_t total, int4* __restrict__ rec) {
+    int CR, int crlg, int64_t total, int4* __restrict__ rec, int2* __restrict__ rech) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= total) return;
   const int p = par[idx];
@@ -645,7 +664,7 @@ __global__ __launch_bounds__(256) void record_wide_kernel(
     if (lst[mid] >= 0) lo = mid + 1; else hi = mid;
   }
   const int np = lo;
-  unsigned long long drop = 0ull;  // children of p passed to level l-1
+  unsigned long long drop = 0ull, drop_hi = 0ull;  // children of p passed to level l-1
   if (par_next) {
     const int32_t* nx = par_next + grp * TK;
     const int first = p << crlg;
@@ -658,7 +677,7 @@ __global__ __launch_bounds__(256) void record_wide_kernel(
     for (int i = a; i < TK; ++i) {
       const int v = nx[i];
       if (v < 0 || (v >> crlg) != p) break;
-      drop |= 1ull << (v & (CR - 1));
+      drop_child(v & (CR - 1), drop, drop_hi);
     }
   }
   const int h = (int)(grp % Hkv);
@@ -668,13 +687,13 @@ __global__ __launch_bounds__(256) void record_wide_kernel(
   const int ct = (int)((t / pw) & (CR - 1));
   const int nc = ((np - 1) << crlg) + ct + 1;
   const int nvalid = nc - (s << crlg);
-  unsigned long long m = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
-  if (CR < 64) m &= (1ull << CR) - 1ull;
-  m &= ~drop;
+  unsigned long long m, mh;
+  child_masks(nvalid, CR, drop, drop_hi, m, mh);
   const int64_t row = (b * Hkv + h) * Pl + p;
   const int64_t wi = row * W + (t >> 5);
   const int e = rowoff[row] + wpre[wi] + __popc(bm[wi] & ((1u << (t & 31)) - 1u));
   rec[e] = make_int4(t, (nc - 1 - (s << crlg)) | (s << 16), (int)(uint32_t)m, (int)(uint32_t)(m >> 32));
+  if (rech) rech[e] = make_int2((int)(uint32_t)mh, (int)(uint32_t)(mh >> 32));
 }
 
 // ---------------------------------------------------------------- dkv
@@ -685,7 +704,8 @@ struct DkvArgs {
   const void* dO;
   const float *gmax, *gsum, *delta;
   const int32_t *ptab, *npieces;
-  const int4* rec;  // per entry: t, rho, accumulate mask (lo, hi)
+  const int4* rec;  // per entry: t, rho, accumulate mask of children 0..63 (lo, hi)
+  const int2* rech;  // CR 128: accumulate mask of children 64..127 (nullptr below)
   const float *cosb, *sinb;
   float* partial;
   uint16_t* ds;  // nullable: dS per (entry, tile) for the dq pass
@@ -934,9 +954,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   const bool live = node0 < a.N;
   if (PW == 1 && !live) return;
   const uint32_t cmask = CR < 16 ? ((1u << CR) - 1u) : 0xffffu;
-  auto tile_mask = [&](const int4& rc) {
-    const unsigned long long m64 = ((unsigned long long)(uint32_t)rc.w << 32) | (uint32_t)rc.z;
-    return (uint32_t)(m64 >> coff) & cmask;
+  // the tile's children of an entry's accumulate mask (children 0..63 in the
+  // record, 64..127 of CR 128 in the second mask)
+  auto tile_mask = [&](const int4& r, const int2& rh) {
+    const bool up = coff >= 64;
+    const uint32_t lo = up ? (uint32_t)rh.x : (uint32_t)r.z, hi = up ? (uint32_t)rh.y : (uint32_t)r.w;
+    const unsigned long long m64 = ((unsigned long long)hi << 32) | lo;
+    return (uint32_t)(m64 >> (coff & 63)) & cmask;
   };
   // stationary K~ / V fragments of the tile's children (lane cand = u16)
   bf16x8 kh[KS], kl[KS], vh[KS], vl[KS];
@@ -962,6 +986,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   // without staging.
   int base = -64;
   int4 rb = make_int4(0, 0, 0, 0);
+  int2 rbh = make_int2(0, 0);
   unsigned long long work = 0ull;
   auto next_work = [&](int e) {  // first entry >= e with work, or ne
     while (e < ne) {
@@ -969,7 +994,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
         base = e & ~63;
         const bool in = base + lane < ne;
         rb = in ? a.rec[e0 + base + lane] : make_int4(0, 0, 0, 0);
-        work = __ballot(in && (PW > 1 ? (rb.z | rb.w) != 0 : tile_mask(rb) != 0u));
+        if (a.rech) rbh = in ? a.rech[e0 + base + lane] : make_int2(0, 0);
+        work = __ballot(in && (PW > 1 ? (rb.z | rb.w) != 0 : tile_mask(rb, rbh) != 0u));
       }
       const unsigned long long m = work >> (e - base);
       if (m) return e + (int)__builtin_ctzll(m);
@@ -977,10 +1003,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     }
     return ne;
   };
-  auto rec_of = [&](int e) {  // e lies in the held batch
+  // (t, rho | s << 16, this wave's tile mask, 0) of entry e (in the held batch)
+  auto rec_of = [&](int e) {
     const int i = e - base;
-    return make_int4(__builtin_amdgcn_readlane(rb.x, i), __builtin_amdgcn_readlane(rb.y, i),
-                     __builtin_amdgcn_readlane(rb.z, i), __builtin_amdgcn_readlane(rb.w, i));
+    const int4 r = make_int4(__builtin_amdgcn_readlane(rb.x, i), __builtin_amdgcn_readlane(rb.y, i),
+                             __builtin_amdgcn_readlane(rb.z, i), __builtin_amdgcn_readlane(rb.w, i));
+    const int2 rh = make_int2(__builtin_amdgcn_readlane(rbh.x, i), __builtin_amdgcn_readlane(rbh.y, i));
+    return make_int4(r.x, r.y, (int)tile_mask(r, rh), 0);
   };
   int e = next_work(0);
   int4 rc = e < ne ? rec_of(e) : make_int4(0, 0, 0, 0);
@@ -997,7 +1026,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     if (nxt && en < ne) stage_issue<D, TIn, HAS_S, NT, !HAS_S>(nxt, a, grp_of(rn.x), rn.y, tile, lane, wv, PW);
     const float* tab = (const float*)(S0 + St::OFF_TAB);  // cos [HALF], sin [HALF]
     const float* sm = (const float*)(S0 + St::OFF_SM);    // gmax, gsum, delta [16 each]
-    const bool ok = (tile_mask(rc) >> u16) & 1u;
+    const bool ok = ((uint32_t)rc.z >> u16) & 1u;
 
     f32x4 S = {0.f, 0.f, 0.f, 0.f};
     if constexpr (HAS_S) {
@@ -1783,15 +1812,16 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
                          rowoff, poff, nrows, (int)BP.piece[l], ptab, npieces);
     }
     int4* recs = (int4*)(ws + BP.off_rec[l]);
+    int2* rech = BP.off_rech >= 0 ? (int2*)(ws + BP.off_rech) : nullptr;  // CR 128
     if (d->top_k > 64)
       hipLaunchKernelGGL(record_wide_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
                          parents + l * lstride, l > 0 ? parents + (l - 1) * lstride : nullptr, bm,
                          wpre, rowoff, d->T, d->H_kv, d->top_k, Pl, BP.W, P.pw[l], CR, P.cr_log2,
-                         ent, recs);
+                         ent, recs, rech);
     else
       hipLaunchKernelGGL(record_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
                          parl, l > 0 ? parents + (l - 1) * lstride : nullptr, bm, wpre, rowoff,
-                         d->T, d->H_kv, d->top_k, Pl, BP.W, P.pw[l], CRl, lgl, ent, recs,
+                         d->T, d->H_kv, d->top_k, Pl, BP.W, P.pw[l], CRl, lgl, ent, recs, rech,
                          BP.use_ds ? (int4*)(ws + BP.off_emap[l]) : nullptr);
     DkvArgs a;
     memset(&a, 0, sizeof(a));
@@ -1807,6 +1837,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.ptab = ptab;
     a.npieces = npieces;
     a.rec = recs;
+    a.rech = rech;
     a.cosb = cosb;
     a.sinb = sinb;
     a.partial = partial;

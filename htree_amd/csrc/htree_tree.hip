@@ -23,14 +23,16 @@ int make_plan(const htree_dims* d, Plan* p) {
       (int64_t)d->max_top_nodes > (int64_t)d->top_k * d->compression_rate ||
       d->compression_rate < 2)
     return HTREE_ECONFIG;
-  if ((int64_t)d->rope_rows < (int64_t)d->top_k * d->compression_rate)
+  // the kernels read every candidate position's row and the row of angle CR
+  if ((int64_t)d->rope_rows < (int64_t)d->top_k * d->compression_rate ||
+      d->rope_rows <= d->compression_rate)
     return HTREE_ECONFIG;
   if (d->kv_share < 0 || d->kv_share > 2 || (d->kv_share == 2 && d->H_kv % 2 != 0))
     return HTREE_ESHAPE;
   const int CR = d->compression_rate;
   const int64_t max_tiles = (int64_t)d->top_k * (CR > 16 ? CR : 16) / 16;
   const bool wide = max_tiles > kMaxTiles || d->top_k > kMaxTK;
-  if ((d->D != 32 && d->D != 64 && d->D != 128) || d->H / d->H_kv > 16 || CR < 4 || CR > 64 ||
+  if ((d->D != 32 && d->D != 64 && d->D != 128) || d->H / d->H_kv > 16 || CR < 4 || CR > 128 ||
       (wide && (d->top_k > kWideMaxTK || (int64_t)d->top_k * CR > kWideMaxPos)))
     return HTREE_EUNSUPPORTED;
   // shared selections over KV-head pairs: the paired waves of the
@@ -90,7 +92,7 @@ constexpr int kSpanUpper = 32;
 
 struct BuildArgs {
   const void* x0[2];                    // leaves: k, v [B][N_0][Hkv][D]
-  void* lx[2][HTREE_MAX_LEVELS];        // levels l >= 1: [B][N_l][Hkv][D]
+  void* lx[2][HTREE_MAX_LEVELS];        // every level [B][N_l][Hkv][D] (level 0: the leaves)
   uint16_t* kh[HTREE_MAX_LEVELS];
   uint16_t* kl[HTREE_MAX_LEVELS];
   uint16_t* vh[HTREE_MAX_LEVELS];
@@ -350,10 +352,10 @@ static int tree_build_t(const htree_dims* d, const Plan& P, const void* k, const
   a.x0[0] = k;
   a.x0[1] = v;
   for (int l = 0; l < P.L; ++l) {
-    if (l > 0) {
-      a.lx[0][l] = level_k[l];
-      a.lx[1][l] = level_v[l];
-    }
+    // level 0 is the leaves: build_level_kernel pools level 1 from them when
+    // CR > kSpan (a level-1 node covers more than one span)
+    a.lx[0][l] = l > 0 ? level_k[l] : const_cast<void*>(k);
+    a.lx[1][l] = l > 0 ? level_v[l] : const_cast<void*>(v);
     a.kh[l] = (uint16_t*)(base + P.off_kh[l]);
     a.kl[l] = (uint16_t*)(base + P.off_kl[l]);
     a.vh[l] = (uint16_t*)(base + P.off_vh[l]);
@@ -375,6 +377,9 @@ static int tree_build_t(const htree_dims* d, const Plan& P, const void* k, const
   a.chunks = (P.N[0] + kSpan - 1) / kSpan;
   hipLaunchKernelGGL(build_span_kernel<T>, dim3((unsigned)(BH * a.chunks)), dim3(256), 0, st, a);
   for (int l = ls; l < P.L; ++l) {
+    // the level read and the level written (host-checked before the launch)
+    for (int x = 0; x < 2; ++x)
+      if (!a.lx[x][l - 1] || !a.lx[x][l]) return HTREE_ENULL;
     const int64_t per = (P.N[l] + kLevelNodes - 1) / kLevelNodes;
     hipLaunchKernelGGL(build_level_kernel<T>, dim3((unsigned)(BH * per)), dim3(64), 0, st, a, l);
   }
@@ -398,12 +403,12 @@ const char* htree_strerror(int status) {
     case HTREE_ECONFIG:
       return "invalid tree configuration: compression_rate, top_k_per_layer and max_top_nodes "
              "must be powers of two with max_top_nodes <= top_k_per_layer * compression_rate "
-             "and rope_rows >= top_k_per_layer * compression_rate";
+             "and rope_rows >= top_k_per_layer * compression_rate, rope_rows > compression_rate";
     case HTREE_EUNSUPPORTED:
       return "configuration outside this HIP build: needs D in {32,64,128}, H/H_kv <= 16 "
              "(up to 32 with kv_share 2, where top_k_per_layer <= 64 and "
              "top_k_per_layer * max(compression_rate,16) <= 1024), "
-             "4 <= compression_rate <= 64, top_k_per_layer <= 1024 and "
+             "4 <= compression_rate <= 128, top_k_per_layer <= 1024 and "
              "top_k_per_layer * compression_rate <= 16384 (where top_k_per_layer > 64 or "
              "top_k_per_layer * max(compression_rate,16) / 16 > 64); the backward also needs "
              "B * T * H_kv * min(top_k_per_layer, parents of a level) < 2^31 per level";

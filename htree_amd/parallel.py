@@ -10,7 +10,7 @@ Differences, all deliberate:
   * limits of this HIP build (AssertionError): max(K, V) in {32, 64, 128}
     (K even), H / H_kv <= 16 (or even and <= 32 where top_k_per_layer <= 64
     and top_k_per_layer * max(compression_rate, 16) <= 1024), 4 <= compression_rate
-    <= 64, top_k_per_layer <= 1024 and top_k_per_layer * compression_rate <=
+    <= 128, top_k_per_layer <= 1024 and top_k_per_layer * compression_rate <=
     16384 candidates per level.
   * a query group of G > 16 heads (the reference pads it to G_PAD,
     src/parallel.py:1023) runs as two groups of G/2 heads over duplicated KV
@@ -185,7 +185,8 @@ def make_dims(B, T, H, H_kv, D, compression_rate, max_top_nodes, top_k_per_layer
 
 def check_tables(cos, sin, half: int, rows_min: int, device):
     """RoPE tables handed in by a caller (a bwd_ctx's cos_cache / sin_cache)
-    go to the kernels as they are: fp32 [rows, half], rows >= rows_min."""
+    go to the kernels as they are: fp32 [rows, half], rows >= rows_min (every
+    candidate position, and the row of angle compression_rate)."""
     for name, t in (("cos_cache", cos), ("sin_cache", sin)):
         assert t.dtype == torch.float32 and t.dim() == 2 and t.shape[1] == half, \
             f"{name} must be fp32 [rows, {half}], got {t.dtype} {list(t.shape)}"

@@ -44,7 +44,7 @@ enum htree_status {
   HTREE_EUNSUPPORTED = -4, /* legal for the reference, outside this build:
                               D not in {32, 64, 128}, G = H/H_kv > 16
                               (see kv_share for G <= 32),
-                              compression_rate outside [4, 64],
+                              compression_rate outside [4, 128],
                               top_k > 1024, top_k * compression_rate > 16384,
                               more than HTREE_MAX_LEVELS levels, or a
                               backward level of 2^31 or more entries
@@ -64,7 +64,8 @@ typedef struct htree_dims {
   int32_t top_k;            /* TK: parents kept per layer (top_k_per_layer) */
   int32_t max_top_nodes;    /* MTN: build levels while N_l > MTN            */
   int32_t dtype;            /* enum htree_dtype of q, k, v, out             */
-  int32_t rope_rows;        /* rows of the cos/sin tables (>= top_k * CR)   */
+  int32_t rope_rows;        /* rows of the cos/sin tables (>= top_k * CR,
+                               > CR)                                         */
   int32_t kv_share;         /* 0 or 1: every KV head selects on its own.
                                2: KV heads 2i and 2i+1 hold the same keys and
                                values and share one Top-K selection (their

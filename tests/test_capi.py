@@ -58,6 +58,14 @@ def test_baseline_level_counts():
     assert len(N.levels(dims(T=65536))) == 4
 
 
+def test_compression_rate_128_accepted():
+    # 8 tiles per parent; the RoPE tables need a row past CR
+    assert len(N.levels(dims(T=3000, H=8, compression_rate=128, top_k=4, max_top_nodes=512,
+                             rope_rows=1536))) == 2
+    d = dims(T=3000, H=8, compression_rate=128, top_k=1, max_top_nodes=128, rope_rows=128)
+    assert N.lib().htree_levels(ctypes.byref(d), None, None) == N.HTREE_ECONFIG
+
+
 def test_largest_candidate_sets_accepted():
     # 16384 candidates per level: top_k 1024 at CR 16, top_k 512 at CR 32
     assert len(N.levels(dims(T=20000, H=8, top_k=1024, max_top_nodes=16384, rope_rows=17408))) == 2
@@ -78,6 +86,8 @@ def test_shared_kv_heads_accepted():
     (dict(T=0), N.HTREE_ESHAPE),
     (dict(top_k=12), N.HTREE_ECONFIG),                 # not a power of two
     (dict(compression_rate=24), N.HTREE_ECONFIG),
+    (dict(compression_rate=256, top_k=4, max_top_nodes=512, rope_rows=2048),
+     N.HTREE_EUNSUPPORTED),                            # CR > 128
     (dict(max_top_nodes=512), N.HTREE_ECONFIG),        # > top_k * CR
     (dict(rope_rows=100), N.HTREE_ECONFIG),
     (dict(D=96), N.HTREE_EUNSUPPORTED),

@@ -55,6 +55,9 @@ CASES = [
     # CR 32 with stored scores: the top level (125 nodes) merged into 64-child
     # parents of two real ones, the last one partial
     (1, 4000, 8, 1, 64, 32, 8, 256, "bfloat16", 21),
+    # CR 128: children 64..127 in the records' second mask; dq recomputes
+    (1, 3000, 8, 2, 64, 128, 4, 512, "bfloat16", 22),  # 32 tiles per level
+    (1, 1500, 8, 1, 32, 128, 2, 256, "float32", 23),    # 16 tiles per level
 ]
 
 
@@ -229,6 +232,7 @@ REGIME = [
     (1, 12000, 16, 4, 32, 16, 512, 8192, "float32", 43),  # correctness_test_bwd.py defaults
     (1, 20000, 8, 2, 32, 16, 1024, 16384, "float32", 45),  # top_k 1024: 16384 candidates
     (1, 20000, 8, 2, 64, 32, 512, 512, "bfloat16", 46),    # top_k 512 at CR 32, 3 levels
+    (1, 20000, 8, 2, 32, 128, 128, 16384, "float16", 47),  # CR 128, 16384 candidates
 ]
 
 

@@ -47,6 +47,8 @@ SMALL = [
     (1, 3000, 8, 1, 128, 32, 32, 256, "bfloat16", 12),  # CR 32, top_k 32 (the C4 workload's tree): 64 tiles
     (1, 2200, 8, 2, 64, 16, 32, 256, "float16", 13),    # 32 tiles, fp16 (split V)
     (2, 4096, 16, 2, 128, 16, 16, 16, "bfloat16", 14),  # 16-node top level (keeps every candidate), as C5
+    (1, 3000, 8, 2, 64, 128, 4, 512, "bfloat16", 15),  # CR 128: 32 tiles per level
+    (1, 1500, 8, 1, 32, 128, 2, 256, "float32", 16),    # CR 128: 16 tiles per level
 ]
 
 
@@ -154,6 +156,7 @@ WIDE = [
     # 16384 candidates per level (64 keys per thread in the selection)
     (1, 20000, 8, 2, 32, 16, 1024, 16384, "float32", 26, False),  # top_k 1024
     (1, 20000, 8, 2, 64, 32, 512, 512, "bfloat16", 27, False),    # top_k 512 at CR 32, 3 levels
+    (1, 20000, 8, 2, 32, 128, 128, 16384, "float16", 28, False),  # CR 128
 ]
 
 
