@@ -53,11 +53,22 @@ WORKLOADS = {
 DT_SHORT = {"bfloat16": "bf16", "float16": "f16", "float32": "f32"}
 
 
+def forward_kernel(workload: str) -> str:
+    """The fused forward kernel a workload runs: the wide form for top_k > 64
+    or more than 64 candidate tiles of 16 per level, the register form up to
+    16 tiles, the streaming form between."""
+    (_, _, _, _, _, CR, TK, _), _, _ = WORKLOADS[workload]
+    tiles = TK * max(CR, 16) // 16
+    if TK > 64 or tiles > 64:
+        return "fwd_wide_kernel"
+    return "fwd_reg_kernel" if tiles <= 16 else "fwd_kernel"
+
+
 def measured_traffic(workload: str):
     """HBM bytes per launch of the fused forward kernel from the committed
     rocprofv3 PMC summary of this workload (FETCH_SIZE + WRITE_SIZE, each
     scaled by the same counter's reading of the calibration copy), or None."""
-    kern = "fwd_wide_kernel" if workload.startswith("REF") else "fwd_reg_kernel"
+    kern = forward_kernel(workload)
     path = os.path.join(ROOT, "profiles", f"{kern}_{workload.lower()}_traffic.json")
     try:
         with open(path) as f:
@@ -347,8 +358,7 @@ def main():
             "algorithmic_bytes": w.bwd_bytes},
         "wall_ms_per_step": m["step_ms"],
         "roofline": {
-            "kernel": ("htree::fwd_wide_kernel" if ctx["dims"].top_k > 64 else "htree::fwd_reg_kernel")
-                      + " (fused forward, all levels)",
+            "kernel": f"htree::{forward_kernel(args.workload)} (fused forward, all levels)",
             "bound": "hbm",
             "achieved": achieved / 1e9,
             "peak": HBM_PEAK / 1e9,
