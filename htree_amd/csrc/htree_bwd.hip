@@ -705,7 +705,6 @@ struct DkvArgs {
   const float *gmax, *gsum, *delta;
   const int32_t *ptab, *npieces;
   const int4* rec;  // per entry: t, rho, accumulate mask of children 0..63 (lo, hi)
-  const int2* rech;  // CR 128: accumulate mask of children 64..127 (nullptr below)
   const float *cosb, *sinb;
   float* partial;
   uint16_t* ds;  // nullable: dS per (entry, tile) for the dq pass
@@ -715,6 +714,7 @@ struct DkvArgs {
   int64_t N, Np, pw, Pl, BTH;  // BTH = B*T*H (length of gmax / gsum / delta)
   int32_t T, H, Hkv, G, CR, crlg, TK, tpp, max_tiles;
   float scale;
+  const int2* rech;  // CR 128: accumulate mask of children 64..127 (nullptr below)
 };
 
 // One entry's inputs staged in LDS by asynchronous copies: the 16 query
@@ -796,6 +796,14 @@ __device__ __forceinline__ void stage_issue(char* slot, const DkvArgs& a, int64_
     }
     int off = (g * CPR + (c < CPR ? c : 0)) * 16;
     off = g < G ? off : 0;  // rows past the group: in-bounds filler, never used
+    // rebuilt scores: a copy whose 64 chunks all lie in rows past the group
+    // is skipped (the kernel zeroes those rows once; the test is uniform over
+    // the wave).  C4 backward -3.6%; the stored-score kernels measured slower
+    // with it (their register allocation moves) and keep every copy.
+    if constexpr (!HAS_S) {
+      const int g0 = St::SWZ ? (j * 64) >> 4 : (j * 64) / (CPR + 1);
+      if (g0 >= G) continue;
+    }
     if ((St::NCH % 64 == 0) || P < St::NCH) {
       if (pq) __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void*)(slot + j * 1024), 16, off, 0, 0, 0);
       if (pd)
@@ -917,8 +925,12 @@ struct DoRow<D, __bf16> {
 // tiles per parent (2 or 4, CR 32 / 64): one block of PW waves per piece,
 // wave w taking tile w; the waves share one staged copy of each entry (each
 // issues a part of the copies) and meet at a barrier per entry.
-template <int D, bool PREC, typename TIn, bool HAS_S, int PW>
+// M128: CR 128 (children 64..127 in the records' second mask; one-wave form
+// only), a separate instance so that the other configurations keep the
+// one-mask record handling.
+template <int D, bool PREC, typename TIn, bool HAS_S, int PW, bool M128 = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void dkv_kernel(const DkvArgs a) {
+  static_assert(!M128 || PW == 1, "CR 128 runs the one-wave form");
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
   constexpr int NT = HAS_S ? PW : 0;  // stored-score tiles per staged entry
   using St = Stage<D, TIn, NT>;
@@ -954,9 +966,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   const bool live = node0 < a.N;
   if (PW == 1 && !live) return;
   const uint32_t cmask = CR < 16 ? ((1u << CR) - 1u) : 0xffffu;
-  // the tile's children of an entry's accumulate mask (children 0..63 in the
-  // record, 64..127 of CR 128 in the second mask)
-  auto tile_mask = [&](const int4& r, const int2& rh) {
+  // the tile's children of an entry's accumulate mask
+  auto tile_mask = [&](const int4& rc) {
+    const unsigned long long m64 = ((unsigned long long)(uint32_t)rc.w << 32) | (uint32_t)rc.z;
+    return (uint32_t)(m64 >> coff) & cmask;
+  };
+  // M128: children 0..63 in the record, 64..127 in the second mask
+  auto tile_mask128 = [&](const int4& r, const int2& rh) {
     const bool up = coff >= 64;
     const uint32_t lo = up ? (uint32_t)rh.x : (uint32_t)r.z, hi = up ? (uint32_t)rh.y : (uint32_t)r.w;
     const unsigned long long m64 = ((unsigned long long)hi << 32) | lo;
@@ -979,6 +995,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   for (int n = 0; n < ND; ++n) dv[n] = dk[n] = f32x4{0.f, 0.f, 0.f, 0.f};
   const bool gv = u16 < G;
   auto grp_of = [&](int t) { return (b * a.T + t) * a.Hkv + h; };
+  // rebuilt scores: q / dO rows past the group (G < 16) that no copy
+  // reaches are zero, written once here (the MFMAs read them; their P and dS
+  // are zero)
+  if (!HAS_S && G < 16) {
+    const int nz = (16 - G) * St::RP / 16;  // 16-byte chunks per area
+    const int nthr = PW > 1 ? 64 * PW : 64, me = PW > 1 ? (int)threadIdx.x : lane;
+    for (int s = 0; s < (TWO ? 2 : 1); ++s) {
+      char* slot = s == 0 ? stage_a[sw] : stage_b[sw];
+      for (int i = me; i < 2 * nz; i += nthr) {
+        const int area = i < nz ? 0 : St::OFF_DO;
+        *(uint4*)(slot + area + G * St::RP + (i % nz) * 16) = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+    if (PW > 1) __syncthreads(); else wave_sync();
+  }
 
   // The piece's records are held 64 at a time in the lanes (lane i = entry
   // base + i) with a ballot of the entries whose tile mask (shared block:
@@ -994,8 +1025,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
         base = e & ~63;
         const bool in = base + lane < ne;
         rb = in ? a.rec[e0 + base + lane] : make_int4(0, 0, 0, 0);
-        if (a.rech) rbh = in ? a.rech[e0 + base + lane] : make_int2(0, 0);
-        work = __ballot(in && (PW > 1 ? (rb.z | rb.w) != 0 : tile_mask(rb, rbh) != 0u));
+        if constexpr (M128) {
+          rbh = in ? a.rech[e0 + base + lane] : make_int2(0, 0);
+          work = __ballot(in && tile_mask128(rb, rbh) != 0u);
+        } else {
+          work = __ballot(in && (PW > 1 ? (rb.z | rb.w) != 0 : tile_mask(rb) != 0u));
+        }
       }
       const unsigned long long m = work >> (e - base);
       if (m) return e + (int)__builtin_ctzll(m);
@@ -1003,13 +1038,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     }
     return ne;
   };
-  // (t, rho | s << 16, this wave's tile mask, 0) of entry e (in the held batch)
+  // the record of entry e (in the held batch); M128: (t, rho | s << 16, this
+  // wave's tile mask, 0)
   auto rec_of = [&](int e) {
     const int i = e - base;
-    const int4 r = make_int4(__builtin_amdgcn_readlane(rb.x, i), __builtin_amdgcn_readlane(rb.y, i),
-                             __builtin_amdgcn_readlane(rb.z, i), __builtin_amdgcn_readlane(rb.w, i));
-    const int2 rh = make_int2(__builtin_amdgcn_readlane(rbh.x, i), __builtin_amdgcn_readlane(rbh.y, i));
-    return make_int4(r.x, r.y, (int)tile_mask(r, rh), 0);
+    if constexpr (M128) {
+      const int4 r = make_int4(__builtin_amdgcn_readlane(rb.x, i), __builtin_amdgcn_readlane(rb.y, i),
+                               __builtin_amdgcn_readlane(rb.z, i), __builtin_amdgcn_readlane(rb.w, i));
+      const int2 rh = make_int2(__builtin_amdgcn_readlane(rbh.x, i), __builtin_amdgcn_readlane(rbh.y, i));
+      return make_int4(r.x, r.y, (int)tile_mask128(r, rh), 0);
+    } else {
+      return make_int4(__builtin_amdgcn_readlane(rb.x, i), __builtin_amdgcn_readlane(rb.y, i),
+                       __builtin_amdgcn_readlane(rb.z, i), __builtin_amdgcn_readlane(rb.w, i));
+    }
   };
   int e = next_work(0);
   int4 rc = e < ne ? rec_of(e) : make_int4(0, 0, 0, 0);
@@ -1026,7 +1067,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
     if (nxt && en < ne) stage_issue<D, TIn, HAS_S, NT, !HAS_S>(nxt, a, grp_of(rn.x), rn.y, tile, lane, wv, PW);
     const float* tab = (const float*)(S0 + St::OFF_TAB);  // cos [HALF], sin [HALF]
     const float* sm = (const float*)(S0 + St::OFF_SM);    // gmax, gsum, delta [16 each]
-    const bool ok = ((uint32_t)rc.z >> u16) & 1u;
+    bool ok;
+    if constexpr (M128) ok = ((uint32_t)rc.z >> u16) & 1u;
+    else ok = (tile_mask(rc) >> u16) & 1u;
 
     f32x4 S = {0.f, 0.f, 0.f, 0.f};
     if constexpr (HAS_S) {
@@ -1873,6 +1916,9 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
       if (has_s) HT_DKV(true, 4); else HT_DKV(false, 4);
     } else if (tppl == 2) {
       if (has_s) HT_DKV(true, 2); else HT_DKV(false, 2);
+    } else if (rech) {  // CR 128 (no stored scores)
+      hipLaunchKernelGGL((dkv_kernel<D, PREC, T, false, 1, true>), dim3((unsigned)((waves + 3) / 4)),
+                         dim3(256), 0, st, a);
     } else {
       if (has_s) HT_DKV(true, 1); else HT_DKV(false, 1);
     }
