@@ -74,6 +74,9 @@ struct BwdPlan {
   int vcr[HTREE_MAX_LEVELS], vlg[HTREE_MAX_LEVELS], vtpp[HTREE_MAX_LEVELS], vm[HTREE_MAX_LEVELS];
   int vlevel;
   int64_t off_vlist;                   // the merged level's lists [B,T,H_kv,TK]
+  // stored-dS path: each level's piece offsets / table / count of its own,
+  // so that every level's index can be built ahead of the dK / dV passes
+  int64_t off_lpoff[HTREE_MAX_LEVELS], off_lptab[HTREE_MAX_LEVELS], off_lnp[HTREE_MAX_LEVELS];
   int64_t max_ptiles;                  // pieces x tiles per piece, largest level
   int64_t bytes;
 };
@@ -195,6 +198,12 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true, 
   b->off_ptab = take(b->max_pieces * 3 * 4);
   b->off_vlist = b->vlevel >= 0 ? take(b->max_entries * 4) : -1;
   b->off_rech = CR > 64 ? take(b->max_entries * 8) : -1;
+  for (int l = 0; l < P.L; ++l) {
+    const int64_t np = (b->ent[l] + b->piece[l] - 1) / b->piece[l] + b->rows[l];
+    b->off_lpoff[l] = b->use_ds ? take((b->rows[l] + 1) * 4) : b->off_poff;
+    b->off_lptab[l] = b->use_ds ? take(np * 3 * 4) : b->off_ptab;
+    b->off_lnp[l] = b->use_ds ? take(4) : b->off_npieces;
+  }
   const int64_t* ent = b->ent;
   for (int l = 0; l < P.L; ++l) {
     b->off_rec[l] = b->use_ds ? take(ent[l] * 16) : l == 0 ? take(b->max_entries * 16) : b->off_rec[0];
@@ -1771,13 +1780,56 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void d
 }
 
 // ---------------------------------------------------------------- host
+// Side stream (default priority) for the per-level indexes of a stored-dS
+// backward, with the events that order it against the caller's stream: one
+// set per device, created at the first such backward on it.  g_side_mu is
+// held while a backward enqueues its work on them.
+struct SideStream {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr;
+  hipEvent_t lev[HTREE_MAX_LEVELS] = {};
+};
+constexpr int kMaxSideDevices = 64;
+static std::mutex g_side_mu;
+static SideStream g_side[kMaxSideDevices];
+
+// The current device's side stream (created if needed); g_side_mu held.
+static int side_for_current_device(SideStream** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxSideDevices) return HTREE_EUNSUPPORTED;
+  SideStream& S = g_side[dev];
+  if (!S.s) {
+    SideStream n;
+    e = hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&n.fork, hipEventDisableTiming);
+    for (int l = 0; l < HTREE_MAX_LEVELS && e == hipSuccess; ++l)
+      e = hipEventCreateWithFlags(&n.lev[l], hipEventDisableTiming);
+    if (e != hipSuccess) return (int)e;  // (what was created is kept by the runtime)
+    S = n;
+  }
+  *out = &S;
+  return HTREE_OK;
+}
+
 template <int D, bool PREC, typename T>
 static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const void* q,
                       const void* out, const void* dO, const float* gmax, const float* gsum,
                       const int32_t* parents, const char* tws, const float* cosb, const float* sinb,
                       const char* scores, float* dq, float* dk, float* dv, char* ws,
-                      hipStream_t st) {
+                      hipStream_t st, SideStream* side) {
   const Plan& P = BP.P;
+  if (side && !BP.use_ds) side = nullptr;  // shared records: the levels run in order
+  hipError_t ev_err = hipSuccess;  // first failure of the stream ordering calls
+  auto order = [&](hipError_t e) {
+    if (e != hipSuccess && ev_err == hipSuccess) ev_err = e;
+  };
+  if (side) {
+    // the side stream starts after everything enqueued on st so far
+    order(hipEventRecord(side->fork, st));
+    order(hipStreamWaitEvent(side->s, side->fork, 0));
+  }
   int64_t off_mref = 0;
   train_scores_bytes(d, P, &off_mref);
   const int64_t BH = (int64_t)d->B * d->H_kv;
@@ -1810,19 +1862,25 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
   int32_t* cnt = (int32_t*)(ws + BP.off_cnt);
   int32_t* rowoff = (int32_t*)(ws + BP.off_rowoff);
   int32_t* pcnt = (int32_t*)(ws + BP.off_pcnt);
-  int32_t* poff = (int32_t*)(ws + BP.off_poff);
-  int32_t* npieces = (int32_t*)(ws + BP.off_npieces);
-  int32_t* ptab = (int32_t*)(ws + BP.off_ptab);
   int32_t* wpre = (int32_t*)(ws + BP.off_wpre);
   float* partial = (float*)(ws + BP.off_partial);
   // A top level of <= top_k nodes passes every candidate down and
   // accumulates none (src/naive.py:97-101): it has no dS and no dK / dV of
   // its own, so the passes start one level lower.
   const int Ltop = (P.L > 1 && P.N[P.L - 1] <= d->top_k) ? P.L - 2 : P.L - 1;
-  for (int l = Ltop; l >= 0; --l) {
+  // Per level: the reverse index (bitmap -> row counts -> pieces -> records),
+  // then dK / dV and their reduction.  The index reads only the parent
+  // lists; with stored dS every level has its own records and piece tables,
+  // so the side stream builds all levels' indexes while the caller's stream
+  // runs prep / packing and the dK / dV passes, each level's pass waiting on
+  // its index's event.  Otherwise the levels run in order on one stream.
+  auto index_level = [&](int l, hipStream_t s) {
     // the level's rows: parents of vcr children (64 at the merged level)
     const int CRl = BP.vcr[l], lgl = BP.vlg[l], tppl = BP.vtpp[l];
     const int64_t Pl = (P.N[l] + CRl - 1) / CRl;
+    int32_t* poff = (int32_t*)(ws + BP.off_lpoff[l]);
+    int32_t* npieces = (int32_t*)(ws + BP.off_lnp[l]);
+    int32_t* ptab = (int32_t*)(ws + BP.off_lptab[l]);
     const int64_t nrows = BP.rows[l];
     const int64_t words = nrows * BP.W;
     const int64_t ent = lstride;
@@ -1830,7 +1888,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     if (l == BP.vlevel) {
       // the merged level's lists: 64-child parents 0 .. (t's node) / 64
       int32_t* vl = (int32_t*)(ws + BP.off_vlist);
-      hipLaunchKernelGGL(prefix_list_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
+      hipLaunchKernelGGL(prefix_list_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, s,
                          d->T, d->H_kv, d->top_k, P.pw[l], lgl, ent, vl);
       parl = vl;
     }
@@ -1838,34 +1896,44 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     // C2's and C4's level 0) by columns; sparser ones by global atomics
     // (C5's level 0, one per eight: columns measured +0.6% of its backward)
     if (4 * BP.ent[l] >= words) {
-      hipLaunchKernelGGL(bitmap_cols_kernel, dim3((unsigned)(BH * BP.W)), dim3(256), 0, st,
+      hipLaunchKernelGGL(bitmap_cols_kernel, dim3((unsigned)(BH * BP.W)), dim3(256), 0, s,
                          parl, d->T, d->H_kv, d->top_k, Pl, BP.W, bm);
     } else {
-      hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st,
+      hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, s,
                          bm, words);
-      hipLaunchKernelGGL(bitmap_set_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
+      hipLaunchKernelGGL(bitmap_set_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, s,
                          parl, d->T, d->H_kv, d->top_k, Pl, BP.W, ent, bm);
     }
-    hipLaunchKernelGGL(row_scan_kernel, dim3((unsigned)nrows), dim3(256), 0, st, bm, BP.W,
+    hipLaunchKernelGGL(row_scan_kernel, dim3((unsigned)nrows), dim3(256), 0, s, bm, BP.W,
                        (int)BP.piece[l], wpre, cnt, pcnt);
-    hipLaunchKernelGGL(scan_kernel, dim3(2), dim3(1024), 0, st, cnt, rowoff, pcnt, poff, nrows);
+    hipLaunchKernelGGL(scan_kernel, dim3(2), dim3(1024), 0, s, cnt, rowoff, pcnt, poff, nrows);
     {
       const int64_t np = (BP.ent[l] + BP.piece[l] - 1) / BP.piece[l] + BP.rows[l];  // bound
-      hipLaunchKernelGGL(piece_kernel, dim3((unsigned)((np + 255) / 256)), dim3(256), 0, st, cnt,
+      hipLaunchKernelGGL(piece_kernel, dim3((unsigned)((np + 255) / 256)), dim3(256), 0, s, cnt,
                          rowoff, poff, nrows, (int)BP.piece[l], ptab, npieces);
     }
     int4* recs = (int4*)(ws + BP.off_rec[l]);
     int2* rech = BP.off_rech >= 0 ? (int2*)(ws + BP.off_rech) : nullptr;  // CR 128
     if (d->top_k > 64)
-      hipLaunchKernelGGL(record_wide_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
+      hipLaunchKernelGGL(record_wide_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, s,
                          parents + l * lstride, l > 0 ? parents + (l - 1) * lstride : nullptr, bm,
                          wpre, rowoff, d->T, d->H_kv, d->top_k, Pl, BP.W, P.pw[l], CR, P.cr_log2,
                          ent, recs, rech);
     else
-      hipLaunchKernelGGL(record_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, st,
+      hipLaunchKernelGGL(record_kernel, dim3((unsigned)((ent + 255) / 256)), dim3(256), 0, s,
                          parl, l > 0 ? parents + (l - 1) * lstride : nullptr, bm, wpre, rowoff,
                          d->T, d->H_kv, d->top_k, Pl, BP.W, P.pw[l], CRl, lgl, ent, recs, rech,
                          BP.use_ds ? (int4*)(ws + BP.off_emap[l]) : nullptr);
+  };
+  auto dkv_level = [&](int l) {
+    // the level's rows: parents of vcr children (64 at the merged level)
+    const int CRl = BP.vcr[l], lgl = BP.vlg[l], tppl = BP.vtpp[l];
+    const int64_t Pl = (P.N[l] + CRl - 1) / CRl;
+    int32_t* poff = (int32_t*)(ws + BP.off_lpoff[l]);
+    int32_t* npieces = (int32_t*)(ws + BP.off_lnp[l]);
+    int32_t* ptab = (int32_t*)(ws + BP.off_lptab[l]);
+    int4* recs = (int4*)(ws + BP.off_rec[l]);
+    int2* rech = BP.off_rech >= 0 ? (int2*)(ws + BP.off_rech) : nullptr;  // CR 128
     DkvArgs a;
     memset(&a, 0, sizeof(a));
     a.kh = (const uint16_t*)(tws + P.off_kh[l]);
@@ -1943,6 +2011,21 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     else
       HT_RED(1);
 #undef HT_RED
+  };
+  if (side) {
+    for (int l = Ltop; l >= 0; --l) {
+      index_level(l, side->s);
+      order(hipEventRecord(side->lev[l], side->s));
+    }
+    for (int l = Ltop; l >= 0; --l) {
+      order(hipStreamWaitEvent(st, side->lev[l], 0));
+      dkv_level(l);
+    }
+  } else {
+    for (int l = Ltop; l >= 0; --l) {
+      index_level(l, st);
+      dkv_level(l);
+    }
   }
   // dq over all levels
   if (BP.use_ds) {
@@ -2020,6 +2103,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
       hipLaunchKernelGGL((dq_kernel<D, PREC, T, kWideMaxTK, kWideMaxPos>), grid, dim3(256), 0, st, a);
   }
   hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = ev_err;
   return e == hipSuccess ? HTREE_OK : (int)e;
 }
 
@@ -2054,7 +2138,7 @@ static int backward_impl(const htree_dims* d, float scale, const void* q, const 
                          const int32_t* parents, const void* tree_ws, int64_t tree_ws_bytes,
                          const float* cos_table, const float* sin_table, const void* scores_ws,
                          int64_t scores_bytes, float* dq, float* dk, float* dv, void* bwd_ws,
-                         int64_t bwd_ws_bytes, void* stream) {
+                         int64_t bwd_ws_bytes, void* stream, bool overlap = true) {
   BwdPlan BP;
   int rc = make_bwd_plan(d, &BP);
   if (rc) return rc;
@@ -2077,9 +2161,17 @@ static int backward_impl(const htree_dims* d, float scale, const void* q, const 
   hipStream_t st = (hipStream_t)stream;
   const char* tws = (const char*)tree_ws;
   char* ws = (char*)bwd_ws;
+  // stored dS: the per-level indexes go on the device's side stream
+  std::unique_lock<std::mutex> side_lock;
+  SideStream* side = nullptr;
+  if (overlap && BP.use_ds) {
+    side_lock = std::unique_lock<std::mutex>(g_side_mu);
+    rc = side_for_current_device(&side);
+    if (rc) return rc;
+  }
 #define HT_BWD(DD, PR, TT)                                                                      \
   return backward_t<DD, PR, TT>(d, BP, scale, q, out, dO, gmax, gsum, parents, tws, cos_table, \
-                                sin_table, scores, dq, dk, dv, ws, st)
+                                sin_table, scores, dq, dk, dv, ws, st, side)
   if (d->D == 128) {
     if (d->dtype == HTREE_BF16) HT_BWD(128, false, __bf16);
     if (d->dtype == HTREE_F16) HT_BWD(128, true, _Float16);
@@ -2185,7 +2277,7 @@ int htree_backward_noalloc(const htree_dims* d, float scale, const void* q, cons
   // the stored-dS plan when its workspace fits the array, else the smallest
   // (backward_impl takes the smaller plan for a workspace below the full one)
   return backward_impl(d, scale, q, out, dO, gmax, gsum, parents, tree_ws, tree_ws_bytes,
-                       cos_table, sin_table, scores, scores_bytes, dq, dk, dv, ws, need, stream);
+                       cos_table, sin_table, scores, scores_bytes, dq, dk, dv, ws, need, stream, false);
 }
 
 }  // extern "C"
