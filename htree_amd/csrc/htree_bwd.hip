@@ -938,7 +938,7 @@ struct DoRow<D, __bf16> {
 // only), a separate instance so that the other configurations keep the
 // one-mask record handling.
 template <int D, bool PREC, typename TIn, bool HAS_S, int PW, bool M128 = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void dkv_kernel(const DkvArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2))) void dkv_kernel(const DkvArgs a) {
   static_assert(!M128 || PW == 1, "CR 128 runs the one-wave form");
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
   constexpr int NT = HAS_S ? PW : 0;  // stored-score tiles per staged entry
@@ -1363,7 +1363,7 @@ __device__ __forceinline__ void rot_acc(f32x4 (&x)[D / 16], const float* c, cons
 //   sum_s R^-1(dq~_s, a - s CR) = R^-1(X, n_c-1 - (np-1) CR) = R(X, -c_t)
 // needs one table rotation per level.
 template <int D, bool PREC, typename TIn, int MAXTK, int MAXPOS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 ? 5 : 2))) void dq_kernel(const DqArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 ? 5 : D == 256 ? 1 : 2))) void dq_kernel(const DqArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
   // list capacity; selection bits of the candidate positions (MAXPOS)
   constexpr int SWW = MAXPOS / 32;
@@ -1618,7 +1618,7 @@ struct DqStage {
 // F16: K~^T and dS in fp16 with power-of-two scales (one MFMA per product,
 // scaled into the fp32 accumulator); else bf16 hi + lo of both (three).
 template <int D, bool F16>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void dq_ds_kernel(const DqDsArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 4))) void dq_ds_kernel(const DqDsArgs a) {
   constexpr int ND = D / 16, HALF = D / 2;
   using St = DqStage<D, F16>;
   __shared__ __attribute__((aligned(16))) char stage_all[kWavesPerBlock][St::BYTES];
@@ -2172,7 +2172,11 @@ static int backward_impl(const htree_dims* d, float scale, const void* q, const 
 #define HT_BWD(DD, PR, TT)                                                                      \
   return backward_t<DD, PR, TT>(d, BP, scale, q, out, dO, gmax, gsum, parents, tws, cos_table, \
                                 sin_table, scores, dq, dk, dv, ws, st, side)
-  if (d->D == 128) {
+  if (d->D == 256) {
+    if (d->dtype == HTREE_BF16) HT_BWD(256, false, __bf16);
+    if (d->dtype == HTREE_F16) HT_BWD(256, true, _Float16);
+    HT_BWD(256, true, float);
+  } else if (d->D == 128) {
     if (d->dtype == HTREE_BF16) HT_BWD(128, false, __bf16);
     if (d->dtype == HTREE_F16) HT_BWD(128, true, _Float16);
     HT_BWD(128, true, float);

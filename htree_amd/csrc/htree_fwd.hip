@@ -259,7 +259,7 @@ struct TileStage {
 // by R(., -CR) per slot (a table row in LDS), so a tile reads no global
 // memory besides its copies.
 template <int D, bool PREC, typename TIn, int MAXSLOT, bool TRACE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fwd_kernel(const FwdArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2))) void fwd_kernel(const FwdArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
   using St = FwdStage<D, PREC>;
   __shared__ WaveLds<MAXSLOT> lds_all[kWavesPerBlock];
@@ -714,7 +714,7 @@ __device__ __forceinline__ void rot_by(float (&x)[D / 32][8], const float* __res
 }
 
 template <int D, bool PREC, typename TIn, bool TRACE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fwd_reg_kernel(const FwdArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2))) void fwd_reg_kernel(const FwdArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
   __shared__ WaveLdsR lds_all[kWavesPerBlock];
   __shared__ float rot_cr[2][HALF];  // cos / sin of the angle CR
@@ -1424,7 +1424,9 @@ static int forward_impl(const htree_dims* d, float scale, const void* q, const v
   a.per_xcd = (int32_t)per;
   const dim3 grid((unsigned)(per * 8));
   hipStream_t st = (hipStream_t)stream;
-  if (d->D == 128)
+  if (d->D == 256)
+    launch_fwd_d<256>(d->dtype, a, P, grid, st);
+  else if (d->D == 128)
     launch_fwd_d<128>(d->dtype, a, P, grid, st);
   else if (d->D == 32)
     launch_fwd_d<32>(d->dtype, a, P, grid, st);

@@ -32,7 +32,7 @@ int make_plan(const htree_dims* d, Plan* p) {
   const int CR = d->compression_rate;
   const int64_t max_tiles = (int64_t)d->top_k * (CR > 16 ? CR : 16) / 16;
   const bool wide = max_tiles > kMaxTiles || d->top_k > kMaxTK;
-  if ((d->D != 32 && d->D != 64 && d->D != 128) || d->H / d->H_kv > 16 || CR < 4 || CR > 128 ||
+  if ((d->D != 32 && d->D != 64 && d->D != 128 && d->D != 256) || d->H / d->H_kv > 16 || CR < 4 || CR > 128 ||
       (wide && (d->top_k > kWideMaxTK || (int64_t)d->top_k * CR > kWideMaxPos)))
     return HTREE_EUNSUPPORTED;
   // shared selections over KV-head pairs: the paired waves of the
@@ -73,6 +73,9 @@ int make_plan(const htree_dims* d, Plan* p) {
     p->off_vl[l] = p->precise ? take(elems) : -1;
   }
   p->bytes = off;
+  // one (b, h_kv) block of a level's operand arrays is addressed through a
+  // buffer resource of 32-bit range
+  if (p->Np[0] * d->D * 2 > INT32_MAX) return HTREE_EUNSUPPORTED;
   return HTREE_OK;
 }
 
@@ -86,7 +89,7 @@ int make_plan(const htree_dims* d, Plan* p) {
 // a parent summed in child order in fp32, divided once, rounded to the level
 // dtype, and the next level pools the rounded values.
 constexpr int kSpan = 64;
-constexpr int kBuildMaxD = 128;
+constexpr int kBuildMaxD = 256;
 // nodes above the leaves a span holds: kSpan/CR + kSpan/CR^2 + ... <= 21 (CR 4)
 constexpr int kSpanUpper = 32;
 
@@ -209,10 +212,12 @@ __device__ __forceinline__ void zero_padding(const BuildArgs& a, int64_t bh) {
   }
 }
 
-template <typename T>
+// DM: the largest head dim the instance holds (128, or 256 for D = 256, so
+// that smaller dims keep the smaller LDS and register footprint)
+template <typename T, int DM>
 __global__ __launch_bounds__(256) void build_span_kernel(const BuildArgs a) {
-  __shared__ __attribute__((aligned(16))) T xs[kSpan * kBuildMaxD];       // the span's leaves
-  __shared__ __attribute__((aligned(16))) T us[kSpanUpper * kBuildMaxD];  // its upper nodes
+  __shared__ __attribute__((aligned(16))) T xs[kSpan * DM];       // the span's leaves
+  __shared__ __attribute__((aligned(16))) T us[kSpanUpper * DM];  // its upper nodes
   const int D = a.D, CR = a.CR, Hkv = a.Hkv;
   const int64_t bh = blockIdx.x / a.chunks;
   const int64_t n0 = (blockIdx.x - bh * a.chunks) * kSpan;
@@ -222,7 +227,7 @@ __global__ __launch_bounds__(256) void build_span_kernel(const BuildArgs a) {
   const int nl = (int)(N0 - n0 < kSpan ? N0 - n0 : kSpan);  // leaves of the span (>= 1)
   if (n0 == 0) zero_padding(a, bh);
   constexpr int PER = 16 / (int)sizeof(T);  // elements per 16-byte chunk
-  constexpr int MAXC = kSpan * kBuildMaxD / PER / 256;  // chunks per thread
+  constexpr int MAXC = kSpan * DM / PER / 256;  // chunks per thread
   const int cpr = D / PER;
   // a thread's chunks of the span's rows (zero past N_0), held in registers
   // so that V's loads are in flight while K is packed
@@ -375,7 +380,10 @@ static int tree_build_t(const htree_dims* d, const Plan& P, const void* k, const
   a.lspan = ls;
   const int64_t BH = (int64_t)d->B * d->H_kv;
   a.chunks = (P.N[0] + kSpan - 1) / kSpan;
-  hipLaunchKernelGGL(build_span_kernel<T>, dim3((unsigned)(BH * a.chunks)), dim3(256), 0, st, a);
+  if (d->D > 128)
+    hipLaunchKernelGGL((build_span_kernel<T, 256>), dim3((unsigned)(BH * a.chunks)), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((build_span_kernel<T, 128>), dim3((unsigned)(BH * a.chunks)), dim3(256), 0, st, a);
   for (int l = ls; l < P.L; ++l) {
     // the level read and the level written (host-checked before the launch)
     for (int x = 0; x < 2; ++x)
@@ -405,7 +413,7 @@ const char* htree_strerror(int status) {
              "must be powers of two with max_top_nodes <= top_k_per_layer * compression_rate "
              "and rope_rows >= top_k_per_layer * compression_rate, rope_rows > compression_rate";
     case HTREE_EUNSUPPORTED:
-      return "configuration outside this HIP build: needs D in {32,64,128}, H/H_kv <= 16 "
+      return "configuration outside this HIP build: needs D in {32,64,128,256}, H/H_kv <= 16 "
              "(up to 32 with kv_share 2, where top_k_per_layer <= 64 and "
              "top_k_per_layer * max(compression_rate,16) <= 1024), "
              "4 <= compression_rate <= 128, top_k_per_layer <= 1024 and "

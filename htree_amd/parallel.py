@@ -7,7 +7,7 @@ Differences, all deliberate:
     reference asserts equality, src/parallel.py:917); the algorithm never
     relies on equality.  The reference's Triton-tiling asserts
     (top_k % 64 == 0, top_k % compression_rate == 0, :923,1019) do not apply.
-  * limits of this HIP build (AssertionError): max(K, V) in {32, 64, 128}
+  * limits of this HIP build (AssertionError): max(K, V) in {32, 64, 128, 256}
     (K even), H / H_kv <= 16 (or even and <= 32 where top_k_per_layer <= 64
     and top_k_per_layer * max(compression_rate, 16) <= 1024), 4 <= compression_rate
     <= 128, top_k_per_layer <= 1024 and top_k_per_layer * compression_rate <=
@@ -45,7 +45,7 @@ from . import _native as N
 HTREE_SCORE_NEG_INF = -1.0e10            # src/parallel.py:75
 HTREE_SCORE_VALID_THRESHOLD = HTREE_SCORE_NEG_INF * 0.9  # :81
 
-KERNEL_HEAD_DIMS = (32, 64, 128)
+KERNEL_HEAD_DIMS = (32, 64, 128, 256)
 
 _rope_cache: Dict[Tuple, Tuple[torch.Tensor, torch.Tensor]] = {}
 

@@ -42,7 +42,7 @@ enum htree_status {
                               algorithm's rules (powers of two,
                               max_top_nodes <= top_k * compression_rate) */
   HTREE_EUNSUPPORTED = -4, /* legal for the reference, outside this build:
-                              D not in {32, 64, 128}, G = H/H_kv > 16
+                              D not in {32, 64, 128, 256}, G = H/H_kv > 16
                               (see kv_share for G <= 32),
                               compression_rate outside [4, 128],
                               top_k > 1024, top_k * compression_rate > 16384,

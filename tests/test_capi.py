@@ -58,6 +58,10 @@ def test_baseline_level_counts():
     assert len(N.levels(dims(T=65536))) == 4
 
 
+def test_head_dim_256_accepted():
+    assert len(N.levels(dims(D=256))) == 3
+
+
 def test_compression_rate_128_accepted():
     # 8 tiles per parent; the RoPE tables need a row past CR
     assert len(N.levels(dims(T=3000, H=8, compression_rate=128, top_k=4, max_top_nodes=512,
@@ -91,6 +95,7 @@ def test_shared_kv_heads_accepted():
     (dict(max_top_nodes=512), N.HTREE_ECONFIG),        # > top_k * CR
     (dict(rope_rows=100), N.HTREE_ECONFIG),
     (dict(D=96), N.HTREE_EUNSUPPORTED),
+    (dict(D=512), N.HTREE_EUNSUPPORTED),
     (dict(H=64, H_kv=2), N.HTREE_EUNSUPPORTED),        # group of 32 without kv_share
     (dict(H=96, H_kv=2, kv_share=2), N.HTREE_EUNSUPPORTED),  # 48 heads per kernel group
     (dict(H=32, H_kv=3, kv_share=2), N.HTREE_ESHAPE),  # kv_share 2 needs an even H_kv

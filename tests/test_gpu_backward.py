@@ -58,6 +58,10 @@ CASES = [
     # CR 128: children 64..127 in the records' second mask; dq recomputes
     (1, 3000, 8, 2, 64, 128, 4, 512, "bfloat16", 22),  # 32 tiles per level
     (1, 1500, 8, 1, 32, 128, 2, 256, "float32", 23),    # 16 tiles per level
+    # D = 256: stored scores and dS (bf16), recomputed dq (fp32, fp16)
+    (1, 1200, 16, 2, 256, 16, 16, 128, "bfloat16", 24),
+    (1, 1100, 8, 1, 256, 32, 8, 256, "float32", 25),
+    (1, 900, 8, 2, 256, 8, 16, 128, "float16", 26),
 ]
 
 
@@ -214,6 +218,7 @@ WIDE = [
     # top_k > 64 or more than 64 candidate tiles per level
     (1, 1500, 8, 2, 32, 4, 128, 256, "float32", 41),    # CR 4, 3 levels, evictions at level 1
     (1, 2000, 8, 2, 64, 16, 128, 1024, "bfloat16", 42),  # 125 tiles at the bottom
+    (1, 1500, 8, 2, 256, 16, 128, 1024, "bfloat16", 48),  # D = 256
 ]
 
 

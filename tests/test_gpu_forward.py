@@ -49,6 +49,8 @@ SMALL = [
     (2, 4096, 16, 2, 128, 16, 16, 16, "bfloat16", 14),  # 16-node top level (keeps every candidate), as C5
     (1, 3000, 8, 2, 64, 128, 4, 512, "bfloat16", 15),  # CR 128: 32 tiles per level
     (1, 1500, 8, 1, 32, 128, 2, 256, "float32", 16),    # CR 128: 16 tiles per level
+    (1, 1200, 16, 2, 256, 16, 16, 128, "bfloat16", 17),  # D = 256 (register forward)
+    (1, 1500, 8, 1, 256, 16, 32, 256, "float32", 18),    # D = 256, 32 tiles (streaming forward)
 ]
 
 
@@ -157,6 +159,7 @@ WIDE = [
     (1, 20000, 8, 2, 32, 16, 1024, 16384, "float32", 26, False),  # top_k 1024
     (1, 20000, 8, 2, 64, 32, 512, 512, "bfloat16", 27, False),    # top_k 512 at CR 32, 3 levels
     (1, 20000, 8, 2, 32, 128, 128, 16384, "float16", 28, False),  # CR 128
+    (1, 3000, 8, 2, 256, 16, 128, 2048, "bfloat16", 29, False),   # D = 256
 ]
 
 

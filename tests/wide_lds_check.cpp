@@ -2,7 +2,7 @@
 // against the layout the launch allocates (wide_lds() of htree_common.h, the
 // same function the kernel and its launch call).  For every configuration
 // the library accepts on the wide path (top_k > 64 or more than 64 candidate
-// tiles; top_k <= 1024, top_k * CR <= 16384, CR in [4, 128], D in {32, 64, 128};
+// tiles; top_k <= 1024, top_k * CR <= 16384, CR in [4, 128], D in {32, 64, 128, 256};
 // 32 selection keys per thread up to 8192 positions, 64 above)
 // and every level shape (np parents, child index ct of the query), each LDS
 // index the kernel forms is checked to lie inside its region, and the
@@ -95,7 +95,7 @@ static void check_config(int TK, int CR, int D) {
 
 int main() {
   int n = 0;
-  for (int D : {32, 64, 128})
+  for (int D : {32, 64, 128, 256})
     for (int CR = 4; CR <= 128; CR *= 2)
       for (int TK = 1; TK <= kWideMaxTK; TK *= 2) {
         if ((long)TK * CR > kWideMaxPos) continue;
