@@ -11,9 +11,13 @@ Workload ("C2"): B=1, T=32768, Hq=32, Hkv=2 (group
 16), D=128, bf16, causal, CR=16, MTN=128, TK=16; q/k/v/dO iid N(0,1) drawn
 on the host from a fixed seed and copied to HBM before timing.
 
-A step is one forward (`htree_forward`: tree build + fused kernel) plus one
-backward (`htree_backward` from the saved context) when the backward is
-built; `value` = B*T / step time (tokens/s).  The roofline object is for the
+A step is what the reference's speed_test_bwd.py times: the autograd
+forward (`htree_forward_triton_autograd`: tree build + fused kernel, keeping
+what the backward reads) and `out.backward(dO)`, gradients in the input
+dtype, with q/k/v's gradients cleared before each step; forward-only
+workloads step `htree_forward`.  `value` = B*T / wall-clock step time over
+the timed steps (tokens/s); `fwd` / `bwd` split each step with HIP events
+(speed_test_bwd.py:109-123).  The roofline object is for the
 dominant kernel (the fused forward), timed with HIP events on the stream it
 runs on, against the gathered-bytes model in htree_amd/workmodel.py.
 The CPU baseline times the CPU restatement of src/naive.py (oracle/, C on
@@ -207,9 +211,13 @@ def make_inputs(workload, dev, on_gpu=False):
 
 
 def measure(workload, q, k, v, dO, steps, warmup, kernel_iters):
-    """Times `steps` steps (wall clock, after `warmup`), then the forward and
-    backward apart and `kernel_iters` bare launches of the fused forward
-    kernel with HIP events on their stream.  Returns the figures and the last
+    """Times `steps` steps (wall clock, after `warmup`), with HIP events
+    around each step's forward and backward (speed_test_bwd.py:109-123),
+    then `kernel_iters` bare launches of the fused forward kernel with HIP
+    events on their stream.  A training step is the autograd forward
+    (`htree_forward_triton_autograd`, which keeps what the backward reads)
+    and `out.backward(dO)` with the gradients of q, k, v cleared first, as
+    the reference's speed_test_bwd.py times it.  Returns the figures and a
     forward's output and context."""
     import torch
 
@@ -220,45 +228,46 @@ def measure(workload, q, k, v, dO, steps, warmup, kernel_iters):
     (B, T, H, Hkv, D, CR, TK, MTN), dtype, with_bwd = WORKLOADS[workload]
     dev = q.device
     has_bwd = with_bwd and hasattr(htree_amd, "htree_backward")
+    if has_bwd:
+        q, k, v = (x.detach().requires_grad_(True) for x in (q, k, v))
+    stream = torch.cuda.current_stream(dev)
+    ev = lambda: torch.cuda.Event(enable_timing=True)
 
-    def step():
+    def step(marks=None):
+        if marks:
+            marks[0].record(stream)
         if not has_bwd:  # forward only (speed_test.py): nothing kept for a backward
-            return htree_amd.htree_forward(q, k, v, CR, MTN, TK)
-        out, ctx = htree_amd.htree_forward(q, k, v, CR, MTN, TK, _save_for_backward=True)
-        htree_amd.htree_backward(dO, q, out, ctx)
-        return out
+            htree_amd.htree_forward(q, k, v, CR, MTN, TK)
+            if marks:
+                marks[1].record(stream)
+            return
+        q.grad = k.grad = v.grad = None
+        out = htree_amd.htree_forward_triton_autograd(q, k, v, CR, MTN, TK)
+        if marks:
+            marks[1].record(stream)
+        out.backward(dO)
+        if marks:
+            marks[2].record(stream)
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    marks = [[ev(), ev(), ev()] for _ in range(steps)]
     t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
+    for i in range(steps):
+        step(marks[i])
     torch.cuda.synchronize()
     step_ms = (time.perf_counter() - t0) * 1e3 / steps
-    print(f"# {workload}: timed {steps} steps: {step_ms:.3f} ms/step", file=sys.stderr, flush=True)
+    fwd_ms = sum(m[0].elapsed_time(m[1]) for m in marks) / steps
+    bwd_ms = sum(m[1].elapsed_time(m[2]) for m in marks) / steps if has_bwd else None
+    print(f"# {workload}: timed {steps} steps: {step_ms:.3f} ms/step (forward {fwd_ms:.3f} ms"
+          + (f", backward {bwd_ms:.3f} ms" if has_bwd else "") + ")", file=sys.stderr, flush=True)
 
-    # fwd / bwd split and the fused forward kernel alone, with HIP events
-    stream = torch.cuda.current_stream(dev)
-    ev = lambda: torch.cuda.Event(enable_timing=True)
-    e0, e1, e2 = ev(), ev(), ev()
-    e0.record(stream)
-    for _ in range(steps):
-        if has_bwd:
-            out, ctx = htree_amd.htree_forward(q, k, v, CR, MTN, TK, _save_for_backward=True)
-        else:
-            out = htree_amd.htree_forward(q, k, v, CR, MTN, TK)
-    e1.record(stream)
-    if has_bwd:
-        for _ in range(steps):
-            htree_amd.htree_backward(dO, q, out, ctx)
-    e2.record(stream)
-    torch.cuda.synchronize()
-    fwd_ms = e0.elapsed_time(e1) / steps
-    bwd_ms = e1.elapsed_time(e2) / steps if has_bwd else None
-    if not has_bwd:
-        out, ctx = htree_amd.htree_forward(q, k, v, CR, MTN, TK, _save_for_backward=True)
-
+    # the fused forward kernel alone, with HIP events
+    with torch.no_grad():
+        out, ctx = htree_amd.htree_forward(q.detach(), k.detach(), v.detach(), CR, MTN, TK,
+                                           _save_for_backward=True)
+    q = q.detach()
     d = ctx["dims"]
     ws = ctx["packed_tree"]
     cos, sin = ctx["cos_cache"], ctx["sin_cache"]
@@ -329,7 +338,7 @@ def main():
     traffic = measured_traffic(args.workload)
     achieved = w.fwd_kernel_bytes / (kern_ms * 1e-3)
     fwd_tok = B * T / (fwd_ms * 1e-3)
-    step_s = (fwd_ms + (bwd_ms or 0.0)) * 1e-3
+    step_s = m["step_ms"] * 1e-3
     res = {
         "metric": METRIC if args.workload == "C2" else
         f"{'fwd & bwd' if has_bwd else 'fwd'} tokens/s at {args.workload}; % of HBM roofline",
@@ -338,7 +347,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": fwd_ms + (bwd_ms or 0.0),
+        "ms_per_step": m["step_ms"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -347,7 +356,8 @@ def main():
         "config": {
             "workload": f"{args.workload}: B={B} T={T} Hq={H} Hkv={Hkv} D={D} {DT_SHORT[dtype]} "
                         f"causal CR={CR} MTN={MTN} TK={TK}",
-            "step": "htree_forward + htree_backward" if has_bwd else "htree_forward",
+            "step": ("htree_forward_triton_autograd + out.backward(dO)" if has_bwd
+                     else "htree_forward"),
         },
         "fwd": {"ms": fwd_ms, "tokens_per_s": fwd_tok,
                 "hbm_roofline_frac": w.fwd_bytes / (fwd_ms * 1e-3) / HBM_PEAK,
@@ -356,7 +366,7 @@ def main():
             "ms": bwd_ms, "tokens_per_s": B * T / (bwd_ms * 1e-3),
             "hbm_roofline_frac": w.bwd_bytes / (bwd_ms * 1e-3) / HBM_PEAK,
             "algorithmic_bytes": w.bwd_bytes},
-        "wall_ms_per_step": m["step_ms"],
+        "event_ms_per_step": fwd_ms + (bwd_ms or 0.0),
         "roofline": {
             "kernel": f"htree::{forward_kernel(args.workload)} (fused forward, all levels)",
             "bound": "hbm",
@@ -403,7 +413,7 @@ def main():
                       f"TK={TK2}",
             "data": data2,
             "steps": 3, "warmup": 2,
-            "tokens_per_s": B2 * T2 / ((m2["fwd_ms"] + (m2["bwd_ms"] or 0.0)) * 1e-3),
+            "tokens_per_s": B2 * T2 / (m2["step_ms"] * 1e-3),
             "fwd_ms": m2["fwd_ms"],
             "fwd_hbm_roofline_frac": w2.fwd_bytes / (m2["fwd_ms"] * 1e-3) / HBM_PEAK,
             "bwd_ms": m2["bwd_ms"],
@@ -411,7 +421,7 @@ def main():
                                       if m2["bwd_ms"] else None),
             "kernel_ms": m2["kern_ms"],
             "kernel_hbm_roofline_frac": w2.fwd_kernel_bytes / (m2["kern_ms"] * 1e-3) / HBM_PEAK,
-            "wall_ms_per_step": m2["step_ms"],
+            "ms_per_step": m2["step_ms"],
         }
         del q2, k2, v2, dO2, m2
         torch.cuda.empty_cache()

@@ -40,7 +40,7 @@ EXPORTS = (
 class HtreeDims(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in (
         "B", "T", "H", "H_kv", "D", "compression_rate", "top_k", "max_top_nodes", "dtype",
-        "rope_rows", "kv_share")]
+        "rope_rows", "kv_share", "grad_dtype")]
 
 
 class HtreeError(RuntimeError):
@@ -120,11 +120,21 @@ def check(rc: int, what: str) -> None:
 
 
 def dims(B, T, H, H_kv, D, compression_rate, top_k, max_top_nodes, dtype, rope_rows,
-         kv_share=1) -> HtreeDims:
-    if dtype not in DTYPE_CODE:
-        raise AssertionError(f"unsupported dtype {dtype}: expected float32, bfloat16 or float16")
+         kv_share=1, grad_dtype=None) -> HtreeDims:
+    """grad_dtype: dtype of the backward's dq, dk, dv (None: float32)."""
+    for t in (dtype, grad_dtype):
+        if t is not None and t not in DTYPE_CODE:
+            raise AssertionError(f"unsupported dtype {t}: expected float32, bfloat16 or float16")
     return HtreeDims(B, T, H, H_kv, D, compression_rate, top_k, max_top_nodes,
-                     DTYPE_CODE[dtype], rope_rows, kv_share)
+                     DTYPE_CODE[dtype], rope_rows, kv_share,
+                     DTYPE_CODE[grad_dtype] if grad_dtype is not None else 0)
+
+
+def with_grad_dtype(d: HtreeDims, grad_dtype) -> HtreeDims:
+    """A copy of `d` whose backward writes dq, dk, dv in grad_dtype."""
+    c = HtreeDims.from_buffer_copy(d)
+    c.grad_dtype = DTYPE_CODE[grad_dtype]
+    return c
 
 
 def levels(d: HtreeDims):

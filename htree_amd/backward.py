@@ -80,21 +80,25 @@ def infer_max_top_nodes(T: int, CR: int, TK: int, L: int) -> int:
     return 1 << max(0, (n - 1).bit_length())
 
 
-def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_ctx: dict):
+def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_ctx: dict,
+                   _grad_dtype: Optional[torch.dtype] = None):
     """Gradients of the htree forward wrt q, k, v (fp32), selection fixed.
 
     dO and output are read in q's dtype; the reference upcasts both to fp32
     (src/backward.py:966-967), so the two agree when dO comes in q's dtype,
-    as autograd hands it."""
+    as autograd hands it.  `_grad_dtype` (the autograd path's input dtype)
+    has the kernels round the fp32 gradients into that dtype as they store
+    them: the values `.to(_grad_dtype)` of the fp32 results would give."""
     B, T, H, K = q.shape
     layers_k, layers_v = bwd_ctx["layers_k"], bwd_ctx["layers_v"]
     k, v = layers_k[0], layers_v[0]
     H_kv, V = k.shape[2], v.shape[3]
     dev = q.device
-    f32 = dict(dtype=torch.float32, device=dev)
+    gdt = _grad_dtype or torch.float32
     if B == 0 or T == 0:  # empty inputs: empty gradients, no launch
-        return (torch.empty(B, T, H, K, **f32), torch.empty(B, T, H_kv, K, **f32),
-                torch.empty(B, T, H_kv, V, **f32))
+        e = dict(dtype=gdt, device=dev)
+        return (torch.empty(B, T, H, K, **e), torch.empty(B, T, H_kv, K, **e),
+                torch.empty(B, T, H_kv, V, **e))
     hf = bwd_ctx.get("head_frame") or HeadFrame(K, V, H // H_kv)
     CR = bwd_ctx["compression_rate"]
     TK = bwd_ctx["top_k_per_layer"]
@@ -136,8 +140,13 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
     dOf = hf.pad_v(dO.contiguous().to(q.dtype))
     outf = hf.pad_v(output.contiguous().to(q.dtype))
     D = hf.D
-    dq = torch.empty(B, T, H, D, **f32)
-    dk = torch.empty(B, T, H_kv * hf.share, D, **f32)
+    # KV-head pairs add their halves' dk / dv in fp32 before the rounding
+    kdt = gdt if hf.share == 1 else torch.float32
+    if kdt != torch.float32:
+        d = N.with_grad_dtype(d, kdt)
+    g = dict(dtype=kdt, device=dev)
+    dq = torch.empty(B, T, H, D, **g)
+    dk = torch.empty(B, T, H_kv * hf.share, D, **g)
     dv = torch.empty_like(dk)
     nb = N.ctypes.c_int64()
     N.check(N.lib().htree_backward_workspace_bytes(N.ctypes.byref(d), N.ctypes.byref(nb)),
@@ -164,7 +173,8 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
                 N.ptr(sin_k), N.ptr(dq), N.ptr(dk), N.ptr(dv), N.ptr(bws), bws.numel(),
                 N.stream_ptr(dev))
             N.check(rc, "htree_backward")
-    return hf.unpad_qk(dq), hf.unpad_qk(hf.pair_sum(dk)), hf.unpad_v(hf.pair_sum(dv))
+    return (hf.unpad_qk(dq).to(gdt), hf.unpad_qk(hf.pair_sum(dk)).to(gdt),
+            hf.unpad_v(hf.pair_sum(dv)).to(gdt))
 
 
 _REF_META = ("num_layers", "compression_rate", "top_k_per_layer", "max_top_nodes", "scale",
@@ -197,7 +207,7 @@ class HTreeTritonFunction(torch.autograd.Function):
         bwd_ctx = dict(ctx.meta, global_max=gmax, global_sum=gsum, layers_k=[k], layers_v=[v],
                        cos_cache=cos, sin_cache=sin, parents_stacked=parents,
                        per_layer_parents=None, packed_tree=ws, train_scores=scores)
-        dq, dk, dv = htree_backward(dO, q, out, bwd_ctx)
+        dq, dk, dv = htree_backward(dO, q, out, bwd_ctx, _grad_dtype=q.dtype)
         return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None
 
 
@@ -223,7 +233,7 @@ class HTreeLeanFunction(torch.autograd.Function):
         q, k, v, out, gmax, gsum, cos, sin = ctx.saved_tensors
         bwd_ctx = dict(ctx.meta, global_max=gmax, global_sum=gsum, layers_k=[k], layers_v=[v],
                        cos_cache=cos, sin_cache=sin, per_layer_parents=None)
-        dq, dk, dv = htree_backward(dO, q, out, bwd_ctx)
+        dq, dk, dv = htree_backward(dO, q, out, bwd_ctx, _grad_dtype=q.dtype)
         return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None
 
 

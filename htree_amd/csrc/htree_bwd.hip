@@ -1263,7 +1263,8 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(const float* __restrict
                                                          int Hkv, int D, int CR, int crlg, int tpp,
                                                          int64_t Pl, const float* __restrict__ upk,
                                                          const float* __restrict__ upv, int64_t Nup,
-                                                         float* __restrict__ dk, float* __restrict__ dv) {
+                                                         void* __restrict__ dk, void* __restrict__ dv,
+                                                         int odt) {
   constexpr int TPV = 256 / LG;  // threads per lane group
   __shared__ float4 red[LG][TPV];
   const int j = threadIdx.x % TPV, c = threadIdx.x / TPV;
@@ -1314,7 +1315,7 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(const float* __restrict
     acc.z += u.z / cnt;
     acc.w += u.w / cnt;
   }
-  *(float4*)((kv ? dv : dk) + ((b * N + node) * Hkv + h) * D + dd) = acc;
+  store_grad4(kv ? dv : dk, ((b * N + node) * Hkv + h) * D + dd, acc.x, acc.y, acc.z, acc.w, odt);
 }
 
 // ---------------------------------------------------------------- dq
@@ -1330,8 +1331,9 @@ struct DqArgs {
   const float *gmax, *gsum, *delta;
   const int32_t* parents;  // [L,B,T,Hkv,TK]
   const float *cosb, *sinb;
-  float* dq;
+  void* dq;
   int32_t B, T, H, Hkv, G, CR, crlg, TK, L;
+  int32_t gdt;  // enum htree_dtype of dq
   float scale;
 };
 
@@ -1564,12 +1566,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 ? 5
     }
   }
   if (gv) {
-    float* o = a.dq + hq * D;
 #pragma unroll
     for (int n = 0; n < ND; ++n) {
       const f32x4 v = AC[n][lane];
-      *(float4*)(o + 16 * n + 4 * kg) =
-          make_float4(a.scale * v[0], a.scale * v[1], a.scale * v[2], a.scale * v[3]);
+      store_grad4(a.dq, hq * D + 16 * n + 4 * kg, a.scale * v[0], a.scale * v[1], a.scale * v[2],
+                  a.scale * v[3], a.gdt);
     }
   }
 }
@@ -1600,8 +1601,9 @@ struct DqDsArgs {
   DqDsLevel lv[HTREE_MAX_LEVELS];
   const int32_t* parents;  // [L,B,T,Hkv,TK]
   const float *cosb, *sinb;
-  float* dq;
+  void* dq;
   int32_t B, T, H, Hkv, G, CR, crlg, TK, L, tpp;
+  int32_t gdt;  // enum htree_dtype of dq
   float scale;
 };
 
@@ -1771,11 +1773,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
     }
   }
   if (u16 < a.G) {
-    float* o = a.dq + (bt * a.H + h * a.G + u16) * D;
+    const int64_t o = (bt * a.H + h * a.G + u16) * D;
 #pragma unroll
     for (int n = 0; n < ND; ++n)
-      *(float4*)(o + 16 * n + 4 * kg) =
-          make_float4(a.scale * X[n][0], a.scale * X[n][1], a.scale * X[n][2], a.scale * X[n][3]);
+      store_grad4(a.dq, o + 16 * n + 4 * kg, a.scale * X[n][0], a.scale * X[n][1],
+                  a.scale * X[n][2], a.scale * X[n][3], a.gdt);
   }
 }
 
@@ -1817,7 +1819,7 @@ template <int D, bool PREC, typename T>
 static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const void* q,
                       const void* out, const void* dO, const float* gmax, const float* gsum,
                       const int32_t* parents, const char* tws, const float* cosb, const float* sinb,
-                      const char* scores, float* dq, float* dk, float* dv, char* ws,
+                      const char* scores, void* dq, void* dk, void* dv, char* ws,
                       hipStream_t st, SideStream* side) {
   const Plan& P = BP.P;
   if (side && !BP.use_ds) side = nullptr;  // shared records: the levels run in order
@@ -1991,8 +1993,11 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
       if (has_s) HT_DKV(true, 1); else HT_DKV(false, 1);
     }
 #undef HT_DKV
-    float* dkl = l == 0 ? dk : (float*)(ws + BP.off_dk[l]);
-    float* dvl = l == 0 ? dv : (float*)(ws + BP.off_dv[l]);
+    // level 0 is the caller's dk / dv (in grad_dtype), higher levels fp32
+    // partials of the workspace
+    void* dkl = l == 0 ? dk : (void*)(ws + BP.off_dk[l]);
+    void* dvl = l == 0 ? dv : (void*)(ws + BP.off_dv[l]);
+    const int odt = l == 0 ? d->grad_dtype : HTREE_F32;
     const bool top = l == Ltop;
     const float* upk = top ? nullptr : (const float*)(ws + BP.off_dk[l + 1]);
     const float* upv = top ? nullptr : (const float*)(ws + BP.off_dv[l + 1]);
@@ -2003,7 +2008,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
 #define HT_RED(LG)                                                                              \
   hipLaunchKernelGGL(dkv_reduce_kernel<LG>, dim3((unsigned)(rt * d->D * LG / 32)),            \
                      dim3(256), 0, st, partial, poff, P.N[l], d->H_kv, d->D, CRl, lgl, tppl,  \
-                     Pl, upk, upv, nup, dkl, dvl)
+                     Pl, upk, upv, nup, dkl, dvl, odt)
     if (avg >= 64)
       HT_RED(16);
     else if (avg >= 8)
@@ -2047,6 +2052,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.cosb = cosb;
     a.sinb = sinb;
     a.dq = dq;
+    a.gdt = d->grad_dtype;
     a.B = d->B;
     a.T = d->T;
     a.H = d->H;
@@ -2081,6 +2087,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.cosb = cosb;
     a.sinb = sinb;
     a.dq = dq;
+    a.gdt = d->grad_dtype;
     a.B = d->B;
     a.T = d->T;
     a.H = d->H;
@@ -2137,7 +2144,7 @@ static int backward_impl(const htree_dims* d, float scale, const void* q, const 
                          const void* dO, const float* gmax, const float* gsum,
                          const int32_t* parents, const void* tree_ws, int64_t tree_ws_bytes,
                          const float* cos_table, const float* sin_table, const void* scores_ws,
-                         int64_t scores_bytes, float* dq, float* dk, float* dv, void* bwd_ws,
+                         int64_t scores_bytes, void* dq, void* dk, void* dv, void* bwd_ws,
                          int64_t bwd_ws_bytes, void* stream, bool overlap = true) {
   BwdPlan BP;
   int rc = make_bwd_plan(d, &BP);
@@ -2197,7 +2204,7 @@ extern "C" {
 int htree_backward(const htree_dims* d, float scale, const void* q, const void* out,
                    const void* dO, const float* gmax, const float* gsum, const int32_t* parents,
                    const void* tree_ws, int64_t tree_ws_bytes, const float* cos_table,
-                   const float* sin_table, float* dq, float* dk, float* dv, void* bwd_ws,
+                   const float* sin_table, void* dq, void* dk, void* dv, void* bwd_ws,
                    int64_t bwd_ws_bytes, void* stream) {
   return backward_impl(d, scale, q, out, dO, gmax, gsum, parents, tree_ws, tree_ws_bytes,
                        cos_table, sin_table, nullptr, 0, dq, dk, dv, bwd_ws, bwd_ws_bytes, stream);
@@ -2207,7 +2214,7 @@ int htree_backward_train(const htree_dims* d, float scale, const void* q, const 
                          const void* dO, const float* gmax, const float* gsum,
                          const int32_t* parents, const void* tree_ws, int64_t tree_ws_bytes,
                          const float* cos_table, const float* sin_table, const void* scores,
-                         int64_t scores_bytes, float* dq, float* dk, float* dv, void* bwd_ws,
+                         int64_t scores_bytes, void* dq, void* dk, void* dv, void* bwd_ws,
                          int64_t bwd_ws_bytes, void* stream) {
   return backward_impl(d, scale, q, out, dO, gmax, gsum, parents, tree_ws, tree_ws_bytes,
                        cos_table, sin_table, scores, scores_bytes, dq, dk, dv, bwd_ws,
@@ -2271,7 +2278,7 @@ int htree_backward_noalloc(const htree_dims* d, float scale, const void* q, cons
                            const void* dO, const float* gmax, const float* gsum,
                            const int32_t* parents, const void* tree_ws, int64_t tree_ws_bytes,
                            const float* cos_table, const float* sin_table, const void* scores,
-                           int64_t scores_bytes, float* dq, float* dk, float* dv, void* stream) {
+                           int64_t scores_bytes, void* dq, void* dk, void* dv, void* stream) {
   int64_t need = 0;
   int rc = htree_backward_noalloc_bytes(d, &need);
   if (rc) return rc;  // HTREE_ESCRATCH: the problem's backward needs more than the array holds

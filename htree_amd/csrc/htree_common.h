@@ -161,6 +161,23 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v));
 }
 
+// four fp32 gradient values stored at element i of `out` in the type
+// dt (enum htree_dtype, wave-uniform): fp32, or rounded to nearest even
+// into bf16 / fp16 (8-byte store)
+__device__ __forceinline__ void store_grad4(void* out, int64_t i, float a, float b, float c,
+                                            float d, int dt) {
+  if (dt == HTREE_BF16) {
+    *(uint2*)((uint16_t*)out + i) = make_uint2(cvt_pk_bf16(a, b), cvt_pk_bf16(c, d));
+  } else if (dt == HTREE_F16) {
+    typedef __attribute__((ext_vector_type(4))) _Float16 h4;
+    typedef __attribute__((ext_vector_type(4))) float f4;
+    const f4 v = {a, b, c, d};
+    *(h4*)((uint16_t*)out + i) = __builtin_convertvector(v, h4);
+  } else {
+    *(float4*)((float*)out + i) = make_float4(a, b, c, d);
+  }
+}
+
 // hi + lo bf16 split of 8 fp32 values, in pairs: 6 VALU ops per pair
 __device__ __forceinline__ void split8(const float (&x)[8], bf16x8& hi, bf16x8& lo) {
   uint32_t h[4], l[4];

@@ -78,6 +78,13 @@ typedef struct htree_dims {
                                the pair.  Register and streaming forwards
                                (top_k <= 64, top_k * max(CR, 16) <= 1024),
                                not the wide one. */
+  int32_t grad_dtype;       /* enum htree_dtype of dq, dk, dv written by the
+                               backward entry points: HTREE_F32 (0, as the
+                               reference's htree_backward returns them) or
+                               a 16-bit type, rounded to nearest even from
+                               the same fp32 values (what the reference's
+                               autograd backward casts them to,
+                               src/backward.py:1193). */
 } htree_dims;
 
 /* Static description of a status code (host). */
@@ -145,8 +152,8 @@ int htree_backward_workspace_bytes(const htree_dims* d, int64_t* bytes);
  * (src/backward.py:979-981); for callers short of device memory. */
 int htree_backward_workspace_min_bytes(const htree_dims* d, int64_t* bytes);
 
-/* Backward with the selection held fixed: dq, dk, dv in fp32 (dk, dv after
- * the mean-pool backward onto level 0).  `out` is the forward output handed
+/* Backward with the selection held fixed: dq, dk, dv in d->grad_dtype (dk,
+ * dv after the mean-pool backward onto level 0).  `out` is the forward output handed
  * to the backward (delta = rowsum(dO * out)); gmax, gsum and parents are
  * what htree_forward wrote; tree_ws is the packed tree of htree_tree_build.
  * The parent lists are trusted: other lists must keep the forward's form
@@ -162,8 +169,8 @@ int htree_backward_workspace_min_bytes(const htree_dims* d, int64_t* bytes);
 int htree_backward(const htree_dims* d, float scale, const void* q, const void* out,
                    const void* dO, const float* gmax, const float* gsum,
                    const int32_t* parents, const void* tree_ws, int64_t tree_ws_bytes,
-                   const float* cos_table, const float* sin_table, float* dq, float* dk,
-                   float* dv, void* bwd_ws, int64_t bwd_ws_bytes, void* stream);
+                   const float* cos_table, const float* sin_table, void* dq, void* dk,
+                   void* dv, void* bwd_ws, int64_t bwd_ws_bytes, void* stream);
 
 /* Bytes of the score buffer htree_forward_train writes for
  * htree_backward_train (host): per level, query group and 16-candidate tile
@@ -192,7 +199,7 @@ int htree_backward_train(const htree_dims* d, float scale, const void* q, const 
                          const void* dO, const float* gmax, const float* gsum,
                          const int32_t* parents, const void* tree_ws, int64_t tree_ws_bytes,
                          const float* cos_table, const float* sin_table, const void* scores,
-                         int64_t scores_bytes, float* dq, float* dk, float* dv, void* bwd_ws,
+                         int64_t scores_bytes, void* dq, void* dk, void* dv, void* bwd_ws,
                          int64_t bwd_ws_bytes, void* stream);
 
 /* Backward workspace bytes htree_backward_noalloc would use for `d`
@@ -214,7 +221,7 @@ int htree_backward_noalloc(const htree_dims* d, float scale, const void* q, cons
                            const void* dO, const float* gmax, const float* gsum,
                            const int32_t* parents, const void* tree_ws, int64_t tree_ws_bytes,
                            const float* cos_table, const float* sin_table, const void* scores,
-                           int64_t scores_bytes, float* dq, float* dk, float* dv, void* stream);
+                           int64_t scores_bytes, void* dq, void* dk, void* dv, void* stream);
 
 /* Row-wise Top-K (the selection of the forward's wide kernel, on its own):
  * for each of `rows` rows of n fp32 values (n <= 8192, 1 <= k <= n), the k

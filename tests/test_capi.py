@@ -37,10 +37,14 @@ def test_strerror_covers_codes():
 def dims(**kw):
     base = dict(B=1, T=32768, H=32, H_kv=2, D=128, compression_rate=16, top_k=16,
                 max_top_nodes=128, dtype=torch.bfloat16, rope_rows=1152, kv_share=1)
+    grad_code = kw.pop("grad_dtype_code", None)
     base.update(kw)
-    return N.dims(base["B"], base["T"], base["H"], base["H_kv"], base["D"], base["compression_rate"],
-                  base["top_k"], base["max_top_nodes"], base["dtype"], base["rope_rows"],
-                  base["kv_share"])
+    d = N.dims(base["B"], base["T"], base["H"], base["H_kv"], base["D"], base["compression_rate"],
+               base["top_k"], base["max_top_nodes"], base["dtype"], base["rope_rows"],
+               base["kv_share"])
+    if grad_code is not None:
+        d.grad_dtype = grad_code
+    return d
 
 
 @pytest.mark.parametrize("T,CR,MTN", [(32768, 16, 128), (131072, 32, 256), (65536, 16, 128),
@@ -100,6 +104,8 @@ def test_shared_kv_heads_accepted():
     (dict(H=96, H_kv=2, kv_share=2), N.HTREE_EUNSUPPORTED),  # 48 heads per kernel group
     (dict(H=32, H_kv=3, kv_share=2), N.HTREE_ESHAPE),  # kv_share 2 needs an even H_kv
     (dict(kv_share=3), N.HTREE_ESHAPE),
+    (dict(grad_dtype_code=3), N.HTREE_ESHAPE),         # not an htree_dtype
+    (dict(grad_dtype_code=-1), N.HTREE_ESHAPE),
     (dict(H=64, H_kv=4, kv_share=2, top_k=128, max_top_nodes=128, rope_rows=2048),
      N.HTREE_EUNSUPPORTED),                            # shared selection: not the wide forward
     (dict(D=16), N.HTREE_EUNSUPPORTED),
@@ -171,3 +177,20 @@ def test_work_model_matches_baseline_table():
     w5 = work(2, 65536, 32, 2, 128, 16, 16, 128, 2)
     assert abs(w5.fwd_bytes / 1e9 - 83.63) < 0.01
     assert abs(w2.mean_k_rows - 545.6) < 0.1 and abs(w2.mean_v_rows - 514.6) < 0.1
+
+
+def test_dims_struct_matches_header():
+    """The ctypes mirror has the header's fields, in order (int32 each), and
+    grad_dtype defaults to fp32 (0): zero-initialised callers keep the fp32
+    gradients."""
+    hdr = open(os.path.join(ROOT, "include", "htree.h")).read()
+    body = hdr[hdr.index("typedef struct htree_dims {"):hdr.index("} htree_dims;")]
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    names = re.findall(r"\b([A-Za-z_]+)\s*[,;]", body.split("{", 1)[1])
+    assert [f[0] for f in N.HtreeDims._fields_] == names
+    assert ctypes.sizeof(N.HtreeDims) == 4 * len(names)
+    assert dims().grad_dtype == 0
+    assert N.with_grad_dtype(dims(), torch.bfloat16).grad_dtype == N.DTYPE_CODE[torch.bfloat16]
+    for gd in (torch.bfloat16, torch.float16):
+        d = N.dims(1, 2048, 8, 1, 128, 16, 16, 128, torch.bfloat16, 1152, grad_dtype=gd)
+        assert len(N.levels(d)) == 2

@@ -198,20 +198,45 @@ def test_backward_replaced_parent_lists():
         htree_amd.htree_backward(dO, q, out, dict(ctx, per_layer_parents=bad))
 
 
-def test_autograd_contract():
+AUTOGRAD = [
+    # B, T, H, Hkv, D, CR, TK, MTN, dtype, seed, DS budget (None: default)
+    (1, 1500, 8, 1, 128, 16, 16, 128, "bfloat16", 4, None),   # stored scores and dS
+    (1, 1500, 8, 1, 128, 16, 16, 128, "bfloat16", 4, "0"),    # dq recomputes the scores
+    (1, 1100, 8, 1, 128, 32, 8, 256, "float16", 5, None),
+    (1, 900, 8, 2, 64, 8, 16, 128, "float32", 6, None),
+    (1, 2000, 8, 2, 64, 16, 128, 1024, "bfloat16", 7, None),  # wide forward
+    (1, 1200, 24, 1, 64, 16, 16, 128, "bfloat16", 8, None),   # G 24: KV-head pairs
+    (1, 1000, 8, 2, (32, 64), 16, 16, 128, "float16", 9, None),  # K 32 padded to V 64
+]
+
+
+@pytest.mark.parametrize("cfg", AUTOGRAD, ids=lambda c: f"D{c[4]}G{c[2] // c[3]}tk{c[6]}{c[8]}"
+                         .replace(", ", "x") + ("_recompute" if c[10] else ""))
+def test_autograd_contract(cfg, monkeypatch):
     """HTreeTritonFunction: grads in the input dtype, None for non-tensors,
-    equal to htree_backward cast to the dtype."""
+    equal bit for bit to htree_backward's fp32 gradients cast to the dtype
+    (the reference's backward, src/backward.py:1193).  The kernels round
+    them as they store them, except for KV-head pairs, whose halves are
+    added in fp32 first."""
     import htree_amd
 
-    q, k, v, dO = inputs(1, 1500, 8, 1, 128, "bfloat16", 4, dO=True)
+    B, T, H, Hkv, D, CR, TK, MTN, dtype, seed, budget = cfg
+    print(f"case {cfg}", flush=True)
+    if budget is not None:
+        monkeypatch.setenv("HTREE_DS_BUDGET_MB", budget)
+    dt = getattr(torch, dtype)
+    K, V = D if isinstance(D, tuple) else (D, D)
+    q, k, _ = inputs(B, T, H, Hkv, K, dtype, seed)
+    _, _, v, dO = inputs(B, T, H, Hkv, V, dtype, seed + 100, dO=True)
     qg, kg, vg = (x.to(DEV).requires_grad_(True) for x in (q, k, v))
-    out = htree_amd.htree_forward_triton_autograd(qg, kg, vg, 16, 128, 16)
+    out = htree_amd.htree_forward_triton_autograd(qg, kg, vg, CR, MTN, TK)
     out.backward(dO.to(DEV))
-    assert qg.grad.dtype == torch.bfloat16 and kg.grad.dtype == torch.bfloat16
-    _, _, _, _, dq, dk, dv = run(q, k, v, dO, 16, 16, 128)
-    for got, ref in ((qg.grad, dq), (kg.grad, dk), (vg.grad, dv)):
-        r = torch.from_numpy(ref).bfloat16().float().numpy()
-        assert np.array_equal(got.float().cpu().numpy(), r)
+    for x in (qg, kg, vg):
+        assert x.grad.dtype == dt and x.grad.shape == x.shape and x.grad.is_contiguous()
+    _, _, _, _, dq, dk, dv = run(q, k, v, dO, CR, TK, MTN)
+    for name, got, ref in (("dq", qg.grad, dq), ("dk", kg.grad, dk), ("dv", vg.grad, dv)):
+        r = torch.from_numpy(ref).to(dt).float().numpy()
+        assert np.array_equal(got.float().cpu().numpy(), r), name
 
 
 WIDE = [

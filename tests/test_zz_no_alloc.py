@@ -23,19 +23,20 @@ CASES = [
 ]
 
 
-def grads(cfg, noalloc):
+def grads(cfg, noalloc, grad_dtype=None):
     import htree_amd
     from htree_amd import _native as N
 
     B, T, H, Hkv, D, CR, TK, MTN, dtype, seed = cfg
     q, k, v, dO = (x.to(DEV) for x in inputs(B, T, H, Hkv, D, dtype, seed, dO=True))
     out, par, gmax, gsum, ctx = htree_amd.htree_forward_parents(q, k, v, CR, MTN, TK)
-    d = ctx["dims"]
+    d = ctx["dims"] if grad_dtype is None else N.with_grad_dtype(ctx["dims"], grad_dtype)
     need = ctypes.c_int64()
     N.check(N.lib().htree_backward_noalloc_bytes(ctypes.byref(d), ctypes.byref(need)), "bytes")
     ws, cos, sin, sc = ctx["packed_tree"], ctx["cos_cache"], ctx["sin_cache"], ctx["train_scores"]
-    dq = torch.empty(B, T, H, D, dtype=torch.float32, device=DEV)
-    dk = torch.empty(B, T, Hkv, D, dtype=torch.float32, device=DEV)
+    gdt = grad_dtype or torch.float32
+    dq = torch.empty(B, T, H, D, dtype=gdt, device=DEV)
+    dk = torch.empty(B, T, Hkv, D, dtype=gdt, device=DEV)
     dv = torch.empty_like(dk)
     common = (ctypes.byref(d), float(ctx["scale"]), N.ptr(q), N.ptr(out), N.ptr(dO), N.ptr(gmax),
               N.ptr(gsum), N.ptr(par), N.ptr(ws), ws.numel(), N.ptr(cos), N.ptr(sin), N.ptr(sc),
@@ -48,7 +49,7 @@ def grads(cfg, noalloc):
         rc = N.lib().htree_backward_train(*common, N.ptr(bws), bws.numel(), N.stream_ptr(q.device))
         N.check(rc, "htree_backward_train")
     torch.cuda.synchronize()
-    return [x.cpu().numpy() for x in (dq, dk, dv)]
+    return [x.float().cpu().numpy() for x in (dq, dk, dv)]
 
 
 def test_noalloc_matches_workspace_entry():
@@ -76,3 +77,13 @@ def test_noalloc_rejects_large_problems():
                                         None, None, None, None)
     assert rc == N.HTREE_ESCRATCH
     assert "htree_backward_noalloc" in N.strerror(rc)
+
+
+def test_noalloc_gradients_in_input_dtype():
+    """With grad_dtype bf16 the entry point stores the gradients rounded to
+    bf16: the fp32 call's values cast, bit for bit."""
+    cfg = CASES[0]
+    ref = grads(cfg, True)
+    got = grads(cfg, True, torch.bfloat16)
+    for name, a, b in zip(("dq", "dk", "dv"), got, ref):
+        assert np.array_equal(a, torch.from_numpy(b).bfloat16().float().numpy()), name
