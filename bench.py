@@ -1,6 +1,6 @@
 """Benchmark of the htree hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C2] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C2] [--no-cpu] [--no-lean]
 
 Other workloads (--workload): C3, C4, C5, REF_FWD (the
 reference's speed_test.py defaults: T=120000, Hq=64, Hkv=4, D=32, fp32, CR=16,
@@ -17,7 +17,11 @@ what the backward reads) and `out.backward(dO)`, gradients in the input
 dtype, with q/k/v's gradients cleared before each step; forward-only
 workloads step `htree_forward`.  `value` = B*T / wall-clock step time over
 the timed steps (tokens/s); `fwd` / `bwd` split each step with HIP events
-(speed_test_bwd.py:109-123).  The roofline object is for the
+(speed_test_bwd.py:109-123).  `lean` repeats the measurement (up to 10
+steps) in the lean autograd mode (`_save_parents=False`: only the
+reference's eight tensors kept; the backward rebuilds the tree and replays
+the selection); `saved_bytes_beyond_reference` is what the default mode
+keeps per call beyond them.  The roofline object is for the
 dominant kernel (the fused forward), timed with HIP events on the stream it
 runs on, against the gathered-bytes model in htree_amd/workmodel.py.
 The CPU baseline times the CPU restatement of src/naive.py (oracle/, C on
@@ -210,7 +214,7 @@ def make_inputs(workload, dev, on_gpu=False):
     return q, k, v, dO, data
 
 
-def measure(workload, q, k, v, dO, steps, warmup, kernel_iters):
+def measure(workload, q, k, v, dO, steps, warmup, kernel_iters, lean_steps=0):
     """Times `steps` steps (wall clock, after `warmup`), with HIP events
     around each step's forward and backward (speed_test_bwd.py:109-123),
     then `kernel_iters` bare launches of the fused forward kernel with HIP
@@ -233,7 +237,7 @@ def measure(workload, q, k, v, dO, steps, warmup, kernel_iters):
     stream = torch.cuda.current_stream(dev)
     ev = lambda: torch.cuda.Event(enable_timing=True)
 
-    def step(marks=None):
+    def step(marks=None, lean=False):
         if marks:
             marks[0].record(stream)
         if not has_bwd:  # forward only (speed_test.py): nothing kept for a backward
@@ -242,26 +246,37 @@ def measure(workload, q, k, v, dO, steps, warmup, kernel_iters):
                 marks[1].record(stream)
             return
         q.grad = k.grad = v.grad = None
-        out = htree_amd.htree_forward_triton_autograd(q, k, v, CR, MTN, TK)
+        out = htree_amd.htree_forward_triton_autograd(q, k, v, CR, MTN, TK,
+                                                      _save_parents=not lean)
         if marks:
             marks[1].record(stream)
         out.backward(dO)
         if marks:
             marks[2].record(stream)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    marks = [[ev(), ev(), ev()] for _ in range(steps)]
-    t0 = time.perf_counter()
-    for i in range(steps):
-        step(marks[i])
-    torch.cuda.synchronize()
-    step_ms = (time.perf_counter() - t0) * 1e3 / steps
-    fwd_ms = sum(m[0].elapsed_time(m[1]) for m in marks) / steps
-    bwd_ms = sum(m[1].elapsed_time(m[2]) for m in marks) / steps if has_bwd else None
-    print(f"# {workload}: timed {steps} steps: {step_ms:.3f} ms/step (forward {fwd_ms:.3f} ms"
-          + (f", backward {bwd_ms:.3f} ms" if has_bwd else "") + ")", file=sys.stderr, flush=True)
+    def timed(steps, warmup, lean=False):
+        for _ in range(warmup):
+            step(lean=lean)
+        torch.cuda.synchronize()
+        marks = [[ev(), ev(), ev()] for _ in range(steps)]
+        t0 = time.perf_counter()
+        for i in range(steps):
+            step(marks[i], lean)
+        torch.cuda.synchronize()
+        step_ms = (time.perf_counter() - t0) * 1e3 / steps
+        fwd_ms = sum(m[0].elapsed_time(m[1]) for m in marks) / steps
+        bwd_ms = sum(m[1].elapsed_time(m[2]) for m in marks) / steps if has_bwd else None
+        print(f"# {workload}{' (lean)' if lean else ''}: timed {steps} steps: {step_ms:.3f} ms/step "
+              f"(forward {fwd_ms:.3f} ms" + (f", backward {bwd_ms:.3f} ms" if has_bwd else "") + ")",
+              file=sys.stderr, flush=True)
+        return step_ms, fwd_ms, bwd_ms
+
+    step_ms, fwd_ms, bwd_ms = timed(steps, warmup)
+    # the lean autograd mode (saves only the reference's eight tensors; the
+    # backward rebuilds the tree and replays the selection), after the above
+    lean = None
+    if has_bwd and lean_steps:
+        lean = dict(zip(("step_ms", "fwd_ms", "bwd_ms"), timed(lean_steps, 2, lean=True)))
 
     # the fused forward kernel alone, with HIP events
     with torch.no_grad():
@@ -285,8 +300,13 @@ def measure(workload, q, k, v, dO, steps, warmup, kernel_iters):
     torch.cuda.synchronize()
     kern_ms = k0.elapsed_time(k1) / kernel_iters
     w = work(B, T, H, Hkv, D, CR, TK, MTN, getattr(torch, dtype).itemsize)
+    saved = None
+    if has_bwd:  # bytes the default mode keeps per call beyond the reference's eight tensors
+        saved = sum(t.numel() * t.element_size() for t in
+                    (ctx["parents_stacked"], ctx["packed_tree"], ctx.get("train_scores"))
+                    if t is not None)
     return dict(has_bwd=has_bwd, step_ms=step_ms, fwd_ms=fwd_ms, bwd_ms=bwd_ms, kern_ms=kern_ms,
-                work=w, out=out, ctx=ctx)
+                work=w, out=out, ctx=ctx, lean=lean, saved_bytes=saved)
 
 
 def main():
@@ -297,6 +317,8 @@ def main():
     ap.add_argument("--workload", default="C2", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--kernel-iters", type=int, default=20)
+    ap.add_argument("--no-lean", action="store_true",
+                    help="skip the lean autograd mode's measurement")
     ap.add_argument("--also", default=None,
                     help="comma-separated workloads measured briefly after the main one "
                          "(3 steps each; default for C2: C3,C4,C5,REF_BWD; '' for none)")
@@ -321,7 +343,8 @@ def main():
     torch.cuda.synchronize()
     print(f"# workload {args.workload} B={B} T={T} H={H} Hkv={Hkv} D={D} {dtype} CR={CR} TK={TK} "
           f"MTN={MTN}", file=sys.stderr, flush=True)
-    m = measure(args.workload, q, k, v, dO, args.steps, args.warmup, args.kernel_iters)
+    m = measure(args.workload, q, k, v, dO, args.steps, args.warmup, args.kernel_iters,
+                lean_steps=min(args.steps, 10) if not args.no_lean else 0)
     has_bwd, fwd_ms, bwd_ms, kern_ms, w = m["has_bwd"], m["fwd_ms"], m["bwd_ms"], m["kern_ms"], m["work"]
     out, ctx = m["out"], m["ctx"]
 
@@ -367,6 +390,13 @@ def main():
             "hbm_roofline_frac": w.bwd_bytes / (bwd_ms * 1e-3) / HBM_PEAK,
             "algorithmic_bytes": w.bwd_bytes},
         "event_ms_per_step": fwd_ms + (bwd_ms or 0.0),
+        "saved_bytes_beyond_reference": m["saved_bytes"],
+        "lean": None if not m["lean"] else {
+            "mode": "htree_forward_triton_autograd(..., _save_parents=False): saves the reference's "
+                    "eight tensors only; the backward rebuilds the tree and replays the selection",
+            "ms_per_step": m["lean"]["step_ms"], "tokens_per_s": B * T / (m["lean"]["step_ms"] * 1e-3),
+            "fwd_ms": m["lean"]["fwd_ms"], "bwd_ms": m["lean"]["bwd_ms"],
+            "saved_bytes_beyond_reference": 0},
         "roofline": {
             "kernel": f"htree::{forward_kernel(args.workload)} (fused forward, all levels)",
             "bound": "hbm",
