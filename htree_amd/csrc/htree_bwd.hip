@@ -282,12 +282,6 @@ __device__ __forceinline__ void load_frag_vt(const uint16_t* __restrict__ vt, in
   }
 }
 
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
 __device__ __forceinline__ s16x4 pack4(const float (&p)[4]) {
   return __builtin_bit_cast(s16x4, make_uint2(cvt_pk_bf16(p[0], p[1]), cvt_pk_bf16(p[2], p[3])));
 }
@@ -358,8 +352,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const T* __restrict__ o, cons
 #pragma unroll
     for (int e = 0; e < 8; ++e) dl += df[e] * of[e];
   }
-  dl += __shfl_xor(dl, 16);
-  dl += __shfl_xor(dl, 32);
+  dl = add_xor32(add_xor16(dl));
   if (gv && kg == 0) delta[bt * H + h * G + u16] = dl;
 }
 

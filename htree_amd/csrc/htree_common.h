@@ -219,10 +219,82 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_wave_barrier();
 }
 
+// Cross-row lane exchange by the gfx950 lane swaps (v_permlane16_swap,
+// v_permlane32_swap: no LDS traffic, unlike ds_bpermute).  With x in both
+// operands, the 16-lane swap returns (x of rows 0,0,2,2 ; x of rows 1,1,3,3)
+// and the 32-lane swap (x of lanes 0-31 twice ; x of lanes 32-63 twice), so
+// every lane holds x and x[lane ^ 16] (resp. ^ 32), in an order that
+// commutative operations do not see.
+__device__ __forceinline__ void pair16(float x, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void pair32(float x, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+// x + x[lane ^ 16], x + x[lane ^ 32], and the same for max (every lane)
+__device__ __forceinline__ float add_xor16(float x) {
+  float a, b;
+  pair16(x, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float add_xor32(float x) {
+  float a, b;
+  pair32(x, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float max_xor16(float x) {
+  float a, b;
+  pair16(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  float a, b;
+  pair32(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ int add_xor16i(int x) {
+  const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)x, (uint32_t)x, false, false);
+  return (int)r[0] + (int)r[1];
+}
+__device__ __forceinline__ int add_xor32i(int x) {
+  const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)x, (uint32_t)x, false, false);
+  return (int)r[0] + (int)r[1];
+}
+// x of lane ^ 32
+__device__ __forceinline__ float xor32(float x) {
+  float a, b;
+  pair32(x, a, b);
+  return __lane_id() < 32 ? b : a;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// sum / max over the 16 lanes of a row (quad xor 1, quad xor 2, half-row
+// mirror, row mirror); every lane of the row gets the result
+__device__ __forceinline__ float row_sum16(float x) {
+  x += dpp<0xB1>(x);
+  x += dpp<0x4E>(x);
+  x += dpp<0x141>(x);
+  x += dpp<0x140>(x);
+  return x;
+}
+__device__ __forceinline__ float row_max16(float x) {
+  x = fmaxf(x, dpp<0xB1>(x));
+  x = fmaxf(x, dpp<0x4E>(x));
+  x = fmaxf(x, dpp<0x141>(x));
+  x = fmaxf(x, dpp<0x140>(x));
+  return x;
+}
+
+// max over the wave, in every lane
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+  return max_xor32(max_xor16(row_max16(v)));
 }
 
 __device__ __forceinline__ int mbcnt64(unsigned long long m) {
@@ -259,7 +331,7 @@ __device__ __forceinline__ void rope_frag(const float (&x)[D / 32][8], const flo
     const float sg = kg < 2 ? -1.f : 1.f;  // lo lanes subtract hi sin, hi lanes add lo sin
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float other = __shfl_xor(x[0][e], 32);
+      const float other = xor32(x[0][e]);
       t[e] = x[0][e] * c[e] + sg * other * s[e];
     }
 #pragma unroll
@@ -282,29 +354,6 @@ __device__ __forceinline__ void rope_frag(const float (&x)[D / 32][8], const flo
   }
 }
 
-// sum over the 16 lanes of a DPP row (quad xor 1, quad xor 2, half-row
-// mirror, row mirror); every lane of the row gets the result
-// DPP helpers
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
-}
-// sum / max over the 16 lanes of a row (quad xor 1, quad xor 2, half-row
-// mirror, row mirror); every lane of the row gets the result
-__device__ __forceinline__ float row_sum16(float x) {
-  x += dpp<0xB1>(x);
-  x += dpp<0x4E>(x);
-  x += dpp<0x141>(x);
-  x += dpp<0x140>(x);
-  return x;
-}
-__device__ __forceinline__ float row_max16(float x) {
-  x = fmaxf(x, dpp<0xB1>(x));
-  x = fmaxf(x, dpp<0x4E>(x));
-  x = fmaxf(x, dpp<0x141>(x));
-  x = fmaxf(x, dpp<0x140>(x));
-  return x;
-}
 __device__ __forceinline__ float wave_max_uniform(float x) {
   x = row_max16(x);
   const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
@@ -353,8 +402,7 @@ struct BlockSelect {
       if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // keep the compare masks short-lived
     }
     c = row_sum16i(c);
-    c += __shfl_xor(c, 16);
-    c += __shfl_xor(c, 32);
+    c = add_xor32i(add_xor16i(c));
     int32_t* r = red + 8 * rc;
     rc ^= 1;
     if (lane == 0) r[wv] = c;

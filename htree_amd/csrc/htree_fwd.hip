@@ -101,8 +101,7 @@ __device__ __forceinline__ void to_bf_split(const float (&x)[D / 32][8], bf16x8 
 template <int D>
 __device__ __forceinline__ void trace_store(const FwdArgs& a, int l, int64_t hq, bool gv, int kg,
                                             float m, float lpart, const f32x4 (&O)[D / 16]) {
-  float lt = lpart + __shfl_xor(lpart, 16);
-  lt += __shfl_xor(lt, 32);
+  const float lt = add_xor32(add_xor16(lpart));
   if (!gv) return;
   const int64_t lh = (int64_t)l * a.B * a.T * a.H + hq;
   float* op = a.tout + lh * D;
@@ -406,8 +405,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           if (cv && 4 * kg + r < G) e += expf(S[r] - Mrun);
-        e += __shfl_xor(e, 16);
-        e += __shfl_xor(e, 32);
+        e = add_xor32(add_xor16(e));
         if (kg == 0) W.imp[(tau << 4) + u16] = e;
         if (lane == 0) W.mt[tau] = Mrun;
       }
@@ -538,8 +536,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
         sv[r] = ok ? S[r] : -INFINITY;
       }
       float tm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-      tm = fmaxf(tm, __shfl_xor(tm, 16));
-      tm = fmaxf(tm, __shfl_xor(tm, 32));
+      tm = max_xor32(max_xor16(tm));
       if (!__any(tm > -INFINITY)) continue;  // every candidate of the tile passed down
       const float mnew = fmaxf(m_run, tm);
       const float mref = mnew == -INFINITY ? 0.f : mnew;
@@ -579,8 +576,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
   if (TRACE) {
     lt = trace_merge<D>(a, ((int64_t)b * a.T + t) * a.H + h * G + u16, u16 < G, kg, m_run, O);
   } else {
-    lt = l_part + __shfl_xor(l_part, 16);
-    lt += __shfl_xor(lt, 32);
+    lt = add_xor32(add_xor16(l_part));
   }
   if (u16 < G) {
     const int64_t hq = ((int64_t)b * a.T + t) * a.H + h * G + u16;
@@ -992,8 +988,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
   if (TRACE) {
     lt = trace_merge<D>(a, ((int64_t)b * a.T + t) * a.H + h * G + u16, gv, kg, m_run, O);
   } else {
-    lt = l_part + __shfl_xor(l_part, 16);
-    lt += __shfl_xor(lt, 32);
+    lt = add_xor32(add_xor16(l_part));
   }
   if (gv) {
     const int64_t hq = ((int64_t)b * a.T + t) * a.H + h * G + u16;
@@ -1071,8 +1066,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
   BlockSelect<C> bsel{red, lane, wv};
   // merge of the waves' states; the result (max, sum, output) is valid in wave 0
   auto merge_waves = [&](float& Mo, float& Lo, f32x4 (&Om)[ND]) {
-    float lt = l_part + __shfl_xor(l_part, 16);
-    lt += __shfl_xor(lt, 32);
+    const float lt = add_xor32(add_xor16(l_part));
     constexpr int DP = D + 1;
     float* mw = imp;
     float* lw = imp + NW * 16;
@@ -1170,8 +1164,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           if (cv && 4 * kg + r < G) e += expf(S[r] - Mrun);
-        e += __shfl_xor(e, 16);
-        e += __shfl_xor(e, 32);
+        e = add_xor32(add_xor16(e));
         if (kg == 0 && cv) imp[pos] = e;
         if (lane == 0) mt[tau] = Mrun;
       }
@@ -1253,8 +1246,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
         sv[r] = ok ? S[r] : -INFINITY;
       }
       float tm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-      tm = fmaxf(tm, __shfl_xor(tm, 16));
-      tm = fmaxf(tm, __shfl_xor(tm, 32));
+      tm = max_xor32(max_xor16(tm));
       if (!__any(tm > -INFINITY)) continue;  // every candidate of the tile passed down
       const float mnew = fmaxf(m_run, tm);
       const float mref = mnew == -INFINITY ? 0.f : mnew;
