@@ -161,6 +161,19 @@ __device__ __forceinline__ void load_kfrag(const uint16_t* __restrict__ row, int
   for (int m = 0; m < D / 32; ++m) f[m] = *(const bf16x8*)(row + dslot<D>(kg, m));
 }
 
+// exp(x) for x <= 0 (x = -inf gives 0) including subnormal results, which
+// torch's CPU exp produces and the selection's exact-tie order depends on;
+// v_exp_f32 does not return subnormals, so those are scaled by 2^-64.
+__device__ __forceinline__ float exp_sel(float x) {
+  const float t = x * kLog2e;
+  float r = __builtin_amdgcn_exp2f(t);
+  if (__builtin_expect(__any(t < -126.f), 0)) {
+    const float rs = __builtin_amdgcn_exp2f(t + 64.f) * 5.42101086242752217e-20f;
+    r = t < -126.f ? rs : r;
+  }
+  return r;
+}
+
 // One tile's inputs staged in LDS: the K~ rows (hi, lo; each row padded by
 // 16 bytes, so that the 16 lanes reading one 16-byte column position of 16
 // rows hit distinct banks) and the tile's 16-node V^T block (hi, lo).
@@ -404,7 +417,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
         float e = 0.f;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (cv && 4 * kg + r < G) e += expf(S[r] - Mrun);
+          if (cv && 4 * kg + r < G) e += exp_sel(S[r] - Mrun);
         e = add_xor32(add_xor16(e));
         if (kg == 0) W.imp[(tau << 4) + u16] = e;
         if (lane == 0) W.mt[tau] = Mrun;
@@ -592,19 +605,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
   }
 }
 
-
-// exp(x) for x <= 0 (x = -inf gives 0) including subnormal results, which
-// torch's CPU exp produces and the selection's exact-tie order depends on;
-// v_exp_f32 does not return subnormals, so those are scaled by 2^-64.
-__device__ __forceinline__ float exp_sel(float x) {
-  const float t = x * kLog2e;
-  float r = __builtin_amdgcn_exp2f(t);
-  if (__builtin_expect(__any(t < -126.f), 0)) {
-    const float rs = __builtin_amdgcn_exp2f(t + 64.f) * 5.42101086242752217e-20f;
-    r = t < -126.f ? rs : r;
-  }
-  return r;
-}
 
 // Shared Top-K of the group (src/naive.py:88-105): importance of position j
 // is imp[j] (lane j % 64 of slot j / 64), the rightmost (position apos) is
@@ -1163,7 +1163,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
         float e = 0.f;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (cv && 4 * kg + r < G) e += expf(S[r] - Mrun);
+          if (cv && 4 * kg + r < G) e += exp_sel(S[r] - Mrun);
         e = add_xor32(add_xor16(e));
         if (kg == 0 && cv) imp[pos] = e;
         if (lane == 0) mt[tau] = Mrun;
