@@ -52,6 +52,7 @@ struct BwdPlan {
   int64_t ent[HTREE_MAX_LEVELS];    // entries of a level: at most min(top_k, parent rows) per group
   int64_t piece[HTREE_MAX_LEVELS];  // entries per piece, per level
   int64_t off_delta;
+  int64_t off_dos;                     // fp32 inputs: dO rows split into bf16 hi | lo (or -1)
   int64_t off_kt[2][HTREE_MAX_LEVELS], off_vr[2][HTREE_MAX_LEVELS];
   int64_t off_kexp[HTREE_MAX_LEVELS];  // bf16 inputs: exponent of each K~^T block
   int64_t off_dk[HTREE_MAX_LEVELS], off_dv[HTREE_MAX_LEVELS];
@@ -174,6 +175,7 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true, 
     return o;
   };
   b->off_delta = take((int64_t)d->B * d->T * d->H * 4);
+  b->off_dos = d->dtype == HTREE_F32 ? take((int64_t)d->B * d->T * d->H * d->D * 4) : -1;
   for (int l = 0; l < P.L; ++l) {
     const int64_t elems = BH * P.Np[l] * d->D;
     // K~^T for dq: bf16 hi + lo for fp16 / fp32 inputs (dq = dS K~ cancels:
@@ -329,10 +331,14 @@ struct DoFrag<D, __bf16> {
 // ---------------------------------------------------------------- prep
 // delta[b,t,h] = sum_d dO * O in fp32 (src/backward.py:45-68); one wave per
 // (b, t, h_kv), lane = (head u16, d-slots of kg).
+// fp32 inputs (dos non-null): also each dO row split into bf16 hi and lo,
+// stored as one row [hi D | lo D] (the fp32 row's 4 D bytes), the split dkv
+// would otherwise apply to every staged row.
 template <int D, typename T>
 __global__ __launch_bounds__(256) void prep_kernel(const T* __restrict__ o, const T* __restrict__ dO,
                                                    int64_t ngroups, int H, int G,
-                                                   float* __restrict__ delta) {
+                                                   float* __restrict__ delta,
+                                                   uint16_t* __restrict__ dos) {
   constexpr int KS = D / 32;
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int u16 = lane & 15, kg = lane >> 4;
@@ -351,6 +357,14 @@ __global__ __launch_bounds__(256) void prep_kernel(const T* __restrict__ o, cons
     Io<T>::ld8(dO + row + dslot<D>(kg, m), df);
 #pragma unroll
     for (int e = 0; e < 8; ++e) dl += df[e] * of[e];
+    if constexpr (std::is_same<T, float>::value) {
+      if (dos && gv) {
+        bf16x8 h, l;
+        split8(df, h, l);
+        *(bf16x8*)(dos + 2 * row + dslot<D>(kg, m)) = h;
+        *(bf16x8*)(dos + 2 * row + D + dslot<D>(kg, m)) = l;
+      }
+    }
   }
   dl = add_xor32(add_xor16(dl));
   if (gv && kg == 0) delta[bt * H + h * G + u16] = dl;
@@ -717,6 +731,7 @@ struct DkvArgs {
   int32_t T, H, Hkv, G, CR, crlg, TK, tpp, max_tiles;
   float scale;
   const int2* rech;  // CR 128: accumulate mask of children 64..127 (nullptr below)
+  const uint16_t* dos;  // fp32 inputs: dO rows split, [B,T,H][hi D | lo D] bf16
 };
 
 // One entry's inputs staged in LDS by asynchronous copies: the 16 query
@@ -760,6 +775,14 @@ __device__ __forceinline__ int row_off(int g, int e) {
   return g * St::RP + b;
 }
 
+// byte offset b of head row g in a staged block (chunks swizzled as row_off)
+template <int D, typename TIn>
+__device__ __forceinline__ int row_off_b(int g, int b) {
+  using St = Stage<D, TIn>;
+  if constexpr (St::SWZ) return g * St::RP + ((((b >> 4) ^ swz(g)) << 4) | (b & 15));
+  return g * St::RP + b;
+}
+
 // Asynchronous copies of one entry's inputs into `slot` (buffer loads into
 // LDS: the bases live in scalar registers, the lanes hold 32-bit offsets).
 // The copies come in three parts (q rows, dO rows, the rest); wave w of nw
@@ -784,7 +807,9 @@ __device__ __forceinline__ void stage_issue(char* slot, const DkvArgs& a, int64_
     lane = lane_c;
   }
   const __amdgpu_buffer_rsrc_t rq = buf_rsrc((const char*)a.q + hq0 * D * ES, G * D * ES);
-  const __amdgpu_buffer_rsrc_t rd = buf_rsrc((const char*)a.dO + hq0 * D * ES, G * D * ES);
+  // fp32 inputs: the split rows, whose 4 D bytes stage like an fp32 row
+  const void* dsrc = std::is_same<TIn, float>::value ? (const void*)a.dos : a.dO;
+  const __amdgpu_buffer_rsrc_t rd = buf_rsrc((const char*)dsrc + hq0 * D * ES, G * D * ES);
 #pragma unroll
   for (int j = 0; j < (St::NCH + 63) / 64; ++j) {
     const int P = j * 64 + lane;  // LDS chunk: row g, chunk c (c == CPR: pad)
@@ -876,6 +901,21 @@ struct ColT<D, __bf16> {
   }
 };
 
+// fp32 inputs' staged dO rows, split by prep_kernel into [bf16 hi D | bf16
+// lo D] (an fp32 row's bytes): heads g0..g0+3 of column d, hi and lo, by one
+// transposing read each, addressed as ColT<D, __bf16> addresses its rows
+template <int D>
+struct ColTs {
+  static __device__ __forceinline__ void get(const char* rows, int g0, int d, s16x4& h, s16x4& l) {
+    const int u16 = __lane_id() & 15;
+    const int g = g0 + (u16 >> 2), b = 2 * (d - u16 + 4 * (u16 & 3));
+    h = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(
+        const __attribute__((address_space(3))) void*)(rows + row_off_b<D, float>(g, b)));
+    l = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(
+        const __attribute__((address_space(3))) void*)(rows + row_off_b<D, float>(g, 2 * D + b)));
+  }
+};
+
 // one 16-byte chunk of TIn values as floats
 template <typename TIn>
 __device__ __forceinline__ void ld_chunk(const TIn* p, float* o) {
@@ -910,6 +950,18 @@ struct DoRow {
     row_frag<D, TIn>(rows, u16, kg, df);
 #pragma unroll
     for (int m = 0; m < D / 32; ++m) split8(df[m], h[m], lo[m]);
+  }
+};
+// fp32 inputs: the split rows' hi and lo halves load straight into the operands
+template <int D>
+struct DoRow<D, float> {
+  static __device__ __forceinline__ void get(const char* rows, int u16, int kg, bf16x8 (&h)[D / 32],
+                                             bf16x8 (&lo)[D / 32]) {
+#pragma unroll
+    for (int m = 0; m < D / 32; ++m) {
+      h[m] = *(const bf16x8*)(rows + row_off_b<D, float>(u16, 2 * dslot<D>(kg, m)));
+      lo[m] = *(const bf16x8*)(rows + row_off_b<D, float>(u16, 2 * D + 2 * dslot<D>(kg, m)));
+    }
   }
 };
 template <int D>
@@ -1169,7 +1221,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
 #pragma unroll
     for (int n = 0; n < ND; ++n) {
       s16x4 dot, dotl, qt, qtl;
-      ColT<D, TIn>::get(S0 + St::OFF_DO, 4 * kg, 16 * n + u16, dot, dotl);
+      if constexpr (std::is_same<TIn, float>::value)
+        ColTs<D>::get(S0 + St::OFF_DO, 4 * kg, 16 * n + u16, dot, dotl);
+      else
+        ColT<D, TIn>::get(S0 + St::OFF_DO, 4 * kg, 16 * n + u16, dot, dotl);
       ColT<D, TIn>::get(S0, 4 * kg, 16 * n + u16, qt, qtl);
       dv[n] = mma16(ph, dot, dv[n]);
       dv[n] = mma16(plo, dot, dv[n]);
@@ -1834,8 +1889,9 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
   const int64_t lstride = groups * d->top_k;
   auto U16 = [&](int64_t off) { return off >= 0 ? (uint16_t*)(ws + off) : nullptr; };
   float* delta = (float*)(ws + BP.off_delta);
+  uint16_t* dos = U16(BP.off_dos);
   hipLaunchKernelGGL((prep_kernel<D, T>), dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, st,
-                     (const T*)out, (const T*)dO, groups, d->H, G, delta);
+                     (const T*)out, (const T*)dO, groups, d->H, G, delta, dos);
   for (int l = 0; l < P.L; ++l) {
     const int64_t total = BH * P.Np[l] * d->D;
     // transposed K~ (fp16 / fp32 inputs) and V rows (dq_kernel)
@@ -1937,6 +1993,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.vt_l = P.off_vl[l] >= 0 ? (const uint16_t*)(tws + P.off_vl[l]) : nullptr;
     a.q = q;
     a.dO = dO;
+    a.dos = dos;
     a.gmax = gmax;
     a.gsum = gsum;
     a.delta = delta;
