@@ -82,7 +82,8 @@ def infer_max_top_nodes(T: int, CR: int, TK: int, L: int) -> int:
 
 def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_ctx: dict,
                    _grad_dtype: Optional[torch.dtype] = None):
-    """Gradients of the htree forward wrt q, k, v (fp32), selection fixed.
+    """Gradients of the htree forward wrt q, k, v (fp32 unless `_grad_dtype`),
+    selection fixed.
 
     dO and output are read in q's dtype; the reference upcasts both to fp32
     (src/backward.py:966-967), so the two agree when dO comes in q's dtype,
