@@ -56,18 +56,22 @@ struct Plan {
 // Dynamic LDS of the wide forward (byte offsets): both parent lists, the
 // selection bits, every tile's running max, block reduction slots, and the
 // importance of every candidate position (reused to merge the waves' states).
+// A KV-head pair (`halves` = 2) keeps a running max and an importance array
+// per half, and merges each half's waves in a region of its own.
 struct WideLds {
-  int par, selw, mt, red, imp, bytes;
+  int par, selw, mt, red, imp, merge_half, bytes;
 };
-__host__ __device__ inline WideLds wide_lds(int TK, int maxpos, int max_tiles, int D) {
+__host__ __device__ inline WideLds wide_lds(int TK, int maxpos, int max_tiles, int D,
+                                            int halves = 1) {
   WideLds w;
   w.par = 0;
   w.selw = 8 * TK;
   w.mt = w.selw + (maxpos + 31) / 32 * 4;
-  w.red = w.mt + 4 * max_tiles;
+  w.red = w.mt + 4 * max_tiles * halves;
   w.imp = (w.red + 256 + 15) / 16 * 16;
-  const int imp_bytes = 4 * maxpos;
-  const int merge_bytes = 4 * kWideWaves * 16 * (D + 3);
+  const int imp_bytes = 4 * maxpos * halves;
+  w.merge_half = 4 * (kWideWaves / halves) * 16 * (D + 3);  // a half's waves' states
+  const int merge_bytes = w.merge_half * halves;
   w.bytes = w.imp + (imp_bytes > merge_bytes ? imp_bytes : merge_bytes);
   return w;
 }

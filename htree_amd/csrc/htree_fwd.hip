@@ -1019,28 +1019,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
 // threshold go to the lowest positions (stable descending sort, src/naive.py:
 // 88-105) by an exclusive scan in position order.  The accumulation pass
 // recomputes the scores of the non-selected candidates.
-template <int D, bool PREC, typename TIn, bool TRACE, int C>
+// PAIR (kv_share 2, query groups of 17..32 heads): the block takes KV heads
+// 2h and 2h+1 of one query (their keys and values are the same), waves 2i,
+// 2i+1 the heads of half i.  Each half keeps its own importance array and
+// running maxima; the selection runs once, block-wide, over the pair's
+// importance imp_0 e^{m_0 - M} + imp_1 e^{m_1 - M} (the group-shared sum
+// over all of the group's heads), and both halves take its result.
+template <int D, bool PREC, typename TIn, bool TRACE, int C, bool PAIR = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && C == 32 ? 4 : 1))) void fwd_wide_kernel(const FwdArgs a) {
-  constexpr int KS = D / 32, ND = D / 16, HALF = D / 2, NW = kWideWaves;
+  constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
+  // halves, waves per half, threads
+  constexpr int NH = PAIR ? 2 : 1, NW = kWideWaves / NH, NT = 64 * kWideWaves;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int half = PAIR ? wv / NW : 0, wvh = wv % NW;  // the wave's half, its wave within it
   const int u16 = lane & 15, kg = lane >> 4;
   const int G = a.G, CR = a.CR, crlg = a.crlg, TK = a.TK;
   const int CRU = CR < 16 ? CR : 16;
   const bool wide = CR >= 16;
-  const WideLds LO = wide_lds(TK, TK << crlg, a.max_tiles, D);
+  const WideLds LO = wide_lds(TK, TK << crlg, a.max_tiles, D, NH);
   int32_t* par = (int32_t*)(lds + LO.par);      // [2][TK]
   uint32_t* selw = (uint32_t*)(lds + LO.selw);  // selection bit of every position
-  float* mt = (float*)(lds + LO.mt);            // running max of the wave at each tile
+  // running max of the wave at each tile, importance of every position: per half
+  float* mt0 = (float*)(lds + LO.mt);
+  float* mt = mt0 + half * a.max_tiles;
   int32_t* red = (int32_t*)(lds + LO.red);      // [0,16) counts, [16,32) scans, [32,36) maxima
-  float* imp = (float*)(lds + LO.imp);
+  float* imp0 = (float*)(lds + LO.imp);
+  float* imp = imp0 + half * (TK << crlg);
 
   const int64_t grp = (int64_t)(blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
-  if (grp >= (int64_t)a.B * a.Hkv * a.T) return;  // uniform over the block
-  const int t = (int)(grp % a.T);
-  const int bh = (int)(grp / a.T);
-  const int h = bh % a.Hkv;
-  const int b = bh / a.Hkv;
+  if (grp >= (int64_t)a.B * a.Hkv * a.T / NH) return;  // uniform over the block
+  int t, h, b;
+  if (PAIR) {  // block grp: query t of KV heads 2h', 2h'+1
+    const int Hr = a.Hkv >> 1;
+    t = (int)(grp % a.T);
+    const int64_t bhr = grp / a.T;
+    h = 2 * (int)(bhr % Hr) + half;
+    b = (int)(bhr / Hr);
+  } else {
+    t = (int)(grp % a.T);
+    const int bh = (int)(grp / a.T);
+    h = bh % a.Hkv;
+    b = bh / a.Hkv;
+  }
   const bool gv = u16 < G;
   const int64_t hq = ((int64_t)b * a.T + t) * a.H + h * G + u16;
 
@@ -1060,28 +1081,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
   for (int n = 0; n < ND; ++n) O[n] = f32x4{0.f, 0.f, 0.f, 0.f};
   {
     const int64_t nvp = (t / a.lv[a.L - 1].pw) / CR + 1;  // src/naive.py:108-118
-    for (int i = tid; i < TK; i += 256) par[i] = i < nvp ? i : -1;
+    for (int i = tid; i < TK; i += NT) par[i] = i < nvp ? i : -1;
   }
 
   BlockSelect<C> bsel{red, lane, wv};
-  // merge of the waves' states; the result (max, sum, output) is valid in wave 0
+  // merge of a half's waves' states; the result (max, sum, output) is valid
+  // in the half's first wave
   auto merge_waves = [&](float& Mo, float& Lo, f32x4 (&Om)[ND]) {
     const float lt = add_xor32(add_xor16(l_part));
     constexpr int DP = D + 1;
-    float* mw = imp;
-    float* lw = imp + NW * 16;
-    float* ow = imp + 2 * NW * 16;
+    float* mw = (float*)(lds + LO.imp + half * LO.merge_half);
+    float* lw = mw + NW * 16;
+    float* ow = mw + 2 * NW * 16;
     __syncthreads();
     if (kg == 0) {
-      mw[wv * 16 + u16] = m_run;
-      lw[wv * 16 + u16] = lt;
+      mw[wvh * 16 + u16] = m_run;
+      lw[wvh * 16 + u16] = lt;
     }
 #pragma unroll
     for (int n = 0; n < ND; ++n)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ow[(wv * 16 + u16) * DP + 16 * n + 4 * kg + r] = O[n][r];
+      for (int r = 0; r < 4; ++r) ow[(wvh * 16 + u16) * DP + 16 * n + 4 * kg + r] = O[n][r];
     __syncthreads();
-    if (wv == 0) {
+    if (wvh == 0) {
       float M = -INFINITY, L = 0.f;
 #pragma unroll
       for (int n = 0; n < ND; ++n) Om[n] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1118,8 +1140,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
     const int nc = ((np - 1) << crlg) + ct + 1;
     const int apos = nc - 1;
     const int nt = wide ? (nc + 15) >> 4 : np;
-    if (a.parents)
-      for (int i = tid; i < TK; i += 256)
+    if (a.parents)  // (each half its own head's row)
+      for (int i = tid - half * 64 * NW; i < TK; i += 64 * NW)
         a.parents[((((int64_t)l * a.B + b) * a.T + t) * a.Hkv + h) * TK + i] = pc[i];
     const int64_t hrow = ((int64_t)b * a.Hkv + h) * P.Np;
     const uint16_t* KH = P.kh + hrow * D;
@@ -1135,7 +1157,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
     if (upper) {
       // ---- importance of every candidate (relative to the wave's running max)
       float Mrun = -INFINITY;
-      for (int tau = wv; tau < nt; tau += NW) {
+      for (int tau = wvh; tau < nt; tau += NW) {
         const int prow = apos - (slot_of(tau) << crlg);
         float qr[KS][8];
         rot_q<D>(qf, a.cosb + (int64_t)prow * HALF, a.sinb + (int64_t)prow * HALF, kg, qr);
@@ -1184,9 +1206,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
           if (pos == apos) {
             v = 1e6f;
           } else {
-            v = imp[pos];
-            const float m = mt[wide ? pos >> 4 : pos >> crlg];
+            const int tl = wide ? pos >> 4 : pos >> crlg;
+            v = imp0[pos];
+            const float m = mt0[tl];
             if (m != M) v *= expf(m - M);
+            if (PAIR) {  // the second half's sum, in a fixed order
+              float v1 = imp0[(TK << crlg) + pos];
+              const float m1 = mt0[a.max_tiles + tl];
+              if (m1 != M) v1 *= expf(m1 - M);
+              v += v1;
+            }
           }
           key[i] = __float_as_uint(v) + 1u;
         }
@@ -1204,7 +1233,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
         selw[tid * (C / 32)] = (uint32_t)bits;
         if constexpr (C == 64) selw[tid * 2 + 1] = (uint32_t)((unsigned long long)bits >> 32);
       }
-      for (int i = take + tid; i < TK; i += 256) pn[i] = -1;
+      for (int i = take + tid; i < TK; i += NT) pn[i] = -1;
       __syncthreads();
     }
 
@@ -1215,7 +1244,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
 #pragma unroll
       for (int n = 0; n < ND; ++n) O[n] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    for (int tau = wv; tau < nt; tau += NW) {
+    for (int tau = wvh; tau < nt; tau += NW) {
       const int prow = apos - (slot_of(tau) << crlg);
       const int node0 = node0_of(tau);
       float qr[KS][8];
@@ -1282,18 +1311,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
       float Ml, Ll;
       f32x4 Ol[ND];
       merge_waves(Ml, Ll, Ol);
-      if (wv == 0) trace_store<D>(a, l, hq, gv, kg, Ml, kg == 0 ? Ll : 0.f, Ol);
+      if (wvh == 0) trace_store<D>(a, l, hq, gv, kg, Ml, kg == 0 ? Ll : 0.f, Ol);
     }
     cur ^= 1;
   }
 
   float M, lt;
   if (TRACE) {
-    if (wv != 0) return;
+    if (wvh != 0) return;
     lt = trace_merge<D>(a, hq, gv, kg, M, O);
   } else {
     merge_waves(M, lt, O);
-    if (wv != 0) return;
+    if (wvh != 0) return;
   }
   if (gv) {
     TIn* op = (TIn*)a.out + hq * D;
@@ -1313,7 +1342,21 @@ template <int D, bool PREC, typename TIn>
 static void launch_fwd(const FwdArgs& a, const Plan& P, dim3 grid, hipStream_t st) {
   const bool trace = a.tout != nullptr;
   const int max_tiles = P.max_tiles;
-  if (P.wide) {  // one block per query group
+  if (P.wide && a.kv_share == 2) {  // one block per KV-head pair of a query
+    const unsigned lds = (unsigned)wide_lds(a.TK, a.TK << a.crlg, max_tiles, D, 2).bytes;
+    const bool c64 = (a.TK << a.crlg) > kWideMidPos;
+    if (trace) {
+      if (c64)
+        hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, true, 64, true>), grid, dim3(256), lds, st, a);
+      else
+        hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, true, 32, true>), grid, dim3(256), lds, st, a);
+    } else {
+      if (c64)
+        hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, false, 64, true>), grid, dim3(256), lds, st, a);
+      else
+        hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, false, 32, true>), grid, dim3(256), lds, st, a);
+    }
+  } else if (P.wide) {  // one block per query group
     const unsigned lds = (unsigned)wide_lds(a.TK, a.TK << a.crlg, max_tiles, D).bytes;
     const bool c64 = (a.TK << a.crlg) > kWideMidPos;  // 64 keys per thread
     if (trace) {
@@ -1410,7 +1453,8 @@ static int forward_impl(const htree_dims* d, float scale, const void* q, const v
   const int64_t groups = (int64_t)d->B * d->H_kv * d->T;
   // blocks dealt round-robin to the 8 XCDs: XCD x gets blocks x, x+8, ...,
   // which map to a contiguous range of query groups (one tree per XCD's L2)
-  const int64_t nblk = P.wide ? groups : (groups + kWavesPerBlock - 1) / kWavesPerBlock;
+  const int64_t nblk = P.wide ? groups / (a.kv_share == 2 ? 2 : 1)
+                             : (groups + kWavesPerBlock - 1) / kWavesPerBlock;
   const int64_t per = (nblk + 7) / 8;
   if (per * 8 > 0x7fffffff) return HTREE_EUNSUPPORTED;
   a.per_xcd = (int32_t)per;

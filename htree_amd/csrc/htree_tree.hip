@@ -37,8 +37,11 @@ int make_plan(const htree_dims* d, Plan* p) {
       (wide && (d->top_k > kWideMaxTK || (int64_t)d->top_k * CR > kWideMaxPos)))
     return HTREE_EUNSUPPORTED;
   // shared selections over KV-head pairs: the paired waves of the
-  // one-wave-per-group forwards (not the block-per-group wide forward)
-  if (d->kv_share == 2 && wide) return HTREE_EUNSUPPORTED;
+  // one-wave-per-group forwards, or the two halves of the wide forward's
+  // block (LDS for both halves' importances within one block's 160 KB)
+  if (d->kv_share == 2 && wide &&
+      wide_lds(d->top_k, d->top_k * CR, (int)max_tiles, d->D, 2).bytes > 160 * 1024)
+    return HTREE_EUNSUPPORTED;
 
   memset(p, 0, sizeof(*p));
   p->precise = d->dtype != HTREE_BF16;
@@ -415,8 +418,7 @@ const char* htree_strerror(int status) {
              "and rope_rows >= top_k_per_layer * compression_rate, rope_rows > compression_rate";
     case HTREE_EUNSUPPORTED:
       return "configuration outside this HIP build: needs D in {32,64,128,256}, H/H_kv <= 16 "
-             "(up to 32 with kv_share 2, where top_k_per_layer <= 64 and "
-             "top_k_per_layer * max(compression_rate,16) <= 1024), "
+             "(up to 32 with kv_share 2), "
              "4 <= compression_rate <= 128, top_k_per_layer <= 1024 and "
              "top_k_per_layer * compression_rate <= 16384 (where top_k_per_layer > 64 or "
              "top_k_per_layer * max(compression_rate,16) / 16 > 64); the backward also needs "

@@ -8,10 +8,9 @@ Differences, all deliberate:
     relies on equality.  The reference's Triton-tiling asserts
     (top_k % 64 == 0, top_k % compression_rate == 0, :923,1019) do not apply.
   * limits of this HIP build (AssertionError): max(K, V) in {32, 64, 128, 256}
-    (K even), H / H_kv <= 16 (or even and <= 32 where top_k_per_layer <= 64
-    and top_k_per_layer * max(compression_rate, 16) <= 1024), 4 <= compression_rate
-    <= 128, top_k_per_layer <= 1024 and top_k_per_layer * compression_rate <=
-    16384 candidates per level.
+    (K even), H / H_kv <= 16 (or even and <= 32), 4 <= compression_rate <= 128,
+    top_k_per_layer <= 1024 and top_k_per_layer * compression_rate <= 16384
+    candidates per level.
   * a query group of G > 16 heads (the reference pads it to G_PAD,
     src/parallel.py:1023) runs as two groups of G/2 heads over duplicated KV
     heads that share one selection (the kernels' kv_share mode); each KV

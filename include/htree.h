@@ -75,9 +75,10 @@ typedef struct htree_dims {
                                heads (H_kv here counts the duplicates).  The
                                backward needs nothing more: each KV head of a
                                pair gets its half's dk / dv, the caller adds
-                               the pair.  Register and streaming forwards
-                               (top_k <= 64, top_k * max(CR, 16) <= 1024),
-                               not the wide one. */
+                               the pair.  Every forward: the register and
+                               streaming ones pair two waves of a block, the
+                               wide one (top_k > 64) two halves of one
+                               block. */
   int32_t grad_dtype;       /* enum htree_dtype of dq, dk, dv written by the
                                backward entry points: HTREE_F32 (0, as the
                                reference's htree_backward returns them) or

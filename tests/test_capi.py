@@ -106,8 +106,6 @@ def test_shared_kv_heads_accepted():
     (dict(kv_share=3), N.HTREE_ESHAPE),
     (dict(grad_dtype_code=3), N.HTREE_ESHAPE),         # not an htree_dtype
     (dict(grad_dtype_code=-1), N.HTREE_ESHAPE),
-    (dict(H=64, H_kv=4, kv_share=2, top_k=128, max_top_nodes=128, rope_rows=2048),
-     N.HTREE_EUNSUPPORTED),                            # shared selection: not the wide forward
     (dict(D=16), N.HTREE_EUNSUPPORTED),
     (dict(top_k=2048, compression_rate=4, max_top_nodes=128, rope_rows=16384),
      N.HTREE_EUNSUPPORTED),                            # top_k > 1024
@@ -194,3 +192,13 @@ def test_dims_struct_matches_header():
     for gd in (torch.bfloat16, torch.float16):
         d = N.dims(1, 2048, 8, 1, 128, 16, 16, 128, torch.bfloat16, 1152, grad_dtype=gd)
         assert len(N.levels(d)) == 2
+
+
+def test_wide_pairs_accepted():
+    """Groups of 17..32 heads with top_k > 64 run on the wide forward's
+    KV-head pairs, up to the largest wide configuration (top_k 1024, 16384
+    candidates per level, D 256: both halves' importances fit one block's LDS)."""
+    for kw in (dict(H=64, H_kv=4, kv_share=2, top_k=128, max_top_nodes=128, rope_rows=2048),
+               dict(H=64, H_kv=4, kv_share=2, top_k=1024, max_top_nodes=16384, rope_rows=17408,
+                    T=131072, D=256)):
+        assert len(N.levels(dims(**kw))) >= 1

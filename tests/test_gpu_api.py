@@ -156,6 +156,9 @@ G_CASES = [
     # 64 candidate tiles per level: the streaming forward's paired waves
     (1, 3001, 32, 1, 128, 32, 32, 256, "bfloat16", 74),  # G = 32, C4's CR / top_k
     (1, 2500, 48, 2, 32, 8, 64, 256, "float16", 75),      # G = 24, top_k 64, three levels
+    # top_k > 64: the wide forward's KV-head pairs (one block, two halves)
+    (1, 3000, 48, 2, 32, 16, 128, 256, "float32", 76),    # G = 24
+    (1, 2200, 32, 1, 64, 8, 256, 256, "bfloat16", 77),    # G = 32, CR 8, three levels
 ]
 
 

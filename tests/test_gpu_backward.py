@@ -244,6 +244,8 @@ WIDE = [
     (1, 1500, 8, 2, 32, 4, 128, 256, "float32", 41),    # CR 4, 3 levels, evictions at level 1
     (1, 2000, 8, 2, 64, 16, 128, 1024, "bfloat16", 42),  # 125 tiles at the bottom
     (1, 1500, 8, 2, 256, 16, 128, 1024, "bfloat16", 48),  # D = 256
+    (1, 2000, 32, 1, 64, 16, 128, 1024, "bfloat16", 49),   # G = 32: the wide forward's KV-head pairs
+    (1, 1500, 48, 2, 32, 4, 256, 256, "float32", 50),      # G = 24, CR 4, three levels
 ]
 
 

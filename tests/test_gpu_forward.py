@@ -160,6 +160,10 @@ WIDE = [
     (1, 20000, 8, 2, 64, 32, 512, 512, "bfloat16", 27, False),    # top_k 512 at CR 32, 3 levels
     (1, 20000, 8, 2, 32, 128, 128, 16384, "float16", 28, False),  # CR 128
     (1, 3000, 8, 2, 256, 16, 128, 2048, "bfloat16", 29, False),   # D = 256
+    # groups of 17..32 heads: KV-head pairs, one block of two 2-wave halves
+    (1, 12000, 64, 2, 32, 16, 512, 8192, "float32", 30, False),  # speed_test defaults, G = 32
+    (1, 20000, 48, 2, 32, 16, 1024, 16384, "bfloat16", 31, False),  # G = 24, 64 keys per thread
+    (1, 6000, 32, 1, 128, 32, 128, 4096, "bfloat16", 32, True),  # G = 32, D = 128, CR 32
 ]
 
 
