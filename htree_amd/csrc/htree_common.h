@@ -56,22 +56,23 @@ struct Plan {
 // Dynamic LDS of the wide forward (byte offsets): both parent lists, the
 // selection bits, every tile's running max, block reduction slots, and the
 // importance of every candidate position (reused to merge the waves' states).
-// A KV-head pair (`halves` = 2) keeps a running max and an importance array
-// per half, and merges each half's waves in a region of its own.
+// A block of `parts` KV heads sharing one selection (2: a KV-head pair, 4: a
+// quad) keeps a running max and an importance array per part, and merges
+// each part's waves in a region of its own.
 struct WideLds {
-  int par, selw, mt, red, imp, merge_half, bytes;
+  int par, selw, mt, red, imp, merge_part, bytes;
 };
 __host__ __device__ inline WideLds wide_lds(int TK, int maxpos, int max_tiles, int D,
-                                            int halves = 1) {
+                                            int parts = 1) {
   WideLds w;
   w.par = 0;
   w.selw = 8 * TK;
   w.mt = w.selw + (maxpos + 31) / 32 * 4;
-  w.red = w.mt + 4 * max_tiles * halves;
+  w.red = w.mt + 4 * max_tiles * parts;
   w.imp = (w.red + 256 + 15) / 16 * 16;
-  const int imp_bytes = 4 * maxpos * halves;
-  w.merge_half = 4 * (kWideWaves / halves) * 16 * (D + 3);  // a half's waves' states
-  const int merge_bytes = w.merge_half * halves;
+  const int imp_bytes = 4 * maxpos * parts;
+  w.merge_part = 4 * (kWideWaves / parts) * 16 * (D + 3);  // a part's waves' states
+  const int merge_bytes = w.merge_part * parts;
   w.bytes = w.imp + (imp_bytes > merge_bytes ? imp_bytes : merge_bytes);
   return w;
 }
@@ -79,13 +80,15 @@ __host__ __device__ inline WideLds wide_lds(int TK, int maxpos, int max_tiles, i
 int make_plan(const htree_dims* d, Plan* p);
 
 // Score buffer written by the training forward for the backward (bf16 inputs,
-// levels of <= 16 candidate tiles, CR <= 64): per level, query group and candidate tile
+// levels of <= 16 candidate tiles, CR <= 64, not the KV-head quads of the
+// wide forward): per level, query group and candidate tile
 // 256 fp16 values S - m_ref laid out S[head][cand] (16 x 16), then per level
 // and query group the 16 fp32 m_ref (the head's running max after the
 // level).  0 bytes otherwise.
 inline int64_t train_scores_bytes(const htree_dims* d, const Plan& P, int64_t* off_mref) {
   const int64_t groups = (int64_t)d->B * d->T * d->H_kv;
-  if (d->dtype != HTREE_BF16 || P.max_tiles > 16 || d->compression_rate > 64) {
+  if (d->dtype != HTREE_BF16 || P.max_tiles > 16 || d->compression_rate > 64 ||
+      d->kv_share == 4) {
     if (off_mref) *off_mref = 0;
     return 0;
   }

@@ -57,7 +57,7 @@ struct FwdArgs {
   int32_t B, T, H, Hkv, G, CR, crlg, TK, L, max_tiles;
   float scale;
   int32_t per_xcd;
-  int32_t kv_share;  // 2: KV heads 2i, 2i+1 share one selection (register forward)
+  int32_t kv_share;  // 2 or 4: KV heads kv_share*i .. kv_share*i + kv_share - 1 share one selection
 };
 
 template <int MAXSLOT>
@@ -1019,20 +1019,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
 // threshold go to the lowest positions (stable descending sort, src/naive.py:
 // 88-105) by an exclusive scan in position order.  The accumulation pass
 // recomputes the scores of the non-selected candidates.
-// PAIR (kv_share 2, query groups of 17..32 heads): the block takes KV heads
-// 2h and 2h+1 of one query (their keys and values are the same), waves 2i,
-// 2i+1 the heads of half i.  Each half keeps its own importance array and
-// running maxima; the selection runs once, block-wide, over the pair's
-// importance imp_0 e^{m_0 - M} + imp_1 e^{m_1 - M} (the group-shared sum
-// over all of the group's heads), and both halves take its result.
-template <int D, bool PREC, typename TIn, bool TRACE, int C, bool PAIR = false>
+// NH > 1 (kv_share 2 or 4: query groups of 17..32 or 33..64 heads): the
+// block takes KV heads NH h' .. NH h' + NH - 1 of one query (their keys and
+// values are the same), the kWideWaves / NH waves of part i the heads of KV
+// head NH h' + i.  Each part keeps its own importance array and running
+// maxima; the selection runs once, block-wide, over the parts' importance
+// sum_i imp_i e^{m_i - M} (the group-shared sum over all of the group's
+// heads), and every part takes its result.
+template <int D, bool PREC, typename TIn, bool TRACE, int C, int NH = 1>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && C == 32 ? 4 : 1))) void fwd_wide_kernel(const FwdArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
-  // halves, waves per half, threads
-  constexpr int NH = PAIR ? 2 : 1, NW = kWideWaves / NH, NT = 64 * kWideWaves;
+  static_assert(NH == 1 || NH == 2 || NH == 4, "parts of a block");
+  // waves per part, threads
+  constexpr int NW = kWideWaves / NH, NT = 64 * kWideWaves;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int half = PAIR ? wv / NW : 0, wvh = wv % NW;  // the wave's half, its wave within it
+  const int part = NH > 1 ? wv / NW : 0, wvh = wv % NW;  // the wave's part, its wave within it
   const int u16 = lane & 15, kg = lane >> 4;
   const int G = a.G, CR = a.CR, crlg = a.crlg, TK = a.TK;
   const int CRU = CR < 16 ? CR : 16;
@@ -1040,21 +1042,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
   const WideLds LO = wide_lds(TK, TK << crlg, a.max_tiles, D, NH);
   int32_t* par = (int32_t*)(lds + LO.par);      // [2][TK]
   uint32_t* selw = (uint32_t*)(lds + LO.selw);  // selection bit of every position
-  // running max of the wave at each tile, importance of every position: per half
+  // running max of the wave at each tile, importance of every position: per part
   float* mt0 = (float*)(lds + LO.mt);
-  float* mt = mt0 + half * a.max_tiles;
+  float* mt = mt0 + part * a.max_tiles;
   int32_t* red = (int32_t*)(lds + LO.red);      // [0,16) counts, [16,32) scans, [32,36) maxima
   float* imp0 = (float*)(lds + LO.imp);
-  float* imp = imp0 + half * (TK << crlg);
+  float* imp = imp0 + part * (TK << crlg);
 
   const int64_t grp = (int64_t)(blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
   if (grp >= (int64_t)a.B * a.Hkv * a.T / NH) return;  // uniform over the block
   int t, h, b;
-  if (PAIR) {  // block grp: query t of KV heads 2h', 2h'+1
-    const int Hr = a.Hkv >> 1;
+  if (NH > 1) {  // block grp: query t of KV heads NH h' .. NH h' + NH - 1
+    const int Hr = a.Hkv / NH;
     t = (int)(grp % a.T);
     const int64_t bhr = grp / a.T;
-    h = 2 * (int)(bhr % Hr) + half;
+    h = NH * (int)(bhr % Hr) + part;
     b = (int)(bhr / Hr);
   } else {
     t = (int)(grp % a.T);
@@ -1085,12 +1087,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
   }
 
   BlockSelect<C> bsel{red, lane, wv};
-  // merge of a half's waves' states; the result (max, sum, output) is valid
-  // in the half's first wave
+  // merge of a part's waves' states; the result (max, sum, output) is valid
+  // in the part's first wave
   auto merge_waves = [&](float& Mo, float& Lo, f32x4 (&Om)[ND]) {
     const float lt = add_xor32(add_xor16(l_part));
     constexpr int DP = D + 1;
-    float* mw = (float*)(lds + LO.imp + half * LO.merge_half);
+    float* mw = (float*)(lds + LO.imp + part * LO.merge_part);
     float* lw = mw + NW * 16;
     float* ow = mw + 2 * NW * 16;
     __syncthreads();
@@ -1140,8 +1142,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
     const int nc = ((np - 1) << crlg) + ct + 1;
     const int apos = nc - 1;
     const int nt = wide ? (nc + 15) >> 4 : np;
-    if (a.parents)  // (each half its own head's row)
-      for (int i = tid - half * 64 * NW; i < TK; i += 64 * NW)
+    if (a.parents)  // (each part its own head's row)
+      for (int i = tid - part * 64 * NW; i < TK; i += 64 * NW)
         a.parents[((((int64_t)l * a.B + b) * a.T + t) * a.Hkv + h) * TK + i] = pc[i];
     const int64_t hrow = ((int64_t)b * a.Hkv + h) * P.Np;
     const uint16_t* KH = P.kh + hrow * D;
@@ -1210,11 +1212,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
             v = imp0[pos];
             const float m = mt0[tl];
             if (m != M) v *= expf(m - M);
-            if (PAIR) {  // the second half's sum, in a fixed order
-              float v1 = imp0[(TK << crlg) + pos];
-              const float m1 = mt0[a.max_tiles + tl];
-              if (m1 != M) v1 *= expf(m1 - M);
-              v += v1;
+#pragma unroll
+            for (int j = 1; j < NH; ++j) {  // the other parts' sums, in a fixed order
+              float vj = imp0[j * (TK << crlg) + pos];
+              const float mj = mt0[j * a.max_tiles + tl];
+              if (mj != M) vj *= expf(mj - M);
+              v += vj;
             }
           }
           key[i] = __float_as_uint(v) + 1u;
@@ -1338,38 +1341,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
   }
 }
 
+// the wide forward with NH parts per block (kv_share 1, 2 or 4)
+template <int D, bool PREC, typename TIn, int NH>
+static void launch_wide(const FwdArgs& a, const Plan& P, dim3 grid, hipStream_t st) {
+  const unsigned lds = (unsigned)wide_lds(a.TK, a.TK << a.crlg, P.max_tiles, D, NH).bytes;
+  const bool c64 = (a.TK << a.crlg) > kWideMidPos;  // 64 keys per thread
+  if (a.tout != nullptr) {
+    if (c64)
+      hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, true, 64, NH>), grid, dim3(256), lds, st, a);
+    else
+      hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, true, 32, NH>), grid, dim3(256), lds, st, a);
+  } else {
+    if (c64)
+      hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, false, 64, NH>), grid, dim3(256), lds, st, a);
+    else
+      hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, false, 32, NH>), grid, dim3(256), lds, st, a);
+  }
+}
+
 template <int D, bool PREC, typename TIn>
 static void launch_fwd(const FwdArgs& a, const Plan& P, dim3 grid, hipStream_t st) {
   const bool trace = a.tout != nullptr;
   const int max_tiles = P.max_tiles;
-  if (P.wide && a.kv_share == 2) {  // one block per KV-head pair of a query
-    const unsigned lds = (unsigned)wide_lds(a.TK, a.TK << a.crlg, max_tiles, D, 2).bytes;
-    const bool c64 = (a.TK << a.crlg) > kWideMidPos;
-    if (trace) {
-      if (c64)
-        hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, true, 64, true>), grid, dim3(256), lds, st, a);
-      else
-        hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, true, 32, true>), grid, dim3(256), lds, st, a);
-    } else {
-      if (c64)
-        hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, false, 64, true>), grid, dim3(256), lds, st, a);
-      else
-        hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, false, 32, true>), grid, dim3(256), lds, st, a);
-    }
+  if (a.kv_share == 4) {  // one block per four KV heads of a query (any level size)
+    launch_wide<D, PREC, TIn, 4>(a, P, grid, st);
+  } else if (P.wide && a.kv_share == 2) {  // one block per KV-head pair of a query
+    launch_wide<D, PREC, TIn, 2>(a, P, grid, st);
   } else if (P.wide) {  // one block per query group
-    const unsigned lds = (unsigned)wide_lds(a.TK, a.TK << a.crlg, max_tiles, D).bytes;
-    const bool c64 = (a.TK << a.crlg) > kWideMidPos;  // 64 keys per thread
-    if (trace) {
-      if (c64)
-        hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, true, 64>), grid, dim3(256), lds, st, a);
-      else
-        hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, true, 32>), grid, dim3(256), lds, st, a);
-    } else {
-      if (c64)
-        hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, false, 64>), grid, dim3(256), lds, st, a);
-      else
-        hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, false, 32>), grid, dim3(256), lds, st, a);
-    }
+    launch_wide<D, PREC, TIn, 1>(a, P, grid, st);
   } else if (max_tiles <= 16) {
     if (trace)
       hipLaunchKernelGGL((fwd_reg_kernel<D, PREC, TIn, true>), grid, dim3(256), 0, st, a);
@@ -1446,15 +1445,16 @@ static int forward_impl(const htree_dims* d, float scale, const void* q, const v
   a.TK = d->top_k;
   a.L = P.L;
   a.scale = scale;
-  a.kv_share = d->kv_share == 2 ? 2 : 1;
+  a.kv_share = d->kv_share > 1 ? d->kv_share : 1;
+  const bool wide_fwd = P.wide || a.kv_share == 4;  // one block per a.kv_share KV heads
   // the streaming kernel addresses one (b, h_kv) block of a level array
   // with 32-bit byte offsets
-  if (!P.wide && P.max_tiles > 16 && P.Np[0] * d->D * 2 > 0x7fffffffll) return HTREE_EUNSUPPORTED;
+  if (!wide_fwd && P.max_tiles > 16 && P.Np[0] * d->D * 2 > 0x7fffffffll) return HTREE_EUNSUPPORTED;
   const int64_t groups = (int64_t)d->B * d->H_kv * d->T;
   // blocks dealt round-robin to the 8 XCDs: XCD x gets blocks x, x+8, ...,
   // which map to a contiguous range of query groups (one tree per XCD's L2)
-  const int64_t nblk = P.wide ? groups / (a.kv_share == 2 ? 2 : 1)
-                             : (groups + kWavesPerBlock - 1) / kWavesPerBlock;
+  const int64_t nblk = wide_fwd ? groups / a.kv_share
+                                : (groups + kWavesPerBlock - 1) / kWavesPerBlock;
   const int64_t per = (nblk + 7) / 8;
   if (per * 8 > 0x7fffffff) return HTREE_EUNSUPPORTED;
   a.per_xcd = (int32_t)per;

@@ -28,7 +28,8 @@ int make_plan(const htree_dims* d, Plan* p) {
   if ((int64_t)d->rope_rows < (int64_t)d->top_k * d->compression_rate ||
       d->rope_rows <= d->compression_rate)
     return HTREE_ECONFIG;
-  if (d->kv_share < 0 || d->kv_share > 2 || (d->kv_share == 2 && d->H_kv % 2 != 0))
+  if (d->kv_share < 0 || d->kv_share == 3 || d->kv_share > 4 ||
+      (d->kv_share > 1 && d->H_kv % d->kv_share != 0))
     return HTREE_ESHAPE;
   const int CR = d->compression_rate;
   const int64_t max_tiles = (int64_t)d->top_k * (CR > 16 ? CR : 16) / 16;
@@ -37,10 +38,15 @@ int make_plan(const htree_dims* d, Plan* p) {
       (wide && (d->top_k > kWideMaxTK || (int64_t)d->top_k * CR > kWideMaxPos)))
     return HTREE_EUNSUPPORTED;
   // shared selections over KV-head pairs: the paired waves of the
-  // one-wave-per-group forwards, or the two halves of the wide forward's
-  // block (LDS for both halves' importances within one block's 160 KB)
+  // one-wave-per-group forwards, or the two parts of the wide forward's
+  // block; over KV-head quads: the four parts of the wide forward's block,
+  // at every level size (LDS for every part's importances within one
+  // block's 160 KB)
   if (d->kv_share == 2 && wide &&
       wide_lds(d->top_k, d->top_k * CR, (int)max_tiles, d->D, 2).bytes > 160 * 1024)
+    return HTREE_EUNSUPPORTED;
+  if (d->kv_share == 4 &&
+      wide_lds(d->top_k, d->top_k * CR, (int)max_tiles, d->D, 4).bytes > 160 * 1024)
     return HTREE_EUNSUPPORTED;
 
   memset(p, 0, sizeof(*p));
@@ -411,14 +417,15 @@ const char* htree_strerror(int status) {
     case HTREE_ENULL: return "a required pointer argument is NULL";
     case HTREE_ESHAPE:
       return "invalid shape: need B,T,H,H_kv,D > 0, even D, H % H_kv == 0, dtype and grad_dtype "
-             "in {f32,bf16,f16}, kv_share in {0,1,2} (2: H_kv even)";
+             "in {f32,bf16,f16}, kv_share in {0,1,2,4} (H_kv a multiple of kv_share)";
     case HTREE_ECONFIG:
       return "invalid tree configuration: compression_rate, top_k_per_layer and max_top_nodes "
              "must be powers of two with max_top_nodes <= top_k_per_layer * compression_rate "
              "and rope_rows >= top_k_per_layer * compression_rate, rope_rows > compression_rate";
     case HTREE_EUNSUPPORTED:
       return "configuration outside this HIP build: needs D in {32,64,128,256}, H/H_kv <= 16 "
-             "(up to 32 with kv_share 2), "
+             "(query groups of up to 32 or 64 heads over kv_share 2 or 4 copies of each KV head; "
+             "kv_share 4 also needs the wide forward's four importance arrays in 160 KB of LDS), "
              "4 <= compression_rate <= 128, top_k_per_layer <= 1024 and "
              "top_k_per_layer * compression_rate <= 16384 (where top_k_per_layer > 64 or "
              "top_k_per_layer * max(compression_rate,16) / 16 > 64); the backward also needs "

@@ -8,13 +8,15 @@ Differences, all deliberate:
     relies on equality.  The reference's Triton-tiling asserts
     (top_k % 64 == 0, top_k % compression_rate == 0, :923,1019) do not apply.
   * limits of this HIP build (AssertionError): max(K, V) in {32, 64, 128, 256}
-    (K even), H / H_kv <= 16 (or even and <= 32), 4 <= compression_rate <= 128,
-    top_k_per_layer <= 1024 and top_k_per_layer * compression_rate <= 16384
-    candidates per level.
+    (K even), H / H_kv <= 16 (or even and <= 32, or a multiple of 4 and
+    <= 64), 4 <= compression_rate <= 128, top_k_per_layer <= 1024 and
+    top_k_per_layer * compression_rate <= 16384 candidates per level (8192
+    for groups of more than 32 heads).
   * a query group of G > 16 heads (the reference pads it to G_PAD,
-    src/parallel.py:1023) runs as two groups of G/2 heads over duplicated KV
-    heads that share one selection (the kernels' kv_share mode); each KV
-    head's dk / dv is the sum of its two copies'.
+    src/parallel.py:1023) runs as s = 2 (G <= 32) or s = 4 (G <= 64) groups
+    of G/s heads over s copies of each KV head that share one selection (the
+    kernels' kv_share mode); each KV head's dk / dv is the sum of its
+    copies'.
   * K != V (the reference carries V = v.shape[-1] apart from K,
     src/parallel.py:904) runs the kernels at one head dim D = max(K, V):
     V is zero-padded to D (zero columns add nothing to P.V and come out
@@ -66,16 +68,16 @@ def rope_cache(head_dim: int, rows: int, rope_base: float, device) -> Tuple[torc
 class HeadFrame:
     """Maps the caller's heads onto the kernels': the head dims (K for q/k, V
     for v) onto one head dim D = max(K, V), and a query group of G > 16 heads
-    onto two groups of G/2 over KV heads duplicated in place (KV head h
-    becomes kernel KV heads 2h, 2h+1: query head h*G + g is then kernel
-    group 2h + g // (G/2), so q keeps its layout).  With K == V and G <= 16
-    every method returns its argument."""
+    onto s = 2 (G <= 32) or 4 (G <= 64) groups of G/s over KV heads copied
+    in place (KV head h becomes kernel KV heads s h .. s h + s - 1: query
+    head h*G + g is then kernel group s h + g // (G/s), so q keeps its
+    layout).  With K == V and G <= 16 every method returns its argument."""
 
     def __init__(self, K: int, V: int, G: int = 1):
         self.K, self.V = K, V
         self.D = max(K, V)
         self.same = K == V
-        self.share = 2 if G > 16 else 1
+        self.share = 1 if G <= 16 else 2 if G <= 32 else 4
         self.plain = self.same and self.share == 1
 
     def kv_k(self, k: torch.Tensor) -> torch.Tensor:
@@ -150,9 +152,12 @@ def _validate(q, k, v, compression_rate, max_top_nodes, top_k_per_layer):
     assert k.shape[3] == K, f"q and k must share the head dim K ({K} vs {k.shape[3]})"
     V = v.shape[3]
     G = H // H_kv
-    assert G <= 16 or (G <= 32 and G % 2 == 0), (
-        f"configuration outside this HIP build: query groups of up to 16 heads, or an even "
-        f"number up to 32, got H/H_kv = {G}")
+    assert G <= 16 or (G <= 32 and G % 2 == 0) or (G <= 64 and G % 4 == 0), (
+        f"configuration outside this HIP build: query groups of up to 16 heads, an even "
+        f"number up to 32 or a multiple of 4 up to 64, got H/H_kv = {G}")
+    assert G <= 32 or top_k_per_layer * compression_rate <= 8192, (
+        f"configuration outside this HIP build: query groups of more than 32 heads need "
+        f"top_k_per_layer * compression_rate <= 8192, got {top_k_per_layer * compression_rate}")
     assert K % 2 == 0 and K > 0 and V > 0, "head dims must be positive, K even (RoPE pairs)"
     assert max(K, V) in KERNEL_HEAD_DIMS, (
         f"configuration outside this HIP build: needs max(K, V) in {KERNEL_HEAD_DIMS}, "

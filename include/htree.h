@@ -43,7 +43,7 @@ enum htree_status {
                               max_top_nodes <= top_k * compression_rate) */
   HTREE_EUNSUPPORTED = -4, /* legal for the reference, outside this build:
                               D not in {32, 64, 128, 256}, G = H/H_kv > 16
-                              (see kv_share for G <= 32),
+                              (see kv_share for G <= 64),
                               compression_rate outside [4, 128],
                               top_k > 1024, top_k * compression_rate > 16384,
                               more than HTREE_MAX_LEVELS levels, or a
@@ -67,18 +67,24 @@ typedef struct htree_dims {
   int32_t rope_rows;        /* rows of the cos/sin tables (>= top_k * CR,
                                > CR)                                         */
   int32_t kv_share;         /* 0 or 1: every KV head selects on its own.
-                               2: KV heads 2i and 2i+1 hold the same keys and
-                               values and share one Top-K selection (their
-                               query heads' importances are summed): a query
-                               group of G heads, 16 < G <= 32, G even, runs
-                               as two groups of G/2 heads over duplicated KV
-                               heads (H_kv here counts the duplicates).  The
-                               backward needs nothing more: each KV head of a
-                               pair gets its half's dk / dv, the caller adds
-                               the pair.  Every forward: the register and
-                               streaming ones pair two waves of a block, the
-                               wide one (top_k > 64) two halves of one
-                               block. */
+                               2 or 4: KV heads s*i .. s*i + s - 1 (s =
+                               kv_share) hold the same keys and values and
+                               share one Top-K selection (their query heads'
+                               importances are summed): a query group of G
+                               heads, 16 < G <= 16 s, G a multiple of s, runs
+                               as s groups of G/s heads over duplicated KV
+                               heads (H_kv here counts the duplicates, a
+                               multiple of s).  The backward needs nothing
+                               more: each copy of a KV head gets its part's
+                               dk / dv, the caller adds the copies.  Pairs run
+                               in every forward: the register and streaming
+                               ones pair two waves of a block, the wide one
+                               (top_k > 64) two parts of one block.  Quads
+                               run in the wide forward at every level size
+                               (four one-wave parts of a block), where its
+                               four importance arrays fit 160 KB of LDS
+                               (top_k * compression_rate <= 8192; else
+                               HTREE_EUNSUPPORTED). */
   int32_t grad_dtype;       /* enum htree_dtype of dq, dk, dv written by the
                                backward entry points: HTREE_F32 (0, as the
                                reference's htree_backward returns them) or

@@ -104,6 +104,10 @@ def test_shared_kv_heads_accepted():
     (dict(H=96, H_kv=2, kv_share=2), N.HTREE_EUNSUPPORTED),  # 48 heads per kernel group
     (dict(H=32, H_kv=3, kv_share=2), N.HTREE_ESHAPE),  # kv_share 2 needs an even H_kv
     (dict(kv_share=3), N.HTREE_ESHAPE),
+    (dict(kv_share=5), N.HTREE_ESHAPE),
+    (dict(H=48, H_kv=6, kv_share=4), N.HTREE_ESHAPE),  # kv_share 4 needs H_kv % 4 == 0
+    (dict(H=64, H_kv=4, kv_share=4, T=20000, top_k=1024, max_top_nodes=16384, rope_rows=17408),
+     N.HTREE_EUNSUPPORTED),                            # quads: four 16384-position arrays > LDS
     (dict(grad_dtype_code=3), N.HTREE_ESHAPE),         # not an htree_dtype
     (dict(grad_dtype_code=-1), N.HTREE_ESHAPE),
     (dict(D=16), N.HTREE_EUNSUPPORTED),
@@ -164,6 +168,37 @@ def test_python_api_validates_like_reference():
                                 torch.zeros(1, 64, 2, 64), 16, 64, 8)
     with pytest.raises(AssertionError, match="GPU"):  # no CPU fallback
         htree_amd.htree_forward(q, k, k, 16, 64, 8)
+    # group sizes: up to 16, even up to 32, multiples of 4 up to 64
+    for G, ok in ((16, True), (17, False), (30, True), (31, False), (36, True), (34, False),
+                  (64, True), (68, False)):
+        qg = torch.zeros(1, 64, G, 64)
+        if ok:  # passes the group rules, then stops at the device check
+            with pytest.raises(AssertionError, match="GPU"):
+                htree_amd.htree_forward(qg, k, k, 16, 64, 8)
+        else:
+            with pytest.raises(AssertionError, match="query groups"):
+                htree_amd.htree_forward(qg, k, k, 16, 64, 8)
+    with pytest.raises(AssertionError, match="8192"):  # quads: four importance arrays in LDS
+        htree_amd.htree_forward(torch.zeros(1, 64, 64, 64), k, k, 16, 16384, 1024)
+
+
+def test_head_frame_kv_copies():
+    """Groups of G > 16 heads: s copies of every KV head (s = 2 up to 32
+    heads, 4 up to 64), kernel group s h + g // (G/s) holding query heads
+    h G + g, so q keeps its layout; dk / dv come back as the copies' sum."""
+    from htree_amd.parallel import HeadFrame
+
+    for G, s in ((16, 1), (24, 2), (32, 2), (40, 4), (64, 4)):
+        hf = HeadFrame(64, 64, G)
+        assert hf.share == s
+        k = torch.arange(2 * 3 * 5 * 64, dtype=torch.float32).view(2, 3, 5, 64)
+        kk = hf.kv_k(k)
+        assert kk.shape == (2, 3, 5 * s, 64)
+        for h in range(5):
+            for c in range(s):
+                assert torch.equal(kk[:, :, s * h + c], k[:, :, h])
+        assert torch.equal(hf.pick(kk, 2), k)
+        assert torch.equal(hf.pair_sum(kk), k * s)
 
 
 def test_work_model_matches_baseline_table():
@@ -202,3 +237,19 @@ def test_wide_pairs_accepted():
                dict(H=64, H_kv=4, kv_share=2, top_k=1024, max_top_nodes=16384, rope_rows=17408,
                     T=131072, D=256)):
         assert len(N.levels(dims(**kw))) >= 1
+
+
+def test_wide_quads_accepted():
+    """Groups of 33..64 heads run as four groups over KV-head quads in the
+    wide forward at every level size, up to 8192 candidates per level (all
+    four parts' importances fit one block's LDS), and keep no training
+    scores (the wide forward writes none)."""
+    for kw in (dict(H=64, H_kv=4, kv_share=4),                       # 16 tiles per level
+               dict(H=64, H_kv=4, kv_share=4, top_k=512, max_top_nodes=8192, rope_rows=9216,
+                    T=131072, D=256),
+               dict(H=64, H_kv=4, kv_share=4, top_k=1024, compression_rate=8, max_top_nodes=8192,
+                    rope_rows=9216, T=131072, D=256)):
+        d = dims(**kw)
+        assert len(N.levels(d)) >= 1
+        assert N.train_scores_bytes(d) == 0
+    assert N.train_scores_bytes(dims(H=64, H_kv=4, kv_share=2)) > 0

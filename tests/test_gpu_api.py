@@ -159,12 +159,16 @@ G_CASES = [
     # top_k > 64: the wide forward's KV-head pairs (one block, two halves)
     (1, 3000, 48, 2, 32, 16, 128, 256, "float32", 76),    # G = 24
     (1, 2200, 32, 1, 64, 8, 256, 256, "bfloat16", 77),    # G = 32, CR 8, three levels
+    # groups of 33..64 heads: KV-head quads, the wide forward at every level size
+    (1, 1200, 64, 1, 64, 16, 16, 128, "bfloat16", 78),   # G = 64, 16 tiles per level
+    (1, 1000, 80, 2, 32, 8, 32, 128, "float16", 79),     # G = 40: 10 heads per part
+    (1, 1500, 64, 1, 32, 16, 128, 256, "float32", 80),   # G = 64, top_k 128
 ]
 
 
 @pytest.mark.parametrize("cfg", G_CASES, ids=lambda c: f"G{c[2] // c[3]}D{c[4]}cr{c[5]}{c[8]}")
 def test_query_groups_over_16_heads(cfg):
-    """Groups of 17..32 query heads (the reference pads them to G_PAD,
+    """Groups of 17..64 query heads (the reference pads them to G_PAD,
     src/parallel.py:1023): forward, backward, trace and both autograd modes
     against the oracle, which restates any group size directly."""
     import htree_amd

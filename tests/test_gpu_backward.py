@@ -246,6 +246,7 @@ WIDE = [
     (1, 1500, 8, 2, 256, 16, 128, 1024, "bfloat16", 48),  # D = 256
     (1, 2000, 32, 1, 64, 16, 128, 1024, "bfloat16", 49),   # G = 32: the wide forward's KV-head pairs
     (1, 1500, 48, 2, 32, 4, 256, 256, "float32", 50),      # G = 24, CR 4, three levels
+    (1, 1200, 64, 1, 64, 8, 128, 128, "bfloat16", 51),     # G = 64: KV-head quads, three levels
 ]
 
 

@@ -164,6 +164,9 @@ WIDE = [
     (1, 12000, 64, 2, 32, 16, 512, 8192, "float32", 30, False),  # speed_test defaults, G = 32
     (1, 20000, 48, 2, 32, 16, 1024, 16384, "bfloat16", 31, False),  # G = 24, 64 keys per thread
     (1, 6000, 32, 1, 128, 32, 128, 4096, "bfloat16", 32, True),  # G = 32, D = 128, CR 32
+    # groups of 33..64 heads: KV-head quads, one block of four one-wave parts
+    (1, 12000, 64, 1, 32, 16, 512, 8192, "float32", 33, False),  # speed_test's 64 heads over 1 KV head
+    (1, 8192, 96, 2, 64, 8, 256, 1024, "bfloat16", 34, True),   # G = 48, CR 8, 3 levels
 ]
 
 

@@ -4,8 +4,10 @@
 // the library accepts on the wide path (top_k > 64 or more than 64 candidate
 // tiles; top_k <= 1024, top_k * CR <= 16384, CR in [4, 128], D in {32, 64, 128, 256};
 // 32 selection keys per thread up to 8192 positions, 64 above; with one
-// half, and with the two halves of a KV-head pair where their layout fits
-// 160 KB) and every level shape (np parents, child index ct of the query), each LDS
+// part, and with the two parts of a KV-head pair where their layout fits
+// 160 KB) and for every configuration with the four parts of a KV-head quad
+// (groups of 33..64 heads run the wide forward at any level size) where
+// their layout fits 160 KB, and every level shape (np parents, child index ct of the query), each LDS
 // index the kernel forms is checked to lie inside its region, and the
 // regions to lie inside the allocation without overlapping.  Test
 // infrastructure: built and run by tests/test_wide_lds.py on the CPU.
@@ -33,13 +35,13 @@ struct Region {
   long lo, hi;  // bytes [lo, hi)
 };
 
-static void check_config(int TK, int CR, int D, int halves) {
+static void check_config(int TK, int CR, int D, int parts) {
   int crlg = 0;
   while ((1 << crlg) < CR) ++crlg;
   const int max_tiles = TK * (CR > 16 ? CR : 16) / 16;  // make_plan
   const int maxpos = TK << crlg;                        // launch: TK << crlg
-  const WideLds w = wide_lds(TK, maxpos, max_tiles, D, halves);
-  const int NW = kWideWaves / halves;                   // waves per half
+  const WideLds w = wide_lds(TK, maxpos, max_tiles, D, parts);
+  const int NW = kWideWaves / parts;                    // waves per part
   const int C = maxpos > kWideMidPos ? 2 * kWideC : kWideC;  // the launch's choice
   const int WPT = C / 32;                                    // selection words per thread
   CHECK(256 * C >= maxpos, "TK %d CR %d: %d keys per thread cover %d positions", TK, CR, C, maxpos);
@@ -48,7 +50,7 @@ static void check_config(int TK, int CR, int D, int halves) {
   // regions as the kernel reads them
   const Region par{w.par, (long)w.par + 2L * TK * 4};
   const Region selw{w.selw, (long)w.selw + 256L * WPT * 4};  // selw[tid * WPT + j]
-  const Region mt{w.mt, (long)w.mt + (long)max_tiles * halves * 4};
+  const Region mt{w.mt, (long)w.mt + (long)max_tiles * parts * 4};
   const Region red{w.red, (long)w.red + 36L * 4};       // counts, scans, maxima
   const long imp_floats = (w.bytes - w.imp) / 4;
   const Region all{0, w.bytes};
@@ -77,13 +79,13 @@ static void check_config(int TK, int CR, int D, int halves) {
         for (int u = 0; u < 16; ++u) {
           const int pos = wide ? (tau << 4) + u : (tau << crlg) + u;
           if (!(u < CRU && pos < nc)) continue;
-          for (int hf = 0; hf < halves; ++hf)  // the half's array, read by the keys of both
-            CHECK(hf * maxpos + pos < imp_floats, "imp[%d] of half %d of %ld", pos, hf, imp_floats);
+          for (int hf = 0; hf < parts; ++hf)  // the part's array, read by the keys of all parts
+            CHECK(hf * maxpos + pos < imp_floats, "imp[%d] of part %d of %ld", pos, hf, imp_floats);
           CHECK((pos >> 5) < 256 * WPT && (pos >> 5) * 4 + 4 <= (maxpos + 31) / 32 * 4, "selw word of %d", pos);
           const int mtile = wide ? pos >> 4 : pos >> crlg;
           CHECK(mtile == tau && mtile < max_tiles, "mt index %d for tile %d", mtile, tau);
-          for (int hf = 0; hf < halves; ++hf)
-            CHECK(w.mt + (hf * max_tiles + mtile + 1) * 4 <= mt.hi, "mt of half %d", hf);
+          for (int hf = 0; hf < parts; ++hf)
+            CHECK(w.mt + (hf * max_tiles + mtile + 1) * 4 <= mt.hi, "mt of part %d", hf);
         }
       }
       // the select's parent reads pc[pos >> crlg] and list writes pn[idx], idx < take
@@ -91,17 +93,24 @@ static void check_config(int TK, int CR, int D, int halves) {
       CHECK(take <= TK, "take");
       for (int pos = 0; pos < nc; ++pos) CHECK((pos >> crlg) < np, "pc index of %d", pos);
     }
-  // each half's waves merge in the importance area, half hf from byte
-  // merge_half * hf: mw, lw then ow rows of D + 1
+  // each part's waves merge in the importance area, part hf from byte
+  // merge_part * hf: mw, lw then ow rows of D + 1
   const int DP = D + 1;
-  for (int hf = 0; hf < halves; ++hf) {
-    const long base = (long)hf * w.merge_half / 4;
+  for (int hf = 0; hf < parts; ++hf) {
+    const long base = (long)hf * w.merge_part / 4;
     const long last_ow = base + 2L * NW * 16 + (long)((NW - 1) * 16 + 15) * DP + (D - 1);
     CHECK(last_ow < imp_floats, "TK %d CR %d D %d: merge index %ld of %ld", TK, CR, D, last_ow,
           imp_floats);
-    CHECK(hf == 0 || base >= (long)(hf * w.merge_half / 4), "merge regions");
+    CHECK(last_ow < (long)(hf + 1) * w.merge_part / 4, "merge regions of parts %d, %d", hf, hf + 1);
   }
-  CHECK(w.merge_half % 4 == 0 && w.merge_half >= 4 * (2 * NW * 16 + NW * 16 * DP), "merge region size");
+  CHECK(w.merge_part % 4 == 0 && w.merge_part >= 4 * (2 * NW * 16 + NW * 16 * DP), "merge region size");
+  // the parent-list rows: part hf's waves (threads 64 NW hf .. 64 NW (hf + 1) - 1)
+  // write entries i = tid - 64 NW hf, stride 64 NW
+  for (int tid = 0; tid < 256; ++tid) {
+    const int hf = (tid >> 6) / NW;
+    const int i0 = tid - hf * 64 * NW;
+    CHECK(hf < parts && i0 >= 0 && i0 < 64 * NW, "parent-row index of thread %d", tid);
+  }
 }
 
 int main() {
@@ -112,6 +121,11 @@ int main() {
         if ((long)TK * CR > kWideMaxPos) continue;
         const int max_tiles = TK * (CR > 16 ? CR : 16) / 16;
         const bool wide = max_tiles > kMaxTiles || TK > kMaxTK;  // make_plan
+        // quads: any level size (make_plan's LDS rule)
+        if (wide_lds(TK, TK * CR, max_tiles, D, 4).bytes <= 160 * 1024) {
+          check_config(TK, CR, D, 4);
+          ++n;
+        }
         if (!wide) continue;
         check_config(TK, CR, D, 1);
         ++n;
