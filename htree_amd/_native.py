@@ -40,7 +40,7 @@ EXPORTS = (
 class HtreeDims(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in (
         "B", "T", "H", "H_kv", "D", "compression_rate", "top_k", "max_top_nodes", "dtype",
-        "rope_rows", "kv_share", "grad_dtype")]
+        "rope_rows", "kv_share", "grad_dtype", "group_pad")]
 
 
 class HtreeError(RuntimeError):
@@ -120,14 +120,16 @@ def check(rc: int, what: str) -> None:
 
 
 def dims(B, T, H, H_kv, D, compression_rate, top_k, max_top_nodes, dtype, rope_rows,
-         kv_share=1, grad_dtype=None) -> HtreeDims:
-    """grad_dtype: dtype of the backward's dq, dk, dv (None: float32)."""
+         kv_share=1, grad_dtype=None, group_pad=0) -> HtreeDims:
+    """grad_dtype: dtype of the backward's dq, dk, dv (None: float32).
+    group_pad: padding query heads at the end of every kv_share-th KV
+    head's group (the forward leaves them out of the selection)."""
     for t in (dtype, grad_dtype):
         if t is not None and t not in DTYPE_CODE:
             raise AssertionError(f"unsupported dtype {t}: expected float32, bfloat16 or float16")
     return HtreeDims(B, T, H, H_kv, D, compression_rate, top_k, max_top_nodes,
                      DTYPE_CODE[dtype], rope_rows, kv_share,
-                     DTYPE_CODE[grad_dtype] if grad_dtype is not None else 0)
+                     DTYPE_CODE[grad_dtype] if grad_dtype is not None else 0, group_pad)
 
 
 def with_grad_dtype(d: HtreeDims, grad_dtype) -> HtreeDims:

@@ -112,12 +112,12 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
     if ws is None or d is None:
         # a context of the reference's keys: the kernels run with its own tables
         check_tables(cos, sin, K // 2, max(TK * CR, CR + 1), dev)
-        d = make_dims(B, T, H, H_kv, hf.D, CR, MTN, TK, q.dtype, cos.shape[0], hf.share)
+        d = make_dims(B, T, H, H_kv, hf.D, CR, MTN, TK, q.dtype, cos.shape[0], hf.share, hf.gpad)
         assert len(N.levels(d)) == L, f"num_layers {L} does not match T={T}, CR={CR}, MTN={MTN}"
         ws = None
     cos_k, sin_k = hf.tables(cos, sin)
     q = q.contiguous()
-    qf = hf.pad_qk(q)
+    qf = hf.q_heads(hf.pad_qk(q))
     parents = bwd_ctx.get("parents_stacked")
     plp = bwd_ctx.get("per_layer_parents")
     # per_layer_parents (what the reference reads) are views of the forward's
@@ -138,15 +138,19 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
             True)
     elif ws is None:
         _, _, ws = build_tree(hf.kv_k(k.contiguous()), hf.kv_v(v.contiguous()), d, cos_k, sin_k)
-    dOf = hf.pad_v(dO.contiguous().to(q.dtype))
-    outf = hf.pad_v(output.contiguous().to(q.dtype))
+    # padding heads of a group: zero dO (they add nothing to dk / dv), and
+    # any finite out / max / sum
+    dOf = hf.q_heads(hf.pad_v(dO.contiguous().to(q.dtype)))
+    outf = hf.q_heads(hf.pad_v(output.contiguous().to(q.dtype)))
+    gmax = hf.q_heads(bwd_ctx["global_max"].contiguous(), fill=0.0)
+    gsum = hf.q_heads(bwd_ctx["global_sum"].contiguous(), fill=1.0)
     D = hf.D
     # KV-head pairs add their halves' dk / dv in fp32 before the rounding
     kdt = gdt if hf.share == 1 else torch.float32
     if kdt != torch.float32:
         d = N.with_grad_dtype(d, kdt)
     g = dict(dtype=kdt, device=dev)
-    dq = torch.empty(B, T, H, D, **g)
+    dq = torch.empty(B, T, qf.shape[2], D, **g)
     dk = torch.empty(B, T, H_kv * hf.share, D, **g)
     dv = torch.empty_like(dk)
     nb = N.ctypes.c_int64()
@@ -162,19 +166,19 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
     with torch.cuda.device(dev):
         if scores is not None:
             rc = N.lib().htree_backward_train(
-                d, float(scale), N.ptr(qf), N.ptr(outf), N.ptr(dOf), N.ptr(bwd_ctx["global_max"]),
-                N.ptr(bwd_ctx["global_sum"]), N.ptr(parents), N.ptr(ws), ws.numel(), N.ptr(cos_k),
+                d, float(scale), N.ptr(qf), N.ptr(outf), N.ptr(dOf), N.ptr(gmax),
+                N.ptr(gsum), N.ptr(parents), N.ptr(ws), ws.numel(), N.ptr(cos_k),
                 N.ptr(sin_k), N.ptr(scores), scores.numel(), N.ptr(dq), N.ptr(dk), N.ptr(dv),
                 N.ptr(bws), bws.numel(), N.stream_ptr(dev))
             N.check(rc, "htree_backward_train")
         else:
             rc = N.lib().htree_backward(
-                d, float(scale), N.ptr(qf), N.ptr(outf), N.ptr(dOf), N.ptr(bwd_ctx["global_max"]),
-                N.ptr(bwd_ctx["global_sum"]), N.ptr(parents), N.ptr(ws), ws.numel(), N.ptr(cos_k),
+                d, float(scale), N.ptr(qf), N.ptr(outf), N.ptr(dOf), N.ptr(gmax),
+                N.ptr(gsum), N.ptr(parents), N.ptr(ws), ws.numel(), N.ptr(cos_k),
                 N.ptr(sin_k), N.ptr(dq), N.ptr(dk), N.ptr(dv), N.ptr(bws), bws.numel(),
                 N.stream_ptr(dev))
             N.check(rc, "htree_backward")
-    return (hf.unpad_qk(dq).to(gdt), hf.unpad_qk(hf.pair_sum(dk)).to(gdt),
+    return (hf.unpad_qk(hf.q_heads_back(dq)).to(gdt), hf.unpad_qk(hf.pair_sum(dk)).to(gdt),
             hf.unpad_v(hf.pair_sum(dv)).to(gdt))
 
 

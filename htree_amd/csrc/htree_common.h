@@ -80,15 +80,15 @@ __host__ __device__ inline WideLds wide_lds(int TK, int maxpos, int max_tiles, i
 int make_plan(const htree_dims* d, Plan* p);
 
 // Score buffer written by the training forward for the backward (bf16 inputs,
-// levels of <= 16 candidate tiles, CR <= 64, not the KV-head quads of the
-// wide forward): per level, query group and candidate tile
+// levels of <= 16 candidate tiles, CR <= 64, no padding heads and no KV-head
+// quads: the register forward's configurations): per level, query group and candidate tile
 // 256 fp16 values S - m_ref laid out S[head][cand] (16 x 16), then per level
 // and query group the 16 fp32 m_ref (the head's running max after the
 // level).  0 bytes otherwise.
 inline int64_t train_scores_bytes(const htree_dims* d, const Plan& P, int64_t* off_mref) {
   const int64_t groups = (int64_t)d->B * d->T * d->H_kv;
   if (d->dtype != HTREE_BF16 || P.max_tiles > 16 || d->compression_rate > 64 ||
-      d->kv_share == 4) {
+      d->kv_share == 4 || d->group_pad > 0) {
     if (off_mref) *off_mref = 0;
     return 0;
   }

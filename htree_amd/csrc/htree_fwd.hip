@@ -58,7 +58,14 @@ struct FwdArgs {
   float scale;
   int32_t per_xcd;
   int32_t kv_share;  // 2 or 4: KV heads kv_share*i .. kv_share*i + kv_share - 1 share one selection
+  int32_t gpad;      // padding heads at the end of the group of KV heads h, h % kv_share == kv_share - 1
 };
+
+// query heads of KV head h that take part in the selection (the group's
+// heads but the padding of the last KV head of a shared selection)
+__device__ __forceinline__ int sel_heads(const FwdArgs& a, int h) {
+  return a.G - ((h & (a.kv_share - 1)) == a.kv_share - 1 ? a.gpad : 0);  // kv_share 1, 2, 4
+}
 
 template <int MAXSLOT>
 struct WaveLds {
@@ -317,6 +324,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
     h = bh % a.Hkv;
     b = bh / a.Hkv;
   }
+  const int Gs = sel_heads(a, h);  // heads in the selection
   WaveLds<MAXSLOT>& W = lds_all[wv];
   char* slot = stage_all[wv];
   const int CRU = CR < 16 ? CR : 16;
@@ -411,13 +419,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
         float tm = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (cv && 4 * kg + r < G) tm = fmaxf(tm, S[r]);
+          if (cv && 4 * kg + r < Gs) tm = fmaxf(tm, S[r]);
         tm = wave_max(tm);
         Mrun = fmaxf(Mrun, tm);
         float e = 0.f;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (cv && 4 * kg + r < G) e += exp_sel(S[r] - Mrun);
+          if (cv && 4 * kg + r < Gs) e += exp_sel(S[r] - Mrun);
         e = add_xor32(add_xor16(e));
         if (kg == 0) W.imp[(tau << 4) + u16] = e;
         if (lane == 0) W.mt[tau] = Mrun;
@@ -1064,6 +1072,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
     h = bh % a.Hkv;
     b = bh / a.Hkv;
   }
+  const int Gs = sel_heads(a, h);  // heads in the selection
   const bool gv = u16 < G;
   const int64_t hq = ((int64_t)b * a.T + t) * a.H + h * G + u16;
 
@@ -1182,12 +1191,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
         float tm = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (cv && 4 * kg + r < G) tm = fmaxf(tm, S[r]);
+          if (cv && 4 * kg + r < Gs) tm = fmaxf(tm, S[r]);
         Mrun = fmaxf(Mrun, wave_max(tm));
         float e = 0.f;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (cv && 4 * kg + r < G) e += exp_sel(S[r] - Mrun);
+          if (cv && 4 * kg + r < Gs) e += exp_sel(S[r] - Mrun);
         e = add_xor32(add_xor16(e));
         if (kg == 0 && cv) imp[pos] = e;
         if (lane == 0) mt[tau] = Mrun;
@@ -1369,7 +1378,7 @@ static void launch_fwd(const FwdArgs& a, const Plan& P, dim3 grid, hipStream_t s
     launch_wide<D, PREC, TIn, 2>(a, P, grid, st);
   } else if (P.wide) {  // one block per query group
     launch_wide<D, PREC, TIn, 1>(a, P, grid, st);
-  } else if (max_tiles <= 16) {
+  } else if (max_tiles <= 16 && a.gpad == 0) {  // (padding heads: the streaming form)
     if (trace)
       hipLaunchKernelGGL((fwd_reg_kernel<D, PREC, TIn, true>), grid, dim3(256), 0, st, a);
     else
@@ -1446,10 +1455,12 @@ static int forward_impl(const htree_dims* d, float scale, const void* q, const v
   a.L = P.L;
   a.scale = scale;
   a.kv_share = d->kv_share > 1 ? d->kv_share : 1;
+  a.gpad = d->group_pad;
   const bool wide_fwd = P.wide || a.kv_share == 4;  // one block per a.kv_share KV heads
   // the streaming kernel addresses one (b, h_kv) block of a level array
   // with 32-bit byte offsets
-  if (!wide_fwd && P.max_tiles > 16 && P.Np[0] * d->D * 2 > 0x7fffffffll) return HTREE_EUNSUPPORTED;
+  if (!wide_fwd && (P.max_tiles > 16 || a.gpad > 0) && P.Np[0] * d->D * 2 > 0x7fffffffll)
+    return HTREE_EUNSUPPORTED;
   const int64_t groups = (int64_t)d->B * d->H_kv * d->T;
   // blocks dealt round-robin to the 8 XCDs: XCD x gets blocks x, x+8, ...,
   // which map to a contiguous range of query groups (one tree per XCD's L2)

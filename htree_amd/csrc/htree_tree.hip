@@ -17,6 +17,7 @@ int make_plan(const htree_dims* d, Plan* p) {
     return HTREE_ESHAPE;
   if (d->dtype < HTREE_F32 || d->dtype > HTREE_F16) return HTREE_ESHAPE;
   if (d->grad_dtype < HTREE_F32 || d->grad_dtype > HTREE_F16) return HTREE_ESHAPE;
+  if (d->group_pad < 0 || d->group_pad >= d->H / d->H_kv) return HTREE_ESHAPE;
   // reference rules: powers of two (src/parallel.py:910,921-922); the
   // MTN == TK*CR rule (:917, naive.py:148) is relaxed to MTN <= TK*CR.
   if (!is_pow2(d->compression_rate) || !is_pow2(d->top_k) ||
@@ -417,7 +418,8 @@ const char* htree_strerror(int status) {
     case HTREE_ENULL: return "a required pointer argument is NULL";
     case HTREE_ESHAPE:
       return "invalid shape: need B,T,H,H_kv,D > 0, even D, H % H_kv == 0, dtype and grad_dtype "
-             "in {f32,bf16,f16}, kv_share in {0,1,2,4} (H_kv a multiple of kv_share)";
+             "in {f32,bf16,f16}, kv_share in {0,1,2,4} (H_kv a multiple of kv_share), "
+             "0 <= group_pad < H/H_kv";
     case HTREE_ECONFIG:
       return "invalid tree configuration: compression_rate, top_k_per_layer and max_top_nodes "
              "must be powers of two with max_top_nodes <= top_k_per_layer * compression_rate "

@@ -8,15 +8,16 @@ Differences, all deliberate:
     relies on equality.  The reference's Triton-tiling asserts
     (top_k % 64 == 0, top_k % compression_rate == 0, :923,1019) do not apply.
   * limits of this HIP build (AssertionError): max(K, V) in {32, 64, 128, 256}
-    (K even), H / H_kv <= 16 (or even and <= 32, or a multiple of 4 and
-    <= 64), 4 <= compression_rate <= 128, top_k_per_layer <= 1024 and
-    top_k_per_layer * compression_rate <= 16384 candidates per level (8192
-    for groups of more than 32 heads).
+    (K even), H / H_kv <= 64, 4 <= compression_rate <= 128,
+    top_k_per_layer <= 1024 and top_k_per_layer * compression_rate <= 16384
+    candidates per level (8192 for groups of more than 32 heads).
   * a query group of G > 16 heads (the reference pads it to G_PAD,
     src/parallel.py:1023) runs as s = 2 (G <= 32) or s = 4 (G <= 64) groups
-    of G/s heads over s copies of each KV head that share one selection (the
-    kernels' kv_share mode); each KV head's dk / dv is the sum of its
-    copies'.
+    of ceil(G/s) heads over s copies of each KV head that share one
+    selection (the kernels' kv_share mode); each KV head's dk / dv is the
+    sum of its copies'.  A group that s does not divide gets zero query
+    heads appended to its last copy (the kernels' group_pad): the forward
+    leaves them out of the selection, the backward gives them zero dO.
   * K != V (the reference carries V = v.shape[-1] apart from K,
     src/parallel.py:904) runs the kernels at one head dim D = max(K, V):
     V is zero-padded to D (zero columns add nothing to P.V and come out
@@ -68,17 +69,47 @@ def rope_cache(head_dim: int, rows: int, rope_base: float, device) -> Tuple[torc
 class HeadFrame:
     """Maps the caller's heads onto the kernels': the head dims (K for q/k, V
     for v) onto one head dim D = max(K, V), and a query group of G > 16 heads
-    onto s = 2 (G <= 32) or 4 (G <= 64) groups of G/s over KV heads copied
-    in place (KV head h becomes kernel KV heads s h .. s h + s - 1: query
-    head h*G + g is then kernel group s h + g // (G/s), so q keeps its
-    layout).  With K == V and G <= 16 every method returns its argument."""
+    onto s = 2 (G <= 32) or 4 (G <= 64) groups of Gk = ceil(G/s) over KV
+    heads copied in place (KV head h becomes kernel KV heads s h .. s h + s
+    - 1: query head h*G + g is then kernel group s h + g // Gk, so q keeps
+    its layout; when s Gk > G, q_heads appends the gpad = s Gk - G padding
+    heads to each group).  With K == V and G <= 16 every method returns its
+    argument."""
 
     def __init__(self, K: int, V: int, G: int = 1):
         self.K, self.V = K, V
         self.D = max(K, V)
         self.same = K == V
+        self.G = G
         self.share = 1 if G <= 16 else 2 if G <= 32 else 4
+        # kernel group size; a group that share does not divide gets gpad
+        # zero heads appended (src/parallel.py:1023,428-431 pads to G_PAD)
+        self.Gk = -(-G // self.share)
+        self.gpad = self.share * self.Gk - G
         self.plain = self.same and self.share == 1
+
+    def q_heads(self, x: torch.Tensor, dim: int = 2, fill: float = 0.0) -> torch.Tensor:
+        """Caller heads [.., H_kv*G, ..] -> kernel heads [.., H_kv*(G+gpad), ..]
+        (along `dim`): each KV head's group gets gpad heads of `fill` at its end."""
+        if self.gpad == 0:
+            return x
+        shp = list(x.shape)
+        hkv = shp[dim] // self.G
+        y = x.reshape(shp[:dim] + [hkv, self.G] + shp[dim + 1:])
+        pad = y.new_full(shp[:dim] + [hkv, self.gpad] + shp[dim + 1:], fill)
+        return torch.cat([y, pad], dim + 1).reshape(shp[:dim] + [hkv * (self.G + self.gpad)]
+                                                    + shp[dim + 1:])
+
+    def q_heads_back(self, x: torch.Tensor, dim: int = 2) -> torch.Tensor:
+        """Kernel heads -> caller heads (drops the padding heads)."""
+        if self.gpad == 0:
+            return x
+        shp = list(x.shape)
+        gs = self.G + self.gpad
+        hkv = shp[dim] // gs
+        y = x.reshape(shp[:dim] + [hkv, gs] + shp[dim + 1:])
+        y = y.narrow(dim + 1, 0, self.G)
+        return y.reshape(shp[:dim] + [hkv * self.G] + shp[dim + 1:]).contiguous()
 
     def kv_k(self, k: torch.Tensor) -> torch.Tensor:
         """Caller k [B,T,H_kv,K] -> kernel k [B,T,share*H_kv,D]."""
@@ -152,9 +183,8 @@ def _validate(q, k, v, compression_rate, max_top_nodes, top_k_per_layer):
     assert k.shape[3] == K, f"q and k must share the head dim K ({K} vs {k.shape[3]})"
     V = v.shape[3]
     G = H // H_kv
-    assert G <= 16 or (G <= 32 and G % 2 == 0) or (G <= 64 and G % 4 == 0), (
-        f"configuration outside this HIP build: query groups of up to 16 heads, an even "
-        f"number up to 32 or a multiple of 4 up to 64, got H/H_kv = {G}")
+    assert G <= 64, (
+        f"configuration outside this HIP build: query groups of up to 64 heads, got H/H_kv = {G}")
     assert G <= 32 or top_k_per_layer * compression_rate <= 8192, (
         f"configuration outside this HIP build: query groups of more than 32 heads need "
         f"top_k_per_layer * compression_rate <= 8192, got {top_k_per_layer * compression_rate}")
@@ -180,11 +210,11 @@ def rope_rows_for(max_top_nodes: int, top_k_per_layer: int, compression_rate: in
 
 
 def make_dims(B, T, H, H_kv, D, compression_rate, max_top_nodes, top_k_per_layer, dtype, rope_rows,
-              share=1):
-    """Kernel dims; H_kv counts the caller's KV heads, the kernels see
-    share * H_kv of them."""
-    return N.dims(B, T, H, H_kv * share, D, compression_rate, top_k_per_layer, max_top_nodes, dtype,
-                  rope_rows, share)
+              share=1, gpad=0):
+    """Kernel dims; H and H_kv count the caller's heads, the kernels see
+    share * H_kv KV heads and H + gpad * H_kv query heads."""
+    return N.dims(B, T, H + gpad * H_kv, H_kv * share, D, compression_rate, top_k_per_layer,
+                  max_top_nodes, dtype, rope_rows, share, group_pad=gpad)
 
 
 def check_tables(cos, sin, half: int, rows_min: int, device):
@@ -288,13 +318,14 @@ def htree_forward(
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     rows = rope_rows_for(max_top_nodes, top_k_per_layer, compression_rate)
     d = make_dims(B, T, H, H_kv, hf.D, compression_rate, max_top_nodes, top_k_per_layer, q.dtype,
-                  rows, hf.share)
+                  rows, hf.share, hf.gpad)
     cos, sin = rope_cache(K, rows, rope_base, q.device)
     cos_k, sin_k = hf.tables(cos, sin)
     save_par = _save_for_backward and _save_parents
     out_f, gmax, gsum, parents, lk, lv, ws, scores = forward_frame(
-        hf.pad_qk(q), hf.kv_k(k), hf.kv_v(v), d, cos_k, sin_k, scale, save_par, True)
-    out = hf.unpad_v(out_f)
+        hf.q_heads(hf.pad_qk(q)), hf.kv_k(k), hf.kv_v(v), d, cos_k, sin_k, scale, save_par, True)
+    out = hf.unpad_v(hf.q_heads_back(out_f))
+    gmax, gsum = hf.q_heads_back(gmax), hf.q_heads_back(gsum)
     if not _save_for_backward:
         return out
     L = len(lk)

@@ -56,27 +56,30 @@ def run_parallel_with_trace(
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     rows = rope_rows_for(max_top_nodes, top_k_per_layer, compression_rate)
     d = make_dims(B, T, H, H_kv, hf.D, compression_rate, max_top_nodes, top_k_per_layer, q.dtype,
-                  rows, hf.share)
+                  rows, hf.share, hf.gpad)
     dev = q.device
     with torch.cuda.device(dev):
         cos, sin = hf.tables(*rope_cache(K, rows, rope_base, dev))
-        qf = hf.pad_qk(q)
+        qf = hf.q_heads(hf.pad_qk(q))
+        Hk = qf.shape[2]  # the kernels' query heads (with any group padding)
         layers_k, layers_v, ws = build_tree(hf.kv_k(k), hf.kv_v(v), d, cos, sin)
         L = len(layers_k)
         out = torch.empty_like(qf)
-        gmax = torch.empty(B, T, H, dtype=torch.float32, device=dev)
-        gsum = torch.empty(B, T, H, dtype=torch.float32, device=dev)
+        gmax = torch.empty(B, T, Hk, dtype=torch.float32, device=dev)
+        gsum = torch.empty(B, T, Hk, dtype=torch.float32, device=dev)
         parents = torch.empty(L, B, T, H_kv * hf.share, top_k_per_layer, dtype=torch.int32,
                               device=dev)
-        lmax = torch.empty(L, B, T, H, dtype=torch.float32, device=dev)
-        lsum = torch.empty(L, B, T, H, dtype=torch.float32, device=dev)
-        lout = torch.empty(L, B, T, H, hf.D, dtype=torch.float32, device=dev)
+        lmax = torch.empty(L, B, T, Hk, dtype=torch.float32, device=dev)
+        lsum = torch.empty(L, B, T, Hk, dtype=torch.float32, device=dev)
+        lout = torch.empty(L, B, T, Hk, hf.D, dtype=torch.float32, device=dev)
         rc = N.lib().htree_forward_trace(d, float(scale), N.ptr(qf), N.ptr(ws), ws.numel(),
                                          N.ptr(cos), N.ptr(sin), N.ptr(out), N.ptr(gmax),
                                          N.ptr(gsum), N.ptr(parents), N.ptr(lmax), N.ptr(lsum),
                                          N.ptr(lout), N.stream_ptr(dev))
         N.check(rc, "htree_forward_trace")
-        out, lout = hf.unpad_v(out), hf.unpad_v(lout)
+        out, lout = hf.unpad_v(hf.q_heads_back(out)), hf.unpad_v(hf.q_heads_back(lout, 3))
+        gmax, gsum = hf.q_heads_back(gmax), hf.q_heads_back(gsum)
+        lmax, lsum = hf.q_heads_back(lmax, 3), hf.q_heads_back(lsum, 3)
         parents = hf.pick(parents, 3)
     layers = {
         l: LayerTrace(layer_idx=l,

@@ -92,6 +92,20 @@ typedef struct htree_dims {
                                the same fp32 values (what the reference's
                                autograd backward casts them to,
                                src/backward.py:1193). */
+  int32_t group_pad;        /* padding query heads (0 <= group_pad < G):
+                               a caller's group of G0 heads that kv_share
+                               s does not divide runs as s groups of
+                               G = ceil(G0 / s) heads with group_pad =
+                               s G - G0 zero heads appended, so the last
+                               group_pad heads of KV head i's group, for i
+                               % s == s - 1 (every KV head when s <= 1),
+                               are padding.  The forward leaves them out of
+                               the selection (importances and level maxima)
+                               and still gives them outputs; the backward
+                               needs nothing more when their dO is zero
+                               (they then add nothing to dk / dv).
+                               Reference: G_PAD padding,
+                               src/parallel.py:1023,428-431. */
 } htree_dims;
 
 /* Static description of a status code (host). */

@@ -36,12 +36,12 @@ def test_strerror_covers_codes():
 
 def dims(**kw):
     base = dict(B=1, T=32768, H=32, H_kv=2, D=128, compression_rate=16, top_k=16,
-                max_top_nodes=128, dtype=torch.bfloat16, rope_rows=1152, kv_share=1)
+                max_top_nodes=128, dtype=torch.bfloat16, rope_rows=1152, kv_share=1, group_pad=0)
     grad_code = kw.pop("grad_dtype_code", None)
     base.update(kw)
     d = N.dims(base["B"], base["T"], base["H"], base["H_kv"], base["D"], base["compression_rate"],
                base["top_k"], base["max_top_nodes"], base["dtype"], base["rope_rows"],
-               base["kv_share"])
+               base["kv_share"], group_pad=base["group_pad"])
     if grad_code is not None:
         d.grad_dtype = grad_code
     return d
@@ -105,6 +105,8 @@ def test_shared_kv_heads_accepted():
     (dict(H=32, H_kv=3, kv_share=2), N.HTREE_ESHAPE),  # kv_share 2 needs an even H_kv
     (dict(kv_share=3), N.HTREE_ESHAPE),
     (dict(kv_share=5), N.HTREE_ESHAPE),
+    (dict(group_pad=16), N.HTREE_ESHAPE),              # padding must leave a head
+    (dict(group_pad=-1), N.HTREE_ESHAPE),
     (dict(H=48, H_kv=6, kv_share=4), N.HTREE_ESHAPE),  # kv_share 4 needs H_kv % 4 == 0
     (dict(H=64, H_kv=4, kv_share=4, T=20000, top_k=1024, max_top_nodes=16384, rope_rows=17408),
      N.HTREE_EUNSUPPORTED),                            # quads: four 16384-position arrays > LDS
@@ -168,9 +170,9 @@ def test_python_api_validates_like_reference():
                                 torch.zeros(1, 64, 2, 64), 16, 64, 8)
     with pytest.raises(AssertionError, match="GPU"):  # no CPU fallback
         htree_amd.htree_forward(q, k, k, 16, 64, 8)
-    # group sizes: up to 16, even up to 32, multiples of 4 up to 64
-    for G, ok in ((16, True), (17, False), (30, True), (31, False), (36, True), (34, False),
-                  (64, True), (68, False)):
+    # group sizes: any up to 64 (those 2 or 4 do not divide with padding heads)
+    for G, ok in ((16, True), (17, True), (30, True), (31, True), (36, True), (34, True),
+                  (64, True), (65, False), (68, False)):
         qg = torch.zeros(1, 64, G, 64)
         if ok:  # passes the group rules, then stops at the device check
             with pytest.raises(AssertionError, match="GPU"):
@@ -190,7 +192,7 @@ def test_head_frame_kv_copies():
 
     for G, s in ((16, 1), (24, 2), (32, 2), (40, 4), (64, 4)):
         hf = HeadFrame(64, 64, G)
-        assert hf.share == s
+        assert hf.share == s and hf.gpad == 0
         k = torch.arange(2 * 3 * 5 * 64, dtype=torch.float32).view(2, 3, 5, 64)
         kk = hf.kv_k(k)
         assert kk.shape == (2, 3, 5 * s, 64)
@@ -253,3 +255,38 @@ def test_wide_quads_accepted():
         assert len(N.levels(d)) >= 1
         assert N.train_scores_bytes(d) == 0
     assert N.train_scores_bytes(dims(H=64, H_kv=4, kv_share=2)) > 0
+
+
+def test_head_frame_group_padding():
+    """A group of G heads that s = 2 or 4 does not divide runs as s kernel
+    groups of ceil(G/s) heads, with s ceil(G/s) - G zero heads appended to
+    each KV head's group (the reference pads to G_PAD, src/parallel.py:1023):
+    padding heads sit at the end of each group, the caller's heads keep their
+    order, and the way back drops exactly the padding."""
+    from htree_amd.parallel import HeadFrame
+
+    for G, s, gk, gpad in ((17, 2, 9, 1), (31, 2, 16, 1), (33, 4, 9, 3), (50, 4, 13, 2),
+                           (63, 4, 16, 1)):
+        hf = HeadFrame(64, 64, G)
+        assert (hf.share, hf.Gk, hf.gpad) == (s, gk, gpad)
+        hkv = 3
+        x = torch.arange(2 * 5 * hkv * G * 4, dtype=torch.float32).view(2, 5, hkv * G, 4) + 1
+        y = hf.q_heads(x)
+        assert y.shape == (2, 5, hkv * s * gk, 4)
+        for h in range(hkv):
+            assert torch.equal(y[:, :, h * s * gk:h * s * gk + G], x[:, :, h * G:(h + 1) * G])
+            assert bool((y[:, :, h * s * gk + G:(h + 1) * s * gk] == 0).all())
+        assert torch.equal(hf.q_heads_back(y), x)
+        m = torch.rand(2, 5, hkv * G)
+        assert bool((hf.q_heads(m, fill=1.0).view(2, 5, hkv, s * gk)[..., G:] == 1).all())
+        lv = torch.rand(3, 2, 5, hkv * G, 4)  # per-level states: heads along dim 3
+        assert torch.equal(hf.q_heads_back(hf.q_heads(lv, 3), 3), lv)
+        # the kernels' dims: s copies of each KV head, groups of gk, group_pad heads
+        d = make_dims_for(G, hkv, hf)
+        assert (d.H, d.H_kv, d.kv_share, d.group_pad) == (hkv * s * gk, hkv * s, s, gpad)
+
+
+def make_dims_for(G, hkv, hf):
+    from htree_amd.parallel import make_dims
+    return make_dims(1, 4096, hkv * G, hkv, 64, 16, 128, 16, torch.bfloat16, 1152, hf.share,
+                     hf.gpad)

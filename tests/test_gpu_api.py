@@ -163,6 +163,12 @@ G_CASES = [
     (1, 1200, 64, 1, 64, 16, 16, 128, "bfloat16", 78),   # G = 64, 16 tiles per level
     (1, 1000, 80, 2, 32, 8, 32, 128, "float16", 79),     # G = 40: 10 heads per part
     (1, 1500, 64, 1, 32, 16, 128, 256, "float32", 80),   # G = 64, top_k 128
+    # groups that 2 or 4 does not divide: padding heads left out of the selection
+    (1, 1000, 17, 1, 64, 16, 16, 128, "bfloat16", 81),   # G = 17: pairs of 9, one padding head
+    (1, 900, 62, 2, 32, 8, 32, 128, "float16", 82),      # G = 31: streaming forward's pairs
+    (1, 1500, 23, 1, 32, 16, 128, 256, "float32", 83),   # G = 23: wide forward's pairs
+    (1, 1200, 33, 1, 32, 16, 128, 256, "float32", 84),   # G = 33: quads of 9, three padding heads
+    (1, 1000, 50, 1, 64, 4, 16, 64, "bfloat16", 85),     # G = 50: quads of 13, CR 4
 ]
 
 

@@ -167,6 +167,7 @@ WIDE = [
     # groups of 33..64 heads: KV-head quads, one block of four one-wave parts
     (1, 12000, 64, 1, 32, 16, 512, 8192, "float32", 33, False),  # speed_test's 64 heads over 1 KV head
     (1, 8192, 96, 2, 64, 8, 256, 1024, "bfloat16", 34, True),   # G = 48, CR 8, 3 levels
+    (1, 12000, 57, 1, 32, 16, 512, 8192, "bfloat16", 35, False),  # G = 57: quads of 15, 3 padding heads
 ]
 
 
