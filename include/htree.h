@@ -71,10 +71,11 @@ typedef struct htree_dims {
                                kv_share) hold the same keys and values and
                                share one Top-K selection (their query heads'
                                importances are summed): a query group of G
-                               heads, 16 < G <= 16 s, G a multiple of s, runs
-                               as s groups of G/s heads over duplicated KV
-                               heads (H_kv here counts the duplicates, a
-                               multiple of s).  The backward needs nothing
+                               heads, 16 < G <= 16 s, runs as s groups of
+                               G/s heads (ceil(G/s) with group_pad when s
+                               does not divide G) over duplicated KV heads
+                               (H_kv here counts the duplicates, a multiple
+                               of s).  The backward needs nothing
                                more: each copy of a KV head gets its part's
                                dk / dv, the caller adds the copies.  Pairs run
                                in every forward: the register and streaming
