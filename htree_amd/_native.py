@@ -33,7 +33,7 @@ EXPORTS = (
     "htree_backward",
     "htree_train_scores_bytes", "htree_forward_train", "htree_backward_train",
     "htree_forward_trace", "htree_topk_rows", "htree_backward_noalloc_bytes",
-    "htree_backward_noalloc",
+    "htree_backward_noalloc", "htree_select",
 )
 
 
@@ -79,6 +79,9 @@ def lib() -> ctypes.CDLL:
     if hasattr(L, "htree_forward_trace"):
         L.htree_forward_trace.restype = ctypes.c_int
         L.htree_forward_trace.argtypes = [DP, F, P, P, I64, P, P, P, P, P, P, P, P, P, P]
+    if hasattr(L, "htree_select"):
+        L.htree_select.restype = ctypes.c_int
+        L.htree_select.argtypes = [DP, F, P, P, I64, P, P, P, P]
     if hasattr(L, "htree_topk_rows"):
         L.htree_topk_rows.restype = ctypes.c_int
         L.htree_topk_rows.argtypes = [P, I64, I32, I32, P, I32, P, P, P, P]

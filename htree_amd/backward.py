@@ -6,9 +6,9 @@
 the reference's bwd_ctx keys.  The selection is taken from
 `per_layer_parents` when the context holds them; otherwise (the reference's
 own autograd path saves none, src/backward.py:1138) the forward's selection
-is replayed once, with the context's own RoPE tables (`cos_cache`,
-`sin_cache`), as the reference's `_recompute_parents` does
-(src/backward.py:881-934,1163-1171).  A context without `packed_tree` gets
+is replayed once by the selection-only launch (`htree_select`), with the
+context's own RoPE tables (`cos_cache`, `sin_cache`), as the reference's
+`_recompute_parents` does (src/backward.py:881-934,1163-1171).  A context without `packed_tree` gets
 its operand tree rebuilt from `layers_k[0]` / `layers_v[0]` with those same
 tables (src/backward.py:848-878).
 
@@ -18,9 +18,8 @@ Two autograd modes:
     scores, so the backward replays nothing;
   * `_save_parents=False` (htree_forward_triton_autograd): the Function
     saves only the reference's eight tensors (q, k, v, out, global max / sum,
-    cos / sin, src/backward.py:1141-1145); the backward rebuilds the tree and
-    replays the forward once (keeping its scores for the duration of the
-    backward only).
+    cos / sin, src/backward.py:1141-1145); the backward rebuilds the tree,
+    replays the selection alone and rebuilds the scores.
 """
 from __future__ import annotations
 
@@ -29,8 +28,8 @@ from typing import Optional
 import torch
 
 from . import _native as N
-from .parallel import (HeadFrame, build_tree, check_tables, forward_frame, htree_forward,
-                       make_dims)
+from .parallel import (HeadFrame, build_tree, check_tables, htree_forward, make_dims,
+                       select_frame)
 from .workmodel import level_sizes
 
 
@@ -132,10 +131,11 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
         _check_parents(parents, B, T, H_kv, TK, CR, MTN, dev)
         parents = hf.dup(parents, 3)
     if parents is None:
-        # replay the selection (and keep the replay's scores for this backward)
-        _, _, _, parents, _, _, ws, scores = forward_frame(
-            qf, hf.kv_k(k.contiguous()), hf.kv_v(v.contiguous()), d, cos_k, sin_k, scale, True,
-            True)
+        # replay the selection alone (the lists of every level, no output);
+        # the backward then rebuilds the scores
+        parents, ws = select_frame(qf, hf.kv_k(k.contiguous()), hf.kv_v(v.contiguous()), d, cos_k,
+                                   sin_k, scale)
+        scores = None
     elif ws is None:
         _, _, ws = build_tree(hf.kv_k(k.contiguous()), hf.kv_v(v.contiguous()), d, cos_k, sin_k)
     # padding heads of a group: zero dO (they add nothing to dk / dv), and

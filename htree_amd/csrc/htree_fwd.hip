@@ -277,8 +277,9 @@ struct TileStage {
 // tau is computed.  Tiles run in ascending parent slot and the query turns
 // by R(., -CR) per slot (a table row in LDS), so a tile reads no global
 // memory besides its copies.
-template <int D, bool PREC, typename TIn, int MAXSLOT, bool TRACE>
+template <int D, bool PREC, typename TIn, int MAXSLOT, bool TRACE, bool SEL = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2))) void fwd_kernel(const FwdArgs a) {
+  static_assert(!(SEL && TRACE), "selection only: no trace");
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
   using St = FwdStage<D, PREC>;
   __shared__ WaveLds<MAXSLOT> lds_all[kWavesPerBlock];
@@ -362,6 +363,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
     const int nt = wide ? (nc + 15) >> 4 : np;
     if (a.parents && lane < TK)
       a.parents[((((int64_t)l * a.B + b) * a.T + t) * a.Hkv + h) * TK + lane] = pv;
+    if (SEL && l == 0) break;  // the bottom level selects nothing
     const int64_t hrow = ((int64_t)b * a.Hkv + h) * P.Np;
     const int lvl_bytes = (int)(P.Np * D * 2);  // one (b, h_kv) block of a level array
     const TileStage<D, PREC> stg{slot, buf_rsrc(P.kh + hrow * D, lvl_bytes),
@@ -515,6 +517,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
       if (lane >= take && lane < TK) W.par[nxt][lane] = -1;
       wave_sync();
     }
+    if constexpr (SEL) {  // (the scoring pass left no copy in flight)
+      cur ^= 1;
+      continue;
+    }
 
     // ------------------------------------------------ accumulation
     if (TRACE) {
@@ -592,6 +598,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
     cur ^= 1;
   }
 
+  if constexpr (SEL) return;
   // final normalisation (src/parallel.py:321-363): out = o / s
   float lt;
   if (TRACE) {
@@ -717,8 +724,12 @@ __device__ __forceinline__ void rot_by(float (&x)[D / 32][8], const float* __res
   rope_frag<D>(x, cosr, sinr, kg, x);
 }
 
-template <int D, bool PREC, typename TIn, bool TRACE>
+// SEL: selection only (the reference's htree_recompute_selection_kernel,
+// src/parallel.py:1168): the parent lists of every level, no accumulation
+// and no output.
+template <int D, bool PREC, typename TIn, bool TRACE, bool SEL = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2))) void fwd_reg_kernel(const FwdArgs a) {
+  static_assert(!(SEL && TRACE), "selection only: no trace");
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
   __shared__ WaveLdsR lds_all[kWavesPerBlock];
   __shared__ float rot_cr[2][HALF];  // cos / sin of the angle CR
@@ -804,6 +815,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
     const int nt = wide ? (nc + 15) >> 4 : np;
     if (a.parents && lane < TK)
       a.parents[((((int64_t)l * a.B + b) * a.T + t) * a.Hkv + h) * TK + lane] = pv;
+    if (SEL && l == 0) break;  // the bottom level selects nothing
     const int64_t hrow = ((int64_t)b * a.Hkv + h) * P.Np;
     const uint16_t* KH = P.kh + hrow * D;
     const uint16_t* KL = P.kl + hrow * D;
@@ -887,6 +899,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
                        W.par[cur ^ 1], W.selmask, lane);
         wave_sync();
       }
+    }
+    if constexpr (SEL) {
+      cur ^= 1;
+      continue;
     }
 
     // ---- per-head max over the accumulated candidates (rows kg via LDS)
@@ -992,6 +1008,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
     cur ^= 1;
   }
 
+  if constexpr (SEL) return;
   float lt;
   if (TRACE) {
     lt = trace_merge<D>(a, ((int64_t)b * a.T + t) * a.H + h * G + u16, gv, kg, m_run, O);
@@ -1034,8 +1051,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
 // maxima; the selection runs once, block-wide, over the parts' importance
 // sum_i imp_i e^{m_i - M} (the group-shared sum over all of the group's
 // heads), and every part takes its result.
-template <int D, bool PREC, typename TIn, bool TRACE, int C, int NH = 1>
+template <int D, bool PREC, typename TIn, bool TRACE, int C, int NH = 1, bool SEL = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && C == 32 ? 4 : 1))) void fwd_wide_kernel(const FwdArgs a) {
+  static_assert(!(SEL && TRACE), "selection only: no trace");
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
   static_assert(NH == 1 || NH == 2 || NH == 4, "parts of a block");
   // waves per part, threads
@@ -1154,6 +1172,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
     if (a.parents)  // (each part its own head's row)
       for (int i = tid - part * 64 * NW; i < TK; i += 64 * NW)
         a.parents[((((int64_t)l * a.B + b) * a.T + t) * a.Hkv + h) * TK + i] = pc[i];
+    if (SEL && l == 0) break;  // the bottom level selects nothing (uniform over the block)
     const int64_t hrow = ((int64_t)b * a.Hkv + h) * P.Np;
     const uint16_t* KH = P.kh + hrow * D;
     const uint16_t* KL = P.kl + hrow * D;
@@ -1248,6 +1267,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
       for (int i = take + tid; i < TK; i += NT) pn[i] = -1;
       __syncthreads();
     }
+    if constexpr (SEL) {
+      cur ^= 1;
+      continue;
+    }
 
     // ---- accumulation of the candidates not passed down
     if (TRACE) {
@@ -1328,6 +1351,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
     cur ^= 1;
   }
 
+  if constexpr (SEL) return;
   float M, lt;
   if (TRACE) {
     if (wvh != 0) return;
@@ -1350,12 +1374,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
   }
 }
 
-// the wide forward with NH parts per block (kv_share 1, 2 or 4)
+// the wide forward with NH parts per block (kv_share 1, 2 or 4); sel: the
+// selection-only instances
 template <int D, bool PREC, typename TIn, int NH>
-static void launch_wide(const FwdArgs& a, const Plan& P, dim3 grid, hipStream_t st) {
+static void launch_wide(const FwdArgs& a, const Plan& P, dim3 grid, hipStream_t st, bool sel) {
   const unsigned lds = (unsigned)wide_lds(a.TK, a.TK << a.crlg, P.max_tiles, D, NH).bytes;
   const bool c64 = (a.TK << a.crlg) > kWideMidPos;  // 64 keys per thread
-  if (a.tout != nullptr) {
+  if (sel) {
+    if (c64)
+      hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, false, 64, NH, true>), grid, dim3(256), lds, st, a);
+    else
+      hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, false, 32, NH, true>), grid, dim3(256), lds, st, a);
+  } else if (a.tout != nullptr) {
     if (c64)
       hipLaunchKernelGGL((fwd_wide_kernel<D, PREC, TIn, true, 64, NH>), grid, dim3(256), lds, st, a);
     else
@@ -1369,22 +1399,26 @@ static void launch_wide(const FwdArgs& a, const Plan& P, dim3 grid, hipStream_t 
 }
 
 template <int D, bool PREC, typename TIn>
-static void launch_fwd(const FwdArgs& a, const Plan& P, dim3 grid, hipStream_t st) {
+static void launch_fwd(const FwdArgs& a, const Plan& P, dim3 grid, hipStream_t st, bool sel) {
   const bool trace = a.tout != nullptr;
   const int max_tiles = P.max_tiles;
   if (a.kv_share == 4) {  // one block per four KV heads of a query (any level size)
-    launch_wide<D, PREC, TIn, 4>(a, P, grid, st);
+    launch_wide<D, PREC, TIn, 4>(a, P, grid, st, sel);
   } else if (P.wide && a.kv_share == 2) {  // one block per KV-head pair of a query
-    launch_wide<D, PREC, TIn, 2>(a, P, grid, st);
+    launch_wide<D, PREC, TIn, 2>(a, P, grid, st, sel);
   } else if (P.wide) {  // one block per query group
-    launch_wide<D, PREC, TIn, 1>(a, P, grid, st);
+    launch_wide<D, PREC, TIn, 1>(a, P, grid, st, sel);
   } else if (max_tiles <= 16 && a.gpad == 0) {  // (padding heads: the streaming form)
-    if (trace)
+    if (sel)
+      hipLaunchKernelGGL((fwd_reg_kernel<D, PREC, TIn, false, true>), grid, dim3(256), 0, st, a);
+    else if (trace)
       hipLaunchKernelGGL((fwd_reg_kernel<D, PREC, TIn, true>), grid, dim3(256), 0, st, a);
     else
       hipLaunchKernelGGL((fwd_reg_kernel<D, PREC, TIn, false>), grid, dim3(256), 0, st, a);
   } else {
-    if (trace)
+    if (sel)
+      hipLaunchKernelGGL((fwd_kernel<D, PREC, TIn, 16, false, true>), grid, dim3(256), 0, st, a);
+    else if (trace)
       hipLaunchKernelGGL((fwd_kernel<D, PREC, TIn, 16, true>), grid, dim3(256), 0, st, a);
     else
       hipLaunchKernelGGL((fwd_kernel<D, PREC, TIn, 16, false>), grid, dim3(256), 0, st, a);
@@ -1392,13 +1426,14 @@ static void launch_fwd(const FwdArgs& a, const Plan& P, dim3 grid, hipStream_t s
 }
 
 template <int D>
-static void launch_fwd_d(int dtype, const FwdArgs& a, const Plan& P, dim3 grid, hipStream_t st) {
+static void launch_fwd_d(int dtype, const FwdArgs& a, const Plan& P, dim3 grid, hipStream_t st,
+                         bool sel) {
   if (dtype == HTREE_BF16)
-    launch_fwd<D, false, __bf16>(a, P, grid, st);
+    launch_fwd<D, false, __bf16>(a, P, grid, st, sel);
   else if (dtype == HTREE_F16)
-    launch_fwd<D, true, _Float16>(a, P, grid, st);
+    launch_fwd<D, true, _Float16>(a, P, grid, st, sel);
   else
-    launch_fwd<D, true, float>(a, P, grid, st);
+    launch_fwd<D, true, float>(a, P, grid, st, sel);
 }
 
 }  // namespace htree
@@ -1409,11 +1444,14 @@ static int forward_impl(const htree_dims* d, float scale, const void* q, const v
                         int64_t tree_ws_bytes, const float* cos_table, const float* sin_table,
                         void* out, float* gmax, float* gsum, int32_t* parents, void* scores,
                         int64_t scores_bytes, float* tmax, float* tsum, float* tout,
-                        void* stream) {
+                        void* stream, bool sel = false) {
   Plan P;
   int rc = make_plan(d, &P);
   if (rc) return rc;
-  if (!q || !tree_ws || !cos_table || !sin_table || !out || !gmax || !gsum) return HTREE_ENULL;
+  if (!q || !tree_ws || !cos_table || !sin_table) return HTREE_ENULL;
+  // the selection-only launch writes the lists alone
+  if (sel ? !parents : (!out || !gmax || !gsum)) return HTREE_ENULL;
+  if (sel) scores = nullptr, tout = nullptr;
   if (tree_ws_bytes < P.bytes) return HTREE_EWORKSPACE;
   int64_t off_mref = 0;
   const int64_t sbytes = train_scores_bytes(d, P, &off_mref);
@@ -1472,13 +1510,13 @@ static int forward_impl(const htree_dims* d, float scale, const void* q, const v
   const dim3 grid((unsigned)(per * 8));
   hipStream_t st = (hipStream_t)stream;
   if (d->D == 256)
-    launch_fwd_d<256>(d->dtype, a, P, grid, st);
+    launch_fwd_d<256>(d->dtype, a, P, grid, st, sel);
   else if (d->D == 128)
-    launch_fwd_d<128>(d->dtype, a, P, grid, st);
+    launch_fwd_d<128>(d->dtype, a, P, grid, st, sel);
   else if (d->D == 32)
-    launch_fwd_d<32>(d->dtype, a, P, grid, st);
+    launch_fwd_d<32>(d->dtype, a, P, grid, st, sel);
   else
-    launch_fwd_d<64>(d->dtype, a, P, grid, st);
+    launch_fwd_d<64>(d->dtype, a, P, grid, st, sel);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? HTREE_OK : (int)e;
 }
@@ -1518,4 +1556,11 @@ extern "C" int htree_forward_trace(const htree_dims* d, float scale, const void*
   if (!parents || !level_max || !level_sum || !level_out) return HTREE_ENULL;
   return forward_impl(d, scale, q, tree_ws, tree_ws_bytes, cos_table, sin_table, out, gmax, gsum,
                       parents, nullptr, 0, level_max, level_sum, level_out, stream);
+}
+
+extern "C" int htree_select(const htree_dims* d, float scale, const void* q, const void* tree_ws,
+                            int64_t tree_ws_bytes, const float* cos_table, const float* sin_table,
+                            int32_t* parents, void* stream) {
+  return forward_impl(d, scale, q, tree_ws, tree_ws_bytes, cos_table, sin_table, nullptr, nullptr,
+                      nullptr, parents, nullptr, 0, nullptr, nullptr, nullptr, stream, true);
 }

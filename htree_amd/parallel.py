@@ -249,6 +249,22 @@ def build_tree(k, v, d, cos, sin):
     return layers_k, layers_v, ws
 
 
+def select_frame(qf, kf, vf, d, cos_k, sin_k, scale):
+    """The selection alone on kernel-frame tensors (htree_select: the lists
+    of every level, no output), as the reference's backward replays it
+    (src/backward.py:881-934).  Returns (parents [L,B,T,H_kv,TK], packed tree)."""
+    B, T = qf.shape[:2]
+    H_kv = kf.shape[2]
+    dev = qf.device
+    with torch.cuda.device(dev):
+        layers_k, _, ws = build_tree(kf, vf, d, cos_k, sin_k)
+        parents = torch.empty(len(layers_k), B, T, H_kv, d.top_k, dtype=torch.int32, device=dev)
+        rc = N.lib().htree_select(d, float(scale), N.ptr(qf), N.ptr(ws), ws.numel(), N.ptr(cos_k),
+                                  N.ptr(sin_k), N.ptr(parents), N.stream_ptr(dev))
+        N.check(rc, "htree_select")
+    return parents, ws
+
+
 def forward_frame(qf, kf, vf, d, cos_k, sin_k, scale, save_parents, keep_scores):
     """The HIP forward on kernel-frame tensors.  cos_k / sin_k: the kernel
     frame's tables.  Returns (out, gmax, gsum, parents | None, layers_k,

@@ -162,6 +162,18 @@ int htree_forward_trace(const htree_dims* d, float scale, const void* q, const v
                         void* out, float* gmax, float* gsum, int32_t* parents, float* level_max,
                         float* level_sum, float* level_out, void* stream);
 
+/* Selection only: every level's parent lists, as htree_forward writes them
+ * into `parents` ([L, B, T, H_kv, top_k] int32, required), with no
+ * accumulation and no output: each query group stops after the last level
+ * that selects.  The same selections as htree_forward's, bit for bit (the
+ * same scoring and select code).  For a backward that replays the selection
+ * instead of keeping the lists.  Replaces the reference's
+ * htree_recompute_selection_kernel (src/parallel.py:1168-1399), launched per
+ * level by _recompute_parents (src/backward.py:881-934). */
+int htree_select(const htree_dims* d, float scale, const void* q, const void* tree_ws,
+                 int64_t tree_ws_bytes, const float* cos_table, const float* sin_table,
+                 int32_t* parents, void* stream);
+
 /* Bytes of the backward workspace (host).  This size lets the backward keep
  * every (entry, tile)'s dS for its dq pass, when that fits a third of the
  * current device's memory (HTREE_DS_BUDGET_MB in the environment overrides

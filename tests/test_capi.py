@@ -148,6 +148,11 @@ def test_null_pointers_rejected_without_launch():
     nb = ctypes.c_int64()
     assert lib.htree_backward_workspace_bytes(ctypes.byref(d), ctypes.byref(nb)) == 0 and nb.value > 0
     assert lib.htree_backward(d, 0.1, *([None] * 7), 0, *([None] * 6), 0, None) == N.HTREE_ENULL
+    # selection only: the lists are its one output, and required
+    fake = 256  # never dereferenced: the checks fail first
+    assert lib.htree_select(d, 0.1, fake, fake, 1 << 40, fake, fake, None, None) == N.HTREE_ENULL
+    assert lib.htree_select(d, 0.1, None, fake, 1 << 40, fake, fake, fake, None) == N.HTREE_ENULL
+    assert lib.htree_select(d, 0.1, fake, fake, 1, fake, fake, fake, None) == N.HTREE_EWORKSPACE
 
 
 def test_workspace_too_small_rejected():

@@ -5,7 +5,8 @@
   (without per_layer_parents) replays the selection with the context's own
   RoPE tables, as src/backward.py:848-934 does;
 * the lean autograd mode (only the reference's eight saved tensors,
-  src/backward.py:1141-1145): the same gradients as the default mode;
+  src/backward.py:1141-1145): the same gradients as the default mode, from
+  the selection-only replay (htree_select), whose lists are the forward's;
 * K != V head dims (src/parallel.py:904, src/naive.py:144): forward and
   backward against the oracle's native two-dim restatement."""
 import numpy as np
@@ -53,8 +54,10 @@ def test_reference_keys_context(with_parents, dtype):
                          f(ctx["global_sum"]), *[f(x) for x in got], tree=tree)
     print(rep, flush=True)
     if not with_parents:
-        # the replay selects the same lists (and keeps the same scores)
-        for a, b in zip(got, full):
+        # the selection-only replay selects the same lists; the backward then
+        # rebuilds the scores, as the full context's does without its stored ones
+        rebuilt = htree_amd.htree_backward(dOd, qd, out, dict(ctx, train_scores=None))
+        for a, b in zip(got, rebuilt):
             assert torch.equal(a, b)
     # the forward at this base is the oracle's at this base, not at 10000
     rows = orc.all_rows(B, T)[::3]
@@ -85,11 +88,15 @@ def test_reference_keys_context_without_max_top_nodes():
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
 def test_lean_autograd_mode(dtype):
     """_save_parents=False keeps the reference's eight tensors and replays
-    the selection in the backward: bitwise the default mode's gradients."""
+    the selection alone in the backward: bitwise the gradients of the default
+    mode's lists with rebuilt scores (bf16 here: the default mode keeps the
+    forward's fp16 scores, so it agrees within the bar; fp16 inputs keep no
+    scores, so there the two agree bitwise)."""
     import htree_amd
 
     B, T, H, Hkv, D, CR, TK, MTN = 1, 2500, 16, 2, 128, 16, 16, 128
     q, k, v, dO = seeded(B, T, H, Hkv, D, D, dtype, 53)
+    dOd = dO.to(DEV)
     grads = []
     for save in (True, False):
         qg, kg, vg = (x.to(DEV).requires_grad_(True) for x in (q, k, v))
@@ -97,11 +104,60 @@ def test_lean_autograd_mode(dtype):
                                                       _save_parents=save)
         n_saved = len(out.grad_fn.saved_tensors)
         assert n_saved == (11 if save else 8), n_saved
-        out.backward(dO.to(DEV))
+        out.backward(dOd)
         torch.cuda.synchronize()
         grads.append((out.detach(), qg.grad, kg.grad, vg.grad))
-    for a, b in zip(*grads):
+    (o0, *g_default), (o1, *g_lean) = grads
+    assert torch.equal(o0, o1)
+    qd, kd, vd = (x.to(DEV) for x in (q, k, v))
+    out, ctx = htree_amd.htree_forward(qd, kd, vd, CR, MTN, TK, rope_base=2000.0,
+                                       _save_for_backward=True)
+    rebuilt = htree_amd.htree_backward(dOd, qd, out, dict(ctx, train_scores=None),
+                                       _grad_dtype=q.dtype)
+    torch.cuda.synchronize()
+    f = lambda x: x.float().cpu().numpy()
+    for a, b, c in zip(g_lean, rebuilt, g_default):
         assert torch.equal(a, b)
+        if ctx["train_scores"] is None:
+            assert torch.equal(a, c)
+        ok, w = close(f(a), f(c), dtype)
+        assert ok, w
+
+
+SELECT_CASES = [
+    # B, T, H, Hkv, D, CR, TK, MTN, dtype, seed: every forward and group form
+    (1, 2500, 16, 2, 128, 16, 16, 128, "bfloat16", 91),   # register forward, 3 levels
+    (1, 3001, 8, 1, 64, 8, 32, 64, "float16", 92),        # streaming forward, 3 levels
+    (1, 3000, 16, 4, 32, 4, 128, 256, "float32", 93),     # wide forward, 3 levels
+    (1, 20000, 8, 2, 32, 16, 1024, 16384, "bfloat16", 94),  # wide, 64 keys per thread
+    (1, 1501, 32, 1, 128, 16, 16, 128, "bfloat16", 95),   # KV-head pairs (register)
+    (1, 2200, 32, 1, 64, 8, 256, 256, "bfloat16", 96),    # KV-head pairs (wide), 3 levels
+    (1, 1500, 64, 1, 32, 4, 64, 64, "bfloat16", 97),      # KV-head quads, 4 levels
+    (1, 1000, 17, 1, 64, 4, 16, 32, "float32", 98),       # padding heads (streaming), 4 levels
+    (1, 1200, 33, 1, 32, 16, 128, 256, "float16", 99),    # quads with padding heads
+    (2, 500, 8, 2, 64, 16, 32, 512, "bfloat16", 100),     # one level: no selection at all
+]
+
+
+@pytest.mark.parametrize("cfg", SELECT_CASES, ids=lambda c: f"G{c[2] // c[3]}D{c[4]}cr{c[5]}tk{c[6]}{c[8]}")
+def test_select_matches_forward_lists(cfg):
+    """htree_select (selection only) writes the forward's parent lists of
+    every level, bit for bit, in every forward form and group layout."""
+    import htree_amd
+    from htree_amd.parallel import select_frame
+
+    B, T, H, Hkv, D, CR, TK, MTN, dtype, seed = cfg
+    print(f"case {cfg}", flush=True)
+    q, k, v, _ = seeded(B, T, H, Hkv, D, D, dtype, seed)
+    qd, kd, vd = (x.to(DEV) for x in (q, k, v))
+    out, ctx = htree_amd.htree_forward(qd, kd, vd, CR, MTN, TK, _save_for_backward=True)
+    hf = ctx["head_frame"]
+    cos_k, sin_k = hf.tables(ctx["cos_cache"], ctx["sin_cache"])
+    sel, _ = select_frame(hf.q_heads(hf.pad_qk(qd)), hf.kv_k(kd), hf.kv_v(vd), ctx["dims"], cos_k,
+                          sin_k, ctx["scale"])
+    torch.cuda.synchronize()
+    assert sel.shape == ctx["parents_stacked"].shape
+    assert torch.equal(sel, ctx["parents_stacked"])
 
 
 KV_CASES = [
