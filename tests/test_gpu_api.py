@@ -132,6 +132,7 @@ SELECT_CASES = [
     (1, 20000, 8, 2, 32, 16, 1024, 16384, "bfloat16", 94),  # wide, 64 keys per thread
     (1, 1501, 32, 1, 128, 16, 16, 128, "bfloat16", 95),   # KV-head pairs (register)
     (1, 2200, 32, 1, 64, 8, 256, 256, "bfloat16", 96),    # KV-head pairs (wide), 3 levels
+    (1, 3001, 32, 1, 128, 32, 32, 256, "bfloat16", 101),  # KV-head pairs (streaming)
     (1, 1500, 64, 1, 32, 4, 64, 64, "bfloat16", 97),      # KV-head quads, 4 levels
     (1, 1000, 17, 1, 64, 4, 16, 32, "float32", 98),       # padding heads (streaming), 4 levels
     (1, 1200, 33, 1, 32, 16, 128, 256, "float16", 99),    # quads with padding heads
