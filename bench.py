@@ -1,6 +1,6 @@
 """Benchmark of the htree hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C2] [--no-cpu] [--no-lean]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C2] [--no-cpu] [--no-modes]
 
 Other workloads (--workload): C3, C4, C5, REF_FWD (the
 reference's speed_test.py defaults: T=120000, Hq=64, Hkv=4, D=32, fp32, CR=16,
@@ -12,27 +12,32 @@ Workload ("C2"): B=1, T=32768, Hq=32, Hkv=2 (group
 on the host from a fixed seed and copied to HBM before timing.
 
 A step is what the reference's speed_test_bwd.py times: the autograd
-forward (`htree_forward_triton_autograd`: tree build + fused kernel, keeping
-what the backward reads) and `out.backward(dO)`, gradients in the input
-dtype, with q/k/v's gradients cleared before each step; forward-only
-workloads step `htree_forward`.  `value` = B*T / wall-clock step time over
+forward (`htree_forward_triton_autograd`: tree build + fused kernel) and
+`out.backward(dO)`, gradients in the input dtype, with q/k/v's gradients
+cleared before each step; forward-only workloads step `htree_forward`.  The
+autograd mode is the drop-in's default: it keeps the reference's eight
+tensors plus the parent lists and the packed tree
+(`saved_bytes_beyond_reference`), so the backward replays no selection and
+rebuilds the candidate scores.  `value` = B*T / wall-clock step time over
 the timed steps (tokens/s); `fwd` / `bwd` split each step with HIP events
-(speed_test_bwd.py:109-123).  `lean` repeats the measurement (up to 10
-steps) in the lean autograd mode (`_save_parents=False`: only the
-reference's eight tensors kept; the backward rebuilds the tree and replays
-the selection); `saved_bytes_beyond_reference` is what the default mode
-keeps per call beyond them.  The roofline object is for the
-dominant kernel (the fused forward), timed with HIP events on the stream it
-runs on, against the gathered-bytes model in htree_amd/workmodel.py.
+(speed_test_bwd.py:109-123).  `modes` repeats the measurement (up to 10
+steps) in the two other autograd modes: `scores` (`_save_scores=True`: the
+candidate scores kept too, the backward reads them) and `lean`
+(`_save_parents=False`: the reference's eight tensors only; the backward
+rebuilds the tree and replays the selection).  The roofline object is for
+the largest kernel (the fused forward), timed with HIP events on the stream
+it runs on, against the gathered-bytes model in htree_amd/workmodel.py.
 The CPU baseline times the CPU restatement of src/naive.py (oracle/, C on
 every host core up to 16) on a bounded random sample of the same workload's
-query rows, and, as cpu_baseline.c1, on the whole of the CPU config C1
-(forward and backward, median of 3); it is a reported baseline only.
+query rows: their whole forward and their whole backward (dq and the dK/dV
+of every candidate they accumulate), and, as cpu_baseline.c1, the whole of
+the CPU config C1 (forward and backward, median of 3); it is a reported
+baseline only.
 
-After those, the default C2 run measures C3, C4, C5 and REF_BWD briefly
-(inputs drawn on the GPU, 2 warm-up + 3 timed steps, forward / backward /
-bare-kernel times with HIP events) into `other_workloads` of the same line;
-`--also ''` skips them.
+After those, the default C2 run measures C3, C4, C5 and REF_BWD (inputs
+drawn on the GPU, 2 warm-up + 20 timed steps, 10 for C4; forward /
+backward / bare-kernel times with HIP events) into `other_workloads` of the
+same line; `--also ''` skips them.
 """
 from __future__ import annotations
 
@@ -106,8 +111,9 @@ def host_threads() -> int:
 def cpu_baseline(q, k, v, dO, out, gmax, gsum, parents, CR, TK, MTN, dtype, budget_s=10.0):
     """Oracle (CPU restatement of src/naive.py, C, on host_threads() threads)
     on random query rows of the workload until `budget_s` seconds of forward
-    work have run, then the same rows through the backward's per-row (dq)
-    work."""
+    work have run, then the same rows through the whole backward
+    (src/naive.py:320-386 for those rows: dq, and the dK / dV of every
+    candidate they accumulate scattered into the per-level gradients)."""
     import numpy as np
 
     from oracle import oracle as orc
@@ -139,8 +145,8 @@ def cpu_baseline(q, k, v, dO, out, gmax, gsum, parents, CR, TK, MTN, dtype, budg
         parts = orc.split_rows(np.arange(len(rows)), th)
         t0 = time.perf_counter()
         with ThreadPoolExecutor(len(parts)) as ex:
-            list(ex.map(lambda i: orc.backward_dq_rows(qn, tree, D ** -0.5, rows[i], par[:, i], gm[i],
-                                                       gs[i], delta[i], d[i]), parts))
+            list(ex.map(lambda i: orc.backward_rows(qn, tree, D ** -0.5, rows[i], par[:, i], gm[i],
+                                                    gs[i], delta[i], d[i], with_dkv=False), parts))
         t_bwd = time.perf_counter() - t0
         res.update(bwd_tok_s=len(rows) / t_bwd, bwd_s=t_bwd)
     return res
@@ -214,15 +220,27 @@ def make_inputs(workload, dev, on_gpu=False):
     return q, k, v, dO, data
 
 
-def measure(workload, q, k, v, dO, steps, warmup, kernel_iters, lean_steps=0):
+MODES = {
+    # autograd mode: (htree_forward_triton_autograd keyword arguments, what it keeps)
+    "default": ({}, "the reference's eight tensors + the parent lists and the packed tree; "
+                    "the backward rebuilds the candidate scores"),
+    "scores": ({"_save_scores": True}, "the default's tensors + every candidate tile's scores; "
+                                       "the backward reads them"),
+    "lean": ({"_save_parents": False}, "the reference's eight tensors only; the backward rebuilds "
+                                       "the tree and replays the selection"),
+}
+
+
+def measure(workload, q, k, v, dO, steps, warmup, kernel_iters, mode_steps=0):
     """Times `steps` steps (wall clock, after `warmup`), with HIP events
     around each step's forward and backward (speed_test_bwd.py:109-123),
-    then `kernel_iters` bare launches of the fused forward kernel with HIP
-    events on their stream.  A training step is the autograd forward
-    (`htree_forward_triton_autograd`, which keeps what the backward reads)
-    and `out.backward(dO)` with the gradients of q, k, v cleared first, as
-    the reference's speed_test_bwd.py times it.  Returns the figures and a
-    forward's output and context."""
+    then `mode_steps` steps in each other autograd mode, then `kernel_iters`
+    bare launches of the fused forward kernel with HIP events on their
+    stream.  A training step is the autograd forward
+    (`htree_forward_triton_autograd`, default mode) and `out.backward(dO)`
+    with the gradients of q, k, v cleared first, as the reference's
+    speed_test_bwd.py times it.  Returns the figures and a forward's output
+    and context."""
     import torch
 
     import htree_amd
@@ -237,7 +255,7 @@ def measure(workload, q, k, v, dO, steps, warmup, kernel_iters, lean_steps=0):
     stream = torch.cuda.current_stream(dev)
     ev = lambda: torch.cuda.Event(enable_timing=True)
 
-    def step(marks=None, lean=False):
+    def step(marks=None, mode="default"):
         if marks:
             marks[0].record(stream)
         if not has_bwd:  # forward only (speed_test.py): nothing kept for a backward
@@ -246,42 +264,41 @@ def measure(workload, q, k, v, dO, steps, warmup, kernel_iters, lean_steps=0):
                 marks[1].record(stream)
             return
         q.grad = k.grad = v.grad = None
-        out = htree_amd.htree_forward_triton_autograd(q, k, v, CR, MTN, TK,
-                                                      _save_parents=not lean)
+        out = htree_amd.htree_forward_triton_autograd(q, k, v, CR, MTN, TK, **MODES[mode][0])
         if marks:
             marks[1].record(stream)
         out.backward(dO)
         if marks:
             marks[2].record(stream)
 
-    def timed(steps, warmup, lean=False):
+    def timed(steps, warmup, mode="default"):
         for _ in range(warmup):
-            step(lean=lean)
+            step(mode=mode)
         torch.cuda.synchronize()
         marks = [[ev(), ev(), ev()] for _ in range(steps)]
         t0 = time.perf_counter()
         for i in range(steps):
-            step(marks[i], lean)
+            step(marks[i], mode)
         torch.cuda.synchronize()
         step_ms = (time.perf_counter() - t0) * 1e3 / steps
         fwd_ms = sum(m[0].elapsed_time(m[1]) for m in marks) / steps
         bwd_ms = sum(m[1].elapsed_time(m[2]) for m in marks) / steps if has_bwd else None
-        print(f"# {workload}{' (lean)' if lean else ''}: timed {steps} steps: {step_ms:.3f} ms/step "
+        print(f"# {workload} ({mode} mode): timed {steps} steps: {step_ms:.3f} ms/step "
               f"(forward {fwd_ms:.3f} ms" + (f", backward {bwd_ms:.3f} ms" if has_bwd else "") + ")",
               file=sys.stderr, flush=True)
         return step_ms, fwd_ms, bwd_ms
 
     step_ms, fwd_ms, bwd_ms = timed(steps, warmup)
-    # the lean autograd mode (saves only the reference's eight tensors; the
-    # backward rebuilds the tree and replays the selection), after the above
-    lean = None
-    if has_bwd and lean_steps:
-        lean = dict(zip(("step_ms", "fwd_ms", "bwd_ms"), timed(lean_steps, 2, lean=True)))
+    # the other autograd modes, after the above
+    modes = {}
+    if has_bwd and mode_steps:
+        for mode in ("scores", "lean"):
+            modes[mode] = dict(zip(("step_ms", "fwd_ms", "bwd_ms"), timed(mode_steps, 2, mode)))
 
     # the fused forward kernel alone, with HIP events
     with torch.no_grad():
         out, ctx = htree_amd.htree_forward(q.detach(), k.detach(), v.detach(), CR, MTN, TK,
-                                           _save_for_backward=True)
+                                           _save_for_backward=True, _save_scores=has_bwd)
     q = q.detach()
     d = ctx["dims"]
     ws = ctx["packed_tree"]
@@ -300,13 +317,14 @@ def measure(workload, q, k, v, dO, steps, warmup, kernel_iters, lean_steps=0):
     torch.cuda.synchronize()
     kern_ms = k0.elapsed_time(k1) / kernel_iters
     w = work(B, T, H, Hkv, D, CR, TK, MTN, getattr(torch, dtype).itemsize)
-    saved = None
-    if has_bwd:  # bytes the default mode keeps per call beyond the reference's eight tensors
-        saved = sum(t.numel() * t.element_size() for t in
-                    (ctx["parents_stacked"], ctx["packed_tree"], ctx.get("train_scores"))
-                    if t is not None)
+    saved = {}
+    if has_bwd:  # bytes each mode keeps per call beyond the reference's eight tensors
+        nb = lambda t: 0 if t is None else t.numel() * t.element_size()
+        saved["default"] = nb(ctx["parents_stacked"]) + nb(ctx["packed_tree"])
+        saved["scores"] = saved["default"] + nb(ctx.get("train_scores"))
+        saved["lean"] = 0
     return dict(has_bwd=has_bwd, step_ms=step_ms, fwd_ms=fwd_ms, bwd_ms=bwd_ms, kern_ms=kern_ms,
-                work=w, out=out, ctx=ctx, lean=lean, saved_bytes=saved)
+                work=w, out=out, ctx=ctx, modes=modes, saved_bytes=saved)
 
 
 def main():
@@ -317,11 +335,11 @@ def main():
     ap.add_argument("--workload", default="C2", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--kernel-iters", type=int, default=20)
-    ap.add_argument("--no-lean", action="store_true",
-                    help="skip the lean autograd mode's measurement")
+    ap.add_argument("--no-modes", action="store_true",
+                    help="skip the other autograd modes' measurement")
     ap.add_argument("--also", default=None,
-                    help="comma-separated workloads measured briefly after the main one "
-                         "(3 steps each; default for C2: C3,C4,C5,REF_BWD; '' for none)")
+                    help="comma-separated workloads measured after the main one "
+                         "(20 steps each, 10 for C4; default for C2: C3,C4,C5,REF_BWD; '' for none)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported in this build "
@@ -344,7 +362,7 @@ def main():
     print(f"# workload {args.workload} B={B} T={T} H={H} Hkv={Hkv} D={D} {dtype} CR={CR} TK={TK} "
           f"MTN={MTN}", file=sys.stderr, flush=True)
     m = measure(args.workload, q, k, v, dO, args.steps, args.warmup, args.kernel_iters,
-                lean_steps=min(args.steps, 10) if not args.no_lean else 0)
+                mode_steps=min(args.steps, 10) if not args.no_modes else 0)
     has_bwd, fwd_ms, bwd_ms, kern_ms, w = m["has_bwd"], m["fwd_ms"], m["bwd_ms"], m["kern_ms"], m["work"]
     out, ctx = m["out"], m["ctx"]
 
@@ -381,6 +399,7 @@ def main():
                         f"causal CR={CR} MTN={MTN} TK={TK}",
             "step": ("htree_forward_triton_autograd + out.backward(dO)" if has_bwd
                      else "htree_forward"),
+            "autograd_mode": "default: " + MODES["default"][1] if has_bwd else None,
         },
         "fwd": {"ms": fwd_ms, "tokens_per_s": fwd_tok,
                 "hbm_roofline_frac": w.fwd_bytes / (fwd_ms * 1e-3) / HBM_PEAK,
@@ -390,13 +409,17 @@ def main():
             "hbm_roofline_frac": w.bwd_bytes / (bwd_ms * 1e-3) / HBM_PEAK,
             "algorithmic_bytes": w.bwd_bytes},
         "event_ms_per_step": fwd_ms + (bwd_ms or 0.0),
-        "saved_bytes_beyond_reference": m["saved_bytes"],
-        "lean": None if not m["lean"] else {
-            "mode": "htree_forward_triton_autograd(..., _save_parents=False): saves the reference's "
-                    "eight tensors only; the backward rebuilds the tree and replays the selection",
-            "ms_per_step": m["lean"]["step_ms"], "tokens_per_s": B * T / (m["lean"]["step_ms"] * 1e-3),
-            "fwd_ms": m["lean"]["fwd_ms"], "bwd_ms": m["lean"]["bwd_ms"],
-            "saved_bytes_beyond_reference": 0},
+        "saved_bytes_beyond_reference": m["saved_bytes"].get("default"),
+        "modes": {
+            mode: {
+                "call": "htree_forward_triton_autograd(..., "
+                        + ", ".join(f"{a}={b}" for a, b in MODES[mode][0].items()) + ")",
+                "keeps": MODES[mode][1],
+                "ms_per_step": r["step_ms"], "tokens_per_s": B * T / (r["step_ms"] * 1e-3),
+                "fwd_ms": r["fwd_ms"], "bwd_ms": r["bwd_ms"],
+                "bwd_hbm_roofline_frac": w.bwd_bytes / (r["bwd_ms"] * 1e-3) / HBM_PEAK,
+                "saved_bytes_beyond_reference": m["saved_bytes"][mode]}
+            for mode, r in m["modes"].items()} or None,
         "roofline": {
             "kernel": f"htree::{forward_kernel(args.workload)} (fused forward, all levels)",
             "bound": "hbm",
@@ -417,8 +440,9 @@ def main():
         res["cpu_baseline"] = {
             "value": tot, "unit": "tokens/s", "cores": cb["threads"], "kind": "port",
             "sample": f"{cb['fwd_rows']} random query rows (b,t) of {args.workload} through the "
-                      f"oracle's forward ({cb['fwd_s']:.1f} s)"
-                      + (f" and backward per-row (dq) work ({cb['bwd_s']:.1f} s)" if "bwd_s" in cb else "")
+                      f"oracle's whole forward ({cb['fwd_s']:.1f} s)"
+                      + (f" and whole backward (dq, and the dK/dV of every candidate they "
+                         f"accumulate, {cb['bwd_s']:.1f} s)" if "bwd_s" in cb else "")
                       + f", {cb['threads']} host threads; host CPU: {cpu_model()}, "
                       f"os.cpu_count()={os.cpu_count()}",
             "fwd_tokens_per_s": cb["fwd_tok_s"],
@@ -436,13 +460,14 @@ def main():
     for wl in also:
         (B2, T2, H2, Hkv2, D2, CR2, TK2, MTN2), dt2, _ = WORKLOADS[wl]
         q2, k2, v2, dO2, data2 = make_inputs(wl, dev, on_gpu=True)
-        m2 = measure(wl, q2, k2, v2, dO2, steps=3, warmup=2, kernel_iters=3)
+        n2 = 10 if wl == "C4" else 20
+        m2 = measure(wl, q2, k2, v2, dO2, steps=n2, warmup=2, kernel_iters=3)
         w2 = m2["work"]
         res["other_workloads"][wl] = {
             "config": f"B={B2} T={T2} Hq={H2} Hkv={Hkv2} D={D2} {DT_SHORT[dt2]} CR={CR2} MTN={MTN2} "
                       f"TK={TK2}",
             "data": data2,
-            "steps": 3, "warmup": 2,
+            "steps": n2, "warmup": 2,
             "tokens_per_s": B2 * T2 / (m2["step_ms"] * 1e-3),
             "fwd_ms": m2["fwd_ms"],
             "fwd_hbm_roofline_frac": w2.fwd_bytes / (m2["fwd_ms"] * 1e-3) / HBM_PEAK,

@@ -12,14 +12,22 @@ context's own RoPE tables (`cos_cache`, `sin_cache`), as the reference's
 its operand tree rebuilt from `layers_k[0]` / `layers_v[0]` with those same
 tables (src/backward.py:848-878).
 
-Two autograd modes:
-  * default: the Function saves the parent lists, the packed tree and (bf16
-    configurations with <= 16 candidate tiles per level) the candidate
-    scores, so the backward replays nothing;
-  * `_save_parents=False` (htree_forward_triton_autograd): the Function
-    saves only the reference's eight tensors (q, k, v, out, global max / sum,
-    cos / sin, src/backward.py:1141-1145); the backward rebuilds the tree,
-    replays the selection alone and rebuilds the scores.
+Three autograd modes (htree_forward_triton_autograd):
+  * default: the Function saves the reference's eight tensors (q, k, v, out,
+    global max / sum, cos / sin, src/backward.py:1141-1145) plus the parent
+    lists and the packed operand tree (C2: 13 MB + 54 MB), so the backward
+    replays no selection and rebuilds only the candidate scores;
+  * `_save_scores=True`: also the candidate scores (bf16 configurations with
+    <= 16 candidate tiles per level; C2: 1.6 GB), so the backward reads them
+    instead of rebuilding them;
+  * `_save_parents=False`: the reference's eight tensors only; the backward
+    rebuilds the tree, replays the selection alone and rebuilds the scores.
+
+Workspace: the backward keeps every entry's dS for the dq pass when the
+stored-dS workspace fits what the device can spare (free memory plus what
+torch's caching allocator holds unused, less a margin); otherwise it runs in
+the smallest workspace and dq recomputes the scores.  The plan taken is
+written into the context under `backward_plan`.
 """
 from __future__ import annotations
 
@@ -79,8 +87,47 @@ def infer_max_top_nodes(T: int, CR: int, TK: int, L: int) -> int:
     return 1 << max(0, (n - 1).bit_length())
 
 
+# memory left free on the device after the backward's workspace: the larger
+# of 2 GiB and 5% of the device
+WORKSPACE_MARGIN_FRACTION = 0.05
+WORKSPACE_MARGIN_MIN = 2 << 30
+
+
+def spare_device_bytes(device) -> int:
+    """Bytes a workspace can take on `device`: free device memory plus what
+    torch's caching allocator holds without using, less the margin."""
+    free, total = torch.cuda.mem_get_info(device)
+    idle = torch.cuda.memory_reserved(device) - torch.cuda.memory_allocated(device)
+    margin = max(WORKSPACE_MARGIN_MIN, int(WORKSPACE_MARGIN_FRACTION * total))
+    return max(0, free + idle - margin)
+
+
+def backward_workspace(d, device, limit: Optional[int] = None):
+    """Allocates the backward's workspace: the stored-dS plan where it fits
+    `limit` bytes (default: what the device can spare), else the smallest
+    plan (dq recomputes the scores).  Returns (workspace, plan name)."""
+    nb = N.ctypes.c_int64()
+    N.check(N.lib().htree_backward_workspace_bytes(N.ctypes.byref(d), N.ctypes.byref(nb)),
+            "htree_backward_workspace_bytes")
+    full = nb.value
+    N.check(N.lib().htree_backward_workspace_min_bytes(N.ctypes.byref(d), N.ctypes.byref(nb)),
+            "htree_backward_workspace_min_bytes")
+    small = nb.value
+    if limit is None:
+        limit = spare_device_bytes(device)
+    if full > small and full <= limit:
+        try:
+            return torch.empty(full, dtype=torch.uint8, device=device), "stored_ds"
+        except torch.OutOfMemoryError:
+            pass
+    # (full == small: the configuration has no stored-dS plan: top_k > 64,
+    # CR 128, or dS beyond the library's own cap of a third of the device)
+    return torch.empty(small, dtype=torch.uint8, device=device), "recompute"
+
+
 def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_ctx: dict,
-                   _grad_dtype: Optional[torch.dtype] = None):
+                   _grad_dtype: Optional[torch.dtype] = None,
+                   _workspace_limit: Optional[int] = None):
     """Gradients of the htree forward wrt q, k, v (fp32 unless `_grad_dtype`),
     selection fixed.
 
@@ -88,7 +135,9 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
     (src/backward.py:966-967), so the two agree when dO comes in q's dtype,
     as autograd hands it.  `_grad_dtype` (the autograd path's input dtype)
     has the kernels round the fp32 gradients into that dtype as they store
-    them: the values `.to(_grad_dtype)` of the fp32 results would give."""
+    them: the values `.to(_grad_dtype)` of the fp32 results would give.
+    `_workspace_limit` caps the workspace in bytes (default: what the device
+    can spare)."""
     B, T, H, K = q.shape
     layers_k, layers_v = bwd_ctx["layers_k"], bwd_ctx["layers_v"]
     k, v = layers_k[0], layers_v[0]
@@ -120,14 +169,21 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
     parents = bwd_ctx.get("parents_stacked")
     plp = bwd_ctx.get("per_layer_parents")
     # per_layer_parents (what the reference reads) are views of the forward's
-    # stacked lists; a caller that replaced them gets its own lists
+    # stacked lists.  Lists a caller replaced, or edited in place (views
+    # share their base's version counter), are the caller's own: checked,
+    # copied to every KV-head copy, and without the forward's stored scores.
+    own = parents is not None and parents._version == bwd_ctx.get("parents_version",
+                                                                   parents._version)
     if parents is not None and plp is not None and any(
             plp[l].data_ptr() != parents[l].data_ptr() for l in range(L)):
-        parents = None
+        own, parents = False, None
     # the training forward's stored scores go with its own parent lists
-    scores = bwd_ctx.get("train_scores") if parents is not None else None
-    if parents is None and plp is not None:
+    scores = bwd_ctx.get("train_scores") if own else None
+    if not own and plp is not None:
         parents = _stack_parents(plp, L)
+    elif not own and parents is not None:
+        parents = hf.pick(parents, 3).contiguous()
+    if not own and parents is not None:
         _check_parents(parents, B, T, H_kv, TK, CR, MTN, dev)
         parents = hf.dup(parents, 3)
     if parents is None:
@@ -153,17 +209,9 @@ def htree_backward(dO: torch.Tensor, q: torch.Tensor, output: torch.Tensor, bwd_
     dq = torch.empty(B, T, qf.shape[2], D, **g)
     dk = torch.empty(B, T, H_kv * hf.share, D, **g)
     dv = torch.empty_like(dk)
-    nb = N.ctypes.c_int64()
-    N.check(N.lib().htree_backward_workspace_bytes(N.ctypes.byref(d), N.ctypes.byref(nb)),
-            "htree_backward_workspace_bytes")
-    try:
-        bws = torch.empty(nb.value, dtype=torch.uint8, device=dev)
-    except torch.OutOfMemoryError:
-        # no room for the stored dS: the smallest workspace, dq recomputes
-        N.check(N.lib().htree_backward_workspace_min_bytes(N.ctypes.byref(d), N.ctypes.byref(nb)),
-                "htree_backward_workspace_min_bytes")
-        bws = torch.empty(nb.value, dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
+        bws, plan = backward_workspace(d, dev, _workspace_limit)
+        bwd_ctx["backward_plan"] = plan
         if scores is not None:
             rc = N.lib().htree_backward_train(
                 d, float(scale), N.ptr(qf), N.ptr(outf), N.ptr(dOf), N.ptr(gmax),
@@ -186,34 +234,61 @@ _REF_META = ("num_layers", "compression_rate", "top_k_per_layer", "max_top_nodes
              "rope_base", "NUM_GROUPS", "G_PAD", "TILE_P", "DROP_BLOCK")
 
 
+def _save_forward(ctx, q, k, v, compression_rate, max_top_nodes, top_k_per_layer, scale,
+                  rope_base, save_scores):
+    out, bwd_ctx = htree_forward(q, k, v, compression_rate=compression_rate,
+                                 max_top_nodes=max_top_nodes, top_k_per_layer=top_k_per_layer,
+                                 scale=scale, rope_base=rope_base, _save_for_backward=True,
+                                 _save_parents=True, _save_scores=save_scores)
+    ctx.save_for_backward(q, k, v, out, bwd_ctx["global_max"], bwd_ctx["global_sum"],
+                          bwd_ctx["cos_cache"], bwd_ctx["sin_cache"],
+                          bwd_ctx["parents_stacked"], bwd_ctx["packed_tree"],
+                          bwd_ctx["train_scores"])
+    ctx.meta = {key: bwd_ctx[key] for key in _REF_META}
+    ctx.meta.update(dims=bwd_ctx["dims"], head_frame=bwd_ctx["head_frame"])
+    return out
+
+
+def _saved_backward(ctx, dO):
+    q, k, v, out, gmax, gsum, cos, sin, parents, ws, scores = ctx.saved_tensors
+    bwd_ctx = dict(ctx.meta, global_max=gmax, global_sum=gsum, layers_k=[k], layers_v=[v],
+                   cos_cache=cos, sin_cache=sin, parents_stacked=parents,
+                   parents_version=parents._version, per_layer_parents=None, packed_tree=ws,
+                   train_scores=scores)
+    dq, dk, dv = htree_backward(dO, q, out, bwd_ctx, _grad_dtype=q.dtype)
+    return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None
+
+
 class HTreeTritonFunction(torch.autograd.Function):
     """Autograd contract of the reference (src/backward.py:1126-1193): grads
     in the input dtypes and None for the five non-tensor arguments.  Saves
-    the parent lists, the packed tree and the candidate scores, so that the
-    backward replays nothing."""
+    the reference's eight tensors plus the parent lists and the packed
+    operand tree (C2: 67 MB beyond the eight), so that the backward replays
+    no selection; it rebuilds the candidate scores."""
 
     @staticmethod
     def forward(ctx, q, k, v, compression_rate, max_top_nodes, top_k_per_layer, scale, rope_base):
-        out, bwd_ctx = htree_forward(q, k, v, compression_rate=compression_rate,
-                                     max_top_nodes=max_top_nodes, top_k_per_layer=top_k_per_layer,
-                                     scale=scale, rope_base=rope_base, _save_for_backward=True,
-                                     _save_parents=True)
-        ctx.save_for_backward(q, k, v, out, bwd_ctx["global_max"], bwd_ctx["global_sum"],
-                              bwd_ctx["cos_cache"], bwd_ctx["sin_cache"],
-                              bwd_ctx["parents_stacked"], bwd_ctx["packed_tree"],
-                              bwd_ctx["train_scores"])
-        ctx.meta = {key: bwd_ctx[key] for key in _REF_META}
-        ctx.meta.update(dims=bwd_ctx["dims"], head_frame=bwd_ctx["head_frame"])
-        return out
+        return _save_forward(ctx, q, k, v, compression_rate, max_top_nodes, top_k_per_layer, scale,
+                             rope_base, False)
 
     @staticmethod
     def backward(ctx, dO):
-        q, k, v, out, gmax, gsum, cos, sin, parents, ws, scores = ctx.saved_tensors
-        bwd_ctx = dict(ctx.meta, global_max=gmax, global_sum=gsum, layers_k=[k], layers_v=[v],
-                       cos_cache=cos, sin_cache=sin, parents_stacked=parents,
-                       per_layer_parents=None, packed_tree=ws, train_scores=scores)
-        dq, dk, dv = htree_backward(dO, q, out, bwd_ctx, _grad_dtype=q.dtype)
-        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None
+        return _saved_backward(ctx, dO)
+
+
+class HTreeScoresFunction(torch.autograd.Function):
+    """HTreeTritonFunction that also keeps every candidate tile's scores
+    (bf16 configurations with <= 16 candidate tiles per level; C2: 1.6 GB),
+    so that the backward reads them instead of rebuilding them."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, compression_rate, max_top_nodes, top_k_per_layer, scale, rope_base):
+        return _save_forward(ctx, q, k, v, compression_rate, max_top_nodes, top_k_per_layer, scale,
+                             rope_base, True)
+
+    @staticmethod
+    def backward(ctx, dO):
+        return _saved_backward(ctx, dO)
 
 
 class HTreeLeanFunction(torch.autograd.Function):
@@ -248,15 +323,21 @@ HTreeFunction = HTreeTritonFunction
 def htree_forward_triton_autograd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                   compression_rate: int = 16, max_top_nodes: int = 8192,
                                   top_k_per_layer: int = 512, scale: Optional[float] = None,
-                                  rope_base: float = 10000.0, _save_parents: bool = True
-                                  ) -> torch.Tensor:
+                                  rope_base: float = 10000.0, _save_parents: bool = True,
+                                  _save_scores: bool = False) -> torch.Tensor:
     """Differentiable htree forward (name of src/backward.py:1196 kept for
-    drop-in use; the kernels are the HIP ones).  `_save_parents=False`
-    selects the lean mode (HTreeLeanFunction): only the reference's eight
-    tensors are kept between forward and backward."""
+    drop-in use; the kernels are the HIP ones).  Default: the reference's
+    eight tensors plus the parent lists and the packed tree are kept between
+    forward and backward (HTreeTritonFunction).  `_save_scores=True` also
+    keeps the candidate scores (HTreeScoresFunction, faster backward);
+    `_save_parents=False` keeps only the eight tensors (HTreeLeanFunction:
+    the backward replays the selection)."""
     if scale is None:
         scale = q.shape[-1] ** -0.5
-    fn = HTreeTritonFunction if _save_parents else HTreeLeanFunction
+    if not _save_parents:
+        fn = HTreeLeanFunction
+    else:
+        fn = HTreeScoresFunction if _save_scores else HTreeTritonFunction
     return fn.apply(q.contiguous(), k.contiguous(), v.contiguous(), compression_rate, max_top_nodes,
                     top_k_per_layer, scale, rope_base)
 

@@ -71,10 +71,14 @@ struct BwdPlan {
   // or every top node up to t's when the top level keeps all of them) is
   // viewed with 64-child parents (vcr = 64, four 16-child tiles, vm real
   // parents each), so each query is staged once per 64 children instead of
-  // once per CR.  Used with the training forward's stored scores.
+  // once per CR.
   int vcr[HTREE_MAX_LEVELS], vlg[HTREE_MAX_LEVELS], vtpp[HTREE_MAX_LEVELS], vm[HTREE_MAX_LEVELS];
   int vlevel;
   int64_t off_vlist;                   // the merged level's lists [B,T,H_kv,TK]
+  // the merged level's K~ rows (hi, lo) turned from the angle of the node's
+  // child index (node mod CR) to that of its index in the 64-child parent
+  // (node mod 64), for a backward that rebuilds the scores (or -1)
+  int64_t off_vk[2];
   // stored-dS path: each level's piece offsets / table / count of its own,
   // so that every level's index can be built ahead of the dK / dV passes
   int64_t off_lpoff[HTREE_MAX_LEVELS], off_lptab[HTREE_MAX_LEVELS], off_lnp[HTREE_MAX_LEVELS];
@@ -84,8 +88,11 @@ struct BwdPlan {
 
 // allow_ds = false: the plan without the stored dS (dq recomputes the scores),
 // the smallest workspace the backward runs in.  view = true: the merged
-// top level where it applies (stored scores and stored dS required).
-static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true, bool view = false) {
+// top level where it applies (stored dS required; with scores = true, for a
+// backward that reads the training forward's stored scores, which adds the
+// conditions of their tile index).
+static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true, bool view = false,
+                         bool scores = false) {
   memset(b, 0, sizeof(*b));
   int rc = make_plan(d, &b->P);
   if (rc) return rc;
@@ -95,6 +102,7 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true, 
   b->tpp = CR > 16 ? CR / 16 : 1;
   b->W = (d->T + 31) / 32;
   b->vlevel = -1;
+  b->off_vk[0] = b->off_vk[1] = -1;
   const int64_t BH = (int64_t)d->B * d->H_kv;
   for (int l = 0; l < P.L; ++l) {
     b->vcr[l] = CR;
@@ -154,12 +162,16 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true, 
   if (const char* e = getenv("HTREE_DS_BUDGET_MB")) budget = (int64_t)atoll(e) << 20;
   // (CR 128: the per-entry maps carry 64 children, so dq recomputes)
   b->use_ds = allow_ds && !P.wide && CR <= 64 && ds_total <= budget;
-  // the merged top level (stored scores: bf16, <= 16 tiles per level)
+  // the merged top level: CR 16 or 32 (whole real parents per 64-child
+  // parent), a level of more than one parent, and RoPE rows for every child
+  // index below 64 (the final R^-1(dK~, node mod 64))
   const int Ltop = (P.L > 1 && P.N[P.L - 1] <= d->top_k) ? P.L - 2 : P.L - 1;
-  // (a merged entry's four tiles index the stored scores of tiles 4 s' .. 4 s' + 3
-  // of the query: they must lie within the query's max_tiles)
-  if (view && b->use_ds && !P.precise && P.max_tiles <= 16 && (CR == 16 || CR == 32) &&
-      P.N[Ltop] > CR && 4 * ((P.N[Ltop] + 63) / 64) <= P.max_tiles) {
+  bool vok = (CR == 16 || CR == 32) && P.N[Ltop] > CR && d->rope_rows >= 64;
+  // stored scores (bf16, <= 16 tiles per level): a merged entry's four tiles
+  // index the stored scores of tiles 4 s' .. 4 s' + 3 of the query, which
+  // must lie within the query's max_tiles
+  if (scores) vok = vok && !P.precise && P.max_tiles <= 16 && 4 * ((P.N[Ltop] + 63) / 64) <= P.max_tiles;
+  if (view && b->use_ds && vok) {
     b->vlevel = Ltop;
     b->vcr[Ltop] = 64;
     b->vlg[Ltop] = 6;
@@ -199,6 +211,8 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true, 
   b->off_npieces = take(4);
   b->off_ptab = take(b->max_pieces * 3 * 4);
   b->off_vlist = b->vlevel >= 0 ? take(b->max_entries * 4) : -1;
+  if (b->vlevel >= 0)
+    for (int s = 0; s < 2; ++s) b->off_vk[s] = take(BH * P.Np[b->vlevel] * d->D * 2);
   b->off_rech = CR > 64 ? take(b->max_entries * 8) : -1;
   for (int l = 0; l < P.L; ++l) {
     const int64_t np = (b->ent[l] + b->piece[l] - 1) / b->piece[l] + b->rows[l];
@@ -219,12 +233,13 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true, 
 }
 
 // Workspace for the stored-dS backward, with or without the merged top
-// level (the call takes the merged plan when it gets stored scores).
+// level (the call takes the merged plan where it applies; the plan for
+// rebuilt scores applies wherever the one for stored scores does).
 static int bwd_full_bytes(const htree_dims* d, int64_t* bytes) {
   BwdPlan a, m;
   int rc = make_bwd_plan(d, &a, true, false);
   if (rc) return rc;
-  rc = make_bwd_plan(d, &m, true, true);
+  rc = make_bwd_plan(d, &m, true, true, false);
   if (rc) return rc;
   *bytes = a.bytes > m.bytes ? a.bytes : m.bytes;
   return HTREE_OK;
@@ -433,6 +448,32 @@ __global__ __launch_bounds__(256) void pack_kt16_kernel(const uint16_t* __restri
   for (int i = 0; i < PER; ++i)
     kt[blk * 16 * D + i * 64 + lane] = __builtin_bit_cast(uint16_t, (_Float16)__builtin_amdgcn_ldexpf(x[i], -e));
   if (lane == 0) kexp[blk] = e;
+}
+
+// The merged level's K~ rows for a backward that rebuilds its scores: the
+// packed tree holds R(K, node mod CR); a 64-child parent's tile w (children
+// 16 w .. 16 w + 15) is scored with its entry's one rotation row, so its
+// rows are turned on by the angle CR * ((node / CR) mod (64 / CR)) into
+// R(K, node mod 64) (rotations compose by adding angles).  The sum hi + lo
+// is exact in fp32; the turned value is split again into hi + lo.  One
+// thread per (bh, node, RoPE pair i); padding rows stay zero.
+__global__ __launch_bounds__(256) void pack_vrot_kernel(
+    const uint16_t* __restrict__ kh, const uint16_t* __restrict__ kl, int64_t Np, int D, int crlg,
+    int vmask, const float* __restrict__ cosb, const float* __restrict__ sinb, int64_t total,
+    uint16_t* __restrict__ oh, uint16_t* __restrict__ ol) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int half = D / 2;
+  const int i = (int)(idx % half);
+  const int64_t r = idx / half;  // bh * Np + node
+  const int64_t node = r % Np;
+  const int64_t a = ((node >> crlg) & vmask) << crlg;  // table row of the added angle
+  const int64_t e0 = r * D + i, e1 = e0 + half;
+  const float x0 = bf_to_f(kh[e0]) + bf_to_f(kl[e0]);
+  const float x1 = bf_to_f(kh[e1]) + bf_to_f(kl[e1]);
+  const float c = cosb[a * half + i], sn = sinb[a * half + i];
+  split_bf(x0 * c - x1 * sn, oh[e0], ol[e0]);
+  split_bf(x0 * sn + x1 * c, oh[e1], ol[e1]);
 }
 
 // ---------------------------------------------------------------- index
@@ -1890,6 +1931,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
   auto U16 = [&](int64_t off) { return off >= 0 ? (uint16_t*)(ws + off) : nullptr; };
   float* delta = (float*)(ws + BP.off_delta);
   uint16_t* dos = U16(BP.off_dos);
+  const bool has_scores = !PREC && scores;  // dkv reads the stored scores
   hipLaunchKernelGGL((prep_kernel<D, T>), dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, st,
                      (const T*)out, (const T*)dO, groups, d->H, G, delta, dos);
   for (int l = 0; l < P.L; ++l) {
@@ -1907,6 +1949,14 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
       hipLaunchKernelGGL(pack_kt16_kernel<D>, dim3((unsigned)((nblk + 3) / 4)), dim3(256), 0, st,
                          (const uint16_t*)(tws + P.off_kh[l]), (const uint16_t*)(tws + P.off_kl[l]),
                          P.Np[l], nblk, U16(BP.off_kt[0][l]), (int32_t*)(ws + BP.off_kexp[l]));
+    }
+    // the merged level's K~ in the 64-child frame (rebuilt scores only)
+    if (l == BP.vlevel && !has_scores) {
+      const int64_t n = BH * P.Np[l] * (d->D / 2);
+      hipLaunchKernelGGL(pack_vrot_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                         (const uint16_t*)(tws + P.off_kh[l]), (const uint16_t*)(tws + P.off_kl[l]),
+                         P.Np[l], d->D, P.cr_log2, BP.vm[l] - 1, cosb, sinb, n, U16(BP.off_vk[0]),
+                         U16(BP.off_vk[1]));
     }
   }
   uint32_t* bm = (uint32_t*)(ws + BP.off_bitmap);
@@ -1987,8 +2037,9 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     int2* rech = BP.off_rech >= 0 ? (int2*)(ws + BP.off_rech) : nullptr;  // CR 128
     DkvArgs a;
     memset(&a, 0, sizeof(a));
-    a.kh = (const uint16_t*)(tws + P.off_kh[l]);
-    a.kl = (const uint16_t*)(tws + P.off_kl[l]);
+    const bool vrot = l == BP.vlevel && !has_scores;  // K~ of the 64-child frame
+    a.kh = vrot ? U16(BP.off_vk[0]) : (const uint16_t*)(tws + P.off_kh[l]);
+    a.kl = vrot ? U16(BP.off_vk[1]) : (const uint16_t*)(tws + P.off_kl[l]);
     a.vt_h = (const uint16_t*)(tws + P.off_vh[l]);
     a.vt_l = P.off_vl[l] >= 0 ? (const uint16_t*)(tws + P.off_vl[l]) : nullptr;
     a.q = q;
@@ -2022,7 +2073,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.max_tiles = P.max_tiles;  // the forward's tiles per level (stored-score index)
     a.scale = scale;
     const int64_t waves = BP.max_pieces * tppl;
-    const bool has_s = !PREC && scores;
+    const bool has_s = has_scores;
     if (has_s) {
       a.sc = (const uint16_t*)scores + (int64_t)l * groups * P.max_tiles * 256;
       a.smref = (const float*)(scores + off_mref) + (int64_t)l * groups * 16;
@@ -2205,10 +2256,11 @@ static int backward_impl(const htree_dims* d, float scale, const void* q, const 
   const int64_t sbytes = train_scores_bytes(d, BP.P, nullptr);
   const char* scores = sbytes > 0 ? (const char*)scores_ws : nullptr;
   if (scores && scores_bytes < sbytes) return HTREE_EWORKSPACE;
-  // with stored scores, the plan with the merged top level when it fits
-  if (scores) {
+  // the plan with the merged top level when it applies and fits
+  {
     BwdPlan M;
-    if (make_bwd_plan(d, &M, true, true) == HTREE_OK && M.vlevel >= 0 && bwd_ws_bytes >= M.bytes)
+    if (make_bwd_plan(d, &M, true, true, scores != nullptr) == HTREE_OK && M.vlevel >= 0 &&
+        bwd_ws_bytes >= M.bytes)
       BP = M;
   }
   // a workspace too small for the stored dS but large enough without it:

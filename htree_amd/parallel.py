@@ -31,10 +31,12 @@ Differences, all deliberate:
     (src/parallel.py:983-988) and copied to the device.
   * bwd_ctx carries extra keys: `rope_base`, `packed_tree` (the MFMA operand
     copy of the tree, reused by the backward), `dims`, `parents_stacked`,
-    `train_scores` (every candidate tile's scores, fp16 relative to the
-    head's running max, so that the backward does not rebuild them; None
-    where the configuration rebuilds them) and `head_frame` (how K and V
-    map onto the kernels' head dim).
+    `parents_version` (the version counter of `parents_stacked` when the
+    forward wrote them: lists edited in place afterwards are the caller's),
+    `train_scores` (with `_save_scores=True` only: every candidate tile's
+    scores, fp16 relative to the head's running max, so that the backward
+    does not rebuild them; None where the configuration rebuilds them) and
+    `head_frame` (how K and V map onto the kernels' head dim).
 """
 from __future__ import annotations
 
@@ -317,13 +319,16 @@ def htree_forward(
     rope_base: float = 10000.0,
     _save_for_backward: bool = False,
     _save_parents: bool = True,
+    _save_scores: bool = False,
 ):
     """htree forward.  q [B,T,H,K], k [B,T,H_kv,K], v [B,T,H_kv,V] ->
     output [B,T,H,V] (q.dtype); with _save_for_backward also the bwd_ctx dict.
     With _save_parents (the default, as in the reference) the context holds
-    every level's parent lists and, where the configuration keeps them, the
-    candidate scores for the backward; without it the backward replays the
-    selection (src/backward.py:881-934)."""
+    every level's parent lists for the backward; without it the backward
+    replays the selection (src/backward.py:881-934).  _save_scores (not in
+    the reference) also keeps every candidate tile's scores, where the
+    configuration allows it, so that the backward reads them instead of
+    rebuilding them: faster, at 1.6 GB for a C2-sized call."""
     _validate(q, k, v, compression_rate, max_top_nodes, top_k_per_layer)
     B, T, H, K = q.shape
     H_kv = k.shape[2]
@@ -339,7 +344,8 @@ def htree_forward(
     cos_k, sin_k = hf.tables(cos, sin)
     save_par = _save_for_backward and _save_parents
     out_f, gmax, gsum, parents, lk, lv, ws, scores = forward_frame(
-        hf.q_heads(hf.pad_qk(q)), hf.kv_k(k), hf.kv_v(v), d, cos_k, sin_k, scale, save_par, True)
+        hf.q_heads(hf.pad_qk(q)), hf.kv_k(k), hf.kv_v(v), d, cos_k, sin_k, scale, save_par,
+        _save_scores)
     out = hf.unpad_v(hf.q_heads_back(out_f))
     gmax, gsum = hf.q_heads_back(gmax), hf.q_heads_back(gsum)
     if not _save_for_backward:
@@ -369,6 +375,7 @@ def htree_forward(
         packed_tree=ws,
         dims=d,
         parents_stacked=parents,
+        parents_version=parents._version if parents is not None else None,
         train_scores=scores,
         head_frame=hf,
     )
@@ -376,11 +383,12 @@ def htree_forward(
 
 
 def htree_forward_parents(q, k, v, compression_rate=16, max_top_nodes=8192, top_k_per_layer=512,
-                          scale=None, rope_base=10000.0):
+                          scale=None, rope_base=10000.0, _save_scores=False):
     """Forward that also returns the per-level parent lists [L,B,T,H_kv,TK]
     (the list used at each level: the initial virtual parents at L-1, then
     each level's selection), gmax and gsum.  Used by the trace tests."""
     out, ctx = htree_forward(q, k, v, compression_rate, max_top_nodes, top_k_per_layer, scale,
-                             rope_base, _save_for_backward=True, _save_parents=True)
+                             rope_base, _save_for_backward=True, _save_parents=True,
+                             _save_scores=_save_scores)
     par = ctx["head_frame"].pick(ctx["parents_stacked"], 3)
     return out, par, ctx["global_max"], ctx["global_sum"], ctx

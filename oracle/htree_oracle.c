@@ -249,6 +249,9 @@ static void scores_for(const ctx_t* c, int l, int b, int h, int nc,
  *   imp      [L][nrows][Hkv][TK*CR] importance per flat position (forced
  *            rightmost = 1e6), -1 past nc; level 0 rows untouched
  *   lmax/lsum[L][nrows][H], lout [L][nrows][H][DV]  per-level trace (naive.py:225-227)
+ *   imparg   [L][nrows][Hkv][TK*CR] the largest exponent argument of each
+ *            position's importance, max_g (s_gj - m) (the importance is 0
+ *            exactly when every term underflows), -1e30 past nc
  */
 int orc_forward(const float* q, int B, int T, int H, int Hkv, int D, int DV,
                 const float* levels_k, const float* levels_v,
@@ -258,7 +261,7 @@ int orc_forward(const float* q, int B, int T, int H, int Hkv, int D, int DV,
                 int TK, float scale, const int* rows_bt, int nrows,
                 const int* forced, float* out, float* gmax, float* gsum,
                 int* par_used, int* sel_own, float* imp, float* lmax,
-                float* lsum, float* lout) {
+                float* lsum, float* lout, float* imparg) {
   if (H % Hkv != 0 || D % 2 != 0 || L < 1) return ORC_EARG;
   ctx_t c = {B, T, H, Hkv, D, DV, CR, TK, L, H / Hkv, rope_rows, scale, q,
              levels_k, levels_v, level_off, vlevel_off, level_n, cosc, sinc};
@@ -324,6 +327,18 @@ int orc_forward(const float* q, int B, int T, int H, int Hkv, int D, int DV,
           if (imp) {
             float* ip = imp + lrow * maxc;
             for (int j = 0; j < maxc; ++j) ip[j] = j < nc ? ii[j].imp : -1.0f;
+          }
+          if (imparg) {
+            float* ap = imparg + lrow * maxc;
+            for (int j = 0; j < maxc; ++j) {
+              float a = -1e30f;
+              if (j < nc)
+                for (int g = 0; g < G; ++g) {
+                  float x = s[(int64_t)g * nc + j] - m;
+                  a = x > a ? x : a;
+                }
+              ap[j] = a;
+            }
           }
           qsort(ii, nc, sizeof(impidx_t), cmp_imp_desc_stable);
           int take = TK < nc ? TK : nc;
@@ -662,6 +677,74 @@ int orc_backward_dq_rows(const float* q, int B, int T, int H, int Hkv, int D,
   }
 done:
   free(dqg);
+  scratch_free(&w);
+  return rc;
+}
+
+/*
+ * Row-subset full backward (naive.py:320-386 restricted to the listed query
+ * rows): orc_backward's loop over the given rows only, each group's dq into
+ * dq_rows [nrows][H][D] and every accumulated node's dK/dV scattered (in
+ * double, in row order) into per-level arrays laid out like the tree
+ * levels, BEFORE the mean-pool backward, added as float into dk_lv / dv_lv
+ * when those are non-NULL.  Row inputs as orc_backward_dq_rows.  The CPU
+ * baseline times it for its backward leg; over all rows in order it
+ * reproduces orc_backward bit for bit.
+ */
+int orc_backward_rows(const float* q, int B, int T, int H, int Hkv, int D, int DV,
+                      const float* levels_k, const float* levels_v,
+                      const int64_t* level_off, const int64_t* vlevel_off,
+                      const int* level_n, int L,
+                      const float* cosc, const float* sinc, int rope_rows, int CR,
+                      int TK, float scale, const int* rows_bt, int nrows,
+                      const int* parents_rows, const float* gmax_rows,
+                      const float* gsum_rows, const float* delta_rows,
+                      const float* dO_rows, float* dq_rows, float* dk_lv,
+                      float* dv_lv) {
+  ctx_t c = {B, T, H, Hkv, D, DV, CR, TK, L, H / Hkv, rope_rows, scale, q,
+             levels_k, levels_v, level_off, vlevel_off, level_n, cosc, sinc};
+  int G = c.G, maxc = TK * CR;
+  int64_t tot = level_off[L - 1] + (int64_t)B * level_n[L - 1] * Hkv * D;
+  int64_t vtot = vlevel_off[L - 1] + (int64_t)B * level_n[L - 1] * Hkv * DV;
+  double* dkd = (double*)calloc(tot, sizeof(double));
+  double* dvd = (double*)calloc(vtot, sizeof(double));
+  double* dqg = (double*)malloc(sizeof(double) * G * D);
+  scratch_t w = {0};
+  int rc = ORC_OK;
+  if (!dkd || !dvd || !dqg || !scratch_alloc(&w, G, D, DV, maxc)) {
+    rc = ORC_ENOMEM;
+    goto done;
+  }
+  for (int r = 0; r < nrows && rc == ORC_OK; ++r) {
+    int b = rows_bt[2 * r], t = rows_bt[2 * r + 1];
+    if (b < 0 || b >= B || t < 0 || t >= T) {
+      rc = ORC_EARG;
+      break;
+    }
+    rowp_t rp = {q + ((int64_t)b * T + t) * H * D, gmax_rows + (int64_t)r * H,
+                 gsum_rows + (int64_t)r * H, delta_rows + (int64_t)r * H,
+                 dO_rows + (int64_t)r * H * DV};
+    for (int h = 0; h < Hkv && rc == ORC_OK; ++h) {
+      for (int i = 0; i < G * D; ++i) dqg[i] = 0.0;
+      for (int l = L - 1; l >= 0 && rc == ORC_OK; --l) {
+        const int* par = parents_rows + (((int64_t)l * nrows + r) * Hkv + h) * TK;
+        const int* nxt = l > 0 ? parents_rows + (((int64_t)(l - 1) * nrows + r) * Hkv + h) * TK : NULL;
+        scatter_t sc = {dkd + level_off[l] + ((int64_t)b * level_n[l] * Hkv + h) * D,
+                        dvd + vlevel_off[l] + ((int64_t)b * level_n[l] * Hkv + h) * DV,
+                        (int64_t)Hkv * D, (int64_t)Hkv * DV, D, DV};
+        rc = group_bwd(&c, l, b, t, h, par, nxt, &rp, dqg, scatter_cb, &sc, &w);
+      }
+      for (int g = 0; g < G; ++g)
+        for (int d = 0; d < D; ++d)
+          dq_rows[((int64_t)r * H + h * G + g) * D + d] = (float)dqg[g * D + d];
+    }
+  }
+  if (rc == ORC_OK && dk_lv && dv_lv) {
+    for (int64_t i = 0; i < tot; ++i) dk_lv[i] += (float)dkd[i];
+    for (int64_t i = 0; i < vtot; ++i) dv_lv[i] += (float)dvd[i];
+  }
+done:
+  free(dkd); free(dvd); free(dqg);
   scratch_free(&w);
   return rc;
 }

@@ -19,6 +19,8 @@ Pinning (what each function is checked against, see tests/test_oracle_*.py):
                        torch float64 autograd of the dense form with the
                        selection held fixed
   backward_dq_rows ... the full backward's dq at the same rows
+  backward_rows ...... the full backward over all rows in order, bit for bit;
+                       its row chunks add up to it
   backward_dkv_nodes . the full backward's per-level dK/dV at the same nodes
   final_dkv_level0 ... the full backward's final dk/dv (after the pooling
                        backward) at the same level-0 nodes
@@ -71,11 +73,13 @@ def lib():
         # common prefix: q, B, T, H, Hkv, D, DV, levels k / v, k / v level
         # offsets, level sizes, L, cos, sin, rope_rows, CR, TK, scale
         C = [P, I, I, I, I, I, I, P, P, P, P, P, I, P, P, I, I, I, F]
-        L.orc_forward.argtypes = C + [P, I, P, P, P, P, P, P, P, P, P, P]
+        L.orc_forward.argtypes = C + [P, I, P, P, P, P, P, P, P, P, P, P, P]
         L.orc_backward.restype = I
         L.orc_backward.argtypes = C + [P, P, P, P, P, P, P, P]
         L.orc_backward_dq_rows.restype = I
         L.orc_backward_dq_rows.argtypes = C + [P, I, P, P, P, P, P, P]
+        L.orc_backward_rows.restype = I
+        L.orc_backward_rows.argtypes = C + [P, I, P, P, P, P, P, P, P, P]
         L.orc_backward_dkv_nodes.restype = I
         L.orc_backward_dkv_nodes.argtypes = C + [P, P, P, P, P, P, I, P, P]
         L.orc_delta.argtypes = [P, P, I64, I, P]
@@ -221,8 +225,9 @@ def forward(q, tree: Tree, scale: float, rows: Optional[np.ndarray] = None,
 
     forced: [L, n, Hkv, TK] parent lists to use (teacher forcing).
     Returns out (rounded to the dtype), out_f32, gmax, gsum, parents [L,n,Hkv,TK]
-    (list used per level), sel (own Top-K per level), imp, and the per-level
-    trace lmax/lsum/lout when trace=True."""
+    (list used per level), sel (own Top-K per level), imp, imparg (per
+    position, the largest exponent argument max_g (s_gj - m) of its
+    importance), and the per-level trace lmax/lsum/lout when trace=True."""
     q = _f32(q)
     B, T, H, D = q.shape
     if rows is None:
@@ -236,6 +241,7 @@ def forward(q, tree: Tree, scale: float, rows: Optional[np.ndarray] = None,
     par = np.full((L, n, Hkv, TK), -1, np.int32)
     sel = np.full((L, n, Hkv, TK), -1, np.int32)
     imp = np.full((L, n, Hkv, TK * CR), -1.0, np.float32)
+    imparg = np.full((L, n, Hkv, TK * CR), -1e30, np.float32)
     lmax = lsum = lout = None
     if trace:
         lmax = np.zeros((L, n, H), np.float32)
@@ -246,10 +252,11 @@ def forward(q, tree: Tree, scale: float, rows: Optional[np.ndarray] = None,
         assert forced.shape == (L, n, Hkv, TK)
     rc = lib().orc_forward(*tree._common(q), ctypes.c_float(scale), _ptr(rows), n,
                            _ptr(forced), _ptr(out), _ptr(gmax), _ptr(gsum), _ptr(par),
-                           _ptr(sel), _ptr(imp), _ptr(lmax), _ptr(lsum), _ptr(lout))
+                           _ptr(sel), _ptr(imp), _ptr(lmax), _ptr(lsum), _ptr(lout),
+                           _ptr(imparg))
     _check(rc, "oracle forward")
     res = dict(out_f32=out, out=round_to(out, tree.dtype), gmax=gmax, gsum=gsum,
-               parents=par, sel=sel, imp=imp, rows=rows)
+               parents=par, sel=sel, imp=imp, imparg=imparg, rows=rows)
     if trace:
         res.update(lmax=lmax, lsum=lsum, lout=lout)
     return res
@@ -305,6 +312,29 @@ def backward_dq_rows(q, tree: Tree, scale: float, rows, parents_rows, gmax_rows,
                                     *[_ptr(a) for a in args], _ptr(dq))
     _check(rc, "oracle dq rows")
     return dq
+
+
+def backward_rows(q, tree: Tree, scale: float, rows, parents_rows, gmax_rows, gsum_rows,
+                  delta_rows, dO_rows, with_dkv: bool = True):
+    """The full backward restricted to a subset of rows (naive.py:320-386
+    for those rows): dq [n,H,D] of the rows and, with `with_dkv`, the
+    per-level dK / dV (before the mean-pool backward, levels concatenated
+    like the tree's) that the rows' accumulated candidates receive.  The
+    scatter runs either way; without `with_dkv` its result is dropped.
+    Row inputs as backward_dq_rows.  Returns (dq, dk_lv | None, dv_lv | None)."""
+    q = _f32(q)
+    B, T, H, D = q.shape
+    rows = np.ascontiguousarray(rows, np.int32)
+    n = rows.shape[0]
+    args = [np.ascontiguousarray(parents_rows, np.int32), _f32(gmax_rows), _f32(gsum_rows),
+            _f32(delta_rows), _f32(dO_rows)]
+    dq = np.zeros((n, H, D), np.float32)
+    dk = np.zeros_like(tree.kflat) if with_dkv else None
+    dv = np.zeros_like(tree.vflat) if with_dkv else None
+    rc = lib().orc_backward_rows(*tree._common(q), ctypes.c_float(scale), _ptr(rows), n,
+                                 *[_ptr(a) for a in args], _ptr(dq), _ptr(dk), _ptr(dv))
+    _check(rc, "oracle backward rows")
+    return dq, dk, dv
 
 
 def backward_dkv_nodes(q, tree: Tree, scale: float, parents, gmax, gsum, delta_, dO,

@@ -11,6 +11,18 @@ Selection tie rule (the parity bar for node indices):
   covers candidates whose weight is below 1e-6 of the leading one.
   Rows are compared only where the previous level's parents matched (the
   cascade rule of the reference's compare_traces, correctness_test.py:409-431).
+
+Exact ties are held exactly.  An importance is 0 exactly when every term
+exp(s_g - max) underflows in fp32 (argument below ln 2^-150 = -103.97, with
+subnormal results kept, as the oracle's expf and the kernels' exponential
+both do).  Given the oracle's largest exponent argument a(x) of each
+candidate, a candidate with a(x) < ZERO_ARG is 0 on both sides and one with
+a(x) > NONZERO_ARG is positive on both (the margins are orders of magnitude
+above any score error).  If the selection under test took x, a certain
+zero, and left out y that the oracle took, it must have seen y as exactly 0
+too (so y is not a certain nonzero), and then the stable order puts the
+lower flat position first, so x must come before y; anything else is a
+violation that the tie band does not excuse (src/naive.py:94).
 """
 from __future__ import annotations
 
@@ -23,6 +35,9 @@ import torch
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 TIE_RTOL = 1e-3
 TIE_ATOL = 1e-6
+# exp(x) rounds to 0 in fp32 below ln(2^-150) = -103.97; 0.5 of margin each side
+ZERO_ARG = -104.47
+NONZERO_ARG = -103.47
 
 TORCH_DT = {"float32": torch.float32, "bfloat16": torch.bfloat16, "float16": torch.float16}
 
@@ -59,13 +74,17 @@ def load_golden(name: str) -> Dict:
 
 def compare_selection(sel_test: np.ndarray, sel_ref: np.ndarray, imp_ref: np.ndarray,
                       par_ref: np.ndarray, CR: int, prev_ok: np.ndarray = None,
-                      rtol: float = TIE_RTOL, atol: float = TIE_ATOL) -> Dict:
+                      rtol: float = TIE_RTOL, atol: float = TIE_ATOL,
+                      arg_ref: np.ndarray = None) -> Dict:
     """Compare two selections [n, Hkv, TK] (ascending node ids, -1 padded).
 
     imp_ref [n, Hkv, TK*CR]: the oracle's importance per flat position (-1 past nc).
     par_ref [n, Hkv, TK]: the parent list the oracle expanded at this level
     (maps flat position j -> node = valid_parents[j // CR] * CR + j % CR).
     prev_ok [n, Hkv]: rows whose previous-level parents matched (cascade rule).
+    arg_ref [n, Hkv, TK*CR]: the oracle's largest exponent argument per flat
+    position (the oracle forward's `imparg`); with it, swaps that only the
+    tie order decides are held to that order (module docstring).
     Returns counts and a boolean exact-match mask."""
     n, Hkv, TK = sel_test.shape
     exact = np.all(sel_test == sel_ref, axis=-1)
@@ -79,15 +98,26 @@ def compare_selection(sel_test: np.ndarray, sel_ref: np.ndarray, imp_ref: np.nda
         vp = [int(x) for x in par_ref[r, h] if x >= 0]
         imp = imp_ref[r, h]
         nc = int(np.sum(imp >= 0))
-        node_imp = {}
+        node_imp, node_arg = {}, {}
         for j in range(nc):
-            node_imp[vp[j // CR] * CR + j % CR] = float(imp[j])
+            node = vp[j // CR] * CR + j % CR
+            node_imp[node] = float(imp[j])
+            if arg_ref is not None:
+                node_arg[node] = float(arg_ref[r, h, j])
         srt = np.sort(imp[:nc])[::-1]
         th = float(srt[min(TK, nc) - 1])
         ok = True
         for x in A ^ Bset:
             if x not in node_imp or abs(node_imp[x] - th) > rtol * th + atol:
                 ok = False
+        if ok and arg_ref is not None:
+            # (flat position order is node order: the parent lists ascend)
+            for x in A - Bset:
+                if node_arg[x] >= ZERO_ARG:
+                    continue
+                for y in Bset - A:
+                    if node_arg[y] > NONZERO_ARG or y < x:
+                        ok = False
         if ok:
             excused += 1
         else:

@@ -67,3 +67,45 @@ def test_state_checker(case):
         check_state(fw["gmax"] + 0.01, fw["gsum"], fw["gmax"], fw["gsum"], "bfloat16")
     with pytest.raises(AssertionError):
         check_state(fw["gmax"], fw["gsum"] * 1.01, fw["gmax"], fw["gsum"], "bfloat16")
+
+
+def test_selection_rule_holds_exact_ties():
+    """compare_selection with the oracle's exponent arguments: among
+    candidates whose importance underflows to exactly 0 on both sides the
+    lowest flat position must win (src/naive.py:94); the tie band alone
+    would excuse any order among them.  One row, parent list [0, 1] at CR 3
+    (flat position j is node j), top_k 3."""
+    from tests.helpers import compare_selection
+
+    CR, TK = 3, 3
+    par = np.array([[[0, 1, -1]]], np.int32)
+    imp = np.full((1, 1, TK * CR), -1.0, np.float32)
+    arg = np.full((1, 1, TK * CR), -1e30, np.float32)
+    imp[0, 0, :6] = [0.5, 0.0, 0.0, 0.0, 0.0, 1e6]
+    arg[0, 0, :6] = [-0.7, -300.0, -300.0, -300.0, -300.0, 0.0]
+    ref = np.array([[[0, 1, 5]]], np.int32)  # the stable order: zeros by position
+    sel = lambda *n: np.array([[list(n)]], np.int32)
+
+    def check(got, a=arg, i=imp):
+        return compare_selection(got, ref, i, par, CR, arg_ref=a)
+
+    assert check(ref)["exact"] == 1
+    # a higher-position zero in place of the lowest one: a tie-order violation
+    assert check(sel(0, 3, 5))["bad"]
+    assert not compare_selection(sel(0, 3, 5), ref, imp, par, CR)["bad"]  # the band alone excuses it
+    # node 3 near the underflow cut (it may be a subnormal on the side under
+    # test, which then prefers it to the certain zero 1)
+    a2 = arg.copy()
+    a2[0, 0, 3] = -104.0
+    assert not check(sel(0, 3, 5), a2)["bad"]
+    # ... but node 1 near the cut does not excuse a certain zero 3 taken in
+    # its place: 1 is then 0 on that side too, and comes first
+    a2 = arg.copy()
+    a2[0, 0, 1] = -104.0
+    assert check(sel(0, 3, 5), a2)["bad"]
+    # node 1 a certain nonzero of weight 1e-7 (inside the absolute band), node
+    # 3 a certain zero: taking 3 instead is never right
+    i3, a3 = imp.copy(), arg.copy()
+    i3[0, 0, 1], a3[0, 0, 1] = 1e-7, -16.1
+    assert check(sel(0, 3, 5), a3, i3)["bad"]
+    assert not compare_selection(sel(0, 3, 5), ref, i3, par, CR)["bad"]

@@ -4,9 +4,11 @@
   made at a non-default rope_base: the backward rebuilds the operand tree and
   (without per_layer_parents) replays the selection with the context's own
   RoPE tables, as src/backward.py:848-934 does;
-* the lean autograd mode (only the reference's eight saved tensors,
-  src/backward.py:1141-1145): the same gradients as the default mode, from
-  the selection-only replay (htree_select), whose lists are the forward's;
+* the autograd modes: the default (the reference's eight saved tensors,
+  src/backward.py:1141-1145, plus the parent lists and the packed tree), the
+  lean mode (the eight alone: the same gradients from the selection-only
+  replay, htree_select, whose lists are the forward's) and the stored-score
+  mode; the backward's workspace choice under a memory limit;
 * K != V head dims (src/parallel.py:904, src/naive.py:144): forward and
   backward against the oracle's native two-dim restatement."""
 import numpy as np
@@ -86,41 +88,84 @@ def test_reference_keys_context_without_max_top_nodes():
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
-def test_lean_autograd_mode(dtype):
-    """_save_parents=False keeps the reference's eight tensors and replays
-    the selection alone in the backward: bitwise the gradients of the default
-    mode's lists with rebuilt scores (bf16 here: the default mode keeps the
-    forward's fp16 scores, so it agrees within the bar; fp16 inputs keep no
-    scores, so there the two agree bitwise)."""
+def test_autograd_modes(dtype):
+    """The three autograd modes.  Default: the reference's eight tensors plus
+    the parent lists and the packed tree are saved, nothing more (no stored
+    scores); `_save_parents=False` saves the eight alone and replays the
+    selection in the backward: bitwise the default mode's gradients, and
+    those of htree_backward on the forward's own lists with rebuilt scores.
+    `_save_scores=True` also saves the scores (bf16 only) and agrees within
+    the bar; the gradients are checked against the oracle."""
     import htree_amd
 
     B, T, H, Hkv, D, CR, TK, MTN = 1, 2500, 16, 2, 128, 16, 16, 128
     q, k, v, dO = seeded(B, T, H, Hkv, D, D, dtype, 53)
     dOd = dO.to(DEV)
-    grads = []
-    for save in (True, False):
+    grads = {}
+    for mode in ("default", "scores", "lean"):
         qg, kg, vg = (x.to(DEV).requires_grad_(True) for x in (q, k, v))
         out = htree_amd.htree_forward_triton_autograd(qg, kg, vg, CR, MTN, TK, rope_base=2000.0,
-                                                      _save_parents=save)
-        n_saved = len(out.grad_fn.saved_tensors)
-        assert n_saved == (11 if save else 8), n_saved
+                                                      _save_parents=mode != "lean",
+                                                      _save_scores=mode == "scores")
+        saved = [t for t in out.grad_fn.saved_tensors if t is not None]
+        scores = mode == "scores" and dtype == "bfloat16"
+        assert len(saved) == {"default": 10, "scores": 10 + scores, "lean": 8}[mode], len(saved)
         out.backward(dOd)
         torch.cuda.synchronize()
-        grads.append((out.detach(), qg.grad, kg.grad, vg.grad))
-    (o0, *g_default), (o1, *g_lean) = grads
-    assert torch.equal(o0, o1)
+        grads[mode] = (out.detach(), qg.grad, kg.grad, vg.grad)
+    for mode in ("scores", "lean"):
+        assert torch.equal(grads[mode][0], grads["default"][0])
     qd, kd, vd = (x.to(DEV) for x in (q, k, v))
     out, ctx = htree_amd.htree_forward(qd, kd, vd, CR, MTN, TK, rope_base=2000.0,
                                        _save_for_backward=True)
-    rebuilt = htree_amd.htree_backward(dOd, qd, out, dict(ctx, train_scores=None),
-                                       _grad_dtype=q.dtype)
+    assert ctx["train_scores"] is None
+    rebuilt = htree_amd.htree_backward(dOd, qd, out, ctx, _grad_dtype=q.dtype)
     torch.cuda.synchronize()
     f = lambda x: x.float().cpu().numpy()
-    for a, b, c in zip(g_lean, rebuilt, g_default):
+    for a, b, c, s in zip(grads["lean"][1:], rebuilt, grads["default"][1:], grads["scores"][1:]):
         assert torch.equal(a, b)
-        if ctx["train_scores"] is None:
-            assert torch.equal(a, c)
-        ok, w = close(f(a), f(c), dtype)
+        assert torch.equal(a, c)
+        ok, w = close(f(s), f(c), dtype)
+        assert ok, w
+    par = ctx["parents_stacked"].cpu().numpy()
+    tree = orc.Tree(k.float().numpy(), v.float().numpy(), CR, MTN, TK, dtype, 2000.0)
+    for mode in ("default", "scores"):
+        g = [f(x) for x in grads[mode][1:]]
+        rep = check_backward(q, k, v, dO, CR, TK, MTN, dtype, f(out), par, f(ctx["global_max"]),
+                             f(ctx["global_sum"]), *g, tree=tree)
+        print(mode, rep, flush=True)
+
+
+def test_backward_workspace_limit():
+    """The stored-dS workspace is taken only where it fits what may be
+    spent (default: what the device can spare); below it the backward runs
+    in the smallest workspace and dq recomputes the scores.  The plan taken
+    is recorded in the context; both meet the bar against the oracle and
+    agree with each other within it."""
+    import htree_amd
+    from htree_amd import _native as N
+
+    B, T, H, Hkv, D, CR, TK, MTN = 1, 3000, 16, 2, 128, 16, 16, 128
+    q, k, v, dO = seeded(B, T, H, Hkv, D, D, "bfloat16", 54)
+    qd, kd, vd, dOd = (x.to(DEV) for x in (q, k, v, dO))
+    out, ctx = htree_amd.htree_forward(qd, kd, vd, CR, MTN, TK, _save_for_backward=True)
+    nb = N.ctypes.c_int64()
+    N.check(N.lib().htree_backward_workspace_bytes(N.ctypes.byref(ctx["dims"]),
+                                                   N.ctypes.byref(nb)), "bytes")
+    full = nb.value
+    a = htree_amd.htree_backward(dOd, qd, out, ctx)
+    assert ctx["backward_plan"] == "stored_ds"
+    b = htree_amd.htree_backward(dOd, qd, out, ctx, _workspace_limit=full - 1)
+    assert ctx["backward_plan"] == "recompute"
+    torch.cuda.synchronize()
+    f = lambda x: x.float().cpu().numpy()
+    par = ctx["parents_stacked"].cpu().numpy()
+    for g in (a, b):
+        rep = check_backward(q, k, v, dO, CR, TK, MTN, "bfloat16", f(out), par,
+                             f(ctx["global_max"]), f(ctx["global_sum"]), *[f(x) for x in g])
+        print(rep, flush=True)
+    for x, y in zip(a, b):
+        ok, w = close(f(x), f(y), "bfloat16")
         assert ok, w
 
 

@@ -17,11 +17,11 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
 
-def run(q, k, v, dO, CR, TK, MTN):
+def run(q, k, v, dO, CR, TK, MTN, scores=False):
     import htree_amd
 
     out, par, gmax, gsum, ctx = htree_amd.htree_forward_parents(
-        q.to(DEV), k.to(DEV), v.to(DEV), CR, MTN, TK)
+        q.to(DEV), k.to(DEV), v.to(DEV), CR, MTN, TK, _save_scores=scores)
     dq, dk, dv = htree_amd.htree_backward(dO.to(DEV), q.to(DEV), out, ctx)
     torch.cuda.synchronize()
     f = lambda x: x.float().cpu().numpy()
@@ -75,6 +75,22 @@ def test_backward_matches_oracle(cfg):
     print(rep, flush=True)
 
 
+SCORE_CASES = [c for c in CASES if c[8] == "bfloat16"]
+
+
+@pytest.mark.parametrize("cfg", SCORE_CASES,
+                         ids=lambda c: f"T{c[1]}H{c[2]}kv{c[3]}D{c[4]}cr{c[5]}tk{c[6]}{c[8]}")
+def test_backward_stored_scores_matches_oracle(cfg):
+    """The same cases with the forward's stored scores (where the
+    configuration keeps them: <= 16 candidate tiles per level, CR <= 64)."""
+    B, T, H, Hkv, D, CR, TK, MTN, dtype, seed = cfg
+    print(f"case {cfg} stored scores", flush=True)
+    q, k, v, dO = inputs(B, T, H, Hkv, D, dtype, seed, dO=True)
+    out, par, gmax, gsum, dq, dk, dv = run(q, k, v, dO, CR, TK, MTN, scores=True)
+    rep = check_backward(q, k, v, dO, CR, TK, MTN, dtype, out, par, gmax, gsum, dq, dk, dv)
+    print(rep, flush=True)
+
+
 def test_backward_skewed():
     B, T, H, Hkv, D, CR, TK, MTN = 1, 2500, 16, 1, 128, 16, 16, 128
     q, k, v, dO = skewed_inputs(B, T, H, Hkv, D, "bfloat16", 5)
@@ -96,7 +112,7 @@ def test_backward_stored_and_rebuilt_scores(skewed):
     else:
         q, k, v, dO = inputs(B, T, H, Hkv, D, "bfloat16", 8, dO=True)
     out, par, gmax, gsum, ctx = htree_amd.htree_forward_parents(
-        q.to(DEV), k.to(DEV), v.to(DEV), CR, MTN, TK)
+        q.to(DEV), k.to(DEV), v.to(DEV), CR, MTN, TK, _save_scores=True)
     assert ctx["train_scores"] is not None
     f = lambda x: x.float().cpu().numpy()
     for stored in (True, False):
@@ -196,6 +212,32 @@ def test_backward_replaced_parent_lists():
     bad[0][0, 1499, 0, 0] = 94  # level 0 lists name level-1 nodes: 94 of them
     with pytest.raises(AssertionError, match="outside"):
         htree_amd.htree_backward(dO, q, out, dict(ctx, per_layer_parents=bad))
+
+
+@pytest.mark.parametrize("H", [8, 32], ids=["G4", "G16pairs"])
+def test_backward_lists_edited_in_place(H):
+    """per_layer_parents edited in place (views of the forward's stacked
+    lists, which share their version counter) are the caller's lists: the
+    backward drops the scores the forward stored for its own lists, checks
+    the edited lists and copies them to every KV-head copy (G 32 runs as
+    pairs).  An edit that keeps the values gives bitwise the gradients of
+    the rebuilt-score backward; an edit that breaks a list is rejected."""
+    import htree_amd
+
+    q, k, v, dO = (x.to(DEV) for x in inputs(1, 1500, H, 1, 128, "bfloat16", 42, dO=True))
+    out, ctx = htree_amd.htree_forward(q, k, v, 16, 128, 16, _save_for_backward=True,
+                                       _save_scores=True)
+    assert ctx["train_scores"] is not None
+    a = htree_amd.htree_backward(dO, q, out, dict(ctx, train_scores=None))
+    plp = ctx["per_layer_parents"]
+    plp[0][0, 700, 0, 3] = plp[0][0, 700, 0, 3].clone()  # same value, new version
+    b = htree_amd.htree_backward(dO, q, out, ctx)
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+    plp[0][0, 1499, 0, 0] = 94  # a level-1 node past the level's 94
+    with pytest.raises(AssertionError, match="outside"):
+        htree_amd.htree_backward(dO, q, out, ctx)
 
 
 AUTOGRAD = [
@@ -363,8 +405,9 @@ def test_backward_min_workspace():
     """Given the smallest workspace (htree_backward_workspace_min_bytes) the
     backward recomputes the scores in its dq pass instead of storing dS; the
     gradients meet the bar against the oracle and agree with the
-    full-workspace run (dk, dv bit-exact: only dq's product changes), and one
-    byte less is rejected before any launch."""
+    full-workspace run within it (dk, dv differ only at the levels below
+    the top by the rounding of the merged top level's 64-child frame, which
+    the full plan takes), and one byte less is rejected before any launch."""
     import htree_amd
     from htree_amd import _native as N
 
@@ -400,6 +443,9 @@ def test_backward_min_workspace():
     f = lambda x: x.float().cpu().numpy()
     print(check_backward(q, k, v, dO, CR, TK, MTN, "bfloat16", f(out), par.cpu().numpy(), f(gmax),
                          f(gsum), *small), flush=True)
-    assert np.array_equal(small[1], full[1]) and np.array_equal(small[2], full[2])
+    for name, a, b in zip(("dq", "dk", "dv"), small, full):
+        ok, worst = close(a, b, "bfloat16")
+        assert ok, f"{name}: worst {worst:.3f} of the bar"
+        print(name, "small vs full workspace: worst", worst, flush=True)
     ok, worst = close(small[0], full[0], "bfloat16")
     assert ok, worst

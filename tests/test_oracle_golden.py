@@ -29,7 +29,8 @@ def test_selection_matches_reference(golden_run):
     prev_ok = None
     for l in range(g["L"] - 1, 0, -1):
         ref = g[f"parents_l{l}"].reshape(B * T, Hkv, TK)
-        res = compare_selection(fw["sel"][l], ref, fw["imp"][l], fw["parents"][l], g["CR"], prev_ok)
+        res = compare_selection(fw["sel"][l], ref, fw["imp"][l], fw["parents"][l], g["CR"], prev_ok,
+                                arg_ref=fw["imparg"][l])
         assert not res["bad"], f"level {l}: {res['bad'][:5]}"
         # the oracle follows the reference bit for bit at these sizes
         assert res["exact"] >= res["n"] - 2, res

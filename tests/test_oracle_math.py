@@ -282,6 +282,36 @@ def test_dq_rows_matches_full_backward(run):
     np.testing.assert_array_equal(got, bw["dq"][b, t])
 
 
+def test_backward_rows_matches_full_backward(run):
+    """The row-subset full backward (the CPU baseline's backward leg): over
+    every row in order it is the full backward, bit for bit; over two row
+    chunks its dq rows are the full backward's and its scattered per-level
+    dK / dV add up to the full backward's."""
+    bw, par, gm, gs, dl = full_backward(run)
+    B, T, H, D = run["B"], run["T"], run["H"], run["D"]
+    rows = orc.all_rows(B, T)
+    b, t = rows[:, 0], rows[:, 1]
+    args = lambda i: (rows[i], par[:, b[i], t[i]], gm[b[i], t[i]], gs[b[i], t[i]], dl[b[i], t[i]],
+                      run["dO"][b[i], t[i]])
+    dq, dk, dv = orc.backward_rows(run["q"], run["tree"], D ** -0.5, *args(slice(None)))
+    np.testing.assert_array_equal(dq, bw["dq"].reshape(-1, H, D))
+    flat = lambda lv: np.concatenate([x.ravel() for x in lv])
+    np.testing.assert_array_equal(dk, flat(bw["dk_levels"]))
+    np.testing.assert_array_equal(dv, flat(bw["dv_levels"]))
+    cut = len(rows) // 3
+    parts = [orc.backward_rows(run["q"], run["tree"], D ** -0.5, *args(sl))
+             for sl in (slice(0, cut), slice(cut, None))]
+    np.testing.assert_array_equal(np.concatenate([p[0] for p in parts]), dq)
+    for i, ref in ((1, dk), (2, dv)):
+        got = parts[0][i] + parts[1][i]
+        np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
+    # without the dK / dV outputs only dq comes back, the same
+    dq2, none_k, none_v = orc.backward_rows(run["q"], run["tree"], D ** -0.5, *args(slice(0, cut)),
+                                            with_dkv=False)
+    assert none_k is None and none_v is None
+    np.testing.assert_array_equal(dq2, parts[0][0])
+
+
 def test_dkv_nodes_matches_full_backward(run):
     """Per-level dK/dV from each node's own scores (a different route from
     the full backward, which scores whole groups and scatters)."""

@@ -29,7 +29,8 @@ def grads(cfg, noalloc, grad_dtype=None):
 
     B, T, H, Hkv, D, CR, TK, MTN, dtype, seed = cfg
     q, k, v, dO = (x.to(DEV) for x in inputs(B, T, H, Hkv, D, dtype, seed, dO=True))
-    out, par, gmax, gsum, ctx = htree_amd.htree_forward_parents(q, k, v, CR, MTN, TK)
+    out, par, gmax, gsum, ctx = htree_amd.htree_forward_parents(q, k, v, CR, MTN, TK,
+                                                                _save_scores=True)
     d = ctx["dims"] if grad_dtype is None else N.with_grad_dtype(ctx["dims"], grad_dtype)
     need = ctypes.c_int64()
     N.check(N.lib().htree_backward_noalloc_bytes(ctypes.byref(d), ctypes.byref(need)), "bytes")
