@@ -171,6 +171,12 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true, 
   // index the stored scores of tiles 4 s' .. 4 s' + 3 of the query, which
   // must lie within the query's max_tiles
   if (scores) vok = vok && !P.precise && P.max_tiles <= 16 && 4 * ((P.N[Ltop] + 63) / 64) <= P.max_tiles;
+  // rebuilt scores: only above two 64-child parents.  Each wave of a merged
+  // block rebuilds its own tile's scores, so what the view saves is the
+  // shared staging, against a block barrier per entry; measured (same box,
+  // two alternations) C5 (256 nodes) -1.4% with it, C2 (128) +1.1% and C3
+  // (64) +1.8%.
+  else vok = vok && P.N[Ltop] > 128;
   if (view && b->use_ds && vok) {
     b->vlevel = Ltop;
     b->vcr[Ltop] = 64;
@@ -232,16 +238,19 @@ static int make_bwd_plan(const htree_dims* d, BwdPlan* b, bool allow_ds = true, 
   return HTREE_OK;
 }
 
-// Workspace for the stored-dS backward, with or without the merged top
-// level (the call takes the merged plan where it applies; the plan for
-// rebuilt scores applies wherever the one for stored scores does).
+// Workspace for the stored-dS backward: the largest of the plans without
+// the merged top level and with it for stored or rebuilt scores (the call
+// takes the merged plan where it applies).
 static int bwd_full_bytes(const htree_dims* d, int64_t* bytes) {
-  BwdPlan a, m;
+  BwdPlan a, m, r;
   int rc = make_bwd_plan(d, &a, true, false);
   if (rc) return rc;
-  rc = make_bwd_plan(d, &m, true, true, false);
+  rc = make_bwd_plan(d, &m, true, true, true);
   if (rc) return rc;
-  *bytes = a.bytes > m.bytes ? a.bytes : m.bytes;
+  rc = make_bwd_plan(d, &r, true, true, false);
+  if (rc) return rc;
+  int64_t n = a.bytes > m.bytes ? a.bytes : m.bytes;
+  *bytes = n > r.bytes ? n : r.bytes;
   return HTREE_OK;
 }
 
@@ -942,6 +951,12 @@ struct ColT<D, __bf16> {
   }
 };
 
+// one transposing read (ds_read_b64_tr_b16) at byte address p
+__device__ __forceinline__ s16x4 ds_read_tr(const char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(const __attribute__((address_space(3))) void*)p);
+}
+
 // fp32 inputs' staged dO rows, split by prep_kernel into [bf16 hi D | bf16
 // lo D] (an fp32 row's bytes): heads g0..g0+3 of column d, hi and lo, by one
 // transposing read each, addressed as ColT<D, __bf16> addresses its rows
@@ -1106,6 +1121,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
     if (PW > 1) __syncthreads(); else wave_sync();
   }
 
+  // bf16: byte offsets of the transposing column reads within a staged
+  // block (column block n: heads 4 kg .. 4 kg + 3, d = 16 n + u16), computed
+  // once and held in registers (the swizzle makes them costly per entry)
+  int cadr[ND];
+  if constexpr (std::is_same<TIn, __bf16>::value) {
+#pragma unroll
+    for (int n = 0; n < ND; ++n) {
+      cadr[n] = row_off<D, __bf16>(4 * kg + (u16 >> 2), 16 * n + 4 * (u16 & 3));
+      asm volatile("" : "+v"(cadr[n]));
+    }
+  }
+
   // The piece's records are held 64 at a time in the lanes (lane i = entry
   // base + i) with a ballot of the entries whose tile mask (shared block:
   // the masks of all its tiles) is not empty; empty entries are skipped
@@ -1262,11 +1289,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
 #pragma unroll
     for (int n = 0; n < ND; ++n) {
       s16x4 dot, dotl, qt, qtl;
-      if constexpr (std::is_same<TIn, float>::value)
-        ColTs<D>::get(S0 + St::OFF_DO, 4 * kg, 16 * n + u16, dot, dotl);
-      else
-        ColT<D, TIn>::get(S0 + St::OFF_DO, 4 * kg, 16 * n + u16, dot, dotl);
-      ColT<D, TIn>::get(S0, 4 * kg, 16 * n + u16, qt, qtl);
+      if constexpr (std::is_same<TIn, __bf16>::value) {
+        dot = ds_read_tr(S0 + St::OFF_DO + cadr[n]);
+        qt = ds_read_tr(S0 + cadr[n]);
+      } else {
+        if constexpr (std::is_same<TIn, float>::value)
+          ColTs<D>::get(S0 + St::OFF_DO, 4 * kg, 16 * n + u16, dot, dotl);
+        else
+          ColT<D, TIn>::get(S0 + St::OFF_DO, 4 * kg, 16 * n + u16, dot, dotl);
+        ColT<D, TIn>::get(S0, 4 * kg, 16 * n + u16, qt, qtl);
+      }
       dv[n] = mma16(ph, dot, dv[n]);
       dv[n] = mma16(plo, dot, dv[n]);
       u[n] = mma16(dh4, qt, f32x4{0.f, 0.f, 0.f, 0.f});
@@ -1285,8 +1317,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float lo = u[n][r], hi = u[n + ND / 2][r];
-        dk[n][r] += lo * c - hi * sn;
-        dk[n + ND / 2][r] += lo * sn + hi * c;
+        dk[n][r] = fmaf(lo, c, fmaf(-hi, sn, dk[n][r]));
+        dk[n + ND / 2][r] = fmaf(lo, sn, fmaf(hi, c, dk[n + ND / 2][r]));
       }
     }
   };

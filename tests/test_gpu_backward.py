@@ -405,9 +405,9 @@ def test_backward_min_workspace():
     """Given the smallest workspace (htree_backward_workspace_min_bytes) the
     backward recomputes the scores in its dq pass instead of storing dS; the
     gradients meet the bar against the oracle and agree with the
-    full-workspace run within it (dk, dv differ only at the levels below
-    the top by the rounding of the merged top level's 64-child frame, which
-    the full plan takes), and one byte less is rejected before any launch."""
+    full-workspace run (dk, dv bit-exact: only dq's product changes; the
+    94-node top level is too small for the merged 64-child view), and one
+    byte less is rejected before any launch."""
     import htree_amd
     from htree_amd import _native as N
 
@@ -443,9 +443,6 @@ def test_backward_min_workspace():
     f = lambda x: x.float().cpu().numpy()
     print(check_backward(q, k, v, dO, CR, TK, MTN, "bfloat16", f(out), par.cpu().numpy(), f(gmax),
                          f(gsum), *small), flush=True)
-    for name, a, b in zip(("dq", "dk", "dv"), small, full):
-        ok, worst = close(a, b, "bfloat16")
-        assert ok, f"{name}: worst {worst:.3f} of the bar"
-        print(name, "small vs full workspace: worst", worst, flush=True)
+    assert np.array_equal(small[1], full[1]) and np.array_equal(small[2], full[2])
     ok, worst = close(small[0], full[0], "bfloat16")
     assert ok, worst
