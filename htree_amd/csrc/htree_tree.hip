@@ -5,6 +5,7 @@
 #include <string.h>
 
 #include "htree_common.h"
+#include "htree_tree_index.h"
 
 namespace htree {
 
@@ -57,14 +58,9 @@ int make_plan(const htree_dims* d, Plan* p) {
   int lg = 0;
   while ((1 << lg) < CR) ++lg;
   p->cr_log2 = lg;
-  int64_t n = d->T;
   int L = 0;
-  p->N[L++] = n;
-  while (n > d->max_top_nodes) {
-    n = (n + CR - 1) / CR;
-    if (L >= HTREE_MAX_LEVELS) return HTREE_EUNSUPPORTED;
-    p->N[L++] = n;
-  }
+  if (!tree_level_sizes(d->T, CR, d->max_top_nodes, HTREE_MAX_LEVELS, p->N, &L))
+    return HTREE_EUNSUPPORTED;
   p->L = L;
   int64_t off = 0, pw = 1;
   const int64_t BH = (int64_t)d->B * d->H_kv;
@@ -76,7 +72,7 @@ int make_plan(const htree_dims* d, Plan* p) {
   for (int l = 0; l < L; ++l) {
     p->pw[l] = pw;
     pw *= CR;
-    p->Np[l] = (p->N[l] + 15) / 16 * 16;
+    p->Np[l] = tree_padded(p->N[l]);
     const int64_t elems = BH * p->Np[l] * d->D;
     p->off_kh[l] = take(elems);
     p->off_kl[l] = take(elems);
@@ -98,11 +94,9 @@ int make_plan(const htree_dims* d, Plan* p) {
 // level (CR^l > kSpan: nodes covering more than one span) is one more launch
 // over its nodes, pooled from the level below.  Pooling follows src/naive.py:53-57: the <= CR children of
 // a parent summed in child order in fp32, divided once, rounded to the level
-// dtype, and the next level pools the rounded values.
-constexpr int kSpan = 64;
-constexpr int kBuildMaxD = 256;
-// nodes above the leaves a span holds: kSpan/CR + kSpan/CR^2 + ... <= 21 (CR 4)
-constexpr int kSpanUpper = 32;
+// dtype, and the next level pools the rounded values.  The index
+// arithmetic (which nodes a block takes, where a packed element goes) is in
+// htree_tree_index.h, shared with the host replay of these stores.
 
 struct BuildArgs {
   const void* x0[2];                    // leaves: k, v [B][N_0][Hkv][D]
@@ -127,7 +121,8 @@ __device__ __forceinline__ void pack_k(const BuildArgs& a, int l, int64_t bh, in
   uint16_t* kh = a.kh[l];
   uint16_t* kl = a.kl[l];
   for (int it = threadIdx.x; it < cnt * Q; it += blockDim.x) {
-    const int j = it / Q, i0 = (it - j * Q) * 4;
+    int j, i0;
+    pack_k_item(it, D, &j, &i0);
     const int64_t node = nf + j;
     const int c = (int)(node & (a.CR - 1));
     const float* cr = a.cosb + (int64_t)c * HALF + i0;
@@ -150,7 +145,7 @@ __device__ __forceinline__ void pack_k(const BuildArgs& a, int l, int64_t bh, in
       l1[q] = cvt_pk_bf16(r1[2 * q] - __uint_as_float(h1[q] << 16),
                           r1[2 * q + 1] - __uint_as_float(h1[q] & 0xffff0000u));
     }
-    const int64_t row = (bh * a.Np[l] + node) * D;
+    const int64_t row = tree_krow(a.Np[l], D, bh, node);
     *(uint2*)(kh + row + i0) = make_uint2(h0[0], h0[1]);
     *(uint2*)(kh + row + HALF + i0) = make_uint2(h1[0], h1[1]);
     *(uint2*)(kl + row + i0) = make_uint2(l0[0], l0[1]);
@@ -158,12 +153,10 @@ __device__ __forceinline__ void pack_k(const BuildArgs& a, int l, int64_t bh, in
   }
 }
 
-// element (d, node) of the level's V^T blocks: 16-node blocks of four
-// 4-node quads, (d, c) at (c / 4) * 4D + d * 4 + c % 4
+// element (d, node) of the level's V^T blocks
 __device__ __forceinline__ int64_t vt_index(const BuildArgs& a, int l, int64_t bh, int64_t node,
                                             int d) {
-  return (bh * (a.Np[l] / 16) + node / 16) * a.D * 16 + ((node & 15) >> 2) * 4 * a.D +
-         (int64_t)d * 4 + (node & 3);
+  return tree_vt_index(a.Np[l], a.D, bh, node, d);
 }
 
 // V^T of nodes nf .. nf+cnt-1 of level l (bf16 hi, and lo for fp32 / fp16).
@@ -175,7 +168,7 @@ __device__ __forceinline__ void pack_v(const BuildArgs& a, int l, int64_t bh, in
   const int D = a.D;
   uint16_t* vh = a.vh[l];
   uint16_t* vl = a.vl[l];
-  if ((nf & 3) == 0 && (cnt & 3) == 0) {
+  if (pack_v_by_quads(nf, cnt)) {
     for (int it = threadIdx.x; it < (cnt / 4) * D; it += blockDim.x) {
       const int qd = it / D, d = it - qd * D;
       float x[4];
@@ -213,7 +206,7 @@ __device__ __forceinline__ void zero_padding(const BuildArgs& a, int64_t bh) {
     for (int it = threadIdx.x; it < np * D; it += blockDim.x) {
       const int j = it / D, d = it - j * D;
       const int64_t node = a.N[l] + j;
-      const int64_t row = (bh * a.Np[l] + node) * D;
+      const int64_t row = tree_krow(a.Np[l], D, bh, node);
       a.kh[l][row + d] = 0;
       a.kl[l][row + d] = 0;
       const int64_t o = vt_index(a, l, bh, node, d);
@@ -235,7 +228,7 @@ __global__ __launch_bounds__(256) void build_span_kernel(const BuildArgs a) {
   const int h = (int)(bh % Hkv);
   const int64_t b = bh / Hkv;
   const int64_t N0 = a.N[0];
-  const int nl = (int)(N0 - n0 < kSpan ? N0 - n0 : kSpan);  // leaves of the span (>= 1)
+  const int nl = span_leaves(N0, n0);  // leaves of the span (>= 1)
   if (n0 == 0) zero_padding(a, bh);
   constexpr int PER = 16 / (int)sizeof(T);  // elements per 16-byte chunk
   constexpr int MAXC = kSpan * DM / PER / 256;  // chunks per thread
@@ -278,17 +271,16 @@ __global__ __launch_bounds__(256) void build_span_kernel(const BuildArgs a) {
     int64_t pf = n0;  // first node of the previous level held in prev
     int uo = 0;
     for (int l = 1; l < a.lspan; ++l) {
-      const int64_t nf = n0 / a.pw[l];
-      if (nf >= a.N[l]) break;
-      const int64_t cap = kSpan / a.pw[l];
-      const int cnt = (int)(a.N[l] - nf < cap ? a.N[l] - nf : cap);
+      int64_t nf;
+      int cnt;
+      if (!span_level_nodes(a.N[l], a.pw[l], n0, &nf, &cnt)) break;
       const int64_t Nc = a.N[l - 1];
       T* cur = us + uo * D;
       T* dst = (T*)a.lx[x][l];
       for (int it = threadIdx.x; it < cnt * D; it += blockDim.x) {
         const int j = it / D, d = it - j * D;
-        const int64_t s0 = (nf + j) * CR;
-        const int64_t e = s0 + CR < Nc ? s0 + CR : Nc;
+        int64_t s0, e;
+        pool_children(Nc, CR, nf + j, &s0, &e);
         float acc = 0.f;
         for (int64_t c = s0; c < e; ++c) acc += (float)prev[(c - pf) * D + d];
         const T v = (T)(acc / (float)(e - s0));
@@ -312,17 +304,15 @@ __global__ __launch_bounds__(256) void build_span_kernel(const BuildArgs a) {
 // below: kLevelNodes consecutive nodes of one (b, h_kv) per one-wave block,
 // one launch per level.  A thread pools 8 consecutive elements of one node,
 // loading up to 8 children at a time before adding them in child order.
-constexpr int kLevelNodes = 2;
 
 template <typename T>
 __global__ __launch_bounds__(64) void build_level_kernel(const BuildArgs a, int l) {
   __shared__ __attribute__((aligned(16))) T ns[2][kLevelNodes * kBuildMaxD];
   const int D = a.D, CR = a.CR, Hkv = a.Hkv, Q = D / 8;
   const int64_t Nl = a.N[l], Nc = a.N[l - 1];
-  const int64_t per = (Nl + kLevelNodes - 1) / kLevelNodes;  // blocks per (b, h_kv)
-  const int64_t bh = blockIdx.x / per;
-  const int64_t nf = (blockIdx.x - bh * per) * kLevelNodes;
-  const int cnt = (int)(Nl - nf < kLevelNodes ? Nl - nf : kLevelNodes);
+  int64_t bh, nf;
+  int cnt;
+  level_block_nodes(Nl, blockIdx.x, &bh, &nf, &cnt);
   const int h = (int)(bh % Hkv);
   const int64_t b = bh / Hkv;
   const int64_t rs = (int64_t)Hkv * D;  // child row stride
@@ -331,8 +321,8 @@ __global__ __launch_bounds__(64) void build_level_kernel(const BuildArgs a, int 
     const int r = it - x * cnt * Q;
     const int j = r / Q, d0 = (r - j * Q) * 8;
     const T* src = (const T*)a.lx[x][l - 1] + (b * Nc * Hkv + h) * D + d0;
-    const int64_t s0 = (nf + j) * CR;
-    const int64_t e = s0 + CR < Nc ? s0 + CR : Nc;
+    int64_t s0, e;
+    pool_children(Nc, CR, nf + j, &s0, &e);
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int64_t c0 = s0; c0 < e; c0 += 8) {
       float w[8][8];
@@ -386,8 +376,7 @@ static int tree_build_t(const htree_dims* d, const Plan& P, const void* k, const
   a.D = d->D;
   a.CR = d->compression_rate;
   a.L = P.L;
-  int ls = 1;
-  while (ls < P.L && P.pw[ls] <= kSpan) ++ls;
+  const int ls = tree_lspan(P.L, P.pw);
   a.lspan = ls;
   const int64_t BH = (int64_t)d->B * d->H_kv;
   a.chunks = (P.N[0] + kSpan - 1) / kSpan;
@@ -399,7 +388,7 @@ static int tree_build_t(const htree_dims* d, const Plan& P, const void* k, const
     // the level read and the level written (host-checked before the launch)
     for (int x = 0; x < 2; ++x)
       if (!a.lx[x][l - 1] || !a.lx[x][l]) return HTREE_ENULL;
-    const int64_t per = (P.N[l] + kLevelNodes - 1) / kLevelNodes;
+    const int64_t per = level_blocks_per_bh(P.N[l]);
     hipLaunchKernelGGL(build_level_kernel<T>, dim3((unsigned)(BH * per)), dim3(64), 0, st, a, l);
   }
   hipError_t e = hipGetLastError();
