@@ -1371,6 +1371,344 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
   }
 }
 
+// ---------------------------------------------------------------- dkv, entry pairs
+// Query groups of at most 8 heads with rebuilt scores (bf16 inputs): one
+// 16-row MFMA tile holds two entries, rows 0..7 the first entry's heads and
+// rows 8..15 the second's, so the score, dP, P / dS and dV products of two
+// entries cost those of one (with one entry per tile, half of its rows are
+// empty).  Each half keeps its own RoPE row, softmax state and accumulate
+// mask; dK~ needs each entry's u = dS^T q turned by its own angle, so u is
+// formed per entry, the other entry's dS rows masked off.
+template <int D>
+struct PairStage {
+  using S1 = Stage<D, __bf16, 0>;
+  static constexpr int RP = S1::RP, ROWB = S1::ROWB, OFF_DO = S1::OFF_DO;
+  static constexpr int CPR = S1::CPR;                    // 16-byte chunks of a head row
+  static constexpr int CPRP = S1::SWZ ? CPR : CPR + 1;  // chunks of a staged row (with its pad)
+  static constexpr int OFF_TAB = 2 * ROWB;              // per entry: cos [D/2], sin [D/2]
+  static constexpr int OFF_SM = OFF_TAB + 2 * D * 4;    // by row: gmax[16], gsum[16], delta[16]
+  static constexpr int BYTES = OFF_SM + 192;
+};
+
+// Copies of one entry's inputs into half `half` of a pair slot: its query
+// and dO rows into rows 8 half .. 8 half + 7 (rows of heads past the group
+// get head 0's, which the masks leave out), its RoPE row into the half's
+// table and its softmax state into the half's rows.  The copies come in
+// three parts (q rows, dO rows, the rest); wave w of nw issues parts i with
+// i % nw == w.
+template <int D>
+__device__ __forceinline__ void stage_pair_issue(char* slot, const DkvArgs& a, int64_t grp, int rs,
+                                                 int half, int lane, int w, int nw) {
+  using St = PairStage<D>;
+  using S1 = Stage<D, __bf16, 0>;
+  const bool pq = nw == 1 || w == 0, pd = nw == 1 || w == 1 % nw, pr = nw == 1 || w == 2 % nw;
+  const int64_t hq0 = grp * a.G;
+  const int rho = rs & 0xffff;
+  const int G = a.G;
+  {
+    int lane_c = lane;
+    asm volatile("" : "+v"(lane_c));
+    lane = lane_c;
+  }
+  const __amdgpu_buffer_rsrc_t rq = buf_rsrc((const char*)a.q + hq0 * D * 2, G * D * 2);
+  const __amdgpu_buffer_rsrc_t rd = buf_rsrc((const char*)a.dO + hq0 * D * 2, G * D * 2);
+  constexpr int PN = 8 * St::CPRP;  // chunks of the half's eight rows
+  const int P0 = 8 * half * St::CPRP;
+#pragma unroll
+  for (int j = 0; j < (PN + 63) / 64; ++j) {
+    if ((j * 64) / St::CPRP >= G) continue;  // rows past the group only (uniform)
+    const int P = P0 + j * 64 + lane;
+    int g, c;
+    if constexpr (S1::SWZ) {
+      g = P >> 4;
+      c = (P & 15) ^ swz(g);
+    } else {
+      g = P / St::CPRP;
+      c = P - g * St::CPRP;
+    }
+    const int hd = g - 8 * half;  // head of the row in its entry
+    int off = (hd * St::CPR + (c < St::CPR ? c : 0)) * 16;
+    off = hd < G ? off : 0;
+    if ((PN % 64 == 0) || j * 64 + lane < PN) {
+      char* dst = slot + (P0 + j * 64) * 16;
+      if (pq) __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void*)dst, 16, off, 0, 0, 0);
+      if (pd)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_void*)(dst + St::OFF_DO), 16, off, 0, 0, 0);
+    }
+  }
+  if (!pr) return;
+  constexpr int HALF = D / 2, CH = HALF / 4;
+  char* tab = slot + St::OFF_TAB + half * D * 4;
+  if (lane < CH) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(a.cosb + (int64_t)rho * HALF, HALF * 4),
+                                             (lds_void*)tab, 16, lane * 16, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(a.sinb + (int64_t)rho * HALF, HALF * 4),
+                                             (lds_void*)(tab + HALF * 4), 16, lane * 16, 0, 0, 0);
+  }
+  if (lane < 8) {
+    const int i = (lane < G ? lane : 0) * 4;
+    char* sm = slot + St::OFF_SM + half * 32;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(a.gmax + hq0, G * 4), (lds_void*)sm, 4, i, 0,
+                                             0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(a.gsum + hq0, G * 4), (lds_void*)(sm + 64), 4,
+                                             i, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(a.delta + hq0, G * 4), (lds_void*)(sm + 128),
+                                             4, i, 0, 0, 0);
+  }
+}
+
+// dkv_kernel's work (one wave per (piece, tile), or a block of PW waves per
+// piece sharing the staging) for bf16 inputs, rebuilt scores, G <= 8, CR
+// <= 64, with two entries per step.
+template <int D, int PW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2))) void dkv_pair_kernel(const DkvArgs a) {
+  constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
+  using St = PairStage<D>;
+  constexpr int NSW = PW > 1 ? 1 : kWavesPerBlock;  // staging areas per block
+  __shared__ __attribute__((aligned(16))) char stage_a[NSW][St::BYTES];
+  __shared__ __attribute__((aligned(16))) char stage_b[NSW][St::BYTES];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int u16 = lane & 15, kg = lane >> 4;
+  const int sw = PW > 1 ? 0 : wv;
+  int64_t pc;
+  int tile;
+  if (PW > 1) {
+    pc = blockIdx.x;
+    tile = wv;
+  } else {
+    const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wv;
+    pc = gw / a.tpp;
+    tile = (int)(gw % a.tpp);
+  }
+  if (pc >= *a.npieces) return;
+  const int32_t row = a.ptab[3 * pc], e0 = a.ptab[3 * pc + 1], ne = a.ptab[3 * pc + 2];
+  const int64_t bh = row / a.Pl;
+  const int p = (int)(row % a.Pl);
+  const int h = (int)(bh % a.Hkv);
+  const int64_t b = bh / a.Hkv;
+  const int CR = a.CR, crlg = a.crlg, G = a.G;
+  const int CRU = CR < 16 ? CR : 16;
+  const int coff = CR >= 16 ? tile * 16 : 0;  // first child of the tile
+  const int node0 = (p << crlg) + coff;
+  const bool live = node0 < a.N;  // (a shared block's wave past the last node still stages)
+  if (PW == 1 && !live) return;
+  const uint32_t cmask = CR < 16 ? ((1u << CR) - 1u) : 0xffffu;
+  auto tile_mask = [&](const int4& rc) {
+    const unsigned long long m64 = ((unsigned long long)(uint32_t)rc.w << 32) | (uint32_t)rc.z;
+    return (uint32_t)(m64 >> coff) & cmask;
+  };
+  bf16x8 kh[KS], kl[KS], vh[KS];
+  {
+    const int64_t r = (bh * a.Np + (live ? node0 : 0) + (u16 < CRU ? u16 : 0)) * D;
+    load_frag<D>(a.kh + r, kg, kh);
+    load_frag<D>(a.kl + r, kg, kl);
+    load_frag_vt<D>(a.vt_h, bh, a.Np, (live ? node0 : 0) + (u16 < CRU ? u16 : 0), kg, vh);
+  }
+  f32x4 dv[ND], dk[ND];
+#pragma unroll
+  for (int n = 0; n < ND; ++n) dv[n] = dk[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto grp_of = [&](int t) { return (b * a.T + t) * a.Hkv + h; };
+  // both slots zeroed once: rows no copy reaches, and the second half of a
+  // step without a second entry, hold finite values (the MFMAs read them;
+  // their P and dS are zero)
+  {
+    const int nthr = PW > 1 ? 64 * PW : 64, me = PW > 1 ? (int)threadIdx.x : lane;
+    for (int s = 0; s < 2; ++s) {
+      char* slot = s == 0 ? stage_a[sw] : stage_b[sw];
+      for (int i = me; i < St::BYTES / 16; i += nthr) *(uint4*)(slot + i * 16) = make_uint4(0u, 0u, 0u, 0u);
+    }
+    if (PW > 1) __syncthreads(); else wave_sync();
+  }
+  int cadr[ND];  // byte offsets of the transposing column reads (as dkv_kernel)
+#pragma unroll
+  for (int n = 0; n < ND; ++n) {
+    cadr[n] = row_off<D, __bf16>(4 * kg + (u16 >> 2), 16 * n + 4 * (u16 & 3));
+    asm volatile("" : "+v"(cadr[n]));
+  }
+  // the piece's records, 64 at a time in the lanes, with a ballot of the
+  // entries that accumulate a child of the tile (a shared block: of any tile)
+  int base = -64;
+  int4 rb = make_int4(0, 0, 0, 0);
+  unsigned long long work = 0ull;
+  auto next_work = [&](int e) {
+    while (e < ne) {
+      if (e >= base + 64) {
+        base = e & ~63;
+        const bool in = base + lane < ne;
+        rb = in ? a.rec[e0 + base + lane] : make_int4(0, 0, 0, 0);
+        work = __ballot(in && (PW > 1 ? (rb.z | rb.w) != 0 : tile_mask(rb) != 0u));
+      }
+      const unsigned long long m = work >> (e - base);
+      if (m) return e + (int)__builtin_ctzll(m);
+      e = base + 64;
+    }
+    return ne;
+  };
+  auto rec_of = [&](int e) {
+    const int i = e - base;
+    return make_int4(__builtin_amdgcn_readlane(rb.x, i), __builtin_amdgcn_readlane(rb.y, i),
+                     __builtin_amdgcn_readlane(rb.z, i), __builtin_amdgcn_readlane(rb.w, i));
+  };
+  auto issue = [&](char* slot, const int4 rA, const bool hasB, const int4 rB) {
+    stage_pair_issue<D>(slot, a, grp_of(rA.x), rA.y, 0, lane, wv, PW);
+    if (hasB) stage_pair_issue<D>(slot, a, grp_of(rB.x), rB.y, 1, lane, wv, PW);
+  };
+  // One step: entries eA and eB (eB == ne: none) from `cur`, the next
+  // pair's copies into `nxt` first.
+  auto step = [&](const char* __restrict__ S0, char* __restrict__ nxt, const int eA, const int4 rA,
+                  const int eB, const int4 rB, const int nA, const int4 rnA, const int nB,
+                  const int4 rnB) __attribute__((always_inline)) {
+    wait_stage();
+    if (PW > 1) __syncthreads();
+    if (nA < ne) issue(nxt, rnA, nB < ne, rnB);
+    const bool hasB = eB < ne;
+    const float* tab0 = (const float*)(S0 + St::OFF_TAB);
+    const float* tab1 = tab0 + D;
+    const float* sm = (const float*)(S0 + St::OFF_SM);
+    const uint32_t mA = tile_mask(rA), mB = hasB ? tile_mask(rB) : 0u;
+    // this lane's rows 4 kg .. 4 kg + 3 belong to entry kg / 2
+    const bool ok = (((kg < 2) ? mA : mB) >> u16) & 1u;
+    // S: the query row of lane u16 (entry u16 / 8) turned by its entry's angle
+    f32x4 S = {0.f, 0.f, 0.f, 0.f};
+    {
+      float qr[KS][8];
+      row_frag<D, __bf16>(S0, u16, kg, qr);
+      const float* tq = u16 < 8 ? tab0 : tab1;
+      rot_by_fr<D>(qr, tq, tq + HALF, kg);
+      bf16x8 qh[KS], ql[KS];
+      split_frag<D>(qr, qh, ql);
+#pragma unroll
+      for (int m = 0; m < KS; ++m) {
+        S = mma32(qh[m], kh[m], S);
+        S = mma32(qh[m], kl[m], S);
+        S = mma32(ql[m], kh[m], S);
+      }
+      S *= a.scale;
+    }
+    f32x4 dP = {0.f, 0.f, 0.f, 0.f};
+    {
+      bf16x8 dh[KS], dlo[KS];
+      DoRow<D, __bf16>::get(S0 + St::OFF_DO, u16, kg, dh, dlo);
+#pragma unroll
+      for (int m = 0; m < KS; ++m) dP = mma32(dh[m], vh[m], dP);
+    }
+    float pr[4], ds[4];
+    {
+      const float4 gm4 = *(const float4*)(sm + 4 * kg);
+      const float4 gs4 = *(const float4*)(sm + 16 + 4 * kg);
+      const float4 dl4 = *(const float4*)(sm + 32 + 4 * kg);
+      const float gm[4] = {gm4.x, gm4.y, gm4.z, gm4.w}, gs[4] = {gs4.x, gs4.y, gs4.z, gs4.w};
+      const float dl[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool v = ok && ((4 * kg + r) & 7) < G;
+        pr[r] = v ? __builtin_amdgcn_exp2f((S[r] - gm[r]) * kLog2e) * __builtin_amdgcn_rcpf(gs[r]) : 0.f;
+        ds[r] = v ? pr[r] * (dP[r] - dl[r]) : 0.f;
+      }
+    }
+    s16x4 ph, plo, dh4, dl4;
+    pack4_split(ds, dh4, dl4);
+    pack4_split(pr, ph, plo);
+    if (a.ds) {
+      // each entry's 8 rows of dS into its own tile (fp16 by 2^-e, e from its
+      // largest |dS|); rows 8..15 of a stored tile are not written (dq drops
+      // the heads past the group)
+      const float am = fmaxf(fmaxf(fabsf(ds[0]), fabsf(ds[1])), fmaxf(fabsf(ds[2]), fabsf(ds[3])));
+      const float mr = row_max16(am);
+      const float m0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mr), 0));
+      const float m1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mr), 16));
+      const float m2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mr), 32));
+      const float m3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mr), 48));
+      const int exA = fp16_block_exp(fmaxf(m0, m1)), exB = fp16_block_exp(fmaxf(m2, m3));
+      const bool mine = kg < 2 || hasB;
+      const int ex = kg < 2 ? exA : exB;
+      const int64_t et = (int64_t)(e0 + (kg < 2 ? eA : eB)) * a.tpp + tile;
+      if (mine) {
+        uint16_t* o = a.ds + et * 256 + (u16 >> 2) * 64 + 16 * (kg & 1) + (u16 & 3);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          o[4 * r] = __builtin_bit_cast(uint16_t, (_Float16)__builtin_amdgcn_ldexpf(ds[r], -ex));
+      }
+      if (lane == 0) a.dsexp[(int64_t)(e0 + eA) * a.tpp + tile] = exA;
+      if (lane == 32 && hasB) a.dsexp[(int64_t)(e0 + eB) * a.tpp + tile] = exB;
+    }
+    // dV[cand][d] += sum over both entries' rows of P[row][cand] dO[row][d]
+    s16x4 qt[ND];
+#pragma unroll
+    for (int n = 0; n < ND; ++n) {
+      const s16x4 dot = ds_read_tr(S0 + St::OFF_DO + cadr[n]);
+      qt[n] = ds_read_tr(S0 + cadr[n]);
+      dv[n] = mma16(ph, dot, dv[n]);
+      dv[n] = mma16(plo, dot, dv[n]);
+    }
+    // u = dS^T q of each entry alone, turned by its own angle into dK~
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      if (hf == 1 && !hasB) break;
+      const bool sel = (kg >> 1) == hf;
+      const s16x4 z = {0, 0, 0, 0};
+      const s16x4 dhh = sel ? dh4 : z, dlh = sel ? dl4 : z;
+      const float* tb = hf == 0 ? tab0 : tab1;
+      f32x4 u[ND];
+#pragma unroll
+      for (int n = 0; n < ND; ++n) {
+        u[n] = mma16(dhh, qt[n], f32x4{0.f, 0.f, 0.f, 0.f});
+        u[n] = mma16(dlh, qt[n], u[n]);
+      }
+#pragma unroll
+      for (int n = 0; n < ND / 2; ++n) {
+        const int i = 16 * n + u16;
+        const float c = tb[i], sn = tb[HALF + i];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float lo = u[n][r], hi = u[n + ND / 2][r];
+          dk[n][r] = fmaf(lo, c, fmaf(-hi, sn, dk[n][r]));
+          dk[n + ND / 2][r] = fmaf(lo, sn, fmaf(hi, c, dk[n + ND / 2][r]));
+        }
+      }
+    }
+  };
+  int eA = next_work(0);
+  int4 rA = eA < ne ? rec_of(eA) : make_int4(0, 0, 0, 0);
+  int eB = eA < ne ? next_work(eA + 1) : ne;
+  int4 rB = eB < ne ? rec_of(eB) : make_int4(0, 0, 0, 0);
+  if (eA < ne) issue(stage_a[sw], rA, eB < ne, rB);
+  while (eA < ne) {
+    int nA = eB < ne ? next_work(eB + 1) : ne;
+    int4 rnA = nA < ne ? rec_of(nA) : make_int4(0, 0, 0, 0);
+    int nB = nA < ne ? next_work(nA + 1) : ne;
+    int4 rnB = nB < ne ? rec_of(nB) : make_int4(0, 0, 0, 0);
+    step(stage_a[sw], stage_b[sw], eA, rA, eB, rB, nA, rnA, nB, rnB);
+    eA = nA; rA = rnA; eB = nB; rB = rnB;
+    if (eA >= ne) break;
+    nA = eB < ne ? next_work(eB + 1) : ne;
+    rnA = nA < ne ? rec_of(nA) : make_int4(0, 0, 0, 0);
+    nB = nA < ne ? next_work(nA + 1) : ne;
+    rnB = nB < ne ? rec_of(nB) : make_int4(0, 0, 0, 0);
+    step(stage_b[sw], stage_a[sw], eA, rA, eB, rB, nA, rnA, nB, rnB);
+    eA = nA; rA = rnA; eB = nB; rB = rnB;
+  }
+  wait_stage();
+  if (!live) return;
+  // dk of the node = scale R^-1(dK~, node mod CR); write this piece's partial
+  float* out = a.partial + ((pc * a.tpp + tile) * 16) * (int64_t)D * 2;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int cand = 4 * kg + r;
+    const int c = (coff + cand) & (CR - 1);
+#pragma unroll
+    for (int n = 0; n < ND / 2; ++n) {
+      const int i = 16 * n + u16;
+      const float cs = a.cosb[(int64_t)c * HALF + i], sn = a.sinb[(int64_t)c * HALF + i];
+      const float lo = dk[n][r], hi = dk[n + ND / 2][r];
+      out[cand * D + i] = a.scale * (lo * cs + hi * sn);
+      out[cand * D + i + HALF] = a.scale * (hi * cs - lo * sn);
+    }
+#pragma unroll
+    for (int n = 0; n < ND; ++n) out[16 * D + cand * D + 16 * n + u16] = dv[n][r];
+  }
+}
+
 // dK_l / dV_l [B, N, Hkv, D] of one level: the pieces of each tile are summed
 // (pieces k = first + c + LG i by lane group c, the LG sums then added in a
 // fixed order: deterministic), plus the mean-pool backward of the level above,
@@ -2115,7 +2453,15 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
   hipLaunchKernelGGL((dkv_kernel<D, PREC, T, HS, PW>),                                         \
                      dim3((unsigned)(PW > 1 ? BP.max_pieces : (waves + 3) / 4)), dim3(PW > 1 ? 64 * PW : 256), \
                      0, st, a)
-    if (tppl == 4) {
+    // bf16, rebuilt scores, groups of <= 8 heads: two entries per MFMA tile
+    const bool pair = !PREC && !has_s && !rech && G <= 8;
+#define HT_PAIR(PW)                                                                             \
+  hipLaunchKernelGGL((dkv_pair_kernel<D, PW>),                                                  \
+                     dim3((unsigned)(PW > 1 ? BP.max_pieces : (waves + 3) / 4)), dim3(PW > 1 ? 64 * PW : 256), \
+                     0, st, a)
+    if (pair) {
+      if (tppl == 4) HT_PAIR(4); else if (tppl == 2) HT_PAIR(2); else HT_PAIR(1);
+    } else if (tppl == 4) {
       if (has_s) HT_DKV(true, 4); else HT_DKV(false, 4);
     } else if (tppl == 2) {
       if (has_s) HT_DKV(true, 2); else HT_DKV(false, 2);
@@ -2126,6 +2472,7 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
       if (has_s) HT_DKV(true, 1); else HT_DKV(false, 1);
     }
 #undef HT_DKV
+#undef HT_PAIR
     // level 0 is the caller's dk / dv (in grad_dtype), higher levels fp32
     // partials of the workspace
     void* dkl = l == 0 ? dk : (void*)(ws + BP.off_dk[l]);
