@@ -17,7 +17,7 @@ LIB = os.path.join(HERE, "libhtree_amd.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["htree_tree.hip", "htree_fwd.hip", "htree_bwd.hip", "htree_topk.hip"]
+SOURCES = ["htree_tree.hip", "htree_fwd.hip", "htree_bwd.hip", "htree_topk.hip", "htree_split.hip"]
 
 # packed fp32 ops are disabled on purpose: some of their forms have given
 # silently wrong results on these machines.

@@ -28,6 +28,13 @@ constexpr int kWideC = 32;
 constexpr int kWideMidPos = 64 * kWideWaves * kWideC;  // 8192: kWideC keys per thread
 constexpr int kWideMaxPos = 2 * kWideMidPos;           // top_k * CR <= 16384
 constexpr int kWideMaxTK = 1024;
+// Split selection (htree_split.hip): the parts of a shared selection score
+// in blocks of their own and meet through device memory, level by level.
+// It takes KV-head shares above 4 (query groups above 64 heads), candidate
+// sets above kWideMaxPos, and the shares whose in-block importance arrays
+// do not fit one block's LDS.
+constexpr int kSplitMaxShare = 64;     // query groups of up to 1024 heads
+constexpr int kSplitMaxPos = 65536;    // top_k * CR
 
 // ---------------------------------------------------------------- plan
 // Packed operand tree, per level l (all bf16, Np = N rounded up to 16):
@@ -51,6 +58,7 @@ struct Plan {
   int max_tiles;  // candidate tiles of 16 per level: TK * max(CR,16) / 16
   int cr_log2;
   bool wide;      // top_k > kMaxTK or max_tiles > kMaxTiles
+  bool split;     // the selection runs through device memory (htree_split.hip)
 };
 
 // Dynamic LDS of the wide forward (byte offsets): both parent lists, the
@@ -79,16 +87,28 @@ __host__ __device__ inline WideLds wide_lds(int TK, int maxpos, int max_tiles, i
 
 int make_plan(const htree_dims* d, Plan* p);
 
+// The forward of a split-selection configuration (Plan::split): per
+// selecting level one scoring launch and one combine-and-select launch,
+// then one accumulation launch over the fixed lists (none with `sel`).
+// Works in stream-ordered scratch (hipMallocAsync) of
+// split_scratch_bytes(d, P) bytes, freed on the stream at the end.
+int split_forward(const htree_dims* d, const Plan& P, float scale, const void* q,
+                  const void* tree_ws, const float* cos_table, const float* sin_table, void* out,
+                  float* gmax, float* gsum, int32_t* parents, float* tmax, float* tsum,
+                  float* tout, void* stream, bool sel);
+int64_t split_scratch_bytes(const htree_dims* d, const Plan& P, bool with_lists);
+
 // Score buffer written by the training forward for the backward (bf16 inputs,
-// levels of <= 16 candidate tiles, CR <= 64, no padding heads and no KV-head
-// quads: the register forward's configurations): per level, query group and candidate tile
-// 256 fp16 values S - m_ref laid out S[head][cand] (16 x 16), then per level
-// and query group the 16 fp32 m_ref (the head's running max after the
-// level).  0 bytes otherwise.
+// levels of <= 16 candidate tiles, CR <= 64, no padding heads, KV-head shares
+// of at most 2 and no split selection: the register forward's
+// configurations): per level, query group and candidate tile 256 fp16
+// values S - m_ref laid out S[head][cand] (16 x 16), then per level and
+// query group the 16 fp32 m_ref (the head's running max after the level).
+// 0 bytes otherwise.
 inline int64_t train_scores_bytes(const htree_dims* d, const Plan& P, int64_t* off_mref) {
   const int64_t groups = (int64_t)d->B * d->T * d->H_kv;
   if (d->dtype != HTREE_BF16 || P.max_tiles > 16 || d->compression_rate > 64 ||
-      d->kv_share == 4 || d->group_pad > 0) {
+      d->kv_share >= 4 || d->group_pad > 0 || P.split) {
     if (off_mref) *off_mref = 0;
     return 0;
   }
@@ -390,9 +410,11 @@ __device__ __forceinline__ int row_sum16i(int x) {
 // selected positions below this thread's first (their rank in ascending
 // position order).  `red` is 32 ints of LDS.  C = 32 or 64 (the selection
 // bits are one 32- or 64-bit word per thread).
-template <int C>
+template <int C, int NWV = kWideWaves>
 struct BlockSelect {
   static_assert(C == 32 || C == 64, "selection bits are one 32- or 64-bit word per thread");
+  // per-wave slots of the counts ([0, 2 S)) and scans ([2 S, 4 S)) in red
+  static constexpr int S = NWV > 8 ? NWV : 8;
   typedef typename std::conditional<C == 32, uint32_t, unsigned long long>::type Mask;
   static __device__ __forceinline__ int popc(Mask m) {
     if constexpr (C == 32) return __popc(m); else return __popcll(m);
@@ -410,13 +432,13 @@ struct BlockSelect {
     }
     c = row_sum16i(c);
     c = add_xor32i(add_xor16i(c));
-    int32_t* r = red + 8 * rc;
+    int32_t* r = red + S * rc;
     rc ^= 1;
     if (lane == 0) r[wv] = c;
     __syncthreads();
     int tot = 0;
 #pragma unroll
-    for (int w = 0; w < kWideWaves; ++w) tot += r[w];
+    for (int w = 0; w < NWV; ++w) tot += r[w];
     return tot;
   }
   // exclusive scan in thread order
@@ -427,7 +449,7 @@ struct BlockSelect {
       const int y = __shfl_up(x, o);
       if (lane >= o) x += y;
     }
-    int32_t* r = red + 16 + 8 * rs;
+    int32_t* r = red + 2 * S + S * rs;
     rs ^= 1;
     if (lane == 63) r[wv] = x;
     __syncthreads();
@@ -501,5 +523,35 @@ struct QFrag<D, __bf16> {
     }
   }
 };
+
+// One level of the packed operand tree as the forward kernels read it.
+struct LevelPtrs {
+  const uint16_t* kh;
+  const uint16_t* kl;
+  const uint16_t* vh;
+  const uint16_t* vl;
+  int64_t N, Np, pw;
+};
+
+// The lane's K~ fragment of one candidate row (the lane group's d-slots).
+template <int D>
+__device__ __forceinline__ void load_kfrag(const uint16_t* __restrict__ row, int kg,
+                                           bf16x8 (&f)[D / 32]) {
+#pragma unroll
+  for (int m = 0; m < D / 32; ++m) f[m] = *(const bf16x8*)(row + dslot<D>(kg, m));
+}
+
+// exp(x) for x <= 0 (x = -inf gives 0) including subnormal results, which
+// torch's CPU exp produces and the selection's exact-tie order depends on;
+// v_exp_f32 does not return subnormals, so those are scaled by 2^-64.
+__device__ __forceinline__ float exp_sel(float x) {
+  const float t = x * kLog2e;
+  float r = __builtin_amdgcn_exp2f(t);
+  if (__builtin_expect(__any(t < -126.f), 0)) {
+    const float rs = __builtin_amdgcn_exp2f(t + 64.f) * 5.42101086242752217e-20f;
+    r = t < -126.f ? rs : r;
+  }
+  return r;
+}
 
 }  // namespace htree

@@ -32,14 +32,6 @@ namespace htree {
 // max of a level that accumulated nothing (src/naive.py:9, src/parallel.py:75)
 constexpr float kNegInfSentinel = -1.0e10f;
 
-struct LevelPtrs {
-  const uint16_t* kh;
-  const uint16_t* kl;
-  const uint16_t* vh;
-  const uint16_t* vl;
-  int64_t N, Np, pw;
-};
-
 struct FwdArgs {
   LevelPtrs lv[HTREE_MAX_LEVELS];
   const void* q;
@@ -159,26 +151,6 @@ __device__ __forceinline__ float trace_merge(const FwdArgs& a, int64_t hq, bool 
   }
   m = gm;
   return gs;
-}
-
-template <int D>
-__device__ __forceinline__ void load_kfrag(const uint16_t* __restrict__ row, int kg,
-                                           bf16x8 (&f)[D / 32]) {
-#pragma unroll
-  for (int m = 0; m < D / 32; ++m) f[m] = *(const bf16x8*)(row + dslot<D>(kg, m));
-}
-
-// exp(x) for x <= 0 (x = -inf gives 0) including subnormal results, which
-// torch's CPU exp produces and the selection's exact-tie order depends on;
-// v_exp_f32 does not return subnormals, so those are scaled by 2^-64.
-__device__ __forceinline__ float exp_sel(float x) {
-  const float t = x * kLog2e;
-  float r = __builtin_amdgcn_exp2f(t);
-  if (__builtin_expect(__any(t < -126.f), 0)) {
-    const float rs = __builtin_amdgcn_exp2f(t + 64.f) * 5.42101086242752217e-20f;
-    r = t < -126.f ? rs : r;
-  }
-  return r;
 }
 
 // One tile's inputs staged in LDS: the K~ rows (hi, lo; each row padded by
@@ -1453,6 +1425,9 @@ static int forward_impl(const htree_dims* d, float scale, const void* q, const v
   if (sel ? !parents : (!out || !gmax || !gsum)) return HTREE_ENULL;
   if (sel) scores = nullptr, tout = nullptr;
   if (tree_ws_bytes < P.bytes) return HTREE_EWORKSPACE;
+  if (P.split)  // the shared selection does not fit one block
+    return split_forward(d, P, scale, q, tree_ws, cos_table, sin_table, out, gmax, gsum, parents,
+                         tmax, tsum, tout, stream, sel);
   int64_t off_mref = 0;
   const int64_t sbytes = train_scores_bytes(d, P, &off_mref);
   if (scores && sbytes == 0) scores = nullptr;  // this configuration recomputes in the backward

@@ -30,31 +30,39 @@ int make_plan(const htree_dims* d, Plan* p) {
   if ((int64_t)d->rope_rows < (int64_t)d->top_k * d->compression_rate ||
       d->rope_rows <= d->compression_rate)
     return HTREE_ECONFIG;
-  if (d->kv_share < 0 || d->kv_share == 3 || d->kv_share > 4 ||
-      (d->kv_share > 1 && d->H_kv % d->kv_share != 0))
+  if (d->kv_share < 0 ||
+      (d->kv_share > 1 && (!is_pow2(d->kv_share) || d->kv_share > kSplitMaxShare ||
+                           d->H_kv % d->kv_share != 0)))
     return HTREE_ESHAPE;
   const int CR = d->compression_rate;
+  const int64_t npos = (int64_t)d->top_k * CR;  // candidate positions of a full level
   const int64_t max_tiles = (int64_t)d->top_k * (CR > 16 ? CR : 16) / 16;
   const bool wide = max_tiles > kMaxTiles || d->top_k > kMaxTK;
-  if ((d->D != 32 && d->D != 64 && d->D != 128 && d->D != 256) || d->H / d->H_kv > 16 || CR < 4 || CR > 128 ||
-      (wide && (d->top_k > kWideMaxTK || (int64_t)d->top_k * CR > kWideMaxPos)))
+  if ((d->D != 32 && d->D != 64 && d->D != 128 && d->D != 256) || d->H / d->H_kv > 16 || CR < 4 ||
+      CR > 128 || d->top_k > kWideMaxTK || npos > kSplitMaxPos)
     return HTREE_EUNSUPPORTED;
-  // shared selections over KV-head pairs: the paired waves of the
+  // above kWideMaxPos positions the backward's recomputing dq pass holds a
+  // wave's position bits in LDS beside its D-wide tiles: D <= 128 there
+  if (npos > kWideMaxPos && d->D > 128) return HTREE_EUNSUPPORTED;
+  // Shared selections over KV-head pairs: the paired waves of the
   // one-wave-per-group forwards, or the two parts of the wide forward's
   // block; over KV-head quads: the four parts of the wide forward's block,
-  // at every level size (LDS for every part's importances within one
-  // block's 160 KB)
+  // at every level size, while every part's importances fit one block's
+  // 160 KB of LDS.  Shares above 4, candidate sets above kWideMaxPos and
+  // the pairs / quads that do not fit take the split selection.
+  bool split = d->kv_share > 4 || npos > kWideMaxPos;
   if (d->kv_share == 2 && wide &&
-      wide_lds(d->top_k, d->top_k * CR, (int)max_tiles, d->D, 2).bytes > 160 * 1024)
-    return HTREE_EUNSUPPORTED;
+      wide_lds(d->top_k, (int)npos, (int)max_tiles, d->D, 2).bytes > 160 * 1024)
+    split = true;
   if (d->kv_share == 4 &&
-      wide_lds(d->top_k, d->top_k * CR, (int)max_tiles, d->D, 4).bytes > 160 * 1024)
-    return HTREE_EUNSUPPORTED;
+      wide_lds(d->top_k, (int)npos, (int)max_tiles, d->D, 4).bytes > 160 * 1024)
+    split = true;
 
   memset(p, 0, sizeof(*p));
   p->precise = d->dtype != HTREE_BF16;
   p->max_tiles = (int)max_tiles;
   p->wide = wide;
+  p->split = split;
   int lg = 0;
   while ((1 << lg) < CR) ++lg;
   p->cr_log2 = lg;

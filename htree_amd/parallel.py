@@ -8,16 +8,19 @@ Differences, all deliberate:
     relies on equality.  The reference's Triton-tiling asserts
     (top_k % 64 == 0, top_k % compression_rate == 0, :923,1019) do not apply.
   * limits of this HIP build (AssertionError): max(K, V) in {32, 64, 128, 256}
-    (K even), H / H_kv <= 64, 4 <= compression_rate <= 128,
-    top_k_per_layer <= 1024 and top_k_per_layer * compression_rate <= 16384
-    candidates per level (8192 for groups of more than 32 heads).
+    (K even), H / H_kv <= 1024, 4 <= compression_rate <= 128,
+    top_k_per_layer <= 1024 and top_k_per_layer * compression_rate <= 65536
+    candidates per level (16384 for max(K, V) = 256).
   * a query group of G > 16 heads (the reference pads it to G_PAD,
-    src/parallel.py:1023) runs as s = 2 (G <= 32) or s = 4 (G <= 64) groups
-    of ceil(G/s) heads over s copies of each KV head that share one
-    selection (the kernels' kv_share mode); each KV head's dk / dv is the
-    sum of its copies'.  A group that s does not divide gets zero query
-    heads appended to its last copy (the kernels' group_pad): the forward
-    leaves them out of the selection, the backward gives them zero dO.
+    src/parallel.py:1023) runs as s = 2 (G <= 32), 4 (G <= 64) or the power
+    of two s >= G / 16 (up to 64) groups of ceil(G/s) heads over s copies of
+    each KV head that share one selection (the kernels' kv_share mode); each
+    KV head's dk / dv is the sum of its copies'.  A group that s does not
+    divide gets zero query heads appended to its last copy (the kernels'
+    group_pad): the forward leaves them out of the selection, the backward
+    gives them zero dO.  Shares above 4 and candidate sets above 16384 (or
+    a pair's / quad's importances beyond one block's LDS) run the split
+    selection: the parts meet through device memory level by level.
   * K != V (the reference carries V = v.shape[-1] apart from K,
     src/parallel.py:904) runs the kernels at one head dim D = max(K, V):
     V is zero-padded to D (zero columns add nothing to P.V and come out
@@ -50,6 +53,9 @@ HTREE_SCORE_NEG_INF = -1.0e10            # src/parallel.py:75
 HTREE_SCORE_VALID_THRESHOLD = HTREE_SCORE_NEG_INF * 0.9  # :81
 
 KERNEL_HEAD_DIMS = (32, 64, 128, 256)
+MAX_GROUP = 1024              # query heads per KV head (kernel shares up to 64)
+MAX_CANDIDATES = 65536        # top_k_per_layer * compression_rate
+MAX_CANDIDATES_D256 = 16384   # the same at head dim 256
 
 _rope_cache: Dict[Tuple, Tuple[torch.Tensor, torch.Tensor]] = {}
 
@@ -71,7 +77,8 @@ def rope_cache(head_dim: int, rows: int, rope_base: float, device) -> Tuple[torc
 class HeadFrame:
     """Maps the caller's heads onto the kernels': the head dims (K for q/k, V
     for v) onto one head dim D = max(K, V), and a query group of G > 16 heads
-    onto s = 2 (G <= 32) or 4 (G <= 64) groups of Gk = ceil(G/s) over KV
+    onto s = 2 (G <= 32), 4 (G <= 64) or 2^ceil(log2(G/16)) (G <= 1024)
+    groups of Gk = ceil(G/s) over KV
     heads copied in place (KV head h becomes kernel KV heads s h .. s h + s
     - 1: query head h*G + g is then kernel group s h + g // Gk, so q keeps
     its layout; when s Gk > G, q_heads appends the gpad = s Gk - G padding
@@ -83,7 +90,9 @@ class HeadFrame:
         self.D = max(K, V)
         self.same = K == V
         self.G = G
-        self.share = 1 if G <= 16 else 2 if G <= 32 else 4
+        self.share = 1
+        while self.share * 16 < G:
+            self.share *= 2
         # kernel group size; a group that share does not divide gets gpad
         # zero heads appended (src/parallel.py:1023,428-431 pads to G_PAD)
         self.Gk = -(-G // self.share)
@@ -185,11 +194,16 @@ def _validate(q, k, v, compression_rate, max_top_nodes, top_k_per_layer):
     assert k.shape[3] == K, f"q and k must share the head dim K ({K} vs {k.shape[3]})"
     V = v.shape[3]
     G = H // H_kv
-    assert G <= 64, (
-        f"configuration outside this HIP build: query groups of up to 64 heads, got H/H_kv = {G}")
-    assert G <= 32 or top_k_per_layer * compression_rate <= 8192, (
-        f"configuration outside this HIP build: query groups of more than 32 heads need "
-        f"top_k_per_layer * compression_rate <= 8192, got {top_k_per_layer * compression_rate}")
+    assert G <= MAX_GROUP, (
+        f"configuration outside this HIP build: query groups of up to {MAX_GROUP} heads, "
+        f"got H/H_kv = {G}")
+    npos = top_k_per_layer * compression_rate
+    assert npos <= MAX_CANDIDATES, (
+        f"configuration outside this HIP build: top_k_per_layer * compression_rate <= "
+        f"{MAX_CANDIDATES}, got {npos}")
+    assert npos <= MAX_CANDIDATES_D256 or max(K, v.shape[3]) <= 128, (
+        f"configuration outside this HIP build: above {MAX_CANDIDATES_D256} candidates per "
+        f"level the head dim max(K, V) must be <= 128, got {max(K, v.shape[3])}")
     assert K % 2 == 0 and K > 0 and V > 0, "head dims must be positive, K even (RoPE pairs)"
     assert max(K, V) in KERNEL_HEAD_DIMS, (
         f"configuration outside this HIP build: needs max(K, V) in {KERNEL_HEAD_DIMS}, "

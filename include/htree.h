@@ -43,9 +43,10 @@ enum htree_status {
                               max_top_nodes <= top_k * compression_rate) */
   HTREE_EUNSUPPORTED = -4, /* legal for the reference, outside this build:
                               D not in {32, 64, 128, 256}, G = H/H_kv > 16
-                              (see kv_share for G <= 64),
+                              (see kv_share for G <= 1024),
                               compression_rate outside [4, 128],
-                              top_k > 1024, top_k * compression_rate > 16384,
+                              top_k > 1024, top_k * compression_rate > 65536
+                              (> 16384 with D = 256),
                               more than HTREE_MAX_LEVELS levels, or a
                               backward level of 2^31 or more entries
                               (B * T * H_kv * min(top_k, parents)) */
@@ -67,8 +68,9 @@ typedef struct htree_dims {
   int32_t rope_rows;        /* rows of the cos/sin tables (>= top_k * CR,
                                > CR)                                         */
   int32_t kv_share;         /* 0 or 1: every KV head selects on its own.
-                               2 or 4: KV heads s*i .. s*i + s - 1 (s =
-                               kv_share) hold the same keys and values and
+                               A power of two s = 2 .. 64: KV heads s*i ..
+                               s*i + s - 1 (s = kv_share) hold the same keys
+                               and values and
                                share one Top-K selection (their query heads'
                                importances are summed): a query group of G
                                heads, 16 < G <= 16 s, runs as s groups of
@@ -82,10 +84,21 @@ typedef struct htree_dims {
                                ones pair two waves of a block, the wide one
                                (top_k > 64) two parts of one block.  Quads
                                run in the wide forward at every level size
-                               (four one-wave parts of a block), where its
+                               (four one-wave parts of a block) where its
                                four importance arrays fit 160 KB of LDS
-                               (top_k * compression_rate <= 8192; else
-                               HTREE_EUNSUPPORTED). */
+                               (top_k * compression_rate <= 8192).  Shares
+                               above 4, candidate sets above 16384, and
+                               pairs / quads beyond that LDS run the split
+                               selection: the parts score in blocks of their
+                               own and meet through device memory, one
+                               scoring and one select launch per level,
+                               then one accumulation launch; the forward
+                               then takes stream-ordered scratch
+                               (hipMallocAsync, freed on the stream) of
+                               4 B * H_kv * B * T * (top_k * compression_rate
+                               + top_k * max(compression_rate, 16) / 16),
+                               plus the parent lists when `parents` is
+                               NULL. */
   int32_t grad_dtype;       /* enum htree_dtype of dq, dk, dv written by the
                                backward entry points: HTREE_F32 (0, as the
                                reference's htree_backward returns them) or

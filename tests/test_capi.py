@@ -105,18 +105,20 @@ def test_shared_kv_heads_accepted():
     (dict(H=32, H_kv=3, kv_share=2), N.HTREE_ESHAPE),  # kv_share 2 needs an even H_kv
     (dict(kv_share=3), N.HTREE_ESHAPE),
     (dict(kv_share=5), N.HTREE_ESHAPE),
+    (dict(H=128 * 16, H_kv=128, kv_share=128), N.HTREE_ESHAPE),  # shares up to 64
+    (dict(H=128, H_kv=8, kv_share=16), N.HTREE_ESHAPE),  # kv_share 16 needs H_kv % 16 == 0
     (dict(group_pad=16), N.HTREE_ESHAPE),              # padding must leave a head
     (dict(group_pad=-1), N.HTREE_ESHAPE),
     (dict(H=48, H_kv=6, kv_share=4), N.HTREE_ESHAPE),  # kv_share 4 needs H_kv % 4 == 0
-    (dict(H=64, H_kv=4, kv_share=4, T=20000, top_k=1024, max_top_nodes=16384, rope_rows=17408),
-     N.HTREE_EUNSUPPORTED),                            # quads: four 16384-position arrays > LDS
     (dict(grad_dtype_code=3), N.HTREE_ESHAPE),         # not an htree_dtype
     (dict(grad_dtype_code=-1), N.HTREE_ESHAPE),
     (dict(D=16), N.HTREE_EUNSUPPORTED),
     (dict(top_k=2048, compression_rate=4, max_top_nodes=128, rope_rows=16384),
      N.HTREE_EUNSUPPORTED),                            # top_k > 1024
-    (dict(top_k=512, compression_rate=64, max_top_nodes=128, rope_rows=32768),
-     N.HTREE_EUNSUPPORTED),                            # 32768 candidates per level
+    (dict(top_k=1024, compression_rate=128, max_top_nodes=128, rope_rows=131072),
+     N.HTREE_EUNSUPPORTED),                            # 131072 candidates per level
+    (dict(top_k=512, compression_rate=64, max_top_nodes=128, rope_rows=32768, D=256),
+     N.HTREE_EUNSUPPORTED),                            # above 16384 candidates: D <= 128
 ])
 def test_invalid_configs_raise_assertion(kw, code):
     d = dims(**kw)
@@ -175,9 +177,9 @@ def test_python_api_validates_like_reference():
                                 torch.zeros(1, 64, 2, 64), 16, 64, 8)
     with pytest.raises(AssertionError, match="GPU"):  # no CPU fallback
         htree_amd.htree_forward(q, k, k, 16, 64, 8)
-    # group sizes: any up to 64 (those 2 or 4 do not divide with padding heads)
+    # group sizes: any up to 1024 (those the share does not divide with padding heads)
     for G, ok in ((16, True), (17, True), (30, True), (31, True), (36, True), (34, True),
-                  (64, True), (65, False), (68, False)):
+                  (64, True), (65, True), (68, True), (1000, True), (1024, True), (1025, False)):
         qg = torch.zeros(1, 64, G, 64)
         if ok:  # passes the group rules, then stops at the device check
             with pytest.raises(AssertionError, match="GPU"):
@@ -185,17 +187,26 @@ def test_python_api_validates_like_reference():
         else:
             with pytest.raises(AssertionError, match="query groups"):
                 htree_amd.htree_forward(qg, k, k, 16, 64, 8)
-    with pytest.raises(AssertionError, match="8192"):  # quads: four importance arrays in LDS
+    # candidate sets: up to 65536 per level, above 16384 at head dims <= 128
+    with pytest.raises(AssertionError, match="GPU"):
         htree_amd.htree_forward(torch.zeros(1, 64, 64, 64), k, k, 16, 16384, 1024)
+    with pytest.raises(AssertionError, match="GPU"):
+        htree_amd.htree_forward(q, k, k, 64, 16, 1024)
+    with pytest.raises(AssertionError, match="65536"):
+        htree_amd.htree_forward(q, k, k, 128, 16, 1024)
+    k256 = torch.zeros(1, 64, 1, 256)
+    with pytest.raises(AssertionError, match="head dim"):
+        htree_amd.htree_forward(torch.zeros(1, 64, 4, 256), k256, k256, 64, 16, 1024)
 
 
 def test_head_frame_kv_copies():
     """Groups of G > 16 heads: s copies of every KV head (s = 2 up to 32
-    heads, 4 up to 64), kernel group s h + g // (G/s) holding query heads
+    heads, 4 up to 64, then the power of two >= G / 16), kernel group
+    s h + g // (G/s) holding query heads
     h G + g, so q keeps its layout; dk / dv come back as the copies' sum."""
     from htree_amd.parallel import HeadFrame
 
-    for G, s in ((16, 1), (24, 2), (32, 2), (40, 4), (64, 4)):
+    for G, s in ((16, 1), (24, 2), (32, 2), (40, 4), (64, 4), (128, 8), (256, 16)):
         hf = HeadFrame(64, 64, G)
         assert hf.share == s and hf.gpad == 0
         k = torch.arange(2 * 3 * 5 * 64, dtype=torch.float32).view(2, 3, 5, 64)
@@ -262,8 +273,25 @@ def test_wide_quads_accepted():
     assert N.train_scores_bytes(dims(H=64, H_kv=4, kv_share=2)) > 0
 
 
+def test_split_selection_accepted():
+    """The split selection takes what one block's shared Top-K cannot hold:
+    query groups above 64 heads (kv_share 8 .. 64), candidate sets above
+    16384 per level (up to 65536, D <= 128), and quads whose four importance
+    arrays exceed one block's LDS.  It keeps no training scores."""
+    for kw in (dict(H=128, H_kv=8, kv_share=8),                                  # G = 128
+               dict(H=1024, H_kv=64, kv_share=64, D=64),                         # G = 1024
+               dict(H=64, H_kv=4, kv_share=4, T=20000, top_k=1024, max_top_nodes=16384,
+                    rope_rows=17408),                                            # quads, 16384
+               dict(top_k=512, compression_rate=64, max_top_nodes=128, rope_rows=32768),
+               dict(H=16, H_kv=1, top_k=1024, compression_rate=64, max_top_nodes=16,
+                    rope_rows=65536, T=65536, D=32)):                            # 65536
+        d = dims(**kw)
+        assert len(N.levels(d)) >= 1
+        assert N.train_scores_bytes(d) == 0
+
+
 def test_head_frame_group_padding():
-    """A group of G heads that s = 2 or 4 does not divide runs as s kernel
+    """A group of G heads that s = 2, 4, 8, .. 64 does not divide runs as s kernel
     groups of ceil(G/s) heads, with s ceil(G/s) - G zero heads appended to
     each KV head's group (the reference pads to G_PAD, src/parallel.py:1023):
     padding heads sit at the end of each group, the caller's heads keep their
@@ -271,7 +299,8 @@ def test_head_frame_group_padding():
     from htree_amd.parallel import HeadFrame
 
     for G, s, gk, gpad in ((17, 2, 9, 1), (31, 2, 16, 1), (33, 4, 9, 3), (50, 4, 13, 2),
-                           (63, 4, 16, 1)):
+                           (63, 4, 16, 1), (65, 8, 9, 7), (100, 8, 13, 4), (128, 8, 16, 0),
+                           (129, 16, 9, 15), (1000, 64, 16, 24), (1024, 64, 16, 0)):
         hf = HeadFrame(64, 64, G)
         assert (hf.share, hf.Gk, hf.gpad) == (s, gk, gpad)
         hkv = 3
