@@ -39,6 +39,8 @@ CASES = [
     (1, 700, 8, 2, 64, 8, 16, 128, "float32", 15),      # CR < 16
     (1, 1200, 16, 4, 32, 16, 16, 128, "float16", 16),   # D = 32
     (1, 1500, 8, 2, 32, 4, 128, 256, "float32", 17),    # top_k 128: block-per-group kernel
+    (1, 1500, 128, 1, 32, 16, 16, 64, "bfloat16", 18),  # G = 128: split selection
+    (1, 1200, 100, 1, 64, 8, 16, 64, "float32", 19),    # G = 100: split, 4 padding heads
 ]
 
 
