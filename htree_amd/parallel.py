@@ -7,8 +7,8 @@ Differences, all deliberate:
     reference asserts equality, src/parallel.py:917); the algorithm never
     relies on equality.  The reference's Triton-tiling asserts
     (top_k % 64 == 0, top_k % compression_rate == 0, :923,1019) do not apply.
-  * limits of this HIP build (AssertionError): max(K, V) in {32, 64, 128, 256}
-    (K even), H / H_kv <= 1024, 4 <= compression_rate <= 128,
+  * limits of this HIP build (AssertionError): max(K, V) <= 256 (K even),
+    H / H_kv <= 1024, 4 <= compression_rate <= 128,
     top_k_per_layer <= 1024 and top_k_per_layer * compression_rate <= 65536
     candidates per level (16384 for max(K, V) = 256).
   * a query group of G > 16 heads (the reference pads it to G_PAD,
@@ -22,12 +22,14 @@ Differences, all deliberate:
     a pair's / quad's importances beyond one block's LDS) run the split
     selection: the parts meet through device memory level by level.
   * K != V (the reference carries V = v.shape[-1] apart from K,
-    src/parallel.py:904) runs the kernels at one head dim D = max(K, V):
-    V is zero-padded to D (zero columns add nothing to P.V and come out
-    zero), and for K < V the query / key halves of each RoPE pair are placed
-    at [0, K/2) and [D/2, D/2 + K/2) with zeros between, rotated by tables
-    whose first K/2 columns are the K-dim tables (the zero columns stay zero
-    under any rotation), so every score is the K-dim score.
+    src/parallel.py:904), and head dims that are not a kernel head dim
+    (32, 64, 128, 256; e.g. 16, or 96), run the kernels at one head dim D,
+    the smallest kernel head dim >= max(K, V): V is zero-padded to D (zero
+    columns add nothing to P.V and come out zero), and for K < D the query
+    / key halves of each RoPE pair are placed at [0, K/2) and
+    [D/2, D/2 + K/2) with zeros between, rotated by tables whose first K/2
+    columns are the K-dim tables (the zero columns stay zero under any
+    rotation), so every score is the K-dim score.
   * empty inputs (B == 0 or T == 0) give empty outputs (and a bwd_ctx whose
     backward gives empty gradients) without a launch.
   * the RoPE tables are built on the host with the reference's recipe
@@ -76,19 +78,20 @@ def rope_cache(head_dim: int, rows: int, rope_base: float, device) -> Tuple[torc
 
 class HeadFrame:
     """Maps the caller's heads onto the kernels': the head dims (K for q/k, V
-    for v) onto one head dim D = max(K, V), and a query group of G > 16 heads
-    onto s = 2 (G <= 32), 4 (G <= 64) or 2^ceil(log2(G/16)) (G <= 1024)
-    groups of Gk = ceil(G/s) over KV
-    heads copied in place (KV head h becomes kernel KV heads s h .. s h + s
-    - 1: query head h*G + g is then kernel group s h + g // Gk, so q keeps
-    its layout; when s Gk > G, q_heads appends the gpad = s Gk - G padding
-    heads to each group).  With K == V and G <= 16 every method returns its
+    for v) onto one head dim D (the smallest kernel head dim >= max(K, V)),
+    and a query group of G > 16 heads onto s = 2 (G <= 32), 4 (G <= 64) or
+    2^ceil(log2(G/16)) (G <= 1024) groups of Gk = ceil(G/s) over KV heads
+    copied in place (KV head h becomes kernel KV heads s h .. s h + s - 1:
+    query head h*G + g is then kernel group s h + g // Gk, so q keeps its
+    layout; when s Gk > G, q_heads appends the gpad = s Gk - G padding heads
+    to each group).  With K == V == D and G <= 16 every method returns its
     argument."""
 
     def __init__(self, K: int, V: int, G: int = 1):
         self.K, self.V = K, V
-        self.D = max(K, V)
-        self.same = K == V
+        # the kernels' head dim: the smallest of KERNEL_HEAD_DIMS that holds both
+        self.D = next(d for d in KERNEL_HEAD_DIMS if d >= max(K, V))
+        self.same = K == V == self.D
         self.G = G
         self.share = 1
         while self.share * 16 < G:
@@ -205,8 +208,8 @@ def _validate(q, k, v, compression_rate, max_top_nodes, top_k_per_layer):
         f"configuration outside this HIP build: above {MAX_CANDIDATES_D256} candidates per "
         f"level the head dim max(K, V) must be <= 128, got {max(K, v.shape[3])}")
     assert K % 2 == 0 and K > 0 and V > 0, "head dims must be positive, K even (RoPE pairs)"
-    assert max(K, V) in KERNEL_HEAD_DIMS, (
-        f"configuration outside this HIP build: needs max(K, V) in {KERNEL_HEAD_DIMS}, "
+    assert max(K, V) <= KERNEL_HEAD_DIMS[-1], (
+        f"configuration outside this HIP build: needs max(K, V) <= {KERNEL_HEAD_DIMS[-1]}, "
         f"got K={K}, V={V}")
     assert q.dtype == k.dtype == v.dtype, "q, k, v must share one dtype"
     assert (top_k_per_layer & (top_k_per_layer - 1)) == 0, "top_k_per_layer (TOP_K) must be a power of 2"

@@ -167,6 +167,7 @@ def test_workspace_too_small_rejected():
 
 def test_python_api_validates_like_reference():
     import htree_amd
+    from htree_amd.parallel import HeadFrame
 
     q = torch.zeros(1, 64, 4, 64)
     k = torch.zeros(1, 64, 1, 64)
@@ -197,6 +198,14 @@ def test_python_api_validates_like_reference():
     k256 = torch.zeros(1, 64, 1, 256)
     with pytest.raises(AssertionError, match="head dim"):
         htree_amd.htree_forward(torch.zeros(1, 64, 4, 256), k256, k256, 64, 16, 1024)
+    # head dims: any even K and any V up to 256 (zero-padded to the next kernel head dim)
+    for K, V, ok in ((16, 16, True), (96, 96, True), (80, 48, True), (256, 200, True),
+                     (512, 512, False), (96, 300, False)):
+        kk, vv = torch.zeros(1, 64, 1, K), torch.zeros(1, 64, 1, V)
+        with pytest.raises(AssertionError, match="GPU" if ok else "max\\(K, V\\)"):
+            htree_amd.htree_forward(torch.zeros(1, 64, 4, K), kk, vv, 16, 64, 8)
+    for K, V, D in ((16, 16, 32), (32, 32, 32), (96, 96, 128), (80, 48, 128), (256, 200, 256)):
+        assert HeadFrame(K, V).D == D
 
 
 def test_head_frame_kv_copies():

@@ -212,6 +212,10 @@ KV_CASES = [
     (1, 1500, 8, 1, 64, 128, 16, 8, 128, "bfloat16", 62),
     (1, 1200, 8, 2, 32, 64, 8, 16, 128, "float32", 63),
     (2, 900, 4, 1, 64, 32, 4, 32, 64, "float16", 64),
+    # head dims that are not a kernel head dim: zero-padded to the next one
+    (1, 1500, 8, 1, 16, 16, 16, 16, 128, "bfloat16", 65),   # K = V = 16 on D = 32
+    (1, 1200, 8, 2, 96, 96, 16, 16, 128, "float32", 66),    # K = V = 96 on D = 128
+    (1, 1000, 4, 1, 80, 48, 8, 16, 64, "float16", 67),      # K = 80, V = 48 on D = 128
 ]
 
 
