@@ -595,8 +595,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
 
 // Shared Top-K of the group (src/naive.py:88-105): importance of position j
 // is imp[j] (lane j % 64 of slot j / 64), the rightmost (position apos) is
-// forced first; a 31-step bitwise radix select on float bits + 1 finds the
-// take-th largest key, ties at the threshold go to the lowest positions
+// forced first; a bitwise radix select on float bits + 1 finds the take-th
+// largest key (16 steps, then 15 more only when the keys sharing its top 16
+// bits do not settle it), ties at the threshold go to the lowest positions
 // (stable descending sort).  Writes the selected nodes in ascending order
 // (= ascending position) to par_next, -1 padded to TK, and one selection
 // bitmask per slot to selmask.
@@ -613,8 +614,8 @@ __device__ __forceinline__ void select_topk(const float* __restrict__ imp, const
                                             const float* __restrict__ imp2 = nullptr,
                                             float f1 = 1.f, float f2 = 0.f) {
   const int u16 = lane & 15, kg = lane >> 4;
-  const int take = TK < nc ? TK : nc;
-  const int nslot = (nt + 3) >> 2;
+  const int take = uniform(TK < nc ? TK : nc);
+  const int nslot = uniform((nt + 3) >> 2);
   uint32_t key[MAXSLOT];
 #pragma unroll
   for (int sl = 0; sl < MAXSLOT; ++sl) {
@@ -637,19 +638,53 @@ __device__ __forceinline__ void select_topk(const float* __restrict__ imp, const
       }
     }
   }
-  uint32_t thr = 0u;
-  for (int bit = 30; bit >= 0; --bit) {
-    const uint32_t c = thr | (1u << bit);
-    int cnt = 0;
+  // The take-th largest key, bit by bit from the top.  The keys of the
+  // slots past nslot are 0 and never counted (c >= 1), so up to four slots
+  // are counted unconditionally.
+  auto radix = [&](uint32_t thr, int hi, int lo) {
+    for (int bit = hi; bit >= lo; --bit) {
+      const uint32_t c = thr | (1u << bit);
+      int cnt = 0;
 #pragma unroll
-    for (int sl = 0; sl < MAXSLOT; ++sl)
-      if (sl < nslot) cnt += __popcll(__ballot(key[sl] >= c));
-    if (cnt >= take) thr = c;
+      for (int sl = 0; sl < MAXSLOT; ++sl)
+        if (MAXSLOT <= 4 || sl < nslot) cnt += __popcll(__ballot(key[sl] >= c));
+      if (cnt >= take) thr = c;
+    }
+    return thr;
+  };
+  // bits 30..15 first; the keys that share them hold the take-th largest,
+  // which is their largest when one more is needed, their smallest when all
+  // of them are, the common value when they are equal, else bits 14..0
+  uint32_t thr = radix(0u, 30, 15);
+  {
+    int above = 0, neq = 0;
+    float emax = 0.f, emin = -INFINITY;  // keys read as floats keep their order
+#pragma unroll
+    for (int sl = 0; sl < MAXSLOT; ++sl) {
+      if (MAXSLOT <= 4 || sl < nslot) {
+        const bool in = (key[sl] >> 15) == (thr >> 15);
+        above += __popcll(__ballot((key[sl] >> 15) > (thr >> 15)));
+        neq += __popcll(__ballot(in));
+        if (in) {
+          emax = fmaxf(emax, __uint_as_float(key[sl]));
+          emin = fmaxf(emin, -__uint_as_float(key[sl]));
+        }
+      }
+    }
+    const int need2 = take - above;  // 1 <= need2 <= neq
+    const uint32_t kmax = __float_as_uint(wave_max_uniform(emax));
+    const uint32_t kmin = __float_as_uint(-wave_max_uniform(emin));
+    if (need2 == 1 || kmin == kmax)
+      thr = kmax;
+    else if (need2 == neq)
+      thr = kmin;
+    else
+      thr = radix(thr, 14, 0);
   }
   int ngt = 0;
 #pragma unroll
   for (int sl = 0; sl < MAXSLOT; ++sl)
-    if (sl < nslot) ngt += __popcll(__ballot(key[sl] > thr));
+    if (MAXSLOT <= 4 || sl < nslot) ngt += __popcll(__ballot(key[sl] > thr));
   const int need = take - ngt;
   int eq_before = 0, sel_before = 0;
 #pragma unroll
@@ -781,7 +816,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
     const int pv = lane < TK ? W.par[cur][lane] : -1;
     const int np = __popcll(__ballot(pv >= 0));
     if (np <= 0) break;  // unreachable: every level keeps >= 1 parent
-    const int ct = (int)((t / P.pw) & (CR - 1));
+    // t is the same in every lane: so are the level's sizes (scalar loops)
+    const int ct = uniform((int)((t / P.pw) & (CR - 1)));
     const int nc = ((np - 1) << crlg) + ct + 1;
     const int apos = nc - 1;
     const int nt = wide ? (nc + 15) >> 4 : np;
