@@ -884,11 +884,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
       const float M = wave_max_uniform(lmax);
       for (int tau = 0; tau < nt; ++tau) {
         const f32x4 S = W.st[tau][lane];
-        float e[4];
+        float x[4], e[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) e[r] = row_sum16(exp_sel(S[r] - M));
-        const float mine = u16 == 0 ? e[0] : u16 == 1 ? e[1] : u16 == 2 ? e[2] : e[3];
-        if (u16 < 4) W.imp[(tau << 4) + 4 * kg + u16] = mine;
+        for (int r = 0; r < 4; ++r) {
+          x[r] = (S[r] - M) * kLog2e;
+          e[r] = __builtin_amdgcn_exp2f(x[r]);
+        }
+        // subnormal results (exp_sel), one wave test for the tile
+        if (__builtin_expect(__any(fminf(fminf(x[0], x[1]), fminf(x[2], x[3])) < -126.f), 0)) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (x[r] < -126.f) e[r] = __builtin_amdgcn_exp2f(x[r] + 64.f) * 5.42101086242752217e-20f;
+        }
+        // sum over the row's 16 lanes (heads) of each candidate r, by
+        // recursive halving: lane bit 0 keeps r in {0,1} or {2,3}, bit 1 one
+        // of those, then the four quads add up; lane u16 ends with candidate
+        // r = 2 (u16 & 1) + ((u16 >> 1) & 1)
+        const bool b0 = u16 & 1, b1 = (u16 >> 1) & 1;
+        const float k0 = b0 ? e[2] : e[0], k1 = b0 ? e[3] : e[1];
+        const float s0 = b0 ? e[0] : e[2], s1 = b0 ? e[1] : e[3];
+        const float h0 = k0 + dpp<0xB1>(s0), h1 = k1 + dpp<0xB1>(s1);
+        float c = (b1 ? h1 : h0) + dpp<0x4E>(b1 ? h0 : h1);
+        c += dpp<0x124>(c);   // row rotate right by 4
+        c += dpp<0x128>(c);   // row rotate right by 8
+        if (u16 < 4) W.imp[(tau << 4) + 4 * kg + 2 * b0 + b1] = c;
       }
       if (pair) {
         // the pair's importance: both halves' sums taken to the pair's max
