@@ -97,7 +97,15 @@ __device__ __forceinline__ void to_bf_split(const float (&x)[D / 32][8], bf16x8 
 // src/naive.py:13-19, filled at :225-227): max and output relative to the
 // max over the level's accumulated candidates, -1e10 / 0 / 0 where the level
 // accumulated nothing.  O[n][r] is output dim 16n + 4kg + r of head u16.
-template <int D>
+// Output dim of row i of O tile n.  PERM (the register forward): tiles 2j
+// and 2j + 1 hold the even and the odd dims of 32j .. 32j + 31, so that the
+// V^T fragments of a tile pair are one 16-byte load.
+template <bool PERM>
+__device__ __forceinline__ int odim(int n, int i) {
+  return PERM ? 32 * (n >> 1) + 2 * i + (n & 1) : 16 * n + i;
+}
+
+template <int D, bool PERM = false>
 __device__ __forceinline__ void trace_store(const FwdArgs& a, int l, int64_t hq, bool gv, int kg,
                                             float m, float lpart, const f32x4 (&O)[D / 16]) {
   const float lt = add_xor32(add_xor16(lpart));
@@ -107,7 +115,7 @@ __device__ __forceinline__ void trace_store(const FwdArgs& a, int l, int64_t hq,
 #pragma unroll
   for (int n = 0; n < D / 16; ++n)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) op[16 * n + 4 * kg + r] = O[n][r];
+    for (int r = 0; r < 4; ++r) op[odim<PERM>(n, 4 * kg + r)] = O[n][r];
   if (kg == 0) {
     a.tmax[lh] = m == -INFINITY ? kNegInfSentinel : m;
     a.tsum[lh] = lt;
@@ -118,7 +126,7 @@ __device__ __forceinline__ void trace_store(const FwdArgs& a, int l, int64_t hq,
 // src/naive.py:215-223 (a state counts only where its sum > 1e-10); returns
 // the merged sum, the merged max in m and output in O.  Reads back what this
 // lane's trace_store calls wrote.
-template <int D>
+template <int D, bool PERM = false>
 __device__ __forceinline__ float trace_merge(const FwdArgs& a, int64_t hq, bool gv, int kg,
                                              float& m, f32x4 (&O)[D / 16]) {
   float gm = kNegInfSentinel, gs = 0.f;
@@ -137,14 +145,14 @@ __device__ __forceinline__ float trace_merge(const FwdArgs& a, int64_t hq, bool 
 #pragma unroll
         for (int n = 0; n < D / 16; ++n)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) O[n][r] = O[n][r] * sg + op[16 * n + 4 * kg + r] * sc;
+          for (int r = 0; r < 4; ++r) O[n][r] = O[n][r] * sg + op[odim<PERM>(n, 4 * kg + r)] * sc;
         gm = nm;
       } else {
         gs = ls;
 #pragma unroll
         for (int n = 0; n < D / 16; ++n)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) O[n][r] = op[16 * n + 4 * kg + r];
+          for (int r = 0; r < 4; ++r) O[n][r] = op[odim<PERM>(n, 4 * kg + r)];
         gm = lm;
       }
     }
@@ -988,11 +996,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
     // ---- O^T += V^T P^T over the tiles, V double-buffered
     auto vload = [&](int tau, s16x4 (&vh)[ND], s16x4 (&vl)[ND]) {
       const int vn = node0_of(tau) + (4 * kg < CRU ? 4 * kg : 0);
-      const int64_t vbase = (int64_t)(vn >> 4) * 16 * D + ((vn & 15) >> 2) * 4 * D + u16 * 4;
+      // dims 32j + 2 u16 and 32j + 2 u16 + 1 (tiles 2j, 2j + 1): 16 bytes
+      const int64_t vbase = (int64_t)(vn >> 4) * 16 * D + ((vn & 15) >> 2) * 4 * D + u16 * 8;
 #pragma unroll
-      for (int n = 0; n < ND; ++n) {
-        vh[n] = *(const s16x4*)(VH + vbase + (int64_t)n * 64);
-        if (PREC) vl[n] = *(const s16x4*)(VL + vbase + (int64_t)n * 64);
+      for (int j = 0; j < ND / 2; ++j) {
+        const uint4 w = *(const uint4*)(VH + vbase + (int64_t)j * 128);
+        vh[2 * j] = __builtin_bit_cast(s16x4, make_uint2(w.x, w.y));
+        vh[2 * j + 1] = __builtin_bit_cast(s16x4, make_uint2(w.z, w.w));
+        if (PREC) {
+          const uint4 wl = *(const uint4*)(VL + vbase + (int64_t)j * 128);
+          vl[2 * j] = __builtin_bit_cast(s16x4, make_uint2(wl.x, wl.y));
+          vl[2 * j + 1] = __builtin_bit_cast(s16x4, make_uint2(wl.z, wl.w));
+        }
       }
     };
     auto pv_tile = [&](int tau, const s16x4 (&vh)[ND], const s16x4 (&vl)[ND]) {
@@ -1031,14 +1046,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
       }
     }
     if (TRACE)
-      trace_store<D>(a, l, ((int64_t)b * a.T + t) * a.H + h * G + u16, gv, kg, m_run, l_part, O);
+      trace_store<D, true>(a, l, ((int64_t)b * a.T + t) * a.H + h * G + u16, gv, kg, m_run, l_part, O);
     cur ^= 1;
   }
 
   if constexpr (SEL) return;
   float lt;
   if (TRACE) {
-    lt = trace_merge<D>(a, ((int64_t)b * a.T + t) * a.H + h * G + u16, gv, kg, m_run, O);
+    lt = trace_merge<D, true>(a, ((int64_t)b * a.T + t) * a.H + h * G + u16, gv, kg, m_run, O);
   } else {
     lt = add_xor32(add_xor16(l_part));
   }
@@ -1049,7 +1064,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
 #pragma unroll
     for (int n = 0; n < ND; ++n)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Io<TIn>::st(op + 16 * n + 4 * kg + r, O[n][r] * inv);
+      for (int r = 0; r < 4; ++r) Io<TIn>::st(op + odim<true>(n, 4 * kg + r), O[n][r] * inv);
     if (kg == 0) {
       a.gmax[hq] = m_run;
       a.gsum[hq] = lt;
