@@ -234,15 +234,22 @@ struct TileStage {
     }
   }
   // V^T fragments: nodes c0 .. c0+3 (one quad, c0 % 4 == 0) of the staged
-  // block at d = 16n + u16: the 16 lanes of a lane group read 128
+  // block, output tiles 2j and 2j + 1 at dims 32j + 2 u16 and 32j + 2 u16 + 1
+  // (odim<true>) in one 16-byte read: the 16 lanes of a lane group read 256
   // contiguous bytes (no bank conflicts)
   __device__ __forceinline__ void vread(s16x4 (&vh)[D / 16], s16x4 (&vl)[D / 16], int c0,
                                         int u16) const {
 #pragma unroll
-    for (int n = 0; n < D / 16; ++n) {
-      const int e = (c0 >> 2) * 4 * D + (16 * n + u16) * 4;
-      vh[n] = *(const s16x4*)(slot + St::OFF_V + e * 2);
-      if (PREC) vl[n] = *(const s16x4*)(slot + St::OFF_VL + e * 2);
+    for (int j = 0; j < D / 32; ++j) {
+      const int e = (c0 >> 2) * 4 * D + (32 * j + 2 * u16) * 4;
+      const uint4 w = *(const uint4*)(slot + St::OFF_V + e * 2);
+      vh[2 * j] = __builtin_bit_cast(s16x4, make_uint2(w.x, w.y));
+      vh[2 * j + 1] = __builtin_bit_cast(s16x4, make_uint2(w.z, w.w));
+      if (PREC) {
+        const uint4 wl = *(const uint4*)(slot + St::OFF_VL + e * 2);
+        vl[2 * j] = __builtin_bit_cast(s16x4, make_uint2(wl.x, wl.y));
+        vl[2 * j + 1] = __builtin_bit_cast(s16x4, make_uint2(wl.z, wl.w));
+      }
     }
   }
 };
@@ -573,8 +580,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
     }
     wait_copies();  // no copy into the slot is left in flight past the level
     if (TRACE)
-      trace_store<D>(a, l, ((int64_t)b * a.T + t) * a.H + h * G + u16, u16 < G, kg, m_run,
-                     l_part, O);
+      trace_store<D, true>(a, l, ((int64_t)b * a.T + t) * a.H + h * G + u16, u16 < G, kg, m_run,
+                           l_part, O);
     cur ^= 1;
   }
 
@@ -582,7 +589,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
   // final normalisation (src/parallel.py:321-363): out = o / s
   float lt;
   if (TRACE) {
-    lt = trace_merge<D>(a, ((int64_t)b * a.T + t) * a.H + h * G + u16, u16 < G, kg, m_run, O);
+    lt = trace_merge<D, true>(a, ((int64_t)b * a.T + t) * a.H + h * G + u16, u16 < G, kg, m_run, O);
   } else {
     lt = add_xor32(add_xor16(l_part));
   }
@@ -592,7 +599,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
 #pragma unroll
     for (int n = 0; n < ND; ++n)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Io<TIn>::st(op + 16 * n + 4 * kg + r, O[n][r] / lt);
+      for (int r = 0; r < 4; ++r) Io<TIn>::st(op + odim<true>(n, 4 * kg + r), O[n][r] / lt);
     if (kg == 0) {
       a.gmax[hq] = m_run;
       a.gsum[hq] = lt;
@@ -1372,15 +1379,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
         pl[r] = PREC ? f_to_bfs(p[r] - bf_to_f(hb)) : (short)0;
       }
       const int vn = node0 + (4 * kg < CRU ? 4 * kg : 0);
-      const int64_t vbase = (int64_t)(vn >> 4) * 16 * D + ((vn & 15) >> 2) * 4 * D + u16 * 4;
+      // dims 32j + 2 u16 and 32j + 2 u16 + 1 (tiles 2j, 2j + 1): 16 bytes
+      const int64_t vbase = (int64_t)(vn >> 4) * 16 * D + ((vn & 15) >> 2) * 4 * D + u16 * 8;
 #pragma unroll
-      for (int n = 0; n < ND; ++n) {
-        const s16x4 vf = *(const s16x4*)(VH + vbase + (int64_t)n * 64);
-        O[n] = mma16(vf, ph, O[n]);
+      for (int j = 0; j < ND / 2; ++j) {
+        const uint4 w = *(const uint4*)(VH + vbase + (int64_t)j * 128);
+        const s16x4 v0 = __builtin_bit_cast(s16x4, make_uint2(w.x, w.y));
+        const s16x4 v1 = __builtin_bit_cast(s16x4, make_uint2(w.z, w.w));
+        O[2 * j] = mma16(v0, ph, O[2 * j]);
+        O[2 * j + 1] = mma16(v1, ph, O[2 * j + 1]);
         if (PREC) {
-          const s16x4 vfl = *(const s16x4*)(VL + vbase + (int64_t)n * 64);
-          O[n] = mma16(vf, pl, O[n]);
-          O[n] = mma16(vfl, ph, O[n]);
+          const uint4 wl = *(const uint4*)(VL + vbase + (int64_t)j * 128);
+          const s16x4 l0 = __builtin_bit_cast(s16x4, make_uint2(wl.x, wl.y));
+          const s16x4 l1 = __builtin_bit_cast(s16x4, make_uint2(wl.z, wl.w));
+          O[2 * j] = mma16(v0, pl, O[2 * j]);
+          O[2 * j] = mma16(l0, ph, O[2 * j]);
+          O[2 * j + 1] = mma16(v1, pl, O[2 * j + 1]);
+          O[2 * j + 1] = mma16(l1, ph, O[2 * j + 1]);
         }
       }
     }
@@ -1388,7 +1403,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
       float Ml, Ll;
       f32x4 Ol[ND];
       merge_waves(Ml, Ll, Ol);
-      if (wvh == 0) trace_store<D>(a, l, hq, gv, kg, Ml, kg == 0 ? Ll : 0.f, Ol);
+      if (wvh == 0) trace_store<D, true>(a, l, hq, gv, kg, Ml, kg == 0 ? Ll : 0.f, Ol);
     }
     cur ^= 1;
   }
@@ -1397,7 +1412,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
   float M, lt;
   if (TRACE) {
     if (wvh != 0) return;
-    lt = trace_merge<D>(a, hq, gv, kg, M, O);
+    lt = trace_merge<D, true>(a, hq, gv, kg, M, O);
   } else {
     merge_waves(M, lt, O);
     if (wvh != 0) return;
@@ -1408,7 +1423,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 32 && 
 #pragma unroll
     for (int n = 0; n < ND; ++n)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Io<TIn>::st(op + 16 * n + 4 * kg + r, O[n][r] * inv);
+      for (int r = 0; r < 4; ++r) Io<TIn>::st(op + odim<true>(n, 4 * kg + r), O[n][r] * inv);
     if (kg == 0) {
       a.gmax[hq] = M;
       a.gsum[hq] = lt;
