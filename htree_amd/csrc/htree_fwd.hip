@@ -735,7 +735,6 @@ struct WaveLdsR {
   f32x4 st[16][64];  // S^T of every tile, one f32x4 per lane
   int32_t par[2][kMaxTK];
   float imp[256];
-  float xrow[64];
   unsigned long long selmask[4];
   float lvl_max;     // the level's max score of this wave's heads (KV-head pairs)
 };
@@ -959,17 +958,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
       }
       return S;
     };
-    float gmx = -INFINITY;
-    for (int tau = 0; tau < nt; ++tau) {
-      const f32x4 S = masked(tau);
-      gmx = fmaxf(fmaxf(gmx, fmaxf(S[0], S[1])), fmaxf(S[2], S[3]));
+    float gmx = lmax;  // the bottom level accumulates every candidate: the scores' max
+    if (upper) {
+      gmx = -INFINITY;
+      for (int tau = 0; tau < nt; ++tau) {
+        const f32x4 S = masked(tau);
+        gmx = fmaxf(fmaxf(gmx, fmaxf(S[0], S[1])), fmaxf(S[2], S[3]));
+      }
     }
-    W.xrow[u16 * 4 + kg] = gmx;
-    wave_sync();
-    {
-      const float4 x4 = *(const float4*)(&W.xrow[u16 * 4]);
-      gmx = fmaxf(fmaxf(x4.x, x4.y), fmaxf(x4.z, x4.w));
-    }
+    gmx = max_xor32(max_xor16(gmx));  // over the lane groups (candidates) of the head
     if (TRACE) {
       m_run = -INFINITY;
       l_part = 0.f;
