@@ -844,9 +844,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
     const uint16_t* VH = P.vh + hrow * D;
     const uint16_t* VL = PREC ? P.vl + hrow * D : nullptr;
     const int32_t* pc = W.par[cur];
-    auto node0_of = [&](int tau) {
+    auto node0_of = [&](int tau) {  // (the list is in pv: lane s holds parent s)
       const int s = wide ? (tau << 4) >> crlg : tau;
-      return (pc[s] << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0);
+      return (__builtin_amdgcn_readlane(pv, s) << crlg) + (wide ? ((tau << 4) & (CR - 1)) : 0);
     };
     auto kload = [&](int tau, bf16x8 (&kh)[KS], bf16x8 (&kl)[KS]) {
       const int posk = wide ? (tau << 4) + u16 : (tau << crlg) + u16;
