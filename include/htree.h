@@ -2,8 +2,11 @@
  * htree.h -- C ABI of the MI355X (gfx950) hierarchical tree sparse attention.
  *
  * Every pointer argument is a DEVICE pointer unless stated otherwise; the
- * library never allocates device memory on these entry points and keeps no
- * pointer after it returns.  Work is enqueued on `stream` (a hipStream_t
+ * library allocates no device memory on these entry points (except the
+ * forward entry points of split-selection configurations, see kv_share,
+ * which take stream-ordered scratch with hipMallocAsync and free it with
+ * hipFreeAsync on the same stream) and keeps no pointer after it returns.
+ * Work is enqueued on `stream` (a hipStream_t
  * passed as void*, NULL = the default stream) and is stream-ordered; the
  * entry points do not synchronise.
  *
