@@ -140,6 +140,24 @@ def test_forward_skewed_sample():
     print(rep, flush=True)
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+def test_forward_clustered_importances(dtype):
+    """Keys of small spread (0.05 N(0,1)): every candidate's importance lies
+    within a few percent of the others', so many keys share the top 16 bits
+    of the selection threshold and the radix select's low 15 bits decide.
+    Selections against the oracle (tie band and exact ties as everywhere)."""
+    B, T, H, Hkv, D, CR, TK, MTN = 1, 6000, 32, 2, 128, 16, 16, 128
+    q, k, v = inputs(B, T, H, Hkv, D, dtype, 78)
+    k = (k.float() * 0.05).to(k.dtype)
+    out, par, gmax, gsum, ctx = run_fwd(q, k, v, CR, TK, MTN)
+    assert np.all(np.isfinite(out))
+    rng = np.random.default_rng(2)
+    rows = np.stack([np.zeros(300, int), np.sort(rng.choice(T, 300, replace=False))], 1)
+    rep = check_forward(q, k, v, CR, TK, MTN, dtype, rows=rows, out_dev=out, parents_dev=par,
+                        gmax_dev=gmax, gsum_dev=gsum)
+    print(rep, flush=True)
+
+
 def test_forward_deterministic():
     q, k, v = inputs(1, 3000, 16, 2, 128, "bfloat16", 9)
     a = run_fwd(q, k, v, 16, 16, 128)
