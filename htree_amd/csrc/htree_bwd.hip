@@ -1797,7 +1797,12 @@ struct DqArgs {
 };
 
 // rotation of a dq^T accumulator (C layout: d = 16n + 4kg + r, head u16)
-// by the angle whose cos/sin (length D/2) are c / sn: x <- R(x, angle)
+// by the angle whose cos/sin (length D/2) are c / sn: x <- R(x, angle).
+// Each pair is turned in place (lo' = lo c - hi s, hi' = hi c + lo s, the
+// products hi s and lo s rounded first, then one fma each): written in C the
+// compiler gives the results new registers, and inside the per-slot loop of
+// the dq passes that costs one register move per value at every turn (32 at
+// D = 128).
 template <int D>
 __device__ __forceinline__ void rot_acc(f32x4 (&x)[D / 16], const float* c, const float* sn,
                                         int kg) {
@@ -1810,9 +1815,15 @@ __device__ __forceinline__ void rot_acc(f32x4 (&x)[D / 16], const float* c, cons
     const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float lo = x[n][r], hi = x[n + ND / 2][r];
-      x[n][r] = lo * cc[r] - hi * ss[r];
-      x[n + ND / 2][r] = lo * ss[r] + hi * cc[r];
+      float lo = x[n][r], hi = x[n + ND / 2][r], ta, tb;
+      asm("v_mul_f32 %2, %1, %4\n\t"
+          "v_mul_f32 %3, %0, %4\n\t"
+          "v_fma_f32 %0, %0, %5, -%2\n\t"
+          "v_fma_f32 %1, %1, %5, %3"
+          : "+v"(lo), "+v"(hi), "=&v"(ta), "=&v"(tb)
+          : "v"(ss[r]), "v"(cc[r]));
+      x[n][r] = lo;
+      x[n + ND / 2][r] = hi;
     }
   }
 }
