@@ -2591,20 +2591,24 @@ static int backward_t(const htree_dims* d, const BwdPlan& BP, float scale, const
     a.scale = scale;
     // LDS sized for the lists and positions: one-wave-per-group forwards
     // (64, 64 tiles), the reference's default regime (512, 8192), beyond
-    // (1024, 16384), and the split selection's larger candidate sets
-    // (1024, 65536; D <= 128, which make_plan enforces)
+    // (1024, 16384), and the split selection's longer lists and larger
+    // candidate sets (2048, 65536; D <= 128, which make_plan enforces)
     const dim3 grid((unsigned)((groups + 3) / 4));
     const int64_t npos = (int64_t)d->top_k << P.cr_log2;
     if (!P.wide)
       hipLaunchKernelGGL((dq_kernel<D, PREC, T, kMaxTK, kMaxTiles * 16>), grid, dim3(256), 0, st, a);
     else if (d->top_k <= 512 && npos <= kWideMidPos)
       hipLaunchKernelGGL((dq_kernel<D, PREC, T, 512, kWideMidPos>), grid, dim3(256), 0, st, a);
-    else if (npos <= kWideMaxPos)
+    else if (d->top_k <= kWideMaxTK && npos <= kWideMaxPos)
       hipLaunchKernelGGL((dq_kernel<D, PREC, T, kWideMaxTK, kWideMaxPos>), grid, dim3(256), 0, st, a);
-    else if constexpr (D <= 128)
-      hipLaunchKernelGGL((dq_kernel<D, PREC, T, kWideMaxTK, kSplitMaxPos>), grid, dim3(256), 0, st, a);
-    else
+    else if constexpr (D <= 128) {
+      if (d->top_k <= kWideMaxTK)
+        hipLaunchKernelGGL((dq_kernel<D, PREC, T, kWideMaxTK, kSplitMaxPos>), grid, dim3(256), 0, st, a);
+      else
+        hipLaunchKernelGGL((dq_kernel<D, PREC, T, kSplitMaxTK, kSplitMaxPos>), grid, dim3(256), 0, st, a);
+    } else {
       return HTREE_EUNSUPPORTED;
+    }
   }
   hipError_t e = hipGetLastError();
   if (e == hipSuccess) e = ev_err;

@@ -33,8 +33,11 @@ constexpr int kWideMaxTK = 1024;
 // It takes KV-head shares above 4 (query groups above 64 heads), candidate
 // sets above kWideMaxPos, and the shares whose in-block importance arrays
 // do not fit one block's LDS.
+// It also takes every top_k above kWideMaxTK (lists of up to kSplitMaxTK
+// parents, held in LDS sized at launch).
 constexpr int kSplitMaxShare = 64;     // query groups of up to 1024 heads
 constexpr int kSplitMaxPos = 65536;    // top_k * CR
+constexpr int kSplitMaxTK = 2048;
 
 // ---------------------------------------------------------------- plan
 // Packed operand tree, per level l (all bf16, Np = N rounded up to 16):

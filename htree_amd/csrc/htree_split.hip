@@ -93,11 +93,12 @@ __global__ __launch_bounds__(256) void split_top_kernel(const SplitArgs a) {
 // ascending tile order, each tile's scores for the part's heads, the running
 // max over the tiles so far, and sum_g exp(s - running max) per position
 // (the wide forward's importance pass, src/naive.py:204-205 per part).
-template <int D, bool PREC, typename TIn>
+// MAXTK: list capacity in LDS (kWideMaxTK, or kSplitMaxTK at D <= 128)
+template <int D, bool PREC, typename TIn, int MAXTK>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2))) void split_imp_kernel(
     const SplitArgs a) {
   constexpr int KS = D / 32, HALF = D / 2;
-  __shared__ int32_t lists[kWavesPerBlock][kWideMaxTK];
+  __shared__ int32_t lists[kWavesPerBlock][MAXTK];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int u16 = lane & 15, kg = lane >> 4;
   const int G = a.G, CR = a.CR, crlg = a.crlg, TK = a.TK;
@@ -186,7 +187,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
 template <int C, int NWV>
 __global__ __launch_bounds__(64 * NWV) void split_select_kernel(const SplitArgs a) {
   constexpr int NT = 64 * NWV;
-  __shared__ int32_t pc[kWideMaxTK];
+  __shared__ int32_t pc[kSplitMaxTK];
   __shared__ int32_t red[4 * BlockSelect<C, NWV>::S];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int CR = a.CR, crlg = a.crlg, TK = a.TK;
@@ -254,13 +255,13 @@ __global__ __launch_bounds__(64 * NWV) void split_select_kernel(const SplitArgs 
 // down are skipped; the others join one online softmax (the bottom level
 // joins whole), as the wide forward's accumulation pass does.  TRACE: every
 // level from an empty state, its state stored, then the merge of
-// src/naive.py:215-231.
-template <int D, bool PREC, typename TIn, bool TRACE>
+// src/naive.py:215-231.  MAXTK: list capacity in LDS, as split_imp_kernel.
+template <int D, bool PREC, typename TIn, bool TRACE, int MAXTK>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2))) void split_accum_kernel(
     const SplitArgs a) {
   constexpr int KS = D / 32, ND = D / 16, HALF = D / 2;
   constexpr int SWW = kSplitMaxPos / 32;
-  __shared__ int32_t lists[kWavesPerBlock][2][kWideMaxTK];
+  __shared__ int32_t lists[kWavesPerBlock][2][MAXTK];
   __shared__ uint32_t selw[kWavesPerBlock][SWW];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int u16 = lane & 15, kg = lane >> 4;
@@ -495,7 +496,7 @@ int64_t split_scratch_bytes(const htree_dims* d, const Plan& P, bool with_lists)
   return bytes;
 }
 
-template <int D, bool PREC, typename TIn>
+template <int D, bool PREC, typename TIn, int MAXTK>
 static void launch_split(const SplitArgs& base, const Plan& P, hipStream_t st, bool sel,
                          bool trace) {
   SplitArgs a = base;
@@ -506,7 +507,7 @@ static void launch_split(const SplitArgs& base, const Plan& P, hipStream_t st, b
   const unsigned sblocks = (unsigned)(rows / a.share);
   for (int l = P.L - 1; l >= 1; --l) {
     a.level = l;
-    hipLaunchKernelGGL((split_imp_kernel<D, PREC, TIn>), dim3(wblocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((split_imp_kernel<D, PREC, TIn, MAXTK>), dim3(wblocks), dim3(256), 0, st, a);
     if (a.npos <= 8192)
       hipLaunchKernelGGL((split_select_kernel<32, 4>), dim3(sblocks), dim3(256), 0, st, a);
     else if (a.npos <= 16384)
@@ -518,20 +519,32 @@ static void launch_split(const SplitArgs& base, const Plan& P, hipStream_t st, b
   }
   if (sel) return;
   if (trace)
-    hipLaunchKernelGGL((split_accum_kernel<D, PREC, TIn, true>), dim3(wblocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((split_accum_kernel<D, PREC, TIn, true, MAXTK>), dim3(wblocks), dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((split_accum_kernel<D, PREC, TIn, false>), dim3(wblocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((split_accum_kernel<D, PREC, TIn, false, MAXTK>), dim3(wblocks), dim3(256), 0, st, a);
+}
+
+// lists above kWideMaxTK parents (D <= 128, which make_plan enforces) take
+// the instances with kSplitMaxTK-entry lists in LDS (96 KB per accumulation
+// block at 2048: one block per CU)
+template <int D, bool PREC, typename TIn>
+static void launch_split_tk(const SplitArgs& a, const Plan& P, hipStream_t st, bool sel,
+                            bool trace) {
+  if constexpr (D <= 128) {
+    if (a.TK > kWideMaxTK) return launch_split<D, PREC, TIn, kSplitMaxTK>(a, P, st, sel, trace);
+  }
+  launch_split<D, PREC, TIn, kWideMaxTK>(a, P, st, sel, trace);
 }
 
 template <int D>
 static void launch_split_d(int dtype, const SplitArgs& a, const Plan& P, hipStream_t st, bool sel,
                            bool trace) {
   if (dtype == HTREE_BF16)
-    launch_split<D, false, __bf16>(a, P, st, sel, trace);
+    launch_split_tk<D, false, __bf16>(a, P, st, sel, trace);
   else if (dtype == HTREE_F16)
-    launch_split<D, true, _Float16>(a, P, st, sel, trace);
+    launch_split_tk<D, true, _Float16>(a, P, st, sel, trace);
   else
-    launch_split<D, true, float>(a, P, st, sel, trace);
+    launch_split_tk<D, true, float>(a, P, st, sel, trace);
 }
 
 int split_forward(const htree_dims* d, const Plan& P, float scale, const void* q,
@@ -544,6 +557,8 @@ int split_forward(const htree_dims* d, const Plan& P, float scale, const void* q
   // grid sizes of the launches (blocks of 4 rows, of one row per group and
   // of 256 list entries) stay below 2^31
   if ((rows + 3) / 4 > INT32_MAX || rows * d->top_k / 256 + 1 > INT32_MAX) return HTREE_EUNSUPPORTED;
+  // the kernels' list capacity (make_plan refuses the rest before this)
+  if (d->top_k > (d->D <= 128 ? kSplitMaxTK : kWideMaxTK)) return HTREE_EUNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;
   const bool own_lists = parents == nullptr;
   const int64_t bytes = split_scratch_bytes(d, P, own_lists);

@@ -39,18 +39,20 @@ int make_plan(const htree_dims* d, Plan* p) {
   const int64_t max_tiles = (int64_t)d->top_k * (CR > 16 ? CR : 16) / 16;
   const bool wide = max_tiles > kMaxTiles || d->top_k > kMaxTK;
   if ((d->D != 32 && d->D != 64 && d->D != 128 && d->D != 256) || d->H / d->H_kv > 16 || CR < 4 ||
-      CR > 128 || d->top_k > kWideMaxTK || npos > kSplitMaxPos)
+      CR > 128 || d->top_k > kSplitMaxTK || npos > kSplitMaxPos)
     return HTREE_EUNSUPPORTED;
-  // above kWideMaxPos positions the backward's recomputing dq pass holds a
-  // wave's position bits in LDS beside its D-wide tiles: D <= 128 there
-  if (npos > kWideMaxPos && d->D > 128) return HTREE_EUNSUPPORTED;
+  // above kWideMaxPos positions or kWideMaxTK parents the backward's
+  // recomputing dq pass holds a wave's list and position bits in LDS beside
+  // its D-wide tiles: D <= 128 there
+  if ((npos > kWideMaxPos || d->top_k > kWideMaxTK) && d->D > 128) return HTREE_EUNSUPPORTED;
   // Shared selections over KV-head pairs: the paired waves of the
   // one-wave-per-group forwards, or the two parts of the wide forward's
   // block; over KV-head quads: the four parts of the wide forward's block,
   // at every level size, while every part's importances fit one block's
-  // 160 KB of LDS.  Shares above 4, candidate sets above kWideMaxPos and
-  // the pairs / quads that do not fit take the split selection.
-  bool split = d->kv_share > 4 || npos > kWideMaxPos;
+  // 160 KB of LDS.  Shares above 4, candidate sets above kWideMaxPos, lists
+  // above kWideMaxTK and the pairs / quads that do not fit take the split
+  // selection.
+  bool split = d->kv_share > 4 || npos > kWideMaxPos || d->top_k > kWideMaxTK;
   if (d->kv_share == 2 && wide &&
       wide_lds(d->top_k, (int)npos, (int)max_tiles, d->D, 2).bytes > 160 * 1024)
     split = true;
@@ -423,12 +425,12 @@ const char* htree_strerror(int status) {
              "and rope_rows >= top_k_per_layer * compression_rate, rope_rows > compression_rate";
     case HTREE_EUNSUPPORTED:
       return "configuration outside this HIP build: needs D in {32,64,128,256}, H/H_kv <= 16 "
-             "(query groups of up to 32 or 64 heads over kv_share 2 or 4 copies of each KV head; "
-             "kv_share 4 also needs the wide forward's four importance arrays in 160 KB of LDS), "
-             "4 <= compression_rate <= 128, top_k_per_layer <= 1024 and "
-             "top_k_per_layer * compression_rate <= 16384 (where top_k_per_layer > 64 or "
-             "top_k_per_layer * max(compression_rate,16) / 16 > 64); the backward also needs "
-             "B * T * H_kv * min(top_k_per_layer, parents of a level) < 2^31 per level";
+             "per kernel KV head (query groups of up to 1024 heads through kv_share <= 64 copies "
+             "of each KV head), 4 <= compression_rate <= 128, top_k_per_layer <= 2048 and "
+             "top_k_per_layer * compression_rate <= 65536, with D <= 128 where "
+             "top_k_per_layer > 1024 or top_k_per_layer * compression_rate > 16384; the "
+             "backward also needs B * T * H_kv * min(top_k_per_layer, parents of a level) < 2^31 "
+             "per level";
     case HTREE_EWORKSPACE: return "workspace smaller than htree_tree_workspace_bytes()";
     case HTREE_ESCRATCH:
       return "backward needs more scratch than htree_backward_noalloc's device array "

@@ -9,8 +9,9 @@ Differences, all deliberate:
     (top_k % 64 == 0, top_k % compression_rate == 0, :923,1019) do not apply.
   * limits of this HIP build (AssertionError): max(K, V) <= 256 (K even),
     H / H_kv <= 1024, 4 <= compression_rate <= 128,
-    top_k_per_layer <= 1024 and top_k_per_layer * compression_rate <= 65536
-    candidates per level (16384 for max(K, V) = 256).
+    top_k_per_layer <= 2048 and top_k_per_layer * compression_rate <= 65536
+    candidates per level (top_k_per_layer <= 1024 and 16384 candidates for
+    max(K, V) > 128).
   * a query group of G > 16 heads (the reference pads it to G_PAD,
     src/parallel.py:1023) runs as s = 2 (G <= 32), 4 (G <= 64) or the power
     of two s >= G / 16 (up to 64) groups of ceil(G/s) heads over s copies of
@@ -18,9 +19,10 @@ Differences, all deliberate:
     KV head's dk / dv is the sum of its copies'.  A group that s does not
     divide gets zero query heads appended to its last copy (the kernels'
     group_pad): the forward leaves them out of the selection, the backward
-    gives them zero dO.  Shares above 4 and candidate sets above 16384 (or
-    a pair's / quad's importances beyond one block's LDS) run the split
-    selection: the parts meet through device memory level by level.
+    gives them zero dO.  Shares above 4, candidate sets above 16384, lists
+    of more than 1024 parents (or a pair's / quad's importances beyond one
+    block's LDS) run the split selection: the parts meet through device
+    memory level by level.
   * K != V (the reference carries V = v.shape[-1] apart from K,
     src/parallel.py:904), and head dims that are not a kernel head dim
     (32, 64, 128, 256; e.g. 16, or 96), run the kernels at one head dim D,
@@ -58,6 +60,8 @@ KERNEL_HEAD_DIMS = (32, 64, 128, 256)
 MAX_GROUP = 1024              # query heads per KV head (kernel shares up to 64)
 MAX_CANDIDATES = 65536        # top_k_per_layer * compression_rate
 MAX_CANDIDATES_D256 = 16384   # the same at head dim 256
+MAX_TOPK = 2048               # top_k_per_layer (above 1024: head dims <= 128)
+MAX_TOPK_D256 = 1024
 
 _rope_cache: Dict[Tuple, Tuple[torch.Tensor, torch.Tensor]] = {}
 
@@ -207,6 +211,12 @@ def _validate(q, k, v, compression_rate, max_top_nodes, top_k_per_layer):
     assert npos <= MAX_CANDIDATES_D256 or max(K, v.shape[3]) <= 128, (
         f"configuration outside this HIP build: above {MAX_CANDIDATES_D256} candidates per "
         f"level the head dim max(K, V) must be <= 128, got {max(K, v.shape[3])}")
+    assert top_k_per_layer <= MAX_TOPK, (
+        f"configuration outside this HIP build: top_k_per_layer <= {MAX_TOPK}, got "
+        f"{top_k_per_layer}")
+    assert top_k_per_layer <= MAX_TOPK_D256 or max(K, v.shape[3]) <= 128, (
+        f"configuration outside this HIP build: above top_k_per_layer {MAX_TOPK_D256} the "
+        f"head dim max(K, V) must be <= 128, got {max(K, v.shape[3])}")
     assert K % 2 == 0 and K > 0 and V > 0, "head dims must be positive, K even (RoPE pairs)"
     assert max(K, V) <= KERNEL_HEAD_DIMS[-1], (
         f"configuration outside this HIP build: needs max(K, V) <= {KERNEL_HEAD_DIMS[-1]}, "

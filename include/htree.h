@@ -48,8 +48,8 @@ enum htree_status {
                               D not in {32, 64, 128, 256}, G = H/H_kv > 16
                               (see kv_share for G <= 1024),
                               compression_rate outside [4, 128],
-                              top_k > 1024, top_k * compression_rate > 65536
-                              (> 16384 with D = 256),
+                              top_k > 2048, top_k * compression_rate > 65536
+                              (top_k > 1024 or more than 16384 with D = 256),
                               more than HTREE_MAX_LEVELS levels, or a
                               backward level of 2^31 or more entries
                               (B * T * H_kv * min(top_k, parents)) */

@@ -75,6 +75,11 @@ def test_compression_rate_128_accepted():
 
 
 def test_largest_candidate_sets_accepted():
+    # lists of 2048 parents (the split selection): 8192 and 32768 candidates
+    assert len(N.levels(dims(T=12000, H=16, H_kv=1, D=32, compression_rate=4, top_k=2048,
+                             max_top_nodes=8192, rope_rows=9216))) == 2
+    assert len(N.levels(dims(T=36000, H=16, H_kv=1, D=128, top_k=2048, max_top_nodes=32768,
+                             rope_rows=33792))) == 2
     # 16384 candidates per level: top_k 1024 at CR 16, top_k 512 at CR 32
     assert len(N.levels(dims(T=20000, H=8, top_k=1024, max_top_nodes=16384, rope_rows=17408))) == 2
     assert len(N.levels(dims(T=20000, H=8, compression_rate=32, top_k=512, max_top_nodes=512,
@@ -113,8 +118,10 @@ def test_shared_kv_heads_accepted():
     (dict(grad_dtype_code=3), N.HTREE_ESHAPE),         # not an htree_dtype
     (dict(grad_dtype_code=-1), N.HTREE_ESHAPE),
     (dict(D=16), N.HTREE_EUNSUPPORTED),
-    (dict(top_k=2048, compression_rate=4, max_top_nodes=128, rope_rows=16384),
-     N.HTREE_EUNSUPPORTED),                            # top_k > 1024
+    (dict(top_k=4096, compression_rate=4, max_top_nodes=128, rope_rows=16384),
+     N.HTREE_EUNSUPPORTED),                            # top_k > 2048
+    (dict(top_k=2048, compression_rate=4, max_top_nodes=128, rope_rows=8192, D=256),
+     N.HTREE_EUNSUPPORTED),                            # top_k > 1024: D <= 128
     (dict(top_k=1024, compression_rate=128, max_top_nodes=128, rope_rows=131072),
      N.HTREE_EUNSUPPORTED),                            # 131072 candidates per level
     (dict(top_k=512, compression_rate=64, max_top_nodes=128, rope_rows=32768, D=256),
@@ -195,6 +202,11 @@ def test_python_api_validates_like_reference():
         htree_amd.htree_forward(q, k, k, 64, 16, 1024)
     with pytest.raises(AssertionError, match="65536"):
         htree_amd.htree_forward(q, k, k, 128, 16, 1024)
+    # lists: up to 2048 parents, above 1024 at head dims <= 128
+    with pytest.raises(AssertionError, match="GPU"):
+        htree_amd.htree_forward(q, k, k, 4, 8192, 2048)
+    with pytest.raises(AssertionError, match="2048"):
+        htree_amd.htree_forward(q, k, k, 4, 8192, 4096)
     k256 = torch.zeros(1, 64, 1, 256)
     with pytest.raises(AssertionError, match="head dim"):
         htree_amd.htree_forward(torch.zeros(1, 64, 4, 256), k256, k256, 64, 16, 1024)

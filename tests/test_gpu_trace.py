@@ -41,6 +41,7 @@ CASES = [
     (1, 1500, 8, 2, 32, 4, 128, 256, "float32", 17),    # top_k 128: block-per-group kernel
     (1, 1500, 128, 1, 32, 16, 16, 64, "bfloat16", 18),  # G = 128: split selection
     (1, 1200, 100, 1, 64, 8, 16, 64, "float32", 19),    # G = 100: split, 4 padding heads
+    (1, 8500, 16, 1, 32, 4, 2048, 8192, "bfloat16", 20),  # top_k 2048: split, 2048 of <= 2129
 ]
 
 
@@ -57,10 +58,17 @@ def _np(t):
     return t.float().cpu().numpy()
 
 
-def check_levels(tr, fw, dtype, B, T, H):
-    """Device trace vs an oracle trace computed from the same parent lists."""
+def check_levels(tr, fw, dtype, B, T, H, npos=0):
+    """Device trace vs an oracle trace computed from the same parent lists.
+    npos: candidate positions per level (top_k * CR).  The device and the
+    oracle add a level's fp32 terms in different orders, each with rounding
+    of up to about n 2^-24 relative over n terms, so the layer_sum bar grows
+    with n above 2048 positions: at 8192 (the reference's default regime and
+    top_k 2048 at CR 4) the wide and the split forwards both reach 2.3e-4 to
+    2.9e-4 relative on 600 sampled rows, against 1e-5 at the median."""
     L = tr["num_layers"]
     worst = {}
+    sum_scale = max(1.0, npos / 2048)
     for l in range(L - 1, -1, -1):
         lt = tr["layers"][l]
         m, s, o = _np(lt.layer_max), _np(lt.layer_sum), _np(lt.layer_output)
@@ -74,7 +82,7 @@ def check_levels(tr, fw, dtype, B, T, H):
         full = ~empty
         atol, rtol = MAX_TOL[dtype]
         em = np.abs(m[full] - om[full]) / (atol + rtol * np.abs(om[full]))
-        es = np.abs(s[full] - osum[full]) / (SUM_RTOL[dtype] * osum[full])
+        es = np.abs(s[full] - osum[full]) / (SUM_RTOL[dtype] * sum_scale * osum[full])
         worst[l] = (float(em.max(initial=0)), float(es.max(initial=0)))
         assert np.all(em <= 1), f"level {l}: layer_max worst {em.max():.3f} of the bar"
         assert np.all(es <= 1), f"level {l}: layer_sum worst {es.max():.3f} of the bar"
@@ -108,7 +116,7 @@ def test_trace_matches_oracle(cfg):
     rows = orc.all_rows(B, T)
     fw = orc.forward(q.float().numpy(), tree, D ** -0.5, rows=rows,
                      forced=par.reshape(L, B * T, Hkv, TK), trace=True)
-    print(check_levels(tr, fw, dtype, B, T, H), flush=True)
+    print(check_levels(tr, fw, dtype, B, T, H, npos=TK * CR), flush=True)
     # merged state = the forward's global state
     ok, w = close(_np(tr["global_max"]), fw["gmax"].reshape(B, T, H), "float32")
     assert ok, f"global max worst {w:.3f}"
