@@ -78,6 +78,41 @@ __device__ __forceinline__ void rot_q(const float (&qf)[D / 32][8], const float*
   rope_frag<D>(qf, cosr, sinr, kg, qr);
 }
 
+// The query turned in place by the angle of cosr / sinr.  D >= 64: each pair
+// (lo, hi) in one lane becomes (lo c - hi s, hi c + lo s), the products
+// hi s and lo s rounded first, then one fma each: the arithmetic the
+// compiler emits for rope_frag, but written in place, since the C form gets
+// new registers for the turned query and pays a register move per value at
+// every turn of the scoring loop (32 at D = 128).
+template <int D>
+__device__ __forceinline__ void rot_by(float (&x)[D / 32][8], const float* __restrict__ cosr,
+                                       const float* __restrict__ sinr, int kg) {
+  if constexpr (D == 32) {
+    rope_frag<D>(x, cosr, sinr, kg, x);
+  } else {
+    constexpr int SPH = D / 64;
+#pragma unroll
+    for (int m = 0; m < SPH; ++m) {
+      const int i0 = dslot<D>(kg, m);
+      float c[8], s[8];
+      Io<float>::ld8(cosr + i0, c);
+      Io<float>::ld8(sinr + i0, s);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float lo = x[m][e], hi = x[m + SPH][e], ta, tb;
+        asm("v_mul_f32 %2, %1, %4\n\t"
+            "v_mul_f32 %3, %0, %4\n\t"
+            "v_fma_f32 %0, %0, %5, -%2\n\t"
+            "v_fma_f32 %1, %1, %5, %3"
+            : "+v"(lo), "+v"(hi), "=&v"(ta), "=&v"(tb)
+            : "v"(s[e]), "v"(c[e]));
+        x[m][e] = lo;
+        x[m + SPH][e] = hi;
+      }
+    }
+  }
+}
+
 template <int D>
 __device__ __forceinline__ void to_bf(const float (&x)[D / 32][8], bf16x8 (&h)[D / 32]) {
 #pragma unroll
@@ -371,12 +406,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
     int cur_slot = 0;
     auto frame_start = [&]() {
       qin.get(qr, a.scale);
-      rope_frag<D>(qr, a.cosb + (int64_t)apos * HALF, a.sinb + (int64_t)apos * HALF, kg, qr);
+      rot_by<D>(qr, a.cosb + (int64_t)apos * HALF, a.sinb + (int64_t)apos * HALF, kg);
       cur_slot = 0;
     };
     auto frame_to = [&](int s) {
       while (cur_slot < s) {
-        rope_frag<D>(qr, rot_m[0], rot_m[1], kg, qr);
+        rot_by<D>(qr, rot_m[0], rot_m[1], kg);
         ++cur_slot;
       }
     };
@@ -738,41 +773,6 @@ struct WaveLdsR {
   unsigned long long selmask[4];
   float lvl_max;     // the level's max score of this wave's heads (KV-head pairs)
 };
-
-// The query turned in place by the angle of cosr / sinr.  D >= 64: each pair
-// (lo, hi) in one lane becomes (lo c - hi s, hi c + lo s), the products
-// hi s and lo s rounded first, then one fma each: the arithmetic the
-// compiler emits for rope_frag, but written in place, since the C form gets
-// new registers for the turned query and pays a register move per value at
-// every turn of the scoring loop (32 at D = 128).
-template <int D>
-__device__ __forceinline__ void rot_by(float (&x)[D / 32][8], const float* __restrict__ cosr,
-                                       const float* __restrict__ sinr, int kg) {
-  if constexpr (D == 32) {
-    rope_frag<D>(x, cosr, sinr, kg, x);
-  } else {
-    constexpr int SPH = D / 64;
-#pragma unroll
-    for (int m = 0; m < SPH; ++m) {
-      const int i0 = dslot<D>(kg, m);
-      float c[8], s[8];
-      Io<float>::ld8(cosr + i0, c);
-      Io<float>::ld8(sinr + i0, s);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float lo = x[m][e], hi = x[m + SPH][e], ta, tb;
-        asm("v_mul_f32 %2, %1, %4\n\t"
-            "v_mul_f32 %3, %0, %4\n\t"
-            "v_fma_f32 %0, %0, %5, -%2\n\t"
-            "v_fma_f32 %1, %1, %5, %3"
-            : "+v"(lo), "+v"(hi), "=&v"(ta), "=&v"(tb)
-            : "v"(s[e]), "v"(c[e]));
-        x[m][e] = lo;
-        x[m + SPH][e] = hi;
-      }
-    }
-  }
-}
 
 // SEL: selection only (the reference's htree_recompute_selection_kernel,
 // src/parallel.py:1168): the parent lists of every level, no accumulation
