@@ -1798,12 +1798,15 @@ struct DqArgs {
 
 // rotation of a dq^T accumulator (C layout: d = 16n + 4kg + r, head u16)
 // by the angle whose cos/sin (length D/2) are c / sn: x <- R(x, angle).
-// Each pair is turned in place (lo' = lo c - hi s, hi' = hi c + lo s, the
-// products hi s and lo s rounded first, then one fma each): written in C the
-// compiler gives the results new registers, and inside the per-slot loop of
-// the dq passes that costs one register move per value at every turn (32 at
-// D = 128).
-template <int D>
+// INPLACE: each pair turned in place (lo' = lo c - hi s, hi' = hi c + lo s,
+// the products hi s and lo s rounded first, then one fma each, the same
+// operations the C form compiles to).  Written in C the compiler gives the
+// results new registers, and inside the per-slot loop of the dq passes that
+// costs one register move per value at every turn (32 at D = 128).  Only
+// for accumulators that VALU instructions wrote last: the assembly is
+// outside the compiler's wait-state accounting, which an MFMA-written
+// accumulator needs before a VALU read.
+template <int D, bool INPLACE = false>
 __device__ __forceinline__ void rot_acc(f32x4 (&x)[D / 16], const float* c, const float* sn,
                                         int kg) {
   constexpr int ND = D / 16;
@@ -1815,15 +1818,21 @@ __device__ __forceinline__ void rot_acc(f32x4 (&x)[D / 16], const float* c, cons
     const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      float lo = x[n][r], hi = x[n + ND / 2][r], ta, tb;
-      asm("v_mul_f32 %2, %1, %4\n\t"
-          "v_mul_f32 %3, %0, %4\n\t"
-          "v_fma_f32 %0, %0, %5, -%2\n\t"
-          "v_fma_f32 %1, %1, %5, %3"
-          : "+v"(lo), "+v"(hi), "=&v"(ta), "=&v"(tb)
-          : "v"(ss[r]), "v"(cc[r]));
-      x[n][r] = lo;
-      x[n + ND / 2][r] = hi;
+      if constexpr (INPLACE) {
+        float lo = x[n][r], hi = x[n + ND / 2][r], ta, tb;
+        asm("v_mul_f32 %2, %1, %4\n\t"
+            "v_mul_f32 %3, %0, %4\n\t"
+            "v_fma_f32 %0, %0, %5, -%2\n\t"
+            "v_fma_f32 %1, %1, %5, %3"
+            : "+v"(lo), "+v"(hi), "=&v"(ta), "=&v"(tb)
+            : "v"(ss[r]), "v"(cc[r]));
+        x[n][r] = lo;
+        x[n + ND / 2][r] = hi;
+      } else {
+        const float lo = x[n][r], hi = x[n + ND / 2][r];
+        x[n][r] = lo * cc[r] - hi * ss[r];
+        x[n + ND / 2][r] = lo * ss[r] + hi * cc[r];
+      }
     }
   }
 }
@@ -2169,7 +2178,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
         __builtin_amdgcn_global_load_lds(dsp + lane * 16, (lds_void*)(slot + St::OFF_DS), 16, 0, 0);
     };
     // into the frame of slot 0
-    rot_acc<D>(X, a.cosb + (int64_t)apos * HALF, a.sinb + (int64_t)apos * HALF, kg);
+    rot_acc<D, F16>(X, a.cosb + (int64_t)apos * HALF, a.sinb + (int64_t)apos * HALF, kg);
     int s = 0, chunk = 0, cur_slot = 0, ex = 0;
     int tau = next_tile(0, s, chunk);
     if (tau < nt) issue(s, chunk, ex);
@@ -2177,7 +2186,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
       int sn = 0, chn = 0;
       const int tn = next_tile(tau + 1, sn, chn);
       while (cur_slot < s) {  // ascending slots: the frame turns by -CR per slot
-        rot_acc<D>(X, rot_m[0], rot_m[1], kg);
+        rot_acc<D, F16>(X, rot_m[0], rot_m[1], kg);
         ++cur_slot;
       }
       const int node0 = (__builtin_amdgcn_readlane(pe, s) << crlg) + (chunk << 4);
@@ -2220,7 +2229,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
       chunk = chn;
     }
     while (cur_slot < np - 1) {
-      rot_acc<D>(X, rot_m[0], rot_m[1], kg);
+      rot_acc<D, F16>(X, rot_m[0], rot_m[1], kg);
       ++cur_slot;
     }
     // back to the query's frame: R(X, -c_t)
