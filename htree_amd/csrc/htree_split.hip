@@ -1,8 +1,9 @@
 // Split selection: the forward for configurations whose shared Top-K does
 // not fit one block (Plan::split): query groups of more than 64 heads (KV
 // heads shared by s = 8 .. 64 kernel groups of <= 16 heads), candidate
-// sets of more than 16384 positions per level, and the pairs / quads whose
-// importance arrays exceed one block's LDS.
+// sets of more than 16384 positions per level, lists of more than 1024
+// parents (top_k 2048), and the pairs / quads whose importance arrays
+// exceed one block's LDS.
 //
 // The reference scores, selects and accumulates a level in one kernel per
 // level with the whole group padded into one tile (src/parallel.py:537-867,
